@@ -1,0 +1,171 @@
+"""Forward-pass throughput of a KataGo network on one MI355X: evals/s at a fixed batch.
+
+Default workload: b18c384nbt (18 nested-bottleneck blocks, 384 trunk channels, 192 inner), fp16 GEMM operands
+with float accumulate, batch 32, 19x19, seeded synthetic weights and inputs (katago-rs_amd/synth.py). A step is
+one forward pass of the batch plus the readback of all outputs to the host and a sum over them, as the
+reference's bench does (crates/katago-nn-burn/examples/bench.rs:34-41); inputs are already in HBM when timing
+starts.
+
+Prints one JSON line. Besides the throughput it carries
+- "roofline": the dominant kernel class's algorithmic work per launch over its average launch time, measured
+  with HIP events around every kernel launch on the library's stream during a second timed region of the same
+  K steps (events need eager launches; the throughput region replays a HIP graph);
+- "cpu_baseline": the float32 CPU oracle on a bounded sample of the same workload, on this host's cores.
+"""
+
+import argparse
+import ctypes
+import importlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0, "f32": 157.3}  # MI355X dense MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--config", default="b18c384nbt")
+    ap.add_argument("--precision", default="f16", choices=["f16", "bf16", "f32"])
+    ap.add_argument("--batch", type=int, default=0, help="override the config's batch size")
+    ap.add_argument("--cpu-rows", type=int, default=4, help="rows in the CPU-baseline sample (0: skip)")
+    ap.add_argument("--cpu-threads", type=int, default=0, help="CPU-baseline threads (0: min(16, cores))")
+    ap.add_argument("--no-graph", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(json.dumps({"error": "this path runs on one GPU; the forward pass shards by independent batches "
+                                   "with no collective, so a multi-GPU figure is N independent copies. Use --gpus 1."}))
+        sys.exit(2)
+
+    kgx = importlib.import_module("katago-rs_amd")
+    synth = importlib.import_module("katago-rs_amd.synth")
+
+    arch_fn, batch = synth.CONFIGS[args.config]
+    if args.batch:
+        batch = args.batch
+    arch = arch_fn()
+    model = synth.write_model(arch, synth.CONFIG_SEEDS[args.config])
+    net = kgx.Net(model)
+    h = kgx.Handle(net, batch, args.precision, device=0)
+    if args.no_graph:
+        kgx.lib()  # graphs are on by default; eager launches only with profiling
+    sp, gl, me = synth.make_inputs(batch, 1234, meta=arch.meta_encoder)
+
+    # Inputs resident in HBM: copy them into the handle's device buffers once.
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    d_bin, d_glob, d_meta, _ = h.device_buffers()
+    assert hip.hipMemcpy(d_bin, sp.ctypes.data, sp.nbytes, 1) == 0
+    assert hip.hipMemcpy(d_glob, gl.ctypes.data, gl.nbytes, 1) == 0
+    if me is not None:
+        assert hip.hipMemcpy(d_meta, me.ctypes.data, me.nbytes, 1) == 0
+
+    out = np.empty((batch, net.row_len), np.float32)
+    checksum = 0.0
+
+    def step():
+        h.run(batch, out)  # forward + readback + wait
+        return float(out.sum(dtype=np.float64))
+
+    for _ in range(args.warmup):
+        checksum = step()
+    h.sync()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        checksum = step()
+    h.sync()
+    dt = time.perf_counter() - t0
+    ms_per_step = dt / args.steps * 1e3
+    evals_per_s = batch * args.steps / dt
+    if not np.isfinite(checksum):
+        raise RuntimeError("non-finite outputs")
+
+    # Second timed region: the same K steps launched eagerly with HIP events around every kernel.
+    h.profile(True)
+    h.profile_reset()
+    t1 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    prof_ms_per_step = (time.perf_counter() - t1) / args.steps * 1e3
+    prof = h.profile_read()
+    h.profile(False)
+    total_kernel_ms = sum(v["ms"] for v in prof.values())
+    classes = {}
+    for k, v in sorted(prof.items(), key=lambda kv: -kv[1]["ms"]):
+        n = max(v["launches"], 1)
+        avg_ms = v["ms"] / n
+        c = {"launches_per_step": v["launches"] / args.steps, "avg_us": avg_ms * 1e3,
+             "share": v["ms"] / total_kernel_ms if total_kernel_ms else 0.0}
+        if v["flops"] > 0:
+            c["tflops"] = v["flops"] / (v["ms"] * 1e-3) / 1e12
+        if v["bytes"] > 0:
+            c["gbs"] = v["bytes"] / (v["ms"] * 1e-3) / 1e9
+        classes[k] = c
+    dom = max(prof.items(), key=lambda kv: kv[1]["ms"])
+    dname, dv = dom
+    per_launch_ms = dv["ms"] / max(dv["launches"], 1)
+    if dv["flops"] > 0:
+        achieved = dv["flops"] / max(dv["launches"], 1) / (per_launch_ms * 1e-3) / 1e12
+        peak = PEAK_TFLOPS[args.precision]
+        roof = {"bound": "mfma", "kernel": dname, "achieved": achieved, "peak": peak, "unit": "TFLOP/s",
+                "frac": achieved / peak, "traffic": None,
+                "work_per_launch": dv["flops"] / max(dv["launches"], 1), "avg_launch_us": per_launch_ms * 1e3}
+    else:
+        achieved = dv["bytes"] / max(dv["launches"], 1) / (per_launch_ms * 1e-3) / 1e9
+        roof = {"bound": "hbm", "kernel": dname, "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
+                "frac": achieved / PEAK_HBM_GBS, "traffic": None,
+                "work_per_launch": dv["bytes"] / max(dv["launches"], 1), "avg_launch_us": per_launch_ms * 1e3}
+    h.close()
+
+    cpu = None
+    if args.cpu_rows > 0:
+        import oracle
+        threads = args.cpu_threads or min(16, os.cpu_count() or 1)
+        om = oracle.Model(model)
+        n = min(args.cpu_rows, batch)
+        om.forward(sp[:1], gl[:1], None if me is None else me[:1], dtype=np.float32, threads=threads)
+        t2 = time.perf_counter()
+        om.forward(sp[:n], gl[:n], None if me is None else me[:n], dtype=np.float32, threads=threads)
+        cdt = time.perf_counter() - t2
+        cpu = {"value": n / cdt, "unit": "evals/s", "cores": threads, "kind": "port",
+               "sample": f"{n} rows of the same workload through the float32 CPU oracle (direct convolution), "
+                         f"{cdt:.1f} s"}
+
+    res = {
+        "metric": f"evals/s {args.config} {args.precision} batch {batch} on 1 MI355X",
+        "value": evals_per_s,
+        "unit": "evals/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_per_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": args.precision,
+        "data": "synthetic: seeded random-init weights of the named architecture and seeded Bernoulli(0.3) inputs",
+        "config": {"workload": f"{args.config} forward pass, batch {batch}, 19x19, {args.precision} GEMM operands, "
+                               "float accumulate, one readback per batch", "batch": batch,
+                   "network": args.config},
+        "roofline": roof,
+        "cpu_baseline": cpu,
+        "kernels": classes,
+        "profiled_ms_per_step": prof_ms_per_step,
+        "checksum": checksum,
+    }
+    print(json.dumps(res))
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,145 @@
+/*
+ * kgx: the KataGo network forward pass on AMD Instinct MI355X (gfx950), as a C ABI.
+ *
+ * The entry points replace, one for one, what katago-nn-burn's backend does behind katago-core's
+ * `NeuralNet` trait (crates/katago-core/src/neuralnet/nninterface.rs:79-214), so that a thin FFI backend
+ * can implement that trait over them and leave NNEvaluator and `katago-rs analysis` unchanged.
+ * Plain pointers and sizes only. Every function returning int returns 0 on success and nonzero on error,
+ * with the message available from kg_last_error() on the calling thread.
+ *
+ * Threading: kg_net objects are immutable after loading and may be shared between threads. A kg_handle is
+ * used by one thread at a time (calls on one handle are serialized by a lock); different handles may run
+ * concurrently. kg_forward and kg_get_output block the calling thread until the batch's outputs are on the
+ * host, so callers run them on a helper thread when their own thread must not wait
+ * (crates/katago-nn-burn/src/backend.rs:735-753).
+ */
+#ifndef KGX_H
+#define KGX_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KG_PRECISION_F32 0  /* float operands, float accumulate (the f32 tier) */
+#define KG_PRECISION_F16 1  /* float16 GEMM operands, float accumulate and float residual streams */
+#define KG_PRECISION_BF16 2 /* bfloat16 GEMM operands, float accumulate and float residual streams */
+
+#define KG_MAX_POLICY_SIZE 362 /* NNPos::MAX_NN_POLICY_SIZE for 19x19 */
+
+typedef struct kg_net kg_net;
+typedef struct kg_handle kg_handle;
+
+/* Library version string. */
+const char* kg_version(void);
+
+/* The last error message of the calling thread ("" if none). */
+const char* kg_last_error(void);
+
+/* Number of visible GPUs. Replaces the device probing of `katago_nn_burn::device`
+ * (crates/katago-nn-burn/src/lib.rs:238-248). */
+int kg_device_count(int* count);
+
+/* Makes `device` current for this thread and initializes its runtime; a no-op when already open.
+ * Replaces NeuralNet::global_initialize (backend.rs:244-252). */
+int kg_device_open(int device);
+
+/* Parses a KataGo model file (binary or text floats, optionally gzip-compressed) from memory.
+ * Replaces NeuralNet::load_model_file (backend.rs:277-293): like it, a non-empty expected_sha256 is rejected
+ * ("expectedSha256 is not supported"), and a model version above 17 is an error. */
+int kg_net_load(const void* model_bytes, size_t len, const char* expected_sha256, kg_net** out);
+void kg_net_free(kg_net* net);
+
+/* The ModelDesc fields the engine reads (NeuralNet::get_model_desc, backend.rs:296-298). */
+typedef struct {
+  char name[128];
+  int model_version;
+  int num_input_channels;       /* spatial features (22 for v8+) */
+  int num_input_global_channels;/* 19 for v8+ */
+  int num_input_meta_channels;  /* 192 for human-SL nets, else 0 */
+  int num_policy_channels;      /* P */
+  int num_value_channels;       /* 3 */
+  int num_score_value_channels; /* S */
+  int num_ownership_channels;   /* 1 */
+  int trunk_num_channels;
+  int trunk_num_blocks;
+  long num_parameters;
+  float post_process_params[7]; /* td score, score mean, score stdev, lead, variance time, st value err, st score err */
+  int output_row_len;           /* P*362 + 3 + S + 361 floats per row of kg_forward's output */
+} kg_model_desc;
+int kg_net_desc(const kg_net* net, kg_model_desc* out);
+
+/* A device replica of the network with its own stream and workspace for up to max_batch rows.
+ * Replaces create_compute_context + create_compute_handle (backend.rs:300-390) with their checks:
+ * nn_x_len and nn_y_len must be 19 ("nnXLen and nnYLen must equal the network's posLen 19"), and
+ * inputs_use_nhwc must be 0 ("inputsUseNHWC = true unsupported"). precision is a KG_PRECISION_*. */
+int kg_handle_create(const kg_net* net, int device, int max_batch, int precision, int nn_x_len, int nn_y_len,
+                     int inputs_use_nhwc, kg_handle** out);
+void kg_handle_free(kg_handle* handle);
+
+/* Batch-shape buckets (BurnNeuralNet::with_batch_buckets, backend.rs:70-78): a batch of n rows runs as the
+ * smallest bucket in [n, max_batch] (padded_batch_size, backend.rs:82-84); padding rows hold stale inputs.
+ * Buckets <= 0 are dropped; count 0 clears them. */
+int kg_handle_set_batch_buckets(kg_handle* handle, const int* buckets, int count);
+int kg_padded_batch_size(const int* buckets, int count, int n, int max_batch);
+
+/* Whether the handle computes its GEMMs in a 16-bit type (NeuralNet::is_using_fp16, backend.rs:400-404). */
+int kg_handle_is_using_fp16(const kg_handle* handle);
+
+/* One forward pass of n rows (run_network, backend.rs:549-619): bin [n][C][19][19] NCHW float (after
+ * symmetry), global [n][G], meta [n][192] or NULL when the net takes none. Writes n rows of
+ * output_row_len floats: policy P x 362 (pass logit last in each channel), value 3, score S, ownership 361,
+ * all raw (no softmax / tanh), in the order of the reference's concatenated readback (backend.rs:588-597). */
+int kg_forward(kg_handle* handle, int n, const float* bin, const float* global, const float* meta, float* out);
+
+/* The handle's device input and output buffers (max_batch rows each, layouts as in kg_forward). A caller that
+ * fills them on the device can run kg_run without any host copy of the inputs. */
+int kg_handle_device_buffers(kg_handle* handle, float** bin, float** global, float** meta, float** out);
+
+/* The forward pass on the inputs already in the handle's device buffers. With out != NULL, also reads the n
+ * output rows back to `out` and waits for them; with out == NULL, only enqueues the work on the handle's stream
+ * (kg_sync waits). */
+int kg_run(kg_handle* handle, int n, float* out);
+int kg_sync(kg_handle* handle);
+
+/* The handle's stream (a hipStream_t), for callers that order their own device work after kg_run. */
+void* kg_handle_stream(kg_handle* handle);
+
+/* Per-row inputs of get_output (NNResultBuf fields read by copy_inputs, backend.rs:497-546). */
+typedef struct {
+  const float* row_spatial; /* [C][19][19] NCHW, before symmetry */
+  const float* row_global;  /* [G] */
+  const float* row_meta;    /* [192] or NULL */
+  int symmetry;             /* 0..7: bit 0 flipY, bit 1 flipX, bit 2 transpose */
+  float policy_optimism;
+} kg_row_input;
+
+/* NNOutput fields written by copy_outputs (backend.rs:622-731). white_owner_map may be NULL. */
+typedef struct {
+  float policy_probs[KG_MAX_POLICY_SIZE];
+  float white_win_prob, white_loss_prob, white_no_result_prob;
+  float white_score_mean, white_score_mean_sq, white_lead, var_time_left;
+  float shortterm_winloss_error, shortterm_score_error;
+  float* white_owner_map; /* [361] or NULL */
+} kg_nn_output;
+
+/* NeuralNet::get_output (backend.rs:410-464): copy_inputs (symmetry per row), the forward pass (padded to a
+ * bucket), one readback, copy_outputs (policy optimism mix, inverse symmetry, value / score unpacking by model
+ * version). n must be in [1, max_batch]. */
+int kg_get_output(kg_handle* handle, int n, const kg_row_input* rows, kg_nn_output* outputs);
+
+/* Kernel timing, for benchmarks: while enabled, kg_run / kg_forward launch eagerly and bracket every kernel
+ * with events on the handle's stream. kg_profile_read reports, per kernel class, the launch count, the
+ * summed duration in milliseconds and the summed algorithmic work (flops and bytes as defined per class).
+ * Returns the number of classes (at most max_classes are written); names are static strings. */
+int kg_profile_enable(kg_handle* handle, int enable);
+int kg_profile_reset(kg_handle* handle);
+int kg_profile_read(kg_handle* handle, const char** names, long* launches, double* ms, double* flops,
+                    double* bytes, int max_classes);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KGX_H */

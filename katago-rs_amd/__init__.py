@@ -1,0 +1,296 @@
+"""Python binding of libkgx (include/kgx.h), the KataGo forward pass on MI355X.
+
+This mirrors the reference backend's interface (crates/katago-nn-burn/src/backend.rs): a loaded model
+(`Net`, NeuralNet::load_model_file), a device handle (`Handle`, create_compute_context +
+create_compute_handle), the raw forward pass (`Handle.forward`, run_network) and `Handle.get_output`
+(copy_inputs / run_network / copy_outputs). It calls the C ABI through ctypes; there is no other compute path,
+and a missing or unbuilt library is an error.
+
+The package directory name is not a Python identifier; import it with
+``importlib.import_module("katago-rs_amd")`` after putting the repository root on ``sys.path``.
+"""
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libkgx.so")
+CSRC = os.path.join(HERE, "csrc")
+
+PRECISION_F32 = 0
+PRECISION_F16 = 1
+PRECISION_BF16 = 2
+PRECISIONS = {"f32": PRECISION_F32, "f16": PRECISION_F16, "bf16": PRECISION_BF16}
+
+HW = 361
+MAX_POLICY = 362
+
+# Every symbol the C header declares (include/kgx.h).
+EXPORTS = [
+    "kg_version", "kg_last_error", "kg_device_count", "kg_device_open", "kg_net_load", "kg_net_free", "kg_net_desc",
+    "kg_handle_create", "kg_handle_free", "kg_handle_set_batch_buckets", "kg_padded_batch_size",
+    "kg_handle_is_using_fp16", "kg_forward", "kg_handle_device_buffers", "kg_run", "kg_sync", "kg_handle_stream",
+    "kg_get_output", "kg_profile_enable", "kg_profile_reset", "kg_profile_read",
+]
+
+_lib = None
+
+
+def build(jobs: int = 4):
+    """Compiles libkgx.so for gfx950 with hipcc (katago-rs_amd/csrc/Makefile)."""
+    subprocess.run(["make", "-C", CSRC, f"-j{jobs}", "-s"], check=True)
+
+
+class KgError(RuntimeError):
+    pass
+
+
+class ModelDesc(ctypes.Structure):
+    _fields_ = [
+        ("name", ctypes.c_char * 128),
+        ("model_version", ctypes.c_int),
+        ("num_input_channels", ctypes.c_int),
+        ("num_input_global_channels", ctypes.c_int),
+        ("num_input_meta_channels", ctypes.c_int),
+        ("num_policy_channels", ctypes.c_int),
+        ("num_value_channels", ctypes.c_int),
+        ("num_score_value_channels", ctypes.c_int),
+        ("num_ownership_channels", ctypes.c_int),
+        ("trunk_num_channels", ctypes.c_int),
+        ("trunk_num_blocks", ctypes.c_int),
+        ("num_parameters", ctypes.c_long),
+        ("post_process_params", ctypes.c_float * 7),
+        ("output_row_len", ctypes.c_int),
+    ]
+
+
+class RowInput(ctypes.Structure):
+    _fields_ = [
+        ("row_spatial", ctypes.c_void_p),
+        ("row_global", ctypes.c_void_p),
+        ("row_meta", ctypes.c_void_p),
+        ("symmetry", ctypes.c_int),
+        ("policy_optimism", ctypes.c_float),
+    ]
+
+
+class NNOutput(ctypes.Structure):
+    _fields_ = [
+        ("policy_probs", ctypes.c_float * MAX_POLICY),
+        ("white_win_prob", ctypes.c_float),
+        ("white_loss_prob", ctypes.c_float),
+        ("white_no_result_prob", ctypes.c_float),
+        ("white_score_mean", ctypes.c_float),
+        ("white_score_mean_sq", ctypes.c_float),
+        ("white_lead", ctypes.c_float),
+        ("var_time_left", ctypes.c_float),
+        ("shortterm_winloss_error", ctypes.c_float),
+        ("shortterm_score_error", ctypes.c_float),
+        ("white_owner_map", ctypes.c_void_p),
+    ]
+
+
+def lib():
+    """The loaded libkgx.so. Raises if it has not been built: there is no fallback."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise KgError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() (make -C {CSRC})")
+        L = ctypes.CDLL(LIB_PATH)
+        vp, ci, cf = ctypes.c_void_p, ctypes.c_int, ctypes.c_float
+        L.kg_version.restype = ctypes.c_char_p
+        L.kg_last_error.restype = ctypes.c_char_p
+        L.kg_device_count.argtypes = [ctypes.POINTER(ci)]
+        L.kg_device_open.argtypes = [ci]
+        L.kg_net_load.argtypes = [vp, ctypes.c_size_t, ctypes.c_char_p, ctypes.POINTER(vp)]
+        L.kg_net_free.argtypes = [vp]
+        L.kg_net_desc.argtypes = [vp, ctypes.POINTER(ModelDesc)]
+        L.kg_handle_create.argtypes = [vp, ci, ci, ci, ci, ci, ci, ctypes.POINTER(vp)]
+        L.kg_handle_free.argtypes = [vp]
+        L.kg_handle_set_batch_buckets.argtypes = [vp, vp, ci]
+        L.kg_padded_batch_size.argtypes = [vp, ci, ci, ci]
+        L.kg_handle_is_using_fp16.argtypes = [vp]
+        L.kg_forward.argtypes = [vp, ci, vp, vp, vp, vp]
+        L.kg_handle_device_buffers.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.POINTER(vp),
+                                               ctypes.POINTER(vp)]
+        L.kg_run.argtypes = [vp, ci, vp]
+        L.kg_sync.argtypes = [vp]
+        L.kg_handle_stream.argtypes = [vp]
+        L.kg_handle_stream.restype = vp
+        L.kg_get_output.argtypes = [vp, ci, ctypes.POINTER(RowInput), ctypes.POINTER(NNOutput)]
+        L.kg_profile_enable.argtypes = [vp, ci]
+        L.kg_profile_reset.argtypes = [vp]
+        L.kg_profile_read.argtypes = [vp, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_long),
+                                      ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
+                                      ctypes.POINTER(ctypes.c_double), ci]
+        _ = cf
+        _lib = L
+    return _lib
+
+
+def _check(rc):
+    if rc != 0:
+        raise KgError(lib().kg_last_error().decode())
+
+
+def _ptr(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+def version() -> str:
+    return lib().kg_version().decode()
+
+
+def device_count() -> int:
+    c = ctypes.c_int()
+    _check(lib().kg_device_count(ctypes.byref(c)))
+    return c.value
+
+
+def padded_batch_size(buckets, n, max_batch) -> int:
+    b = np.ascontiguousarray(buckets, np.int32)
+    return lib().kg_padded_batch_size(_ptr(b), len(b), n, max_batch)
+
+
+class Net:
+    """A parsed KataGo model (NeuralNet::load_model_file)."""
+
+    def __init__(self, model_bytes: bytes, expected_sha256: str = ""):
+        self._h = None
+        h = ctypes.c_void_p()
+        buf = ctypes.create_string_buffer(model_bytes, len(model_bytes))
+        _check(lib().kg_net_load(buf, len(model_bytes), expected_sha256.encode(), ctypes.byref(h)))
+        self._h = h
+        d = ModelDesc()
+        _check(lib().kg_net_desc(self._h, ctypes.byref(d)))
+        self.desc = d
+        self.name = d.name.decode()
+        self.version = d.model_version
+        self.P = d.num_policy_channels
+        self.S = d.num_score_value_channels
+        self.row_len = d.output_row_len
+        self.num_input_channels = d.num_input_channels
+        self.num_global = d.num_input_global_channels
+        self.num_meta = d.num_input_meta_channels
+
+    def __del__(self):
+        if self._h:
+            lib().kg_net_free(self._h)
+            self._h = None
+
+
+class Handle:
+    """A device replica of a net (create_compute_context + create_compute_handle) for up to max_batch rows."""
+
+    def __init__(self, net: Net, max_batch: int, precision="f16", device: int = 0, nn_x_len: int = 19,
+                 nn_y_len: int = 19, inputs_use_nhwc: bool = False):
+        self._h = None
+        self.net = net
+        self.max_batch = max_batch
+        p = PRECISIONS[precision] if isinstance(precision, str) else int(precision)
+        h = ctypes.c_void_p()
+        _check(lib().kg_handle_create(net._h, device, max_batch, p, nn_x_len, nn_y_len, int(inputs_use_nhwc),
+                                      ctypes.byref(h)))
+        self._h = h
+
+    def close(self):
+        if self._h:
+            lib().kg_handle_free(self._h)
+            self._h = None
+
+    def __del__(self):
+        self.close()
+
+    @property
+    def is_using_fp16(self) -> bool:
+        return bool(lib().kg_handle_is_using_fp16(self._h))
+
+    def set_batch_buckets(self, buckets):
+        b = np.ascontiguousarray(buckets, np.int32)
+        _check(lib().kg_handle_set_batch_buckets(self._h, _ptr(b), len(b)))
+
+    def forward(self, spatial, glob, meta=None) -> np.ndarray:
+        """Raw output rows [n, row_len] for inputs spatial [n, C, 19, 19], glob [n, G] (meta [n, 192])."""
+        n = spatial.shape[0]
+        spatial = np.ascontiguousarray(spatial, np.float32)
+        glob = np.ascontiguousarray(glob, np.float32)
+        meta = None if meta is None else np.ascontiguousarray(meta, np.float32)
+        out = np.empty((n, self.net.row_len), np.float32)
+        _check(lib().kg_forward(self._h, n, _ptr(spatial), _ptr(glob), _ptr(meta), _ptr(out)))
+        return out
+
+    def device_buffers(self):
+        """Device pointers (bin, global, meta, out) of the handle's resident buffers."""
+        ptrs = [ctypes.c_void_p() for _ in range(4)]
+        _check(lib().kg_handle_device_buffers(self._h, *[ctypes.byref(p) for p in ptrs]))
+        return tuple(p.value for p in ptrs)
+
+    def run(self, n: int, out: np.ndarray = None):
+        """Forward pass on the inputs already in the device buffers; reads back into `out` when given."""
+        _check(lib().kg_run(self._h, n, _ptr(out)))
+
+    def sync(self):
+        _check(lib().kg_sync(self._h))
+
+    @property
+    def stream(self) -> int:
+        return lib().kg_handle_stream(self._h)
+
+    def get_output(self, rows, want_ownership=True):
+        """NeuralNet::get_output. rows: list of dicts with spatial [C,19,19], glob [G], meta [192] or None,
+        symmetry, policy_optimism. Returns a list of dicts of NNOutput fields."""
+        n = len(rows)
+        keep = []
+        arr = (RowInput * n)()
+        outs = (NNOutput * n)()
+        owners = []
+        for i, r in enumerate(rows):
+            sp = np.ascontiguousarray(r["spatial"], np.float32)
+            gl = np.ascontiguousarray(r["glob"], np.float32)
+            me = r.get("meta")
+            me = None if me is None else np.ascontiguousarray(me, np.float32)
+            keep += [sp, gl, me]
+            arr[i].row_spatial = _ptr(sp).value
+            arr[i].row_global = _ptr(gl).value
+            arr[i].row_meta = None if me is None else _ptr(me).value
+            arr[i].symmetry = int(r.get("symmetry", 0))
+            arr[i].policy_optimism = float(r.get("policy_optimism", 0.0))
+            own = np.zeros(HW, np.float32) if want_ownership else None
+            owners.append(own)
+            outs[i].white_owner_map = None if own is None else _ptr(own).value
+        _check(lib().kg_get_output(self._h, n, arr, outs))
+        res = []
+        for i in range(n):
+            o = outs[i]
+            res.append({
+                "policy": np.ctypeslib.as_array(o.policy_probs).copy(),
+                "white_win_prob": o.white_win_prob, "white_loss_prob": o.white_loss_prob,
+                "white_no_result_prob": o.white_no_result_prob, "white_score_mean": o.white_score_mean,
+                "white_score_mean_sq": o.white_score_mean_sq, "white_lead": o.white_lead,
+                "var_time_left": o.var_time_left, "shortterm_winloss_error": o.shortterm_winloss_error,
+                "shortterm_score_error": o.shortterm_score_error, "ownership": owners[i],
+            })
+        return res
+
+    # --- kernel timing ---
+    def profile(self, enable: bool):
+        _check(lib().kg_profile_enable(self._h, int(enable)))
+
+    def profile_reset(self):
+        _check(lib().kg_profile_reset(self._h))
+
+    def profile_read(self):
+        k = 32
+        names = (ctypes.c_char_p * k)()
+        launches = (ctypes.c_long * k)()
+        ms = (ctypes.c_double * k)()
+        flops = (ctypes.c_double * k)()
+        byts = (ctypes.c_double * k)()
+        n = lib().kg_profile_read(self._h, names, launches, ms, flops, byts, k)
+        if n < 0:
+            raise KgError("kg_profile_read failed")
+        return {names[i].decode(): {"launches": launches[i], "ms": ms[i], "flops": flops[i], "bytes": byts[i]}
+                for i in range(min(n, k))}

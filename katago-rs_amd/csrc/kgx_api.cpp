@@ -1,0 +1,388 @@
+// The C ABI (include/kgx.h): model loading, handles, the forward pass, and get_output with the reference's
+// input and output handling (crates/katago-nn-burn/src/backend.rs:410-731).
+#include "kgx.h"
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstring>
+#include <memory>
+#include <mutex>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "kgx_model.h"
+#include "kgx_net.h"
+
+struct kg_net {
+  kgx::ModelDesc model;
+};
+
+struct kg_handle {
+  int device = 0;
+  int max_batch = 0;
+  int precision = 0;
+  hipStream_t stream = nullptr;
+  std::unique_ptr<kgx::Net> net;
+  std::vector<int> buckets;
+  int model_version = 0, P = 1, S = 1, nin = 0, nglob = 0, nmeta = 0;
+  // Pinned host staging: the InputBuffers of the reference (backend.rs:150-212) and the readback.
+  float* h_bin = nullptr;
+  float* h_glob = nullptr;
+  float* h_meta = nullptr;
+  float* h_out = nullptr;
+  std::mutex mu;
+};
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(const std::string& msg) {
+  g_last_error = msg;
+  return 1;
+}
+
+template <typename F>
+int guarded(F&& f) {
+  try {
+    f();
+    return 0;
+  } catch (const std::exception& e) {
+    return fail(e.what());
+  }
+}
+
+constexpr int POS = 19;
+constexpr int HW = POS * POS;
+
+// copyWithSymmetry (crates/katago-core/src/neuralnet/nninputs.rs:756-850), NCHW, one row: flipY = bit 0,
+// flipX = bit 1, transpose = bit 2 on square boards; for inputs (reverse = false) a transpose swaps the flips.
+// The destination offset walks h_base + h * h_stride + w_base + w * w_stride with the strides exchanged by a
+// transpose, exactly as the reference.
+void copy_with_symmetry(const float* src, float* dst, int c_size, int h_size, int w_size, int symmetry, bool reverse) {
+  const bool transpose = (symmetry & 0x4) != 0 && h_size == w_size;
+  bool flip_x = (symmetry & 0x2) != 0;
+  bool flip_y = (symmetry & 0x1) != 0;
+  if (transpose && !reverse) std::swap(flip_x, flip_y);
+  const int nc_stride = h_size * w_size;
+  int h_base = 0, h_stride = w_size, w_base = 0, w_stride = 1;
+  if (flip_y) {
+    h_base = (h_size - 1) * h_stride;
+    h_stride = -h_stride;
+  }
+  if (flip_x) {
+    w_base = (w_size - 1) * w_stride;
+    w_stride = -w_stride;
+  }
+  if (transpose) std::swap(h_stride, w_stride);
+  for (int nc = 0; nc < c_size; nc++) {
+    const float* s = src + (size_t)nc * nc_stride;
+    float* d = dst + (size_t)nc * nc_stride;
+    for (int h = 0; h < h_size; h++)
+      for (int w = 0; w < w_size; w++) d[h_base + h * h_stride + w_base + w * w_stride] = s[h * w_size + w];
+  }
+}
+
+int padded_batch_size(const std::vector<int>& buckets, int n, int max_batch) {
+  int best = -1;
+  for (int b : buckets)
+    if (b >= n && b <= max_batch && (best < 0 || b < best)) best = b;
+  return best < 0 ? n : best;
+}
+
+// Runs the first `n_run` rows already staged in the device input buffers; reads `n` rows back into h_out.
+void run_and_read(kg_handle* h, int n_run, int n, float* out) {
+  h->net->forward(n_run, h->stream);
+  const size_t bytes = (size_t)n * h->net->row_len() * sizeof(float);
+  KGX_HIP(hipMemcpyAsync(h->h_out, h->net->d_out(), bytes, hipMemcpyDeviceToHost, h->stream));
+  KGX_HIP(hipStreamSynchronize(h->stream));
+  if (out) std::memcpy(out, h->h_out, bytes);
+}
+
+void upload_rows(kg_handle* h, int n) {
+  KGX_HIP(hipMemcpyAsync(h->net->d_bin(), h->h_bin, (size_t)n * h->nin * HW * 4, hipMemcpyHostToDevice, h->stream));
+  KGX_HIP(hipMemcpyAsync(h->net->d_global(), h->h_glob, (size_t)n * h->nglob * 4, hipMemcpyHostToDevice, h->stream));
+  if (h->nmeta)
+    KGX_HIP(hipMemcpyAsync(h->net->d_meta(), h->h_meta, (size_t)n * h->nmeta * 4, hipMemcpyHostToDevice, h->stream));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* kg_version(void) { return "kgx 0.1.0 (gfx950)"; }
+
+const char* kg_last_error(void) { return g_last_error.c_str(); }
+
+int kg_device_count(int* count) {
+  return guarded([&] {
+    int c = 0;
+    KGX_HIP(hipGetDeviceCount(&c));
+    *count = c;
+  });
+}
+
+int kg_device_open(int device) {
+  return guarded([&] {
+    KGX_HIP(hipSetDevice(device));
+    KGX_HIP(hipFree(nullptr));
+  });
+}
+
+int kg_net_load(const void* model_bytes, size_t len, const char* expected_sha256, kg_net** out) {
+  return guarded([&] {
+    *out = nullptr;
+    if (expected_sha256 && expected_sha256[0])
+      throw std::runtime_error("Error loading or parsing model file: expectedSha256 is not supported by the kgx backend");
+    if (!model_bytes || len == 0) throw std::runtime_error("Error loading or parsing model file: empty model");
+    auto net = std::make_unique<kg_net>();
+    net->model = kgx::parse_model((const uint8_t*)model_bytes, len);
+    *out = net.release();
+  });
+}
+
+void kg_net_free(kg_net* net) { delete net; }
+
+int kg_net_desc(const kg_net* net, kg_model_desc* d) {
+  return guarded([&] {
+    if (!net || !d) throw std::runtime_error("null argument");
+    const kgx::ModelDesc& m = net->model;
+    std::memset(d, 0, sizeof(*d));
+    std::strncpy(d->name, m.name.c_str(), sizeof(d->name) - 1);
+    d->model_version = m.version;
+    d->num_input_channels = m.num_input_channels;
+    d->num_input_global_channels = m.num_global;
+    d->num_input_meta_channels = m.num_meta;
+    d->num_policy_channels = m.P;
+    d->num_value_channels = 3;
+    d->num_score_value_channels = m.S;
+    d->num_ownership_channels = 1;
+    d->trunk_num_channels = m.trunk_c;
+    d->trunk_num_blocks = m.trunk_blocks;
+    d->num_parameters = m.num_parameters();
+    for (int k = 0; k < 7; k++) d->post_process_params[k] = m.post_process[k];
+    d->output_row_len = m.row_len();
+  });
+}
+
+int kg_handle_create(const kg_net* net, int device, int max_batch, int precision, int nn_x_len, int nn_y_len,
+                     int inputs_use_nhwc, kg_handle** out) {
+  return guarded([&] {
+    *out = nullptr;
+    if (!net) throw std::runtime_error("null net");
+    if (nn_x_len != POS || nn_y_len != POS)
+      throw std::runtime_error("kgx backend: nnXLen and nnYLen must equal the network's posLen 19");
+    if (inputs_use_nhwc) throw std::runtime_error("kgx backend: inputsUseNHWC = true unsupported");
+    if (max_batch < 1) throw std::runtime_error("kgx backend: max batch size must be positive");
+    if (precision < KG_PRECISION_F32 || precision > KG_PRECISION_BF16) throw std::runtime_error("kgx backend: unknown precision");
+    auto h = std::make_unique<kg_handle>();
+    h->device = device;
+    h->max_batch = max_batch;
+    h->precision = precision;
+    const kgx::ModelDesc& m = net->model;
+    h->model_version = m.version;
+    h->P = m.P;
+    h->S = m.S;
+    h->nin = m.num_input_channels;
+    h->nglob = m.num_global;
+    h->nmeta = m.num_meta;
+    KGX_HIP(hipSetDevice(device));
+    KGX_HIP(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
+    h->net = std::make_unique<kgx::Net>(m, device, max_batch, precision);
+    KGX_HIP(hipHostMalloc((void**)&h->h_bin, (size_t)max_batch * h->nin * HW * 4, hipHostMallocDefault));
+    KGX_HIP(hipHostMalloc((void**)&h->h_glob, (size_t)max_batch * h->nglob * 4, hipHostMallocDefault));
+    if (h->nmeta) KGX_HIP(hipHostMalloc((void**)&h->h_meta, (size_t)max_batch * h->nmeta * 4, hipHostMallocDefault));
+    KGX_HIP(hipHostMalloc((void**)&h->h_out, (size_t)max_batch * m.row_len() * 4, hipHostMallocDefault));
+    std::memset(h->h_bin, 0, (size_t)max_batch * h->nin * HW * 4);
+    std::memset(h->h_glob, 0, (size_t)max_batch * h->nglob * 4);
+    if (h->nmeta) std::memset(h->h_meta, 0, (size_t)max_batch * h->nmeta * 4);
+    *out = h.release();
+  });
+}
+
+void kg_handle_free(kg_handle* h) {
+  if (!h) return;
+  (void)hipSetDevice(h->device);
+  if (h->stream) (void)hipStreamSynchronize(h->stream);
+  h->net.reset();
+  if (h->h_bin) (void)hipHostFree(h->h_bin);
+  if (h->h_glob) (void)hipHostFree(h->h_glob);
+  if (h->h_meta) (void)hipHostFree(h->h_meta);
+  if (h->h_out) (void)hipHostFree(h->h_out);
+  if (h->stream) (void)hipStreamDestroy(h->stream);
+  delete h;
+}
+
+int kg_handle_set_batch_buckets(kg_handle* h, const int* buckets, int count) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lock(h->mu);
+    h->buckets.clear();
+    for (int k = 0; k < count; k++)
+      if (buckets[k] > 0) h->buckets.push_back(buckets[k]);
+    std::sort(h->buckets.begin(), h->buckets.end());
+    h->buckets.erase(std::unique(h->buckets.begin(), h->buckets.end()), h->buckets.end());
+  });
+}
+
+int kg_padded_batch_size(const int* buckets, int count, int n, int max_batch) {
+  std::vector<int> b(buckets, buckets + (count > 0 ? count : 0));
+  return padded_batch_size(b, n, max_batch);
+}
+
+int kg_handle_is_using_fp16(const kg_handle* h) { return h && h->precision != KG_PRECISION_F32 ? 1 : 0; }
+
+int kg_forward(kg_handle* h, int n, const float* bin, const float* global, const float* meta, float* out) {
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    std::lock_guard<std::mutex> lock(h->mu);
+    if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
+    if (h->nmeta && !meta) throw std::runtime_error("kgx backend: the network needs a meta_input");
+    if (!h->nmeta && meta) throw std::runtime_error("kgx backend: the network takes no meta_input");
+    const int n_run = padded_batch_size(h->buckets, n, h->max_batch);
+    std::memcpy(h->h_bin, bin, (size_t)n * h->nin * HW * 4);
+    std::memcpy(h->h_glob, global, (size_t)n * h->nglob * 4);
+    if (h->nmeta) std::memcpy(h->h_meta, meta, (size_t)n * h->nmeta * 4);
+    KGX_HIP(hipSetDevice(h->device));
+    upload_rows(h, n);
+    run_and_read(h, n_run, n, out);
+  });
+}
+
+int kg_handle_device_buffers(kg_handle* h, float** bin, float** global, float** meta, float** out) {
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    if (bin) *bin = h->net->d_bin();
+    if (global) *global = h->net->d_global();
+    if (meta) *meta = h->net->d_meta();
+    if (out) *out = h->net->d_out();
+  });
+}
+
+int kg_run(kg_handle* h, int n, float* out) {
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    std::lock_guard<std::mutex> lock(h->mu);
+    if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
+    KGX_HIP(hipSetDevice(h->device));
+    const int n_run = padded_batch_size(h->buckets, n, h->max_batch);
+    if (out) run_and_read(h, n_run, n, out);
+    else h->net->forward(n_run, h->stream);
+  });
+}
+
+int kg_sync(kg_handle* h) {
+  return guarded([&] { KGX_HIP(hipStreamSynchronize(h->stream)); });
+}
+
+void* kg_handle_stream(kg_handle* h) { return h ? (void*)h->stream : nullptr; }
+
+int kg_get_output(kg_handle* h, int n, const kg_row_input* rows, kg_nn_output* outputs) {
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    std::lock_guard<std::mutex> lock(h->mu);
+    if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
+    // copy_inputs (backend.rs:497-546).
+    for (int r = 0; r < n; r++) {
+      const kg_row_input& in = rows[r];
+      std::memcpy(h->h_glob + (size_t)r * h->nglob, in.row_global, (size_t)h->nglob * 4);
+      if (h->nmeta) {
+        if (!in.row_meta) throw std::runtime_error("kgx backend: the network needs a meta row");
+        std::memcpy(h->h_meta + (size_t)r * h->nmeta, in.row_meta, (size_t)h->nmeta * 4);
+      } else if (in.row_meta) {
+        throw std::runtime_error("kgx backend: the network takes no meta row");
+      }
+      copy_with_symmetry(in.row_spatial, h->h_bin + (size_t)r * h->nin * HW, h->nin, POS, POS, in.symmetry, false);
+    }
+    // run_network (backend.rs:549-619).
+    KGX_HIP(hipSetDevice(h->device));
+    const int n_run = padded_batch_size(h->buckets, n, h->max_batch);
+    upload_rows(h, n);
+    run_and_read(h, n_run, n, nullptr);
+    // copy_outputs (backend.rs:622-731).
+    const int rl = h->net->row_len();
+    const int P = h->P, S = h->S, v = h->model_version;
+    float tmp[HW];
+    for (int r = 0; r < n; r++) {
+      const float* row = h->h_out + (size_t)r * rl;
+      kg_nn_output& o = outputs[r];
+      const float optimism = rows[r].policy_optimism;
+      const int sym = rows[r].symmetry;
+      const float* pol = row;
+      if (P == 2 || (P == 4 && v >= 16)) {
+        for (int i = 0; i < HW; i++) {
+          const float p = pol[i], po = pol[(HW + 1) + i];
+          tmp[i] = p + (po - p) * optimism;
+        }
+        copy_with_symmetry(tmp, o.policy_probs, 1, POS, POS, sym, true);
+        const float p0 = pol[HW], p1 = pol[(HW + 1) + HW];
+        o.policy_probs[HW] = p0 + (p1 - p0) * optimism;
+      } else {
+        copy_with_symmetry(pol, o.policy_probs, 1, POS, POS, sym, true);
+        o.policy_probs[HW] = pol[HW];
+      }
+      const float* val = row + P * (HW + 1);
+      const float* sc = val + 3;
+      const float* own = sc + S;
+      o.white_win_prob = val[0];
+      o.white_loss_prob = val[1];
+      o.white_no_result_prob = val[2];
+      if (o.white_owner_map) copy_with_symmetry(own, o.white_owner_map, 1, POS, POS, sym, true);
+      if (v >= 9) {
+        o.white_score_mean = sc[0]; o.white_score_mean_sq = sc[1]; o.white_lead = sc[2]; o.var_time_left = sc[3];
+        o.shortterm_winloss_error = sc[4]; o.shortterm_score_error = sc[5];
+      } else if (v >= 8) {
+        o.white_score_mean = sc[0]; o.white_score_mean_sq = sc[1]; o.white_lead = sc[2]; o.var_time_left = sc[3];
+        o.shortterm_winloss_error = 0.f; o.shortterm_score_error = 0.f;
+      } else if (v >= 4) {
+        o.white_score_mean = sc[0]; o.white_score_mean_sq = sc[1]; o.white_lead = o.white_score_mean;
+        o.var_time_left = 0.f; o.shortterm_winloss_error = 0.f; o.shortterm_score_error = 0.f;
+      } else {
+        o.white_score_mean = sc[0]; o.white_score_mean_sq = o.white_score_mean * o.white_score_mean;
+        o.white_lead = o.white_score_mean; o.var_time_left = 0.f; o.shortterm_winloss_error = 0.f;
+        o.shortterm_score_error = 0.f;
+      }
+    }
+  });
+}
+
+int kg_profile_enable(kg_handle* h, int enable) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lock(h->mu);
+    h->net->set_profiling(enable != 0);
+  });
+}
+
+int kg_profile_reset(kg_handle* h) {
+  return guarded([&] {
+    std::lock_guard<std::mutex> lock(h->mu);
+    h->net->reset_profile();
+  });
+}
+
+int kg_profile_read(kg_handle* h, const char** names, long* launches, double* ms, double* flops, double* bytes,
+                    int max_classes) {
+  if (!h) return -1;
+  std::lock_guard<std::mutex> lock(h->mu);
+  int k = 0;
+  for (const auto& kv : h->net->profile()) {
+    if (k < max_classes) {
+      // Class names are string literals of the op table; find the stable pointer by content.
+      static const char* known[] = {"wino_in", "wino_gemm", "wino_out", "gemm_1x1", "conv_direct", "mask_prep",
+                                    "small_matmul", "pool", "head", "rmsnorm", "token_gemm", "attention", "ffn_act"};
+      const char* nm = "other";
+      for (const char* c : known)
+        if (kv.first == c) nm = c;
+      names[k] = nm;
+      launches[k] = kv.second.launches;
+      ms[k] = kv.second.ms;
+      flops[k] = kv.second.flops;
+      bytes[k] = kv.second.bytes;
+    }
+    k++;
+  }
+  return k;
+}
+
+}  // extern "C"

@@ -1,0 +1,114 @@
+// Host-side declarations of the kernel launchers (kgx_kernels.hip). Every launcher enqueues one kernel on
+// `stream` and returns without waiting.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <cstdint>
+
+namespace kgx {
+
+constexpr int POS = 19;
+constexpr int HW = POS * POS;             // board points per row
+constexpr int TILES_X = (POS + 3) / 4;    // Winograd F(4x4,3x3) tiles per board side
+constexpr int TILES = TILES_X * TILES_X;  // tiles per board
+
+enum Prec { PREC_F32 = 0, PREC_F16 = 1, PREC_BF16 = 2 };
+enum Act { ACT_ID = 0, ACT_RELU = 1, ACT_MISH = 2, ACT_SILU = 3 };
+
+inline int round_up(int x, int m) { return (x + m - 1) / m * m; }
+
+// Batch-norm + activation + board-mask prologue applied to a convolution's input as it is loaded:
+// a = (x + prebias[b][c]) * scale[c] + bias[c]; x' = act(a) * mask[b][pos]. scale == nullptr disables it.
+struct Prologue {
+  const float* scale = nullptr;
+  const float* bias = nullptr;
+  const float* prebias = nullptr;  // [B][ld_prebias] or null
+  int ld_prebias = 0;
+  int act = ACT_ID;
+  const float* mask = nullptr;     // [B*HW]
+};
+
+// Winograd input transform: x (NHWC rows of `ldx` floats, or NCHW when `nchw`) -> V[36][t_pad][c_pad].
+void launch_wino_in(int prec, const float* x, int ldx, bool nchw, const Prologue& pro, void* V, int B, int C,
+                    int c_pad, int t_pad, hipStream_t s);
+
+// Winograd output transform: M[36][t_pad][oc_pad] -> out[B*HW][ldo] (+ colbias[b][oc]); add into out when
+// `accumulate`.
+void launch_wino_out(const float* M, int oc_pad, int t_pad, float* out, int ldo, int OC, const float* colbias,
+                     int ld_colbias, bool accumulate, int B, hipStream_t s);
+
+// Filter transform G g G^T of w [oc][ic][3][3] into U[36][oc_pad][ic_pad] (host, double precision).
+void wino_filter_host(const float* w, int oc, int ic, int oc_pad, int ic_pad, float* U);
+
+// C[z] = A[z] * Bt[z]^T on MFMA: A [M][K] (row stride lda; T, or float with a prologue), Bt [N][K].
+struct GemmArgs {
+  const void* A = nullptr; long lda = 0; long sA = 0;
+  const void* Bt = nullptr; long ldb = 0; long sB = 0;
+  void* C = nullptr; long ldc = 0; long sC = 0;
+  int M = 0, N = 0, K = 0, Z = 1;
+  bool a_float = false;        // A holds float (converted, with `pro` applied when pro.scale)
+  Prologue pro;
+  const float* residual = nullptr; long ldr = 0;  // out += residual (may alias C)
+  const float* colbias = nullptr; int ld_colbias = 0;  // + colbias[m / HW][n]
+  const float* rowmask = nullptr;                      // * rowmask[m] (before the residual)
+  bool out_t = false;          // store in the compute type instead of float
+};
+void launch_gemm(int prec, const GemmArgs& g, hipStream_t s);
+
+// Direct odd-k "same" convolution in float, w as [ic][ky][kx][oc]: x (NHWC rows of ldx, or NCHW) -> out.
+void launch_conv_direct(const float* x, int ldx, bool nchw, const Prologue& pro, int IC, const float* w, int OC,
+                        int ky, int kx, int dy, int dx, float* out, int ldo, const float* colbias, int ld_colbias,
+                        bool accumulate, int B, hipStream_t s);
+
+// mask[b][pos] = bin[b][0][pos]; area = sum; s1 = (sqrt(area)-14)*0.1; s2 = (sqrt(area)-14)^2*0.01-0.1.
+void launch_mask_prep(const float* bin, int nin, float* mask, float* area, float* s1, float* s2, int B,
+                      hipStream_t s);
+
+// Board pooling of channels [coff, coff+C) of x [B*HW][ldx] after the prologue:
+// gpool (value=false): [mean, mean*s1, max(x + mask*1e4 - 1e4)]; value pool: [mean, mean*s1, mean*s2].
+void launch_pool(const float* x, int ldx, int coff, int C, const Prologue& pro, const float* area,
+                 const float* s1, const float* s2, bool value, float* out, int B, hipStream_t s);
+
+// out[b][o*ostride] (+)= act(sum_i in[b][i] * W[i][o] + bias[o]).
+void launch_small_matmul(const float* in, int ldin, int IC, const float* W, int OC, const float* bias, int act,
+                         float* out, long ldout, int ostride, bool accumulate, int B, hipStream_t s);
+
+// Per board point: the policy conv p2 over act(BN(p1 + gpool bias)) * mask, and the ownership conv over
+// act(BN(v1)) * mask, written into the readback rows.
+struct HeadSpatialArgs {
+  const float* H = nullptr; int ldh = 0;
+  int p1_off = 0, c_p1 = 0; const float* p1_bias = nullptr;  // [B][c_p1]
+  const float* p1_scale = nullptr; const float* p1_shift = nullptr; int p1_act = 0;
+  const float* w_p2 = nullptr; int P = 0;                     // [c_p1][P]
+  int v1_off = 0, c_v1 = 0;
+  const float* v1_scale = nullptr; const float* v1_shift = nullptr; int v1_act = 0;
+  const float* w_own = nullptr;                               // [c_v1]
+  const float* mask = nullptr;
+  float* out = nullptr; int row_len = 0; int own_off = 0;
+};
+void launch_head_spatial(const HeadSpatialArgs& a, int B, hipStream_t s);
+
+// Per-token RMSNorm of transformer blocks: out = x * (1/sqrt(sum(x^2)/C + eps)) * w * mask[row] (compute type).
+void launch_rmsnorm_tok(int prec, const float* x, int ldx, int C, const float* w, float eps, const float* mask,
+                        void* out, int ldo, int rows, hipStream_t s);
+
+// Trunk-tip RMSNorm: act(x * rms * gamma + beta) * mask, rms per point or over the board (spatial).
+void launch_tip_rms(const float* x, int C, const float* gamma, const float* beta, float eps, bool spatial, int act,
+                    const float* mask, const float* area, float* rs_tmp, float* out, int B, hipStream_t s);
+
+// Softmax attention over the board on the fused projection buffer qkv [B*HW][ldq] (q | k | v columns),
+// RoPE applied on load (cos/sin [ntab][HW][dq/2], pair p <-> p + dq/2), key bias mask*3e4 - 3e4.
+struct AttnArgs {
+  const void* qkv = nullptr; int ldq = 0;
+  int q_off = 0, k_off = 0, v_off = 0;
+  int H = 0, KV = 0, dq = 0, dv = 0;
+  const float* cos_t = nullptr; const float* sin_t = nullptr; int q_tables = 0, k_tables = 0;  // 0 = no RoPE
+  float scale = 1.f;
+  const float* mask = nullptr;
+  void* out = nullptr; int ldo = 0;
+};
+void launch_attention(int prec, const AttnArgs& a, int B, hipStream_t s);
+
+// FFN activation: h = silu(u[:, :F]) * u[:, F:2F] (gated) or mish(u[:, :F]), u float [rows][ldu] -> compute type.
+void launch_ffn_act(int prec, const float* u, int ldu, int F, bool gated, void* h, int ldh, int rows, hipStream_t s);
+
+}  // namespace kgx

@@ -1,0 +1,120 @@
+// A KataGo network on one GPU: device weights in the layouts the kernels read, activation workspace for a
+// maximum batch, and the forward pass as a list of kernel launches (replayed through a HIP graph per batch
+// size, or launched eagerly with per-kernel events when profiling).
+#pragma once
+#include <functional>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "kgx_kernels.h"
+#include "kgx_model.h"
+
+namespace kgx {
+
+#define KGX_HIP(call)                                                                                       \
+  do {                                                                                                      \
+    hipError_t e_ = (call);                                                                                 \
+    if (e_ != hipSuccess) throw std::runtime_error(std::string(#call) + ": " + hipGetErrorString(e_));    \
+  } while (0)
+
+struct DeviceBuffer {
+  void* ptr = nullptr;
+  size_t bytes = 0;
+  DeviceBuffer() = default;
+  DeviceBuffer(const DeviceBuffer&) = delete;
+  DeviceBuffer& operator=(const DeviceBuffer&) = delete;
+  ~DeviceBuffer() {
+    if (ptr) (void)hipFree(ptr);
+  }
+};
+
+// One kernel launch of the forward pass. Work is algorithmic (what the operation must read, write and compute),
+// linear in the batch: per_row * B + fixed.
+struct Op {
+  std::function<void(hipStream_t, int)> launch;
+  const char* cls;
+  double flops_row = 0, bytes_row = 0, bytes_fixed = 0;
+};
+
+struct ProfileClass {
+  long launches = 0;
+  double ms = 0, flops = 0, bytes = 0;
+};
+
+class Net {
+ public:
+  Net(const ModelDesc& model, int device, int max_batch, int prec);
+  ~Net();
+
+  // Enqueues the forward pass over the first B rows of the device input buffers on `stream`.
+  void forward(int B, hipStream_t stream);
+
+  int prec() const { return prec_; }
+  int max_batch() const { return max_batch_; }
+  int row_len() const { return row_len_; }
+  float* d_bin() const { return d_bin_; }
+  float* d_global() const { return d_glob_; }
+  float* d_meta() const { return d_meta_; }
+  float* d_out() const { return d_out_; }
+  size_t bin_row() const { return (size_t)nin_ * HW; }
+  int num_global() const { return nglob_; }
+  int num_meta() const { return nmeta_; }
+
+  void set_profiling(bool on) { profiling_ = on; }
+  void reset_profile() { profile_.clear(); }
+  const std::map<std::string, ProfileClass>& profile() const { return profile_; }
+  void set_use_graphs(bool on) { use_graphs_ = on; }
+
+ private:
+  // Allocation and upload.
+  float* alloc_f(size_t n);
+  void* alloc_bytes(size_t bytes);
+  const float* upload_f(const std::vector<float>& v);
+  const void* upload_t(const std::vector<float>& v);  // converted to the compute type
+  size_t tsize() const { return prec_ == PREC_F32 ? 4 : 2; }
+
+  // Planning.
+  void scan(const std::vector<BlockDesc>& blocks, int c, int depth);
+  void emit_conv(const ConvDesc& c, const float* x, int ldx, bool nchw, const Prologue& pro, float* y, int ldy,
+                 bool accumulate, const float* colbias, int ld_colbias);
+  void emit_stack(const std::vector<BlockDesc>& blocks, float* x, int c, int depth);
+  void emit_attention(const BlockDesc& b, float* x, int c);
+  void emit_ffn(const BlockDesc& b, float* x, int c);
+  void emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, void* C, int ldc, bool out_t,
+                       float* residual_masked, const char* cls);
+  Prologue bn_pro(const BNDesc& bn, int act, const float* prebias = nullptr, int ld_prebias = 0);
+  void build(const ModelDesc& m);
+
+  void run_ops(int B, hipStream_t s);
+
+  int device_, max_batch_, prec_;
+  int nin_ = 0, nglob_ = 0, nmeta_ = 0, row_len_ = 0;
+  std::vector<std::unique_ptr<DeviceBuffer>> mem_;
+  std::vector<Op> ops_;
+
+  // Inputs / outputs and per-row board data.
+  float *d_bin_ = nullptr, *d_glob_ = nullptr, *d_meta_ = nullptr, *d_out_ = nullptr;
+  float *mask_ = nullptr, *area_ = nullptr, *s1_ = nullptr, *s2_ = nullptr;
+
+  // Workspace sizes from scan(), then the buffers.
+  int tmp_c_ = 0, gp_c_ = 0, gb_c_ = 0;
+  std::vector<int> stream_c_;
+  int nrm_c_ = 0, qkv_c_ = 0, ao_c_ = 0, u_c_ = 0, h_c_ = 0;
+  size_t wino_v_elems_ = 0, wino_m_elems_ = 0;
+  float* trunk_ = nullptr;
+  std::vector<float*> streams_;
+  float *tmp_ = nullptr, *gp_ = nullptr, *gb_ = nullptr;
+  void *nrm_ = nullptr, *qkv_ = nullptr, *ao_ = nullptr, *h_ = nullptr;
+  float* u_ = nullptr;
+  void* wino_v_ = nullptr;
+  float* wino_m_ = nullptr;
+
+  bool profiling_ = false, use_graphs_ = true;
+  std::map<std::string, ProfileClass> profile_;
+  std::vector<hipEvent_t> events_;
+  std::map<int, hipGraphExec_t> graphs_;
+};
+
+}  // namespace kgx

@@ -1,0 +1,656 @@
+// Forward-pass planning and execution on one GPU. The op order follows the graph of
+// tools/bin2onnx/bin2onnx.py (trunk :1466-1492, blocks :1243-1269 and :1357-1438, heads :1495-1531); each
+// batch norm + activation + mask that feeds a convolution runs inside that convolution's input loads, as
+// katago-nn-burn's `fuse_bn_act` rewrite does (crates/katago-nn-burn/build.rs:366-600, conv.rs:42-93).
+#include "kgx_net.h"
+
+#include <cmath>
+#include <cstring>
+#include <stdexcept>
+
+namespace kgx {
+namespace {
+
+uint16_t f32_to_f16_bits(float f) {
+  _Float16 h = (_Float16)f;
+  uint16_t b;
+  std::memcpy(&b, &h, 2);
+  return b;
+}
+
+uint16_t f32_to_bf16_bits(float f) {  // round to nearest even
+  uint32_t u;
+  std::memcpy(&u, &f, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u) return (uint16_t)((u >> 16) | ((u & 0xffff) ? 0x40 : 0));
+  const uint32_t lsb = (u >> 16) & 1u;
+  u += 0x7fffu + lsb;
+  return (uint16_t)(u >> 16);
+}
+
+int t_pad(int B) { return round_up(B * TILES, 64); }
+
+}  // namespace
+
+Net::Net(const ModelDesc& m, int device, int max_batch, int prec) : device_(device), max_batch_(max_batch), prec_(prec) {
+  KGX_HIP(hipSetDevice(device));
+  build(m);
+}
+
+Net::~Net() {
+  (void)hipSetDevice(device_);
+  for (auto& kv : graphs_) (void)hipGraphExecDestroy(kv.second);
+  for (hipEvent_t e : events_) (void)hipEventDestroy(e);
+}
+
+float* Net::alloc_f(size_t n) { return (float*)alloc_bytes(n * sizeof(float)); }
+
+void* Net::alloc_bytes(size_t bytes) {
+  auto b = std::make_unique<DeviceBuffer>();
+  bytes = std::max<size_t>(bytes, 256);
+  KGX_HIP(hipMalloc(&b->ptr, bytes));
+  b->bytes = bytes;
+  void* p = b->ptr;
+  mem_.push_back(std::move(b));
+  return p;
+}
+
+const float* Net::upload_f(const std::vector<float>& v) {
+  float* d = alloc_f(v.size());
+  KGX_HIP(hipMemcpy(d, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+  return d;
+}
+
+const void* Net::upload_t(const std::vector<float>& v) {
+  if (prec_ == PREC_F32) return upload_f(v);
+  std::vector<uint16_t> h(v.size());
+  for (size_t k = 0; k < v.size(); k++) h[k] = prec_ == PREC_F16 ? f32_to_f16_bits(v[k]) : f32_to_bf16_bits(v[k]);
+  void* d = alloc_bytes(h.size() * 2);
+  KGX_HIP(hipMemcpy(d, h.data(), h.size() * 2, hipMemcpyHostToDevice));
+  return d;
+}
+
+Prologue Net::bn_pro(const BNDesc& bn, int act, const float* prebias, int ld_prebias) {
+  Prologue p;
+  p.scale = upload_f(bn.scale);
+  p.bias = upload_f(bn.bias);
+  p.prebias = prebias;
+  p.ld_prebias = ld_prebias;
+  p.act = act;
+  p.mask = mask_;
+  return p;
+}
+
+// Workspace needs of a block stack with `c` channels at nesting depth `depth`.
+void Net::scan(const std::vector<BlockDesc>& blocks, int c, int depth) {
+  for (const BlockDesc& b : blocks) {
+    switch (b.kind) {
+      case BLOCK_RES:
+        tmp_c_ = std::max(tmp_c_, b.regular.oc);
+        break;
+      case BLOCK_GPOOL:
+        tmp_c_ = std::max(tmp_c_, b.regular.oc + b.gconv.oc);
+        gp_c_ = std::max(gp_c_, 3 * b.gconv.oc);
+        gb_c_ = std::max(gb_c_, b.regular.oc);
+        break;
+      case BLOCK_NBT:
+        if ((int)stream_c_.size() <= depth + 1) stream_c_.resize(depth + 2, 0);
+        stream_c_[depth + 1] = std::max(stream_c_[depth + 1], b.regular.oc);
+        scan(b.inner, b.regular.oc, depth + 1);
+        break;
+      case BLOCK_ATTN:
+        nrm_c_ = std::max(nrm_c_, c);
+        qkv_c_ = std::max(qkv_c_, b.q.oc + b.k.oc + b.v.oc);
+        ao_c_ = std::max(ao_c_, b.heads * b.dv);
+        break;
+      case BLOCK_FFN:
+        nrm_c_ = std::max(nrm_c_, c);
+        u_c_ = std::max(u_c_, b.swiglu ? 2 * b.ffn_c : b.ffn_c);
+        h_c_ = std::max(h_c_, b.ffn_c);
+        break;
+    }
+  }
+}
+
+// y (= or +=) conv(pro(x)) + colbias. 3x3 undilated convs run as Winograd F(4x4,3x3) (transform, 36 batched MFMA
+// GEMMs, inverse transform: crates/katago-nn-burn/src/wino/ext.rs:324-437); 1x1 convs over NHWC rows as one MFMA
+// GEMM with the prologue on the A loads (wino/ext.rs:278-321); anything else as a direct convolution.
+void Net::emit_conv(const ConvDesc& c, const float* x, int ldx, bool nchw, const Prologue& pro, float* y, int ldy,
+                    bool accumulate, const float* colbias, int ld_colbias) {
+  const int prec = prec_;
+  const double ts = (double)tsize();
+  if (c.ky == 3 && c.kx == 3 && c.dy == 1 && c.dx == 1) {
+    const int icp = round_up(c.ic, 32), ocp = round_up(c.oc, 64);
+    std::vector<float> U((size_t)36 * ocp * icp);
+    wino_filter_host(c.w.data(), c.oc, c.ic, ocp, icp, U.data());
+    const void* dU = upload_t(U);
+    wino_v_elems_ = std::max(wino_v_elems_, (size_t)36 * t_pad(max_batch_) * icp);
+    wino_m_elems_ = std::max(wino_m_elems_, (size_t)36 * t_pad(max_batch_) * ocp);
+    const int ic = c.ic, oc = c.oc;
+    Op in;
+    in.launch = [=](hipStream_t s, int B) { launch_wino_in(prec, x, ldx, nchw, pro, wino_v_, B, ic, icp, t_pad(B), s); };
+    in.cls = "wino_in";
+    in.bytes_row = (double)HW * ic * 4 + 36.0 * TILES * ic * ts;
+    ops_.push_back(in);
+    Op gm;
+    gm.launch = [=](hipStream_t s, int B) {
+      GemmArgs g;
+      const int tp = t_pad(B);
+      g.A = wino_v_; g.lda = icp; g.sA = (long)tp * icp;
+      g.Bt = dU; g.ldb = icp; g.sB = (long)ocp * icp;
+      g.C = wino_m_; g.ldc = ocp; g.sC = (long)tp * ocp;
+      g.M = tp; g.N = ocp; g.K = icp; g.Z = 36;
+      launch_gemm(prec, g, s);
+    };
+    gm.cls = "wino_gemm";
+    gm.flops_row = 2.0 * 36 * TILES * ic * oc;
+    gm.bytes_row = 36.0 * TILES * ic * ts + 36.0 * TILES * oc * 4;
+    gm.bytes_fixed = 36.0 * ic * oc * ts;
+    ops_.push_back(gm);
+    Op out;
+    out.launch = [=](hipStream_t s, int B) {
+      launch_wino_out(wino_m_, ocp, t_pad(B), y, ldy, oc, colbias, ld_colbias, accumulate, B, s);
+    };
+    out.cls = "wino_out";
+    out.bytes_row = 36.0 * TILES * oc * 4 + (double)HW * oc * 4 * (accumulate ? 2 : 1);
+    ops_.push_back(out);
+  } else if (c.ky == 1 && c.kx == 1 && !nchw && !colbias && c.ic % 8 == 0 && ldx % 8 == 0) {
+    const void* dW = upload_t(c.w);  // [oc][ic] is already the B^T layout
+    const int ic = c.ic, oc = c.oc;
+    Op gm;
+    gm.launch = [=](hipStream_t s, int B) {
+      GemmArgs g;
+      g.A = x; g.lda = ldx; g.a_float = true; g.pro = pro;
+      g.Bt = dW; g.ldb = ic;
+      g.C = y; g.ldc = ldy;
+      if (accumulate) { g.residual = y; g.ldr = ldy; }
+      g.M = B * HW; g.N = oc; g.K = ic;
+      launch_gemm(prec, g, s);
+    };
+    gm.cls = "gemm_1x1";
+    gm.flops_row = 2.0 * HW * ic * oc;
+    gm.bytes_row = (double)HW * ic * 4 + (double)HW * oc * 4 * (accumulate ? 2 : 1);
+    gm.bytes_fixed = (double)ic * oc * ts;
+    ops_.push_back(gm);
+  } else {
+    // [oc][ic][ky][kx] -> [ic][ky][kx][oc]
+    std::vector<float> w((size_t)c.ic * c.ky * c.kx * c.oc);
+    for (int o = 0; o < c.oc; o++)
+      for (int i = 0; i < c.ic; i++)
+        for (int a = 0; a < c.ky; a++)
+          for (int b = 0; b < c.kx; b++)
+            w[(((size_t)i * c.ky + a) * c.kx + b) * c.oc + o] = c.w[(((size_t)o * c.ic + i) * c.ky + a) * c.kx + b];
+    const float* dW = upload_f(w);
+    const int ic = c.ic, oc = c.oc, ky = c.ky, kx = c.kx, dy = c.dy, dx = c.dx;
+    Op op;
+    op.launch = [=](hipStream_t s, int B) {
+      launch_conv_direct(x, ldx, nchw, pro, ic, dW, oc, ky, kx, dy, dx, y, ldy, colbias, ld_colbias, accumulate, B, s);
+    };
+    op.cls = "conv_direct";
+    op.flops_row = 2.0 * HW * ic * oc * ky * kx;
+    op.bytes_row = (double)HW * ic * 4 + (double)HW * oc * 4;
+    ops_.push_back(op);
+  }
+}
+
+void Net::emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, void* C, int ldc, bool out_t,
+                          float* residual_masked, const char* cls) {
+  const int prec = prec_;
+  const float* mask = mask_;
+  Op op;
+  op.launch = [=](hipStream_t s, int B) {
+    GemmArgs g;
+    g.A = A; g.lda = lda;
+    g.Bt = Bt; g.ldb = K;
+    g.C = C; g.ldc = ldc; g.out_t = out_t;
+    if (residual_masked) { g.residual = residual_masked; g.ldr = ldc; g.rowmask = mask; }
+    g.M = B * HW; g.N = N; g.K = K;
+    launch_gemm(prec, g, s);
+  };
+  op.cls = cls;
+  const double ts = (double)tsize();
+  op.flops_row = 2.0 * HW * K * N;
+  op.bytes_row = (double)HW * K * ts + (double)HW * N * (out_t ? ts : 4.0) * (residual_masked ? 2 : 1);
+  op.bytes_fixed = (double)K * N * ts;
+  ops_.push_back(op);
+}
+
+// TransformerAttentionBlock (bin2onnx.py:1357-1421): RMSNorm, fused q|k|v projection (RoPE-permuted q and k
+// columns, bin2onnx.py:1369-1374), attention with RoPE on load, out projection * mask + residual.
+void Net::emit_attention(const BlockDesc& b, float* x, int c) {
+  const int prec = prec_;
+  const int H = b.heads, KV = b.kv_heads, dq = b.dq, dv = b.dv;
+  if (dq != dv) throw std::runtime_error(b.name + ": attention with qHeadDim != vHeadDim is not supported");
+  const int nq = H * dq, nk = KV * dq, nv = KV * dv, nqkv = nq + nk + nv;
+  // B^T rows: output features; per head, RoPE pairs (2p, 2p+1) move to (p, p + dq/2).
+  std::vector<float> w((size_t)nqkv * c);
+  auto col_of = [&](int j) {
+    if (!b.rope) return j;
+    const int h = j / dq, r = j - h * dq, half = dq / 2;
+    return h * dq + (r < half ? 2 * r : 2 * (r - half) + 1);
+  };
+  for (int j = 0; j < nq; j++)
+    for (int k = 0; k < c; k++) w[(size_t)j * c + k] = b.q.w[(size_t)k * nq + col_of(j)];
+  for (int j = 0; j < nk; j++)
+    for (int k = 0; k < c; k++) w[(size_t)(nq + j) * c + k] = b.k.w[(size_t)k * nk + col_of(j)];
+  for (int j = 0; j < nv; j++)
+    for (int k = 0; k < c; k++) w[(size_t)(nq + nk + j) * c + k] = b.v.w[(size_t)k * nv + j];
+  const void* dWqkv = upload_t(w);
+  std::vector<float> wo((size_t)c * H * dv);
+  for (int o = 0; o < c; o++)
+    for (int k = 0; k < H * dv; k++) wo[(size_t)o * H * dv + k] = b.o.w[(size_t)k * c + o];
+  const void* dWo = upload_t(wo);
+  // RoPE tables [tables][HW][dq/2], float, as computeRopeCosSin (bin2onnx.py:449-485).
+  const float* dcos = nullptr;
+  const float* dsin = nullptr;
+  int ntab = 0;
+  if (b.rope) {
+    const int pairs = dq / 2;
+    ntab = b.learnable_rope ? KV : 1;
+    std::vector<float> cs((size_t)ntab * HW * pairs), sn(cs.size());
+    for (int t = 0; t < ntab; t++)
+      for (int p = 0; p < pairs; p++)
+        for (int y = 0; y < POS; y++)
+          for (int xx = 0; xx < POS; xx++) {
+            float ang;
+            if (b.learnable_rope) {
+              const float fx = b.rope_freqs[((size_t)t * pairs + p) * 2], fy = b.rope_freqs[((size_t)t * pairs + p) * 2 + 1];
+              ang = (float)xx * fx + (float)y * fy;
+            } else {
+              const int per_dim = pairs / 2;
+              const int padj = p < per_dim ? p : p - per_dim;
+              const float expo = (float)(2 * padj) / (float)(dq / 2);
+              const float powv = (float)std::pow((double)b.rope_theta, (double)expo);
+              const float freq = 1.0f / powv;
+              ang = (p < per_dim ? (float)y : (float)xx) * freq;
+            }
+            const size_t idx = ((size_t)t * HW + y * POS + xx) * pairs + p;
+            cs[idx] = (float)std::cos((double)ang);
+            sn[idx] = (float)std::sin((double)ang);
+          }
+    dcos = upload_f(cs);
+    dsin = upload_f(sn);
+  }
+  const float* lnw = upload_f(b.ln_w);
+  const float eps = b.ln_eps;
+  void* nrm = nrm_;
+  const float* mask = mask_;
+  Op rn;
+  rn.launch = [=](hipStream_t s, int B) { launch_rmsnorm_tok(prec, x, c, c, lnw, eps, mask, nrm, c, B * HW, s); };
+  rn.cls = "rmsnorm";
+  rn.bytes_row = (double)HW * c * (4 + tsize());
+  ops_.push_back(rn);
+  emit_token_gemm(nrm_, c, dWqkv, nqkv, c, qkv_, nqkv, true, nullptr, "token_gemm");
+  void* qkv = qkv_;
+  void* ao = ao_;
+  const float scale = 1.0f / std::sqrt((float)dq);
+  Op at;
+  at.launch = [=](hipStream_t s, int B) {
+    AttnArgs a;
+    a.qkv = qkv; a.ldq = nqkv; a.q_off = 0; a.k_off = nq; a.v_off = nq + nk;
+    a.H = H; a.KV = KV; a.dq = dq; a.dv = dv;
+    a.cos_t = dcos; a.sin_t = dsin; a.q_tables = ntab; a.k_tables = ntab;
+    a.scale = scale; a.mask = mask; a.out = ao; a.ldo = H * dv;
+    launch_attention(prec, a, B, s);
+  };
+  at.cls = "attention";
+  at.flops_row = 2.0 * H * HW * HW * (dq + dv);
+  at.bytes_row = (double)HW * nqkv * tsize() + (double)HW * H * dv * tsize();
+  ops_.push_back(at);
+  emit_token_gemm(ao_, H * dv, dWo, c, H * dv, x, c, false, x, "token_gemm");
+}
+
+// TransformerFFNBlock (bin2onnx.py:1423-1438): RMSNorm, linear1 (| gate), SiLU(l1) * gate (the plain FFN, which
+// the reference rejects, as mish(l1)), linear2 * mask + residual.
+void Net::emit_ffn(const BlockDesc& b, float* x, int c) {
+  const int prec = prec_;
+  const int F = b.ffn_c, Fu = b.swiglu ? 2 * F : F;
+  std::vector<float> w1((size_t)Fu * c);
+  for (int f = 0; f < F; f++)
+    for (int k = 0; k < c; k++) {
+      w1[(size_t)f * c + k] = b.l1.w[(size_t)k * F + f];
+      if (b.swiglu) w1[(size_t)(F + f) * c + k] = b.lg.w[(size_t)k * F + f];
+    }
+  const void* dW1 = upload_t(w1);
+  std::vector<float> w2((size_t)c * F);
+  for (int o = 0; o < c; o++)
+    for (int f = 0; f < F; f++) w2[(size_t)o * F + f] = b.l2.w[(size_t)f * c + o];
+  const void* dW2 = upload_t(w2);
+  const float* lnw = upload_f(b.ln_w);
+  const float eps = b.ln_eps;
+  void* nrm = nrm_;
+  const float* mask = mask_;
+  Op rn;
+  rn.launch = [=](hipStream_t s, int B) { launch_rmsnorm_tok(prec, x, c, c, lnw, eps, mask, nrm, c, B * HW, s); };
+  rn.cls = "rmsnorm";
+  rn.bytes_row = (double)HW * c * (4 + tsize());
+  ops_.push_back(rn);
+  emit_token_gemm(nrm_, c, dW1, Fu, c, u_, Fu, false, nullptr, "token_gemm");
+  float* u = u_;
+  void* h = h_;
+  const bool gated = b.swiglu;
+  Op fa;
+  fa.launch = [=](hipStream_t s, int B) { launch_ffn_act(prec, u, Fu, F, gated, h, F, B * HW, s); };
+  fa.cls = "ffn_act";
+  fa.bytes_row = (double)HW * Fu * 4 + (double)HW * F * tsize();
+  ops_.push_back(fa);
+  emit_token_gemm(h_, F, dW2, c, F, x, c, false, x, "token_gemm");
+}
+
+void Net::emit_stack(const std::vector<BlockDesc>& blocks, float* x, int c, int depth) {
+  for (const BlockDesc& b : blocks) {
+    switch (b.kind) {
+      case BLOCK_RES: {
+        // x += conv2(bnact(conv1(bnact(x)))) (bin2onnx.py:1243-1249)
+        const int cm = b.regular.oc;
+        emit_conv(b.regular, x, c, false, bn_pro(b.pre_bn, b.pre_act), tmp_, cm, false, nullptr, 0);
+        emit_conv(b.final_conv, tmp_, cm, false, bn_pro(b.mid_bn, b.mid_act), x, c, true, nullptr, 0);
+        break;
+      }
+      case BLOCK_GPOOL: {
+        // regular | gpool convs share their input: one convolution with both filters (bin2onnx.py:1250-1261).
+        const int cr = b.regular.oc, cg = b.gconv.oc, ct = cr + cg;
+        ConvDesc both = b.regular;
+        both.oc = ct;
+        both.w.insert(both.w.end(), b.gconv.w.begin(), b.gconv.w.end());
+        if (b.regular.ky != b.gconv.ky || b.regular.kx != b.gconv.kx || b.regular.dy != b.gconv.dy || b.regular.dx != b.gconv.dx)
+          throw std::runtime_error(b.name + ": regular and gpool convolutions differ in shape");
+        emit_conv(both, x, c, false, bn_pro(b.pre_bn, b.pre_act), tmp_, ct, false, nullptr, 0);
+        const Prologue gpro = bn_pro(b.gbn, b.gact);
+        float* tmp = tmp_;
+        float* gp = gp_;
+        float* gb = gb_;
+        const float *area = area_, *s1 = s1_, *s2 = s2_;
+        Op pool;
+        pool.launch = [=](hipStream_t s, int B) { launch_pool(tmp, ct, cr, cg, gpro, area, s1, s2, false, gp, B, s); };
+        pool.cls = "pool";
+        pool.bytes_row = (double)HW * cg * 4;
+        ops_.push_back(pool);
+        const float* gw = upload_f(b.gmul.w);
+        Op mm;
+        mm.launch = [=](hipStream_t s, int B) { launch_small_matmul(gp, 3 * cg, 3 * cg, gw, cr, nullptr, ACT_ID, gb, cr, 1, false, B, s); };
+        mm.cls = "small_matmul";
+        mm.flops_row = 2.0 * 3 * cg * cr;
+        ops_.push_back(mm);
+        emit_conv(b.final_conv, tmp_, ct, false, bn_pro(b.mid_bn, b.mid_act, gb_, cr), x, c, true, nullptr, 0);
+        break;
+      }
+      case BLOCK_NBT: {
+        // x += post(bnact(inner(pre(bnact(x))))) (bin2onnx.py:1263-1269)
+        const int ci = b.regular.oc;
+        float* st = streams_[depth + 1];
+        emit_conv(b.regular, x, c, false, bn_pro(b.pre_bn, b.pre_act), st, ci, false, nullptr, 0);
+        emit_stack(b.inner, st, ci, depth + 1);
+        emit_conv(b.final_conv, st, ci, false, bn_pro(b.mid_bn, b.mid_act), x, c, true, nullptr, 0);
+        break;
+      }
+      case BLOCK_ATTN:
+        emit_attention(b, x, c);
+        break;
+      case BLOCK_FFN:
+        emit_ffn(b, x, c);
+        break;
+    }
+  }
+}
+
+void Net::build(const ModelDesc& m) {
+  const int C = m.trunk_c;
+  const size_t Mx = (size_t)max_batch_ * HW;
+  nin_ = m.num_input_channels;
+  nglob_ = m.num_global;
+  nmeta_ = m.num_meta;
+  row_len_ = m.row_len();
+
+  d_bin_ = alloc_f((size_t)max_batch_ * nin_ * HW);
+  d_glob_ = alloc_f((size_t)max_batch_ * nglob_);
+  d_meta_ = nmeta_ ? alloc_f((size_t)max_batch_ * nmeta_) : nullptr;
+  d_out_ = alloc_f((size_t)max_batch_ * row_len_);
+  KGX_HIP(hipMemset(d_bin_, 0, (size_t)max_batch_ * nin_ * HW * 4));
+  KGX_HIP(hipMemset(d_glob_, 0, (size_t)max_batch_ * nglob_ * 4));
+  if (d_meta_) KGX_HIP(hipMemset(d_meta_, 0, (size_t)max_batch_ * nmeta_ * 4));
+  mask_ = alloc_f(Mx);
+  area_ = alloc_f(max_batch_);
+  s1_ = alloc_f(max_batch_);
+  s2_ = alloc_f(max_batch_);
+
+  stream_c_.assign(1, C);
+  scan(m.blocks, C, 0);
+  trunk_ = alloc_f(Mx * C);
+  streams_.assign(stream_c_.size(), nullptr);
+  streams_[0] = trunk_;
+  for (size_t d = 1; d < stream_c_.size(); d++) streams_[d] = alloc_f(Mx * stream_c_[d]);
+  if (tmp_c_) tmp_ = alloc_f(Mx * tmp_c_);
+  if (gp_c_) gp_ = alloc_f((size_t)max_batch_ * gp_c_);
+  if (gb_c_) gb_ = alloc_f((size_t)max_batch_ * gb_c_);
+  if (nrm_c_) nrm_ = alloc_bytes(Mx * nrm_c_ * tsize());
+  if (qkv_c_) qkv_ = alloc_bytes(Mx * qkv_c_ * tsize());
+  if (ao_c_) ao_ = alloc_bytes(Mx * ao_c_ * tsize());
+  if (u_c_) u_ = alloc_f(Mx * u_c_);
+  if (h_c_) h_ = alloc_bytes(Mx * h_c_ * tsize());
+
+  // --- Trunk input (bin2onnx.py:1466-1492): mask, stem conv + global (and metadata) bias. ---
+  {
+    float *bin = d_bin_, *mask = mask_, *area = area_, *s1 = s1_, *s2 = s2_;
+    const int nin = nin_;
+    Op op;
+    op.launch = [=](hipStream_t s, int B) { launch_mask_prep(bin, nin, mask, area, s1, s2, B, s); };
+    op.cls = "mask_prep";
+    op.bytes_row = HW * 8.0;
+    ops_.push_back(op);
+  }
+  float* gbias = alloc_f((size_t)max_batch_ * C);
+  {
+    const float* w = upload_f(m.stem_mm.w);
+    float* glob = d_glob_;
+    const int G = nglob_;
+    Op op;
+    op.launch = [=](hipStream_t s, int B) { launch_small_matmul(glob, G, G, w, C, nullptr, ACT_ID, gbias, C, 1, false, B, s); };
+    op.cls = "small_matmul";
+    op.flops_row = 2.0 * G * C;
+    ops_.push_back(op);
+  }
+  if (m.meta_version > 0) {
+    const int h1 = m.meta1.oc, h2 = m.meta2.oc;
+    float* t1 = alloc_f((size_t)max_batch_ * h1);
+    float* t2 = alloc_f((size_t)max_batch_ * h2);
+    const float *w1 = upload_f(m.meta1.w), *b1 = upload_f(m.meta_b1.b), *w2 = upload_f(m.meta2.w),
+                *b2 = upload_f(m.meta_b2.b), *w3 = upload_f(m.meta3.w);
+    const int a1 = m.meta_act1, a2 = m.meta_act2;
+    float* meta = d_meta_;
+    Op op;
+    op.launch = [=](hipStream_t s, int B) {
+      launch_small_matmul(meta, 192, 192, w1, h1, b1, a1, t1, h1, 1, false, B, s);
+      launch_small_matmul(t1, h1, h1, w2, h2, b2, a2, t2, h2, 1, false, B, s);
+      launch_small_matmul(t2, h2, h2, w3, C, nullptr, ACT_ID, gbias, C, 1, true, B, s);
+    };
+    op.cls = "small_matmul";
+    op.flops_row = 2.0 * (192.0 * h1 + (double)h1 * h2 + (double)h2 * C);
+    ops_.push_back(op);
+  }
+  emit_conv(m.stem, d_bin_, 0, true, Prologue(), trunk_, C, false, gbias, C);
+
+  // --- Blocks. ---
+  emit_stack(m.blocks, trunk_, C, 0);
+
+  // --- Trunk tip and heads (bin2onnx.py:1489-1531). ---
+  const float* head_in = trunk_;
+  Prologue tip_pro;
+  if (m.trunk_norm_kind == 0) {
+    tip_pro = bn_pro(m.tip_bn, m.tip_act);
+  } else {
+    float* tip = alloc_f(Mx * C);
+    float* rs = alloc_f(max_batch_);
+    const float *gamma = upload_f(m.tip_gamma), *beta = upload_f(m.tip_beta);
+    const float eps = m.tip_rms_eps;
+    const bool spatial = m.tip_rms_spatial;
+    const int act = m.tip_act;
+    float *trunk = trunk_, *mask = mask_, *area = area_;
+    Op op;
+    op.launch = [=](hipStream_t s, int B) { launch_tip_rms(trunk, C, gamma, beta, eps, spatial, act, mask, area, rs, tip, B, s); };
+    op.cls = "rmsnorm";
+    op.bytes_row = HW * C * 8.0;
+    ops_.push_back(op);
+    head_in = tip;
+  }
+  for (const ConvDesc* hc : {&m.p1, &m.g1, &m.v1, &m.p2, &m.own})
+    if (hc->ky != 1 || hc->kx != 1) throw std::runtime_error(hc->name + ": head convolutions must be 1x1");
+  const int cp = m.p1.oc, cg = m.g1.oc, cv = m.v1.oc, nh = cp + cg + cv;
+  if (C % 8 != 0) throw std::runtime_error("trunk channels must be a multiple of 8");
+  std::vector<float> wh((size_t)nh * C);
+  std::memcpy(wh.data(), m.p1.w.data(), (size_t)cp * C * 4);
+  std::memcpy(wh.data() + (size_t)cp * C, m.g1.w.data(), (size_t)cg * C * 4);
+  std::memcpy(wh.data() + (size_t)(cp + cg) * C, m.v1.w.data(), (size_t)cv * C * 4);
+  const void* dWh = upload_t(wh);
+  float* H = alloc_f(Mx * nh);
+  {
+    const int prec = prec_;
+    Op op;
+    op.launch = [=](hipStream_t s, int B) {
+      GemmArgs g;
+      g.A = head_in; g.lda = C; g.a_float = true; g.pro = tip_pro;
+      g.Bt = dWh; g.ldb = C;
+      g.C = H; g.ldc = nh;
+      g.M = B * HW; g.N = nh; g.K = C;
+      launch_gemm(prec, g, s);
+    };
+    op.cls = "gemm_1x1";
+    op.flops_row = 2.0 * HW * C * nh;
+    op.bytes_row = (double)HW * C * 4 + (double)HW * nh * 4;
+    ops_.push_back(op);
+  }
+  const int P = m.P, S = m.S, rl = row_len_;
+  float* out = d_out_;
+  const float *area = area_, *s1 = s1_, *s2 = s2_;
+  // Policy: g1 pooling, gpool bias of p1, pass logits.
+  float* g1p = alloc_f((size_t)max_batch_ * 3 * cg);
+  float* p1b = alloc_f((size_t)max_batch_ * cp);
+  {
+    const Prologue gpro = bn_pro(m.g1_bn, m.g1_act);
+    const float* wgb = upload_f(m.gpool_to_bias.w);
+    const float* wp1 = upload_f(m.pass1.w);
+    const bool v15 = m.version >= 15;
+    const float* pb = v15 ? upload_f(m.pass_bias.b) : nullptr;
+    const float* wp2 = v15 ? upload_f(m.pass2.w) : nullptr;
+    const int pact = m.pass_act, ph = m.pass1.oc;
+    float* pt = v15 ? alloc_f((size_t)max_batch_ * ph) : nullptr;
+    Op op;
+    op.launch = [=](hipStream_t s, int B) {
+      launch_pool(H, nh, cp, cg, gpro, area, s1, s2, false, g1p, B, s);
+      launch_small_matmul(g1p, 3 * cg, 3 * cg, wgb, cp, nullptr, ACT_ID, p1b, cp, 1, false, B, s);
+      if (v15) {
+        launch_small_matmul(g1p, 3 * cg, 3 * cg, wp1, ph, pb, pact, pt, ph, 1, false, B, s);
+        launch_small_matmul(pt, ph, ph, wp2, P, nullptr, ACT_ID, out + HW, rl, HW + 1, false, B, s);
+      } else {
+        launch_small_matmul(g1p, 3 * cg, 3 * cg, wp1, P, nullptr, ACT_ID, out + HW, rl, HW + 1, false, B, s);
+      }
+    };
+    op.cls = "head";
+    op.bytes_row = (double)HW * cg * 4;
+    ops_.push_back(op);
+  }
+  // Value: value pooling, v2, v3, sv3.
+  {
+    const Prologue vpro = bn_pro(m.v1_bn, m.v1_act);
+    float* vp = alloc_f((size_t)max_batch_ * 3 * cv);
+    const int c2 = m.v2.oc;
+    float* v2 = alloc_f((size_t)max_batch_ * c2);
+    const float *w2 = upload_f(m.v2.w), *b2 = upload_f(m.v2_bias.b), *w3 = upload_f(m.v3.w), *b3 = upload_f(m.v3_bias.b),
+                *ws = upload_f(m.sv3.w), *bs = upload_f(m.sv3_bias.b);
+    const int a2 = m.v2_act;
+    Op op;
+    op.launch = [=](hipStream_t s, int B) {
+      launch_pool(H, nh, cp + cg, cv, vpro, area, s1, s2, true, vp, B, s);
+      launch_small_matmul(vp, 3 * cv, 3 * cv, w2, c2, b2, a2, v2, c2, 1, false, B, s);
+      launch_small_matmul(v2, c2, c2, w3, 3, b3, ACT_ID, out + P * (HW + 1), rl, 1, false, B, s);
+      launch_small_matmul(v2, c2, c2, ws, S, bs, ACT_ID, out + P * (HW + 1) + 3, rl, 1, false, B, s);
+    };
+    op.cls = "head";
+    op.bytes_row = (double)HW * cv * 4;
+    ops_.push_back(op);
+  }
+  // Spatial policy and ownership.
+  {
+    HeadSpatialArgs a;
+    a.H = H; a.ldh = nh;
+    a.p1_off = 0; a.c_p1 = cp; a.p1_bias = p1b;
+    a.p1_scale = upload_f(m.p1_bn.scale); a.p1_shift = upload_f(m.p1_bn.bias); a.p1_act = m.p1_act;
+    std::vector<float> wp2((size_t)cp * P);
+    for (int p = 0; p < P; p++)
+      for (int k = 0; k < cp; k++) wp2[(size_t)k * P + p] = m.p2.w[(size_t)p * cp + k];
+    a.w_p2 = upload_f(wp2); a.P = P;
+    a.v1_off = cp + cg; a.c_v1 = cv;
+    a.v1_scale = upload_f(m.v1_bn.scale); a.v1_shift = upload_f(m.v1_bn.bias); a.v1_act = m.v1_act;
+    a.w_own = upload_f(m.own.w);
+    a.mask = mask_;
+    a.out = out; a.row_len = rl; a.own_off = P * (HW + 1) + 3 + S;
+    if (m.p1_act != m.v1_act) throw std::runtime_error("policy p1 and value v1 activations differ");
+    Op op;
+    op.launch = [=](hipStream_t s, int B) { launch_head_spatial(a, B, s); };
+    op.cls = "head";
+    op.bytes_row = (double)HW * (cp + cv) * 4;
+    ops_.push_back(op);
+  }
+
+  // Winograd workspace, sized by the largest convolution.
+  if (wino_v_elems_) wino_v_ = alloc_bytes(wino_v_elems_ * tsize());
+  if (wino_m_elems_) wino_m_ = alloc_f(wino_m_elems_);
+  KGX_HIP(hipDeviceSynchronize());
+}
+
+void Net::run_ops(int B, hipStream_t s) {
+  if (!profiling_) {
+    for (const Op& op : ops_) op.launch(s, B);
+    return;
+  }
+  const size_t need = 2 * ops_.size();
+  while (events_.size() < need) {
+    hipEvent_t e;
+    KGX_HIP(hipEventCreate(&e));
+    events_.push_back(e);
+  }
+  for (size_t k = 0; k < ops_.size(); k++) {
+    KGX_HIP(hipEventRecord(events_[2 * k], s));
+    ops_[k].launch(s, B);
+    KGX_HIP(hipEventRecord(events_[2 * k + 1], s));
+  }
+  KGX_HIP(hipStreamSynchronize(s));
+  for (size_t k = 0; k < ops_.size(); k++) {
+    float ms = 0.f;
+    KGX_HIP(hipEventElapsedTime(&ms, events_[2 * k], events_[2 * k + 1]));
+    ProfileClass& pc = profile_[ops_[k].cls];
+    pc.launches++;
+    pc.ms += ms;
+    pc.flops += ops_[k].flops_row * B;
+    pc.bytes += ops_[k].bytes_row * B + ops_[k].bytes_fixed;
+  }
+}
+
+void Net::forward(int B, hipStream_t s) {
+  if (B < 1 || B > max_batch_) throw std::runtime_error("batch size out of range");
+  KGX_HIP(hipSetDevice(device_));
+  if (profiling_ || !use_graphs_) {
+    run_ops(B, s);
+    return;
+  }
+  auto it = graphs_.find(B);
+  if (it == graphs_.end()) {
+    hipGraph_t graph;
+    KGX_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
+    try {
+      run_ops(B, s);
+    } catch (...) {
+      hipGraph_t g2;
+      (void)hipStreamEndCapture(s, &g2);
+      if (g2) (void)hipGraphDestroy(g2);
+      throw;
+    }
+    KGX_HIP(hipStreamEndCapture(s, &graph));
+    hipGraphExec_t exec;
+    KGX_HIP(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0));
+    (void)hipGraphDestroy(graph);
+    it = graphs_.emplace(B, exec).first;
+  }
+  KGX_HIP(hipGraphLaunch(it->second, s));
+}
+
+}  // namespace kgx

@@ -1,0 +1,134 @@
+"""ctypes binding of the CPU oracle (oracle/kgo_oracle.cpp).
+
+Test infrastructure: imported only by tests/, the smoke check and the benchmark's CPU-baseline leg, as the
+checker. Nothing in the product path imports it.
+"""
+
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "build", "libkgo_oracle.so")
+_lib = None
+
+
+def build():
+    import subprocess
+    subprocess.run(["make", "-C", _HERE, "-s"], check=True)
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            build()
+        L = ctypes.CDLL(LIB_PATH)
+        L.kgo_last_error.restype = ctypes.c_char_p
+        L.kgo_model_parse.argtypes = [ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_void_p)]
+        L.kgo_model_free.argtypes = [ctypes.c_void_p]
+        L.kgo_model_info.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        for fn in (L.kgo_forward_f64, L.kgo_forward_f32):
+            fn.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
+                           ctypes.c_void_p, ctypes.c_int]
+        L.kgo_conv_direct_f64.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p] * 3
+        L.kgo_wino_filter_f64.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
+        L.kgo_conv3x3_winograd_f64.argtypes = [ctypes.c_int] * 3 + [ctypes.c_void_p] * 3
+        L.kgo_copy_with_symmetry.argtypes = [ctypes.c_void_p, ctypes.c_void_p] + [ctypes.c_int] * 7
+        L.kgo_padded_batch_size.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
+        L.kgo_copy_outputs_row.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                           ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        _lib = L
+    return _lib
+
+
+def _p(a):
+    return None if a is None else a.ctypes.data_as(ctypes.c_void_p)
+
+
+class Model:
+    """A parsed KataGo model file, evaluated on the CPU."""
+
+    def __init__(self, model_bytes: bytes):
+        L = lib()
+        self._buf = ctypes.create_string_buffer(model_bytes, len(model_bytes))
+        h = ctypes.c_void_p()
+        if L.kgo_model_parse(self._buf, len(model_bytes), ctypes.byref(h)) != 0:
+            raise ValueError(L.kgo_last_error().decode())
+        self._h = h
+        info = np.zeros(8, np.int32)
+        L.kgo_model_info(self._h, _p(info))
+        (self.version, self.num_input_channels, self.num_global, self.num_meta, self.P, self.S, self.row_len,
+         self.trunk_c) = (int(v) for v in info)
+
+    def __del__(self):
+        if getattr(self, "_h", None):
+            lib().kgo_model_free(self._h)
+            self._h = None
+
+    def forward(self, spatial, glob, meta=None, dtype=np.float64, threads=None):
+        """Raw output rows [n, row_len] (policy P x 362 with pass last, value 3, score S, ownership 361)."""
+        n = spatial.shape[0]
+        spatial = np.ascontiguousarray(spatial, np.float32)
+        glob = np.ascontiguousarray(glob, np.float32)
+        if self.num_meta:
+            meta = np.ascontiguousarray(meta, np.float32)
+        else:
+            meta = None
+        threads = threads or os.cpu_count() or 1
+        out = np.zeros((n, self.row_len), dtype)
+        fn = lib().kgo_forward_f64 if dtype == np.float64 else lib().kgo_forward_f32
+        if fn(self._h, n, _p(spatial), _p(glob), _p(meta), _p(out), threads) != 0:
+            raise RuntimeError(lib().kgo_last_error().decode())
+        return out
+
+
+def conv_direct(x, w):
+    x = np.ascontiguousarray(x, np.float64); w = np.ascontiguousarray(w, np.float64)
+    n, ic = x.shape[:2]; oc, _, k, _ = w.shape
+    y = np.zeros((n, oc, 19, 19))
+    lib().kgo_conv_direct_f64(n, ic, oc, k, _p(x), _p(w), _p(y))
+    return y
+
+
+def wino_filter(w):
+    w = np.ascontiguousarray(w, np.float64)
+    oc, ic = w.shape[:2]
+    out = np.zeros((36, ic, oc))
+    lib().kgo_wino_filter_f64(oc, ic, _p(w), _p(out))
+    return out
+
+
+def conv3x3_winograd(x, w):
+    x = np.ascontiguousarray(x, np.float64); w = np.ascontiguousarray(w, np.float64)
+    n, ic = x.shape[:2]; oc = w.shape[0]
+    y = np.zeros((n, oc, 19, 19))
+    lib().kgo_conv3x3_winograd_f64(n, ic, oc, _p(x), _p(w), _p(y))
+    return y
+
+
+def copy_with_symmetry(src, sym, nhwc=False, reverse=False):
+    """src [n, c, h, w] (or [n, h, w, c] with nhwc)."""
+    src = np.ascontiguousarray(src, np.float32)
+    dst = np.zeros_like(src)
+    if nhwc:
+        n, h, w, c = src.shape
+    else:
+        n, c, h, w = src.shape
+    lib().kgo_copy_with_symmetry(_p(src), _p(dst), n, h, w, c, int(nhwc), sym, int(reverse))
+    return dst
+
+
+def padded_batch_size(buckets, n, max_batch):
+    b = np.ascontiguousarray(buckets, np.int32)
+    return lib().kgo_padded_batch_size(_p(b), len(b), n, max_batch)
+
+
+def copy_outputs_row(row, P, S, version, sym, optimism, want_owner=True):
+    row = np.ascontiguousarray(row, np.float32)
+    pol = np.zeros(362, np.float32)
+    fields = np.zeros(9, np.float32)
+    own = np.zeros(361, np.float32) if want_owner else None
+    lib().kgo_copy_outputs_row(_p(row), P, S, version, sym, ctypes.c_float(optimism), _p(pol), _p(fields), _p(own))
+    return pol, fields, own

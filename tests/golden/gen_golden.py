@@ -1,0 +1,57 @@
+"""Writes the committed fixtures of tests/golden/.
+
+- m0_inputs.npz: four featurized positions taken from the reference's own fixtures
+  (fixtures/m0/b18c384nbt.bin_input.f32, .global_input.f32 and b18c384nbt-humanv0.meta_input.f32; rows 0 and 1
+  are 19x19 boards, row 20 a 9x9 board, row 24 a 13x13 board). These are weight-free data: realistic inputs
+  whose board masks are not full. Reading them needs the reference checkout (REFERENCE env var, default
+  /root/reference); the rest of this script does not.
+- oracle_tiny.npz: for each small test net (katago-rs_amd.synth.tiny_nets, seed 1), the oracle's float64 raw
+  outputs on seeded inputs (3 rows: 19x19, 9x9, 13x13 boards) and on the m0 positions.
+
+Run: python tests/golden/gen_golden.py
+"""
+
+import importlib
+import os
+import sys
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ROOT = os.path.dirname(os.path.dirname(HERE))
+sys.path.insert(0, ROOT)
+
+M0_ROWS = [0, 1, 20, 24]
+
+
+def main():
+    synth = importlib.import_module("katago-rs_amd.synth")
+    import oracle
+
+    ref = os.environ.get("REFERENCE", "/root/reference")
+    m0_path = os.path.join(HERE, "m0_inputs.npz")
+    if os.path.isdir(ref):
+        d = os.path.join(ref, "fixtures", "m0")
+        binp = np.fromfile(os.path.join(d, "b18c384nbt.bin_input.f32"), "<f4").reshape(-1, 22, 19, 19)
+        glob = np.fromfile(os.path.join(d, "b18c384nbt.global_input.f32"), "<f4").reshape(-1, 19)
+        meta = np.fromfile(os.path.join(d, "b18c384nbt-humanv0.meta_input.f32"), "<f4").reshape(-1, 192)
+        np.savez_compressed(m0_path, spatial=binp[M0_ROWS], glob=glob[M0_ROWS], meta=meta[M0_ROWS],
+                            rows=np.array(M0_ROWS))
+    m0 = np.load(m0_path)
+
+    out = {}
+    for name, arch in synth.tiny_nets().items():
+        model = oracle.Model(synth.write_model(arch, 1))
+        sp, gl, me = synth.make_inputs(3, 2, board_sizes=[19, 9, 13], meta=arch.meta_encoder)
+        out[f"{name}.spatial"] = sp
+        out[f"{name}.glob"] = gl
+        if me is not None:
+            out[f"{name}.meta"] = me
+        out[f"{name}.out"] = model.forward(sp, gl, me)
+        out[f"{name}.m0_out"] = model.forward(m0["spatial"], m0["glob"], m0["meta"] if arch.meta_encoder else None)
+    np.savez_compressed(os.path.join(HERE, "oracle_tiny.npz"), **out)
+    print("wrote", m0_path, "and oracle_tiny.npz")
+
+
+if __name__ == "__main__":
+    main()

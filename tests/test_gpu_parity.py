@@ -1,0 +1,183 @@
+"""Parity of the HIP forward pass (through the C ABI) with the float64 CPU oracle, on the device.
+
+Tolerances, per output group (policy, value, score, ownership) of each row block:
+- f32: max |gpu - oracle| <= 1e-4 * max |oracle| over the group (the f32 tier's 1e-4 relative error);
+- f16: max |gpu - oracle| <= 2e-2 absolute;
+- bf16: max |gpu - oracle| <= 1e-1 absolute (8-bit mantissa operands; no reference tier exists).
+Index work (symmetry, padding rows, batch buckets, tile scatter) is checked bit-exactly where the arithmetic
+is identical: a row's outputs must not depend on the batch it runs in.
+"""
+
+import os
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+TOL = {"f32": ("rel", 1e-4), "f16": ("abs", 2e-2), "bf16": ("abs", 1e-1)}
+
+
+def groups(P, S):
+    p = P * 362
+    return {"policy": slice(0, p), "value": slice(p, p + 3), "score": slice(p + 3, p + 3 + S),
+            "ownership": slice(p + 3 + S, p + 3 + S + 361)}
+
+
+def errors(out, ref, P, S):
+    res = {}
+    for k, sl in groups(P, S).items():
+        d = np.abs(out[:, sl].astype(np.float64) - ref[:, sl])
+        res[k] = (float(d.max()), float(np.abs(ref[:, sl]).max()))
+    return res
+
+
+def check(out, ref, P, S, prec, what):
+    assert np.all(np.isfinite(out)), f"{what}: non-finite outputs"
+    kind, tol = TOL[prec]
+    errs = errors(out, ref, P, S)
+    print(f"{what} [{prec}] " + " ".join(f"{k}: err {e:.2e} (|ref| {s:.2e})" for k, (e, s) in errs.items()))
+    for k, (e, s) in errs.items():
+        bound = tol * max(s, 1e-30) if kind == "rel" else tol
+        assert e <= bound, f"{what} [{prec}] {k}: max err {e:.3e} > {bound:.3e} (|ref| max {s:.3e})"
+
+
+@pytest.fixture(scope="module")
+def golden():
+    return np.load(os.path.join(GOLDEN, "oracle_tiny.npz")), np.load(os.path.join(GOLDEN, "m0_inputs.npz"))
+
+
+@pytest.mark.parametrize("prec", ["f32", "f16", "bf16"])
+@pytest.mark.parametrize("name", ["t_res", "t_nbt", "t_v8", "t_tf", "t_human", "t_rms", "t_rmspos"])
+def test_tiny_nets_match_oracle(kgx, synth, golden, name, prec):
+    g, m0 = golden
+    arch = synth.tiny_nets()[name]
+    net = kgx.Net(synth.write_model(arch, 1))
+    h = kgx.Handle(net, 8, prec)
+    meta = g[f"{name}.meta"] if f"{name}.meta" in g else None
+    out = h.forward(g[f"{name}.spatial"], g[f"{name}.glob"], meta)
+    check(out, g[f"{name}.out"], net.P, net.S, prec, name)
+    out = h.forward(m0["spatial"], m0["glob"], m0["meta"] if arch.meta_encoder else None)
+    check(out, g[f"{name}.m0_out"], net.P, net.S, prec, name + " m0")
+    h.close()
+
+
+CONFIG_ROWS = {"b10c128": 8, "b18c384nbt": 2, "b10c384h6": 2, "b10c512h8": 1, "tf3-b11c768": 1}
+
+
+@pytest.mark.parametrize("prec", ["f32", "f16"])
+@pytest.mark.parametrize("name", list(CONFIG_ROWS))
+def test_benchmark_configs_match_oracle(kgx, synth, oracle, name, prec):
+    arch_fn, batch = synth.CONFIGS[name]
+    mb = synth.write_model(arch_fn(), synth.CONFIG_SEEDS[name])
+    n = CONFIG_ROWS[name]
+    sp, gl, _ = synth.make_inputs(batch, 17, board_sizes=[19, 19, 13, 9])
+    net = kgx.Net(mb)
+    h = kgx.Handle(net, batch, prec)
+    out = h.forward(sp, gl)
+    ref = oracle.Model(mb).forward(sp[:n], gl[:n])
+    check(out[:n], ref, net.P, net.S, prec, name)
+    # The full batch stays finite, and a row's outputs do not depend on the rest of its batch.
+    assert np.all(np.isfinite(out))
+    again = h.forward(sp[:n], gl[:n])
+    assert np.array_equal(again, out[:n])
+    h.close()
+
+
+def test_rows_do_not_depend_on_batch_or_bucket(kgx, synth):
+    arch = synth.tiny_nets()["t_nbt"]
+    net = kgx.Net(synth.write_model(arch, 3))
+    h = kgx.Handle(net, 16, "f16")
+    sp, gl, _ = synth.make_inputs(16, 4, board_sizes=[19, 13, 9, 5])
+    full = h.forward(sp, gl)
+    for n in (1, 3, 7, 16):
+        assert np.array_equal(h.forward(sp[:n], gl[:n]), full[:n]), n
+    # Buckets pad with stale rows (backend.rs:549-556); the real rows are unchanged.
+    h.set_batch_buckets([4, 8, 16])
+    for n in (1, 3, 5):
+        assert np.array_equal(h.forward(sp[:n], gl[:n]), full[:n]), n
+    h.close()
+
+
+def test_graph_replays_are_deterministic(kgx, synth):
+    arch = synth.tiny_nets()["t_tf"]
+    net = kgx.Net(synth.write_model(arch, 3))
+    h = kgx.Handle(net, 8, "f16")
+    sp, gl, _ = synth.make_inputs(8, 6)
+    first = h.forward(sp, gl)
+    for n in (8, 2, 8, 5, 8):
+        out = h.forward(sp[:n], gl[:n])
+        assert np.array_equal(out, first[:n])
+    h.close()
+
+
+def test_get_output_applies_symmetry_and_optimism(kgx, synth, oracle):
+    arch = synth.tiny_nets()["t_rms"]  # P = 4 at model version 17: the optimism mix uses channels 0 and 1
+    mb = synth.write_model(arch, 8)
+    net = kgx.Net(mb)
+    h = kgx.Handle(net, 8, "f32")
+    sp, gl, _ = synth.make_inputs(8, 2, board_sizes=[19, 13])
+    rows = [{"spatial": sp[i], "glob": gl[i], "symmetry": i, "policy_optimism": 0.25 * (i % 3)} for i in range(8)]
+    res = h.get_output(rows)
+    # Expected: the raw forward on the symmetrized inputs, then the oracle's copy_outputs.
+    sym_in = np.stack([oracle.copy_with_symmetry(sp[i:i + 1], i)[0] for i in range(8)])
+    raw = h.forward(sym_in, gl)
+    for i in range(8):
+        pol, fields, own = oracle.copy_outputs_row(raw[i], net.P, net.S, net.version, i, 0.25 * (i % 3))
+        assert np.array_equal(res[i]["policy"], pol), i
+        assert np.array_equal(res[i]["ownership"], own), i
+        got = [res[i][k] for k in ("white_win_prob", "white_loss_prob", "white_no_result_prob", "white_score_mean",
+                                   "white_score_mean_sq", "white_lead", "var_time_left", "shortterm_winloss_error",
+                                   "shortterm_score_error")]
+        assert np.array_equal(np.array(got, np.float32), fields), i
+    h.close()
+
+
+def test_old_model_version_output_unpacking(kgx, synth, oracle):
+    arch = synth.tiny_nets()["t_v8"]  # P = 1, S = 4
+    net = kgx.Net(synth.write_model(arch, 8))
+    h = kgx.Handle(net, 2, "f32")
+    sp, gl, _ = synth.make_inputs(2, 2)
+    res = h.get_output([{"spatial": sp[i], "glob": gl[i], "symmetry": 5 + i, "policy_optimism": 1.0}
+                        for i in range(2)])
+    raw = h.forward(np.stack([oracle.copy_with_symmetry(sp[i:i + 1], 5 + i)[0] for i in range(2)]), gl)
+    for i in range(2):
+        pol, fields, own = oracle.copy_outputs_row(raw[i], 1, 4, 8, 5 + i, 1.0)
+        assert np.array_equal(res[i]["policy"], pol)
+        assert res[i]["shortterm_score_error"] == 0.0 and res[i]["var_time_left"] == fields[6]
+    h.close()
+
+
+def test_entry_points_reject_bad_calls(kgx, synth):
+    arch = synth.tiny_nets()["t_human"]
+    net = kgx.Net(synth.write_model(arch, 1))
+    h = kgx.Handle(net, 4, "f16")
+    sp, gl, me = synth.make_inputs(5, 1, meta=1)
+    with pytest.raises(kgx.KgError, match="batch size out of range"):
+        h.forward(sp, gl, me)
+    with pytest.raises(kgx.KgError, match="needs a meta_input"):
+        h.forward(sp[:2], gl[:2], None)
+    out = h.forward(sp[:4], gl[:4], me[:4])
+    assert out.shape == (4, net.row_len) and np.all(np.isfinite(out))
+    h.close()
+
+
+def test_device_resident_run_matches_forward(kgx, synth):
+    import ctypes
+    arch = synth.tiny_nets()["t_res"]
+    net = kgx.Net(synth.write_model(arch, 2))
+    h = kgx.Handle(net, 4, "f16")
+    sp, gl, _ = synth.make_inputs(4, 3)
+    ref = h.forward(sp, gl)
+    h2 = kgx.Handle(net, 4, "f16")
+    d_bin, d_glob, _, _ = h2.device_buffers()
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    assert hip.hipMemcpy(d_bin, sp.ctypes.data, sp.nbytes, 1) == 0
+    assert hip.hipMemcpy(d_glob, gl.ctypes.data, gl.nbytes, 1) == 0
+    out = np.empty_like(ref)
+    h2.run(4, out)
+    assert np.array_equal(out, ref)
+    h.close()
+    h2.close()

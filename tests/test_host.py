@@ -1,0 +1,100 @@
+"""Host-side checks of the product library that need no GPU: every declared entry point is exported, the model
+parser agrees with the oracle's and rejects what the reference rejects, bucket choice matches the reference's
+cases, and handle creation refuses unsupported contexts before touching a device."""
+
+import gzip
+import os
+import re
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_library_exports_every_declared_symbol(kgx):
+    header = open(os.path.join(ROOT, "include", "kgx.h")).read()
+    declared = sorted(set(re.findall(r"\b(kg_[a-z0-9_]+)\s*\(", header)))
+    assert declared, "no declarations found"
+    lib = kgx.lib()
+    missing = [s for s in declared if not hasattr(lib, s)]
+    assert not missing, missing
+    assert sorted(kgx.EXPORTS) == declared
+
+
+def _nets(synth):
+    nets = dict(synth.tiny_nets())
+    for name in ("b10c128", "b18c384nbt", "b10c384h6"):
+        nets[name] = synth.CONFIGS[name][0]()
+    return nets
+
+
+def test_parser_agrees_with_oracle(kgx, synth, oracle):
+    for name, arch in _nets(synth).items():
+        mb = synth.write_model(arch, 5)
+        net = kgx.Net(mb)
+        om = oracle.Model(mb)
+        assert (net.version, net.P, net.S, net.row_len, net.num_input_channels, net.num_global, net.num_meta) == \
+               (om.version, om.P, om.S, om.row_len, om.num_input_channels, om.num_global, om.num_meta), name
+        assert net.desc.trunk_num_channels == arch.trunk_c
+        assert net.name == arch.name
+        assert net.row_len == synth.row_len(arch)
+
+
+def test_parser_reads_gzip_and_text_models(kgx, synth):
+    arch = synth.tiny_nets()["t_tf"]
+    mb, _ = synth.write_model_tree(arch, 2)
+    txt, _ = synth.write_model_tree(arch, 2, text_floats=True)
+    p = [kgx.Net(b).desc.num_parameters for b in (mb, gzip.compress(mb), txt)]
+    assert p[0] == p[1] == p[2] > 0
+
+
+def test_parser_rejections(kgx, synth):
+    arch = synth.tiny_nets()["t_res"]
+    mb = synth.write_model(arch, 1)
+    with pytest.raises(kgx.KgError, match="expectedSha256 is not supported"):
+        kgx.Net(mb, expected_sha256="00" * 32)
+    with pytest.raises(kgx.KgError):
+        kgx.Net(mb[: len(mb) // 2])
+    with pytest.raises(kgx.KgError, match="unparsed trailing bytes"):
+        kgx.Net(mb + b" 7")
+    newer = mb.replace(b"t-res\n14\n", b"t-res\n18\n", 1)
+    with pytest.raises(kgx.KgError, match="requires a newer KataGo version"):
+        kgx.Net(newer)
+    bad_kind = mb.replace(b"ordinary_block", b"mystery_block", 1)
+    with pytest.raises(kgx.KgError, match="unknown block kind"):
+        kgx.Net(bad_kind)
+    with pytest.raises(kgx.KgError, match="Model name"):
+        kgx.Net(mb.replace(b"t-res", b"t.res", 1))
+
+
+def test_padded_batch_size_reference_cases(kgx):
+    # crates/katago-nn-burn/tests/batch_buckets.rs:27-35
+    b = [1, 2, 4, 8, 16, 32]
+    assert kgx.padded_batch_size(b, 1, 32) == 1
+    assert kgx.padded_batch_size(b, 3, 32) == 4
+    assert kgx.padded_batch_size(b, 17, 32) == 32
+    assert kgx.padded_batch_size(b, 17, 24) == 17
+    assert kgx.padded_batch_size([], 5, 32) == 5
+
+
+def test_handle_rejects_unsupported_contexts(kgx, synth):
+    # createComputeContext / createComputeHandle checks (backend.rs:300-372), made before any device call.
+    net = kgx.Net(synth.write_model(synth.tiny_nets()["t_res"], 1))
+    with pytest.raises(kgx.KgError, match="nnXLen and nnYLen must equal"):
+        kgx.Handle(net, 4, "f32", nn_x_len=9, nn_y_len=9)
+    with pytest.raises(kgx.KgError, match="inputsUseNHWC = true unsupported"):
+        kgx.Handle(net, 4, "f32", inputs_use_nhwc=True)
+    with pytest.raises(kgx.KgError, match="max batch size"):
+        kgx.Handle(net, 0, "f32")
+
+
+def test_synthetic_inputs_follow_the_benchmark_distribution(synth):
+    sp, gl, me = synth.make_inputs(64, 0, board_sizes=[19, 9], meta=1)
+    assert sp.shape == (64, 22, 19, 19) and gl.shape == (64, 19) and me.shape == (64, 192)
+    assert set(np.unique(sp)) <= {0.0, 1.0}
+    assert np.all(sp[0::2, 0] == 1) and sp[1, 0].sum() == 81
+    assert np.all(sp[1, :, 9:, :] == 0) and np.all(sp[1, :, :, 9:] == 0)
+    frac = sp[0::2, 1:].mean()
+    assert 0.27 < frac < 0.33
+    assert np.all(np.abs(gl[:, 5]) <= 1) and set(np.unique(np.delete(gl, 5, axis=1))) <= {0.0, 1.0}

@@ -1,0 +1,174 @@
+"""Pins the CPU oracle (CPU-only tests).
+
+The oracle restates the reference's forward pass; these tests check it against what the mathematics and
+independent library routines fix: the Winograd F(4x4,3x3) identity, torch's float64 conv2d, an independent
+float64 forward built from torch library ops over the same weights (tests/torch_ref.py, which follows
+bin2onnx's graph node by node), the dihedral symmetry group, and the reference's bucket cases.
+"""
+
+import gzip
+import os
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+import torch_ref
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def test_winograd_restatement_equals_direct_convolution(oracle):
+    rng = np.random.default_rng(7)
+    for n, ic, oc in [(1, 3, 5), (2, 7, 4)]:
+        x = rng.normal(size=(n, ic, 19, 19))
+        w = rng.normal(size=(oc, ic, 3, 3))
+        y_w = oracle.conv3x3_winograd(x, w)
+        y_d = oracle.conv_direct(x, w)
+        assert np.abs(y_w - y_d).max() <= 1e-12 * np.abs(y_d).max()
+
+
+def test_winograd_filter_transform_against_lavin_gray_matrices(oracle):
+    # F(4x4, 3x3) matrices as published (Lavin & Gray 2015): out = A^T [(G g G^T) * (B^T d B)] A is the 4x4
+    # correlation of the 6x6 tile d with g.
+    G = np.array([[1 / 4, 0, 0], [-1 / 6, -1 / 6, -1 / 6], [-1 / 6, 1 / 6, -1 / 6], [1 / 24, 1 / 12, 1 / 6],
+                  [1 / 24, -1 / 12, 1 / 6], [0, 0, 1]])
+    BT = np.array([[4, 0, -5, 0, 1, 0], [0, -4, -4, 1, 1, 0], [0, 4, -4, -1, 1, 0], [0, -2, -1, 2, 1, 0],
+                   [0, 2, -1, -2, 1, 0], [0, 4, 0, -5, 0, 1]], float)
+    AT = np.array([[1, 1, 1, 1, 1, 0], [0, 1, -1, 2, -2, 0], [0, 1, 1, 4, 4, 0], [0, 1, -1, 8, -8, 1]], float)
+    rng = np.random.default_rng(3)
+    g = rng.normal(size=(3, 3))
+    d = rng.normal(size=(6, 6))
+    direct = np.array([[np.sum(d[i:i + 3, j:j + 3] * g) for j in range(4)] for i in range(4)])
+    assert np.allclose(AT @ ((G @ g @ G.T) * (BT @ d @ BT.T)) @ AT.T, direct, atol=1e-12)
+    # The oracle's filter transform ([36][ic][oc], point p = 6*row + col) equals G g G^T.
+    w = rng.normal(size=(2, 3, 3, 3))
+    U = oracle.wino_filter(w)
+    for o in range(2):
+        for i in range(3):
+            assert np.allclose(U[:, i, o].reshape(6, 6), G @ w[o, i] @ G.T, atol=1e-14)
+
+
+@pytest.mark.parametrize("k", [1, 3, 5])
+def test_direct_convolution_matches_torch(oracle, k):
+    rng = np.random.default_rng(k)
+    x = rng.normal(size=(2, 4, 19, 19))
+    w = rng.normal(size=(3, 4, k, k))
+    y = oracle.conv_direct(x, w)
+    t = F.conv2d(torch.tensor(x), torch.tensor(w), padding=k // 2).numpy()
+    assert np.abs(y - t).max() <= 1e-12 * np.abs(t).max()
+
+
+def _tiny(synth):
+    return synth.tiny_nets()
+
+
+@pytest.mark.parametrize("name", ["t_res", "t_nbt", "t_v8", "t_tf", "t_human", "t_rms", "t_rmspos"])
+def test_oracle_matches_independent_torch_forward(oracle, synth, name):
+    arch = _tiny(synth)[name]
+    mb, tree = synth.write_model_tree(arch, 11)
+    sp, gl, me = synth.make_inputs(3, 5, board_sizes=[19, 9, 13], meta=arch.meta_encoder)
+    out = oracle.Model(mb).forward(sp, gl, me)
+    ref = torch_ref.Ref(tree).forward(sp, gl, me)
+    assert np.abs(out - ref).max() <= 1e-12 * max(1.0, np.abs(ref).max())
+
+
+def test_oracle_reproduces_golden_fixtures(oracle, synth):
+    g = np.load(os.path.join(GOLDEN, "oracle_tiny.npz"))
+    m0 = np.load(os.path.join(GOLDEN, "m0_inputs.npz"))
+    for name, arch in _tiny(synth).items():
+        model = oracle.Model(synth.write_model(arch, 1))
+        meta = g[f"{name}.meta"] if f"{name}.meta" in g else None
+        out = model.forward(g[f"{name}.spatial"], g[f"{name}.glob"], meta)
+        assert np.abs(out - g[f"{name}.out"]).max() <= 1e-12 * max(1.0, np.abs(out).max()), name
+        out = model.forward(m0["spatial"], m0["glob"], m0["meta"] if arch.meta_encoder else None)
+        assert np.abs(out - g[f"{name}.m0_out"]).max() <= 1e-12 * max(1.0, np.abs(out).max()), name
+
+
+def test_oracle_float32_path_close_to_float64(oracle, synth):
+    arch = _tiny(synth)["t_nbt"]
+    model = oracle.Model(synth.write_model(arch, 2))
+    sp, gl, _ = synth.make_inputs(2, 9)
+    a = model.forward(sp, gl)
+    b = model.forward(sp, gl, dtype=np.float32)
+    assert np.abs(a - b).max() <= 1e-5 * np.abs(a).max()
+
+
+def test_oracle_rows_are_independent(oracle, synth):
+    arch = _tiny(synth)["t_tf"]
+    model = oracle.Model(synth.write_model(arch, 4))
+    sp, gl, _ = synth.make_inputs(3, 1, board_sizes=[19, 7, 13])
+    both = model.forward(sp, gl)
+    for i in range(3):
+        one = model.forward(sp[i:i + 1], gl[i:i + 1])
+        assert np.array_equal(one[0], both[i])
+
+
+def test_full_board_pooling_constants(oracle, synth):
+    # On a full 19x19 board area = 361, so (sqrt(area) - 14) * 0.1 = 0.5 and (sqrt - 14)^2 * 0.01 - 0.1 = 0.15
+    # (bin2onnx.py:1203-1220): the value pool of a constant map c is [c, 0.5 c, 0.15 c].
+    r = torch_ref.Ref({})
+    n = 1
+    mask = torch.ones(n, 1, 19, 19, dtype=torch.float64)
+    r.mask = mask
+    r.mask_sum = mask.reshape(n, 1, 361).sum(2)
+    cc = torch.sqrt(r.mask_sum) - 14.0
+    r.s1, r.s2 = cc * 0.1, cc * cc * 0.01 - 0.1
+    x = torch.full((1, 2, 19, 19), 3.0, dtype=torch.float64)
+    vp = r.value_pool(x).numpy()[0]
+    assert np.allclose(vp, [3, 3, 1.5, 1.5, 0.45, 0.45], atol=1e-12)
+
+
+def _dihedral(a, s):
+    """The eight symmetries of a square array by the reference's bit meaning for outputs (reverse)."""
+    out = a
+    if s & 4:
+        out = out.T
+    if s & 1:
+        out = out[::-1, :]
+    if s & 2:
+        out = out[:, ::-1]
+    return out
+
+
+def test_symmetry_group(oracle):
+    rng = np.random.default_rng(0)
+    src = rng.normal(size=(1, 2, 19, 19)).astype(np.float32)
+    imgs = []
+    for s in range(8):
+        fwd = oracle.copy_with_symmetry(src, s)
+        back = oracle.copy_with_symmetry(fwd, s, reverse=True)
+        assert np.array_equal(back, src), s  # outputs map back through the same symmetry
+        rev = oracle.copy_with_symmetry(src, s, reverse=True)
+        assert np.array_equal(rev[0, 0], np.ascontiguousarray(_dihedral(src[0, 0], s))), s
+        imgs.append(fwd[0, 0].tobytes())
+    assert len(set(imgs)) == 8
+    # Bit meanings on inputs: 1 flips rows (y), 2 flips columns (x), 4 transposes.
+    p = src[0, 0]
+    assert np.array_equal(oracle.copy_with_symmetry(src, 1)[0, 0], p[::-1, :])
+    assert np.array_equal(oracle.copy_with_symmetry(src, 2)[0, 0], p[:, ::-1])
+    assert np.array_equal(oracle.copy_with_symmetry(src, 4)[0, 0], p.T)
+    # NHWC and NCHW agree.
+    nhwc = oracle.copy_with_symmetry(np.ascontiguousarray(src.transpose(0, 2, 3, 1)), 6, nhwc=True)
+    assert np.array_equal(nhwc.transpose(0, 3, 1, 2), oracle.copy_with_symmetry(src, 6))
+
+
+def test_padded_batch_size_reference_cases(oracle):
+    # crates/katago-nn-burn/tests/batch_buckets.rs:27-35
+    b = [1, 2, 4, 8, 16, 32]
+    assert oracle.padded_batch_size(b, 1, 32) == 1
+    assert oracle.padded_batch_size(b, 3, 32) == 4
+    assert oracle.padded_batch_size(b, 17, 32) == 32
+    assert oracle.padded_batch_size(b, 17, 24) == 17
+    assert oracle.padded_batch_size([], 5, 32) == 5
+
+
+def test_model_file_variants_parse_alike(oracle, synth):
+    arch = _tiny(synth)["t_human"]
+    mb, _ = synth.write_model_tree(arch, 3)
+    txt, _ = synth.write_model_tree(arch, 3, text_floats=True)
+    sp, gl, me = synth.make_inputs(2, 1, meta=1)
+    a = oracle.Model(mb).forward(sp, gl, me)
+    assert np.array_equal(a, oracle.Model(txt).forward(sp, gl, me))
+    assert np.array_equal(a, oracle.Model(gzip.compress(mb)).forward(sp, gl, me))
