@@ -368,13 +368,7 @@ int kg_profile_read(kg_handle* h, const char** names, long* launches, double* ms
   int k = 0;
   for (const auto& kv : h->net->profile()) {
     if (k < max_classes) {
-      // Class names are string literals of the op table; find the stable pointer by content.
-      static const char* known[] = {"wino_in", "wino_gemm", "wino_out", "gemm_1x1", "conv_direct", "mask_prep",
-                                    "small_matmul", "pool", "head", "rmsnorm", "token_gemm", "attention", "ffn_act"};
-      const char* nm = "other";
-      for (const char* c : known)
-        if (kv.first == c) nm = c;
-      names[k] = nm;
+      names[k] = kv.second.name;
       launches[k] = kv.second.launches;
       ms[k] = kv.second.ms;
       flops[k] = kv.second.flops;

@@ -1,0 +1,103 @@
+// Device-side helpers shared by the kernel translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include <cfloat>
+#include <stdexcept>
+#include <string>
+#include <type_traits>
+
+#include "kgx_kernels.h"
+
+namespace kgx {
+
+typedef _Float16 f16;
+typedef __bf16 bf16;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));  // 16-byte staging (registers, unlike HIP's uint4 struct)
+
+#define KGX_CHECK_LAUNCH()                                                                                    \
+  do {                                                                                                        \
+    hipError_t e_ = hipGetLastError();                                                                        \
+    if (e_ != hipSuccess) throw std::runtime_error(std::string("kernel launch: ") + hipGetErrorString(e_)); \
+  } while (0)
+
+template <int ACT>
+__device__ __forceinline__ float act_f(float a) {
+  if constexpr (ACT == ACT_RELU) {
+    return fmaxf(a, 0.f);
+  } else if constexpr (ACT == ACT_MISH) {
+    // a * tanh(softplus(a)); with e = exp(a), tanh(log(1 + e)) = e (e + 2) / (e (e + 2) + 2). Softplus is the
+    // identity above 20 (burn's threshold), where tanh is 1 in float. Branch-free: the exponent is clamped so
+    // that n stays finite, and the select picks the identity.
+    const float e = __expf(fminf(a, 20.f));
+    const float n = e * (e + 2.f);
+    const float r = a * n * __builtin_amdgcn_rcpf(n + 2.f);
+    return a > 20.f ? a : r;
+  } else if constexpr (ACT == ACT_SILU) {
+    return a * __builtin_amdgcn_rcpf(__expf(-a) + 1.f);  // x / (exp(-x) + 1)
+  } else {
+    return a;
+  }
+}
+
+// The activation chosen at run time (uniform across a launch).
+__device__ __forceinline__ float act_rt(float a, int kind) {
+  switch (kind) {
+    case ACT_RELU: return act_f<ACT_RELU>(a);
+    case ACT_MISH: return act_f<ACT_MISH>(a);
+    case ACT_SILU: return act_f<ACT_SILU>(a);
+    default: return a;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ T to_t(float v) { return (T)v; }
+
+template <typename T> struct Tile;
+template <> struct Tile<float> { static constexpr int VEC = 4; };
+template <> struct Tile<f16> { static constexpr int VEC = 8; };
+template <> struct Tile<bf16> { static constexpr int VEC = 8; };
+
+// 16x16 MFMA over one 16-byte K slice of T operands: f16/bf16 K = 32 (v_mfma_f32_16x16x32_*), float K = 4
+// (v_mfma_f32_16x16x4_f32, called four times per 16 bytes by the callers).
+template <typename T>
+__device__ __forceinline__ floatx4 mfma16(const T* a, const T* b, floatx4 c) {
+  if constexpr (std::is_same<T, f16>::value) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(*(const half8*)a, *(const half8*)b, c, 0, 0, 0);
+  } else if constexpr (std::is_same<T, bf16>::value) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(*(const bf16x8*)a, *(const bf16x8*)b, c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(*a, *b, c, 0, 0, 0);
+  }
+}
+
+// The conv / GEMM epilogue for one output element (row m, column n) with its accumulated value: bias, board mask,
+// compute-type store, float store (or residual add) and emission of the consumer's activation.
+template <typename T>
+__device__ __forceinline__ void conv_store(const ConvOut& o, int m, int n, float v) {
+  if (o.colbias) v += o.colbias[(size_t)(m / HW) * o.ld_colbias + n];
+  if (o.rowmask) v *= o.rowmask[m];
+  if (o.yt) ((T*)o.yt)[(size_t)m * o.ldyt + n] = to_t<T>(v);
+  if (o.y) {
+    float* p = o.y + (size_t)m * o.ldy + n;
+    if (o.accumulate) v += *p;
+    *p = v;
+  }
+  if (o.emit.scale)
+    ((T*)o.emit.out)[(size_t)m * o.emit.ld + n] =
+        to_t<T>(act_rt(v * o.emit.scale[n] + o.emit.bias[n], o.emit.act) * o.emit.mask[m]);
+}
+
+// Winograd F(TM x TM, 3x3) geometry on the 19x19 board.
+template <int TM>
+struct Wino {
+  static constexpr int TI = TM + 2;               // input tile side
+  static constexpr int NP = TI * TI;              // tile points = batched GEMMs
+  static constexpr int TX = (POS + TM - 1) / TM;  // tiles per board side
+  static constexpr int NT = TX * TX;              // tiles per board
+};
+
+}  // namespace kgx

@@ -1,0 +1,224 @@
+// MFMA GEMM for gfx950: C[z][m][n] = sum_k A[z][m][k] * Bt[z][n][k] with float accumulation
+// (v_mfma_f32_16x16x32_{f16,bf16}, v_mfma_f32_16x16x4_f32). Serves the 1x1 convolutions, the F(4x4,3x3) point
+// GEMMs, the transformer linears and the head's first convolutions; its epilogue is conv_store (bias, board mask,
+// compute-type store, float store or residual add, and emission of the next consumer's activation).
+#include "kgx_device.h"
+
+namespace kgx {
+
+// Cfg: BM x BN output tile per 256-thread workgroup, waves in WM x WN, each wave (BM/WM) x (BN/WN) built from
+// 16x16 MFMA blocks. K advances BK at a time (several MFMA K steps), so each stage moves tens of KB: the next
+// stage's global loads are in flight in registers while the current stage, double-buffered in LDS with a 16-byte
+// row pad, feeds the MFMAs; one barrier per stage. A may be float (the head's f32 trunk): a BN + activation + mask
+// prologue then runs as the stage is written to LDS and values are converted to T there.
+template <int BM_, int BN_, int BKH_, int WM_, int WN_>
+struct Cfg {
+  static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
+  static constexpr int BKH = BKH_;  // K per stage for 16-bit types (float uses half as many)
+};
+
+template <typename T, typename C, bool AF, bool PRO, int ACT>
+__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
+  constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN;
+  constexpr int VEC = Tile<T>::VEC;
+  constexpr int BK = sizeof(T) == 2 ? C::BKH : C::BKH / 2;
+  constexpr int LDK = BK + VEC;
+  constexpr int KV = BK / VEC;                       // 16-byte vectors per tile row
+  constexpr int AV = BM * KV / 256, BV = BN * KV / 256;
+  static_assert(AV * 256 == BM * KV && BV * 256 == BN * KV, "tile not divisible over 256 threads");
+  constexpr int WTM = BM / WM, WTN = BN / WN;        // wave tile
+  constexpr int MB = WTM / 16, NB = WTN / 16;        // MFMA blocks per wave
+  constexpr int KS = sizeof(T) == 2 ? 32 : 4;        // K per MFMA
+  __shared__ __align__(16) T As[2][BM * LDK];
+  __shared__ __align__(16) T Bs[2][BN * LDK];
+  typedef u32x4 vec_t;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int z = blockIdx.z;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const int M = g.M, N = g.N, K = g.K;
+
+  const T* At = (const T*)g.A + (size_t)z * g.sA;
+  const float* Af = (const float*)g.A + (size_t)z * g.sA;
+  const T* Bt = (const T*)g.Bt + (size_t)z * g.sB;
+
+  // Thread-invariant parts of the staged vectors' addresses; per stage only the uniform K offset moves.
+  int a_row[AV], a_kk[AV], a_s[AV], b_row[BV], b_kk[BV], b_s[BV];
+#pragma unroll
+  for (int v = 0; v < AV; v++) {
+    const int idx = tid + 256 * v;
+    a_row[v] = idx / KV;
+    a_kk[v] = (idx % KV) * VEC;
+    a_s[v] = a_row[v] * LDK + a_kk[v];
+  }
+#pragma unroll
+  for (int v = 0; v < BV; v++) {
+    const int idx = tid + 256 * v;
+    b_row[v] = idx / KV;
+    b_kk[v] = (idx % KV) * VEC;
+    b_s[v] = b_row[v] * LDK + b_kk[v];
+  }
+  const T* At0 = At + (size_t)m0 * g.lda;
+  const float* Af0 = Af + (size_t)m0 * g.lda;
+  const T* Bt0 = Bt + (size_t)n0 * g.ldb;
+  const int lda = (int)g.lda, ldb = (int)g.ldb;
+
+  vec_t ra[AF ? 1 : AV];
+  float rf[AF ? AV * VEC : 1];
+  vec_t rb[BV];
+
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int v = 0; v < AV; v++) {
+      const bool ok = m0 + a_row[v] < M && k0 + a_kk[v] < K;
+      const int off = ok ? a_row[v] * lda + k0 + a_kk[v] : 0;
+      if constexpr (!AF) {
+        ra[v] = *(const vec_t*)(At0 + off);
+        if (!ok) ra[v] = vec_t{0, 0, 0, 0};
+      } else {
+#pragma unroll
+        for (int e = 0; e < VEC; e += 4) {
+          float4 q = *(const float4*)(Af0 + off + e);
+          if (!ok) q = float4{0.f, 0.f, 0.f, 0.f};
+          rf[v * VEC + e] = q.x; rf[v * VEC + e + 1] = q.y; rf[v * VEC + e + 2] = q.z; rf[v * VEC + e + 3] = q.w;
+        }
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < BV; v++) {
+      const bool ok = n0 + b_row[v] < N && k0 + b_kk[v] < K;
+      const int off = ok ? b_row[v] * ldb + k0 + b_kk[v] : 0;
+      rb[v] = *(const vec_t*)(Bt0 + off);
+      if (!ok) rb[v] = vec_t{0, 0, 0, 0};
+    }
+  };
+  auto store = [&](int buf, int k0) {
+#pragma unroll
+    for (int v = 0; v < AV; v++) {
+      if constexpr (!AF) {
+        *(vec_t*)(&As[buf][a_s[v]]) = ra[v];
+      } else {
+        T t[VEC];
+        if constexpr (PRO) {
+          const int m = m0 + a_row[v], k = k0 + a_kk[v];
+          const bool ok = m < M && k < K;
+          const int mm = ok ? m : 0, kc = ok ? k : 0;
+          const float mk = g.pro.mask[mm];
+          const float* pb = g.pro.prebias ? g.pro.prebias + (size_t)(mm / HW) * g.pro.ld_prebias + kc : nullptr;
+          const float* sc = g.pro.scale + kc;
+          const float* bi = g.pro.bias + kc;
+#pragma unroll
+          for (int e = 0; e < VEC; e++) {
+            float a = rf[v * VEC + e];
+            if (pb) a += pb[e];
+            const float y = act_f<ACT>(a * sc[e] + bi[e]) * mk;
+            t[e] = to_t<T>(ok ? y : 0.f);
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < VEC; e++) t[e] = to_t<T>(rf[v * VEC + e]);
+        }
+        *(vec_t*)(&As[buf][a_s[v]]) = *(const vec_t*)t;
+      }
+    }
+#pragma unroll
+    for (int v = 0; v < BV; v++) *(vec_t*)(&Bs[buf][b_s[v]]) = rb[v];
+  };
+
+  floatx4 acc[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  const int nk = (K + BK - 1) / BK;
+  load(0);
+  store(0, 0);
+  __syncthreads();
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int koff = sizeof(T) == 2 ? g4 * 8 : g4;
+  for (int kt = 0; kt < nk; kt++) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) load((kt + 1) * BK);
+    const T* as = As[cur] + (wm * WTM + r16) * LDK + koff;
+    const T* bs = Bs[cur] + (wn * WTN + r16) * LDK + koff;
+#pragma unroll
+    for (int kk = 0; kk < BK; kk += KS)
+#pragma unroll
+      for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) acc[i][j] = mfma16<T>(as + i * 16 * LDK + kk, bs + j * 16 * LDK + kk, acc[i][j]);
+    if (kt + 1 < nk) store(cur ^ 1, (kt + 1) * BK);
+    __syncthreads();
+  }
+
+  ConvOut o = g.out;
+  if (z) {
+    if (o.y) o.y += (size_t)z * g.sC;
+    if (o.yt) o.yt = (T*)o.yt + (size_t)z * g.sC;
+  }
+  // Output element (i, j, r) of this lane: row wm*WTM + i*16 + 4*(lane/16) + r, column wn*WTN + j*16 + lane%16.
+#pragma unroll
+  for (int i = 0; i < MB; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) {
+        const int m = m0 + wm * WTM + i * 16 + 4 * (lane >> 4) + r;
+        const int nn = n0 + wn * WTN + j * 16 + (lane & 15);
+        if (m < M && nn < N) conv_store<T>(o, m, nn, acc[i][j][r]);
+      }
+}
+
+// Tile configurations: narrow rows over all of a <= 192-wide N (1x1 convolutions, Winograd point GEMMs: the
+// prologue runs once per element), 128x128 for wide GEMMs (transformer linears), 64x64 for the rest.
+typedef Cfg<32, 192, 64, 1, 4> CfgNarrow;
+typedef Cfg<128, 128, 64, 2, 2> CfgWide;
+typedef Cfg<64, 64, 32, 2, 2> CfgSmall;
+
+template <typename T, typename C, bool AF, bool PRO, int ACT>
+static void gemm_launch(const GemmArgs& g, hipStream_t s) {
+  dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM, g.Z);
+  gemm_kernel<T, C, AF, PRO, ACT><<<grid, 256, 0, s>>>(g);
+}
+
+template <typename T, bool AF, bool PRO, int ACT>
+static void gemm_cfg(const GemmArgs& g, hipStream_t s) {
+  const int bkh = 64, bk = sizeof(T) == 2 ? bkh : bkh / 2;
+  if (g.N > 128 && g.N <= 192 && g.K % bk == 0) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
+  else if (g.N > 192 && g.N <= 384 && g.K % bk == 0 && AF) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
+  else if (g.N > 128 && g.K % bk == 0 && (long)((g.M + 127) / 128) * ((g.N + 127) / 128) * g.Z >= 256)
+    gemm_launch<T, CfgWide, AF, PRO, ACT>(g, s);
+  else gemm_launch<T, CfgSmall, AF, PRO, ACT>(g, s);
+}
+
+template <typename T>
+static void gemm_t(const GemmArgs& g, hipStream_t s) {
+  if (!g.a_float) {
+    gemm_cfg<T, false, false, ACT_ID>(g, s);
+  } else if (!g.pro.scale) {
+    gemm_cfg<T, true, false, ACT_ID>(g, s);
+  } else {
+    switch (g.pro.act) {
+      case ACT_RELU: gemm_cfg<T, true, true, ACT_RELU>(g, s); break;
+      case ACT_MISH: gemm_cfg<T, true, true, ACT_MISH>(g, s); break;
+      case ACT_SILU: gemm_cfg<T, true, true, ACT_SILU>(g, s); break;
+      default: gemm_cfg<T, true, true, ACT_ID>(g, s); break;
+    }
+  }
+}
+
+void launch_gemm(int prec, const GemmArgs& g, hipStream_t s) {
+  if (g.M <= 0 || g.N <= 0 || g.K <= 0) return;
+  const int vec = prec == PREC_F32 ? 4 : 8;
+  if (g.K % vec != 0 || g.lda % vec != 0 || g.ldb % vec != 0)
+    throw std::runtime_error("gemm: K and strides must be multiples of the vector width");
+  if (g.Z > 1 && g.out.emit.scale) throw std::runtime_error("gemm: batched GEMMs carry no emission");
+  if (prec == PREC_F16) gemm_t<f16>(g, s);
+  else if (prec == PREC_BF16) gemm_t<bf16>(g, s);
+  else gemm_t<float>(g, s);
+  KGX_CHECK_LAUNCH();
+}
+
+}  // namespace kgx

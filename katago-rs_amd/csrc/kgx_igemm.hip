@@ -1,0 +1,251 @@
+// Implicit-GEMM convolution for gfx950 on 16-bit operands: 1x1 and 3x3 "same" convolutions over NHWC
+// activations as one MFMA GEMM per launch, out[m][o] = sum_{tap, i} x[m + shift(tap)][i] * w[tap][o][i], with
+// m = n * 361 + y * 19 + x and shift(tap) = dy * 19 + dx (taps that leave the board contribute zero).
+//
+// At batch 32 and 192 channels a 3x3 convolution is about 7.7 GFLOP against 5 MB of operands: on CDNA4's matrix
+// cores the direct contraction costs less than the Winograd transforms' extra traffic (F(2x2,3x3) writes and reads
+// back four times the activation and streams 16/9 of the weights per output), and it rounds only the activation
+// and the weights to 16 bits.
+//
+// A workgroup computes BM consecutive pixels x BN output channels. Per K stage (BK input channels) it stages in LDS
+// the pixel rows [m0 - HALO, m0 + BM + HALO) (HALO = 20 covers every 3x3 neighbour) and the stage's weights of all
+// taps; each wave then runs TAPS x (BK / 32) MFMA steps over the staged data, reading the A fragment of tap t from
+// the LDS row shifted by shift(t) and zeroing rows whose neighbour is off the board. The next stage's global loads
+// are in flight in registers during the MFMAs. The epilogue goes through LDS so that every thread finishes four
+// consecutive channels of one pixel with 16-byte loads and stores (conv_store4).
+#include "kgx_device.h"
+
+namespace kgx {
+
+template <int KS_, int BM_, int BN_, int BK_, int WM_, int WN_>
+struct IgCfg {
+  static constexpr int KS = KS_, TAPS = KS_ * KS_, HALO = KS_ == 3 ? POS + 1 : 0;
+  static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
+  static constexpr int NT = WM * WN * 64;
+};
+
+// Epilogue for four consecutive channels n..n+3 of pixel m (conv_store on a float4).
+template <typename T>
+__device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floatx4 v) {
+  if (o.colbias) v += *(const floatx4*)(o.colbias + (size_t)(m / HW) * o.ld_colbias + n);
+  if (o.rowmask) v *= o.rowmask[m];
+  if (o.yt) {
+    T t[4] = {to_t<T>(v[0]), to_t<T>(v[1]), to_t<T>(v[2]), to_t<T>(v[3])};
+    *(uint2*)((T*)o.yt + (size_t)m * o.ldyt + n) = *(const uint2*)t;
+  }
+  if (o.y) {
+    floatx4* p = (floatx4*)(o.y + (size_t)m * o.ldy + n);
+    if (o.accumulate) v += *p;
+    *p = v;
+  }
+  if (o.emit.scale) {
+    const floatx4 s = *(const floatx4*)(o.emit.scale + n), b = *(const floatx4*)(o.emit.bias + n);
+    const float mk = o.emit.mask[m];
+    T t[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) t[e] = to_t<T>(act_rt(v[e] * s[e] + b[e], o.emit.act) * mk);
+    *(uint2*)((T*)o.emit.out + (size_t)m * o.emit.ld + n) = *(const uint2*)t;
+  }
+}
+
+template <typename T, typename C>
+__global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, int ldx, int IC, const T* __restrict__ W,
+                                                      int icp, int OC, int M, ConvOut o) {
+  constexpr int TAPS = C::TAPS, HALO = C::HALO, BM = C::BM, BN = C::BN, BK = C::BK, WM = C::WM, WN = C::WN;
+  constexpr int NT = C::NT;
+  constexpr int LDK = BK + 8;                 // LDS row stride in elements (16-byte pad)
+  constexpr int KV = BK / 8;                  // 16-byte vectors per staged row
+  constexpr int AR = BM + 2 * HALO;           // staged pixel rows
+  constexpr int AVT = AR * KV, BVT = TAPS * BN * KV;
+  constexpr int AV = (AVT + NT - 1) / NT, BV = (BVT + NT - 1) / NT;
+  constexpr int WTM = BM / WM, WTN = BN / WN, MB = WTM / 16, NB = WTN / 16;
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0 && BK % 32 == 0, "bad tile");
+  constexpr int STAGE = (AR + TAPS * BN) * LDK * 2;   // bytes
+  constexpr int EPI = BM * (BN + 4) * 4;              // bytes
+  __shared__ __align__(16) char smem[STAGE > EPI ? STAGE : EPI];
+  T* As = (T*)smem;
+  T* Bs = As + AR * LDK;
+  typedef u32x4 vec_t;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WN, wn = wave % WN;
+  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  const int r16 = lane & 15, g4 = lane >> 4;
+
+  // Staged-vector bookkeeping (thread-invariant): A row / vector, B (tap, row) / vector.
+  int a_goff[AV], a_soff[AV], b_goff[BV], b_soff[BV];
+  unsigned a_ok = 0, b_ok = 0;  // bit v: vector v is live (in the stage and in bounds)
+  int a_k[AV];
+#pragma unroll
+  for (int v = 0; v < AV; v++) {
+    const int idx = tid + NT * v;
+    const int r = idx / KV, kv = idx - r * KV;
+    const int gr = m0 - HALO + r;
+    const bool live = idx < AVT && gr >= 0 && gr < M;
+    a_goff[v] = live ? gr * ldx + kv * 8 : 0;
+    a_soff[v] = idx < AVT ? r * LDK + kv * 8 : 0;
+    a_k[v] = kv * 8;
+    if (live) a_ok |= 1u << v;
+  }
+#pragma unroll
+  for (int v = 0; v < BV; v++) {
+    const int idx = tid + NT * v;
+    const int tr = idx / KV, kv = idx - tr * KV;  // tr = tap * BN + row
+    const int t = tr / BN, row = tr - t * BN;
+    const bool live = idx < BVT && n0 + row < OC;
+    b_goff[v] = live ? ((t * OC + n0 + row) * icp + kv * 8) : 0;
+    b_soff[v] = idx < BVT ? tr * LDK + kv * 8 : 0;
+    if (live) b_ok |= 1u << v;
+  }
+
+  // Tap validity of this lane's A rows: bit t of vmask[i] is set when row m's neighbour at tap t is on the board.
+  unsigned vmask[MB];
+#pragma unroll
+  for (int i = 0; i < MB; i++) {
+    const int m = m0 + wm * WTM + i * 16 + r16;
+    unsigned bits = 0;
+    if (m < M) {
+      const int p = m % HW, y = p / POS, x = p - y * POS;
+#pragma unroll
+      for (int t = 0; t < TAPS; t++) {
+        const int dy = C::KS == 3 ? t / 3 - 1 : 0, dx = C::KS == 3 ? t % 3 - 1 : 0;
+        if ((unsigned)(y + dy) < (unsigned)POS && (unsigned)(x + dx) < (unsigned)POS) bits |= 1u << t;
+      }
+    }
+    vmask[i] = bits;
+  }
+
+  vec_t ra[AV], rb[BV];
+  auto load = [&](int k0) {
+#pragma unroll
+    for (int v = 0; v < AV; v++) {
+      const bool ok = ((a_ok >> v) & 1) && k0 + a_k[v] < IC;
+      ra[v] = ok ? *(const vec_t*)(X + a_goff[v] + k0) : vec_t{0, 0, 0, 0};
+    }
+#pragma unroll
+    for (int v = 0; v < BV; v++) rb[v] = ((b_ok >> v) & 1) ? *(const vec_t*)(W + b_goff[v] + k0) : vec_t{0, 0, 0, 0};
+  };
+  auto store = [&]() {
+#pragma unroll
+    for (int v = 0; v < AV; v++)
+      if (AVT % NT == 0 || tid + NT * v < AVT) *(vec_t*)(As + a_soff[v]) = ra[v];
+#pragma unroll
+    for (int v = 0; v < BV; v++)
+      if (BVT % NT == 0 || tid + NT * v < BVT) *(vec_t*)(Bs + b_soff[v]) = rb[v];
+  };
+
+  floatx4 acc[MB][NB];
+#pragma unroll
+  for (int i = 0; i < MB; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+
+  typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
+  const int nk = icp / BK;
+  load(0);
+  for (int kt = 0; kt < nk; kt++) {
+    store();
+    __syncthreads();
+    if (kt + 1 < nk) load((kt + 1) * BK);
+#pragma unroll
+    for (int t = 0; t < TAPS; t++) {
+      const int shift = C::KS == 3 ? (t / 3 - 1) * POS + (t % 3 - 1) : 0;
+      const T* as = As + (wm * WTM + r16 + HALO + shift) * LDK + g4 * 8;
+      const T* bs = Bs + (t * BN + wn * WTN + r16) * LDK + g4 * 8;
+#pragma unroll
+      for (int kk = 0; kk < BK; kk += 32) {
+        frag_t a[MB], b[NB];
+#pragma unroll
+        for (int i = 0; i < MB; i++) {
+          a[i] = *(const frag_t*)(as + i * 16 * LDK + kk);
+          if (!((vmask[i] >> t) & 1)) a[i] = frag_t{};
+        }
+#pragma unroll
+        for (int j = 0; j < NB; j++) b[j] = *(const frag_t*)(bs + j * 16 * LDK + kk);
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+          for (int j = 0; j < NB; j++) {
+            if constexpr (std::is_same<T, f16>::value)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
+            else
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
+          }
+      }
+    }
+    __syncthreads();
+  }
+
+  // Accumulators to LDS as a float [BM][BN + 4] tile: element (i, j, r) is row wm*WTM + i*16 + 4*(lane/16) + r,
+  // column wn*WTN + j*16 + lane%16.
+  float* Cs = (float*)smem;
+  constexpr int LDC = BN + 4;
+#pragma unroll
+  for (int i = 0; i < MB; i++)
+#pragma unroll
+    for (int j = 0; j < NB; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) Cs[(wm * WTM + i * 16 + 4 * g4 + r) * LDC + wn * WTN + j * 16 + r16] = acc[i][j][r];
+  __syncthreads();
+  constexpr int NV = BM * (BN / 4);
+#pragma unroll 2
+  for (int v = tid; v < NV; v += NT) {
+    const int row = v / (BN / 4), c4 = v - row * (BN / 4);
+    const int m = m0 + row, n = n0 + 4 * c4;
+    if (m < M && n < OC) conv_store4<T>(o, m, n, *(const floatx4*)(Cs + row * LDC + 4 * c4));
+  }
+}
+
+// Configurations: 3x3 with 96x96 tiles (2x2 waves of 48x48), 1x1 with 96x96 tiles and 64 channels per stage.
+typedef IgCfg<3, 96, 96, 32, 2, 2> Ig3;
+typedef IgCfg<1, 96, 96, 64, 2, 2> Ig1;
+
+template <typename T, typename C>
+static void igemm_launch(const void* x, int ldx, int IC, const void* w, int icp, int OC, const ConvOut& o, int M,
+                         hipStream_t s) {
+  if (icp % C::BK != 0) throw std::runtime_error("conv_igemm: padded input channels must be a multiple of the stage");
+  dim3 grid((OC + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM);
+  igemm_kernel<T, C><<<grid, C::NT, 0, s>>>((const T*)x, ldx, IC, (const T*)w, icp, OC, M, o);
+}
+
+int conv_igemm_icp(int ks, int ic) { return round_up(ic, ks == 3 ? Ig3::BK : Ig1::BK); }
+
+void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const void* w, int icp, int OC,
+                       const ConvOut& o, int B, hipStream_t s) {
+  if (prec != PREC_F16 && prec != PREC_BF16) throw std::runtime_error("conv_igemm: 16-bit operands only");
+  if (ks != 1 && ks != 3) throw std::runtime_error("conv_igemm: 1x1 or 3x3 kernels only");
+  if (IC % 8 != 0 || ldx % 8 != 0 || OC % 4 != 0 || icp != conv_igemm_icp(ks, IC))
+    throw std::runtime_error("conv_igemm: channel counts must be multiples of 8 (inputs) and 4 (outputs)");
+  if ((o.y && o.ldy % 4) || (o.yt && o.ldyt % 4) || (o.colbias && o.ld_colbias % 4) || (o.emit.scale && o.emit.ld % 4))
+    throw std::runtime_error("conv_igemm: output strides must be multiples of 4");
+  const int M = B * HW;
+  if (prec == PREC_F16) {
+    if (ks == 3) igemm_launch<f16, Ig3>(x, ldx, IC, w, icp, OC, o, M, s);
+    else igemm_launch<f16, Ig1>(x, ldx, IC, w, icp, OC, o, M, s);
+  } else {
+    if (ks == 3) igemm_launch<bf16, Ig3>(x, ldx, IC, w, icp, OC, o, M, s);
+    else igemm_launch<bf16, Ig1>(x, ldx, IC, w, icp, OC, o, M, s);
+  }
+  KGX_CHECK_LAUNCH();
+}
+
+// Network input planes, float NCHW [B][nin][361], to compute-type NHWC rows [B*361][ldo], channels nin..ldo-1 zero.
+template <typename T>
+__global__ __launch_bounds__(256) void pack_input_kernel(const float* __restrict__ bin, int nin, T* __restrict__ out,
+                                                         int ldo, int rows) {
+  const int m = blockIdx.x * 256 + threadIdx.x;
+  if (m >= rows) return;
+  const int n = m / HW, p = m - n * HW;
+  T* o = out + (size_t)m * ldo;
+  for (int c = 0; c < ldo; c++) o[c] = to_t<T>(c < nin ? bin[((size_t)n * nin + c) * HW + p] : 0.f);
+}
+
+void launch_pack_input(int prec, const float* bin, int nin, void* out, int ldo, int B, hipStream_t s) {
+  const int rows = B * HW;
+  if (prec == PREC_F16) pack_input_kernel<f16><<<(rows + 255) / 256, 256, 0, s>>>(bin, nin, (f16*)out, ldo, rows);
+  else if (prec == PREC_BF16) pack_input_kernel<bf16><<<(rows + 255) / 256, 256, 0, s>>>(bin, nin, (bf16*)out, ldo, rows);
+  else throw std::runtime_error("pack_input: 16-bit only");
+  KGX_CHECK_LAUNCH();
+}
+
+}  // namespace kgx

@@ -8,8 +8,6 @@ namespace kgx {
 
 constexpr int POS = 19;
 constexpr int HW = POS * POS;             // board points per row
-constexpr int TILES_X = (POS + 3) / 4;    // Winograd F(4x4,3x3) tiles per board side
-constexpr int TILES = TILES_X * TILES_X;  // tiles per board
 
 enum Prec { PREC_F32 = 0, PREC_F16 = 1, PREC_BF16 = 2 };
 enum Act { ACT_ID = 0, ACT_RELU = 1, ACT_MISH = 2, ACT_SILU = 3 };
@@ -27,37 +25,77 @@ struct Prologue {
   const float* mask = nullptr;     // [B*HW]
 };
 
-// Winograd input transform: x (NHWC rows of `ldx` floats, or NCHW when `nchw`) -> V[36][t_pad][c_pad].
-void launch_wino_in(int prec, const float* x, int ldx, bool nchw, const Prologue& pro, void* V, int B, int C,
-                    int c_pad, int t_pad, hipStream_t s);
+// Activation of a consumer layer, written by the producer's epilogue from its final float output y[m][n]:
+// out[m][n] = T(act(y * scale[n] + bias[n]) * mask[m]). scale == nullptr disables it.
+struct Emit {
+  const float* scale = nullptr;
+  const float* bias = nullptr;
+  int act = ACT_ID;
+  const float* mask = nullptr;
+  void* out = nullptr;
+  int ld = 0;
+};
 
-// Winograd output transform: M[36][t_pad][oc_pad] -> out[B*HW][ldo] (+ colbias[b][oc]); add into out when
-// `accumulate`.
-void launch_wino_out(const float* M, int oc_pad, int t_pad, float* out, int ldo, int OC, const float* colbias,
-                     int ld_colbias, bool accumulate, int B, hipStream_t s);
+// Output of a convolution or GEMM, element (m, n) with accumulated value v:
+// v += colbias[m / HW][n]; v *= rowmask[m]; yt = T(v); y = (accumulate ? y : 0) + v; then the emission from y.
+struct ConvOut {
+  float* y = nullptr; int ldy = 0;
+  bool accumulate = false;
+  const float* colbias = nullptr; int ld_colbias = 0;
+  const float* rowmask = nullptr;
+  void* yt = nullptr; int ldyt = 0;
+  Emit emit;
+};
 
-// Filter transform G g G^T of w [oc][ic][3][3] into U[36][oc_pad][ic_pad] (host, double precision).
-void wino_filter_host(const float* w, int oc, int ic, int oc_pad, int ic_pad, float* U);
+// Winograd F(tm x tm, 3x3), tm = 4 (36 tile points, 25 tiles per board) or 2 (16 points, 100 tiles).
+// Transformed inputs are tile-major: V[t][point][c_pad].
+int wino_tiles(int tm);
+int wino_points(int tm);
+
+// Winograd input transform of an activation x: compute-type NHWC rows of `ldx` (the consumer activation written
+// by the producer), or float NCHW when `nchw_f32` (the network input).
+void launch_wino_in(int prec, int tm, const void* x, int ldx, bool nchw_f32, void* V, int B, int C, int c_pad,
+                    hipStream_t s);
+
+// F(4x4,3x3) output transform of the point GEMMs M[t][point][oc_pad] (float) into `o`.
+void launch_wino_out(int prec, int tm, const float* M, int oc_pad, int OC, const ConvOut& o, int B, hipStream_t s);
+
+// F(2x2,3x3) point GEMMs fused with the output transform: V [t_pad][16][icp], U [16][ocp][icp] -> `o`.
+void launch_wino2_fused(int prec, const void* V, const void* U, int t_pad, int icp, int ocp, int OC, const ConvOut& o,
+                        int B, hipStream_t s);
+
+// Filter transform G g G^T of w [oc][ic][3][3] into U[points][oc_pad][ic_pad] (host, double precision).
+void wino_filter_host(int tm, const float* w, int oc, int ic, int oc_pad, int ic_pad, float* U);
 
 // C[z] = A[z] * Bt[z]^T on MFMA: A [M][K] (row stride lda; T, or float with a prologue), Bt [N][K].
+// Batch z offsets: A sA, Bt sB, outputs sC (elements, applied to out.y / out.yt).
 struct GemmArgs {
   const void* A = nullptr; long lda = 0; long sA = 0;
   const void* Bt = nullptr; long ldb = 0; long sB = 0;
-  void* C = nullptr; long ldc = 0; long sC = 0;
+  long sC = 0;
   int M = 0, N = 0, K = 0, Z = 1;
   bool a_float = false;        // A holds float (converted, with `pro` applied when pro.scale)
   Prologue pro;
-  const float* residual = nullptr; long ldr = 0;  // out += residual (may alias C)
-  const float* colbias = nullptr; int ld_colbias = 0;  // + colbias[m / HW][n]
-  const float* rowmask = nullptr;                      // * rowmask[m] (before the residual)
-  bool out_t = false;          // store in the compute type instead of float
+  ConvOut out;
 };
 void launch_gemm(int prec, const GemmArgs& g, hipStream_t s);
 
-// Direct odd-k "same" convolution in float, w as [ic][ky][kx][oc]: x (NHWC rows of ldx, or NCHW) -> out.
-void launch_conv_direct(const float* x, int ldx, bool nchw, const Prologue& pro, int IC, const float* w, int OC,
-                        int ky, int kx, int dy, int dx, float* out, int ldo, const float* colbias, int ld_colbias,
-                        bool accumulate, int B, hipStream_t s);
+// Implicit-GEMM 1x1 / 3x3 "same" convolution on 16-bit operands: x compute-type NHWC rows of ldx (IC channels,
+// IC % 8 == 0), w compute-type [ks*ks][OC][icp] with icp = conv_igemm_icp(ks, IC) (zero padded), OC % 4 == 0.
+int conv_igemm_icp(int ks, int ic);
+void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const void* w, int icp, int OC,
+                       const ConvOut& o, int B, hipStream_t s);
+
+// Network input planes, float NCHW [B][nin][361], to compute-type NHWC rows of ldo channels (zero beyond nin).
+void launch_pack_input(int prec, const float* bin, int nin, void* out, int ldo, int B, hipStream_t s);
+
+// Direct odd-k "same" convolution, w as [ic][ky][kx][oc] float: x compute-type NHWC rows of ldx, or float NCHW.
+void launch_conv_direct(int prec, const void* x, int ldx, bool nchw_f32, int IC, const float* w, int OC, int ky, int kx,
+                        int dy, int dx, const ConvOut& o, int B, hipStream_t s);
+
+// out[m][c] = T(act((x[m][c] + prebias[m / HW][c]) * scale[c] + bias[c]) * mask[m]) for c < C.
+void launch_bias_act(int prec, const float* x, int ldx, int C, const float* prebias, int ld_prebias, const float* scale,
+                     const float* bias, int act, const float* mask, void* out, int ldo, int rows, hipStream_t s);
 
 // mask[b][pos] = bin[b][0][pos]; area = sum; s1 = (sqrt(area)-14)*0.1; s2 = (sqrt(area)-14)^2*0.01-0.1.
 void launch_mask_prep(const float* bin, int nin, float* mask, float* area, float* s1, float* s2, int B,

@@ -36,9 +36,26 @@ struct Op {
   std::function<void(hipStream_t, int)> launch;
   const char* cls;
   double flops_row = 0, bytes_row = 0, bytes_fixed = 0;
+  // A convolution / GEMM output whose emission may be attached after the op is planned: its compute-type
+  // activation of `out_c` channels per point is counted when present.
+  std::shared_ptr<ConvOut> out;
+  int out_c = 0;
+};
+
+// Planning state of one residual stream (the trunk, or the inner stream of a nested bottleneck block): its float
+// values, the two compute-type buffers that its consumer activations alternate between (so a producer never
+// writes the buffer its own input was read from), and the op that last wrote the stream, which emits the next
+// consumer's activation.
+struct StreamState {
+  float* x = nullptr;
+  int c = 0;
+  void* act[2] = {nullptr, nullptr};
+  int flip = 0;
+  std::shared_ptr<ConvOut> producer;
 };
 
 struct ProfileClass {
+  const char* name = nullptr;  // the op table's string literal
   long launches = 0;
   double ms = 0, flops = 0, bytes = 0;
 };
@@ -77,19 +94,27 @@ class Net {
 
   // Planning.
   void scan(const std::vector<BlockDesc>& blocks, int c, int depth);
-  void emit_conv(const ConvDesc& c, const float* x, int ldx, bool nchw, const Prologue& pro, float* y, int ldy,
-                 bool accumulate, const float* colbias, int ld_colbias);
-  void emit_stack(const std::vector<BlockDesc>& blocks, float* x, int c, int depth);
-  void emit_attention(const BlockDesc& b, float* x, int c);
-  void emit_ffn(const BlockDesc& b, float* x, int c);
-  void emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, void* C, int ldc, bool out_t,
-                       float* residual_masked, const char* cls);
+  // conv(x) into `o`; x is a compute-type activation [rows][ldx], or the float NCHW network input.
+  std::shared_ptr<ConvOut> emit_conv(const ConvDesc& c, const void* x, int ldx, bool nchw, const ConvOut& o);
+  void emit_stack(const std::vector<BlockDesc>& blocks, int depth);
+  void emit_attention(const BlockDesc& b, int depth);
+  void emit_ffn(const BlockDesc& b, int depth);
+  std::shared_ptr<ConvOut> emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, const ConvOut& o,
+                                           const char* cls);
+  // The activation act(bn(x)) * mask of stream `depth`, emitted by the stream's last producer.
+  void* consume(int depth, const BNDesc& bn, int act);
+  Emit bn_emit(const BNDesc& bn, int act, void* out, int ld);
   Prologue bn_pro(const BNDesc& bn, int act, const float* prebias = nullptr, int ld_prebias = 0);
   void build(const ModelDesc& m);
 
   void run_ops(int B, hipStream_t s);
 
+  int t_pad(int B) const;  // Winograd tiles of B rows, padded to the GEMM's row tile
+
+  enum ConvMode { CONV_IGEMM, CONV_WINO2, CONV_WINO4 };
   int device_, max_batch_, prec_;
+  ConvMode conv_mode_ = CONV_WINO4;
+  int wino_tm_ = 4;
   int nin_ = 0, nglob_ = 0, nmeta_ = 0, row_len_ = 0;
   std::vector<std::unique_ptr<DeviceBuffer>> mem_;
   std::vector<Op> ops_;
@@ -99,12 +124,13 @@ class Net {
   float *mask_ = nullptr, *area_ = nullptr, *s1_ = nullptr, *s2_ = nullptr;
 
   // Workspace sizes from scan(), then the buffers.
-  int tmp_c_ = 0, gp_c_ = 0, gb_c_ = 0;
+  int tmp_c_ = 0, mid_c_ = 0, gp_c_ = 0, gb_c_ = 0;
   std::vector<int> stream_c_;
   int nrm_c_ = 0, qkv_c_ = 0, ao_c_ = 0, u_c_ = 0, h_c_ = 0;
   size_t wino_v_elems_ = 0, wino_m_elems_ = 0;
   float* trunk_ = nullptr;
-  std::vector<float*> streams_;
+  std::vector<StreamState> ss_;
+  void* mid_ = nullptr;  // compute-type mid activation of a residual block
   float *tmp_ = nullptr, *gp_ = nullptr, *gb_ = nullptr;
   void *nrm_ = nullptr, *qkv_ = nullptr, *ao_ = nullptr, *h_ = nullptr;
   float* u_ = nullptr;

@@ -1,10 +1,13 @@
 // Forward-pass planning and execution on one GPU. The op order follows the graph of
-// tools/bin2onnx/bin2onnx.py (trunk :1466-1492, blocks :1243-1269 and :1357-1438, heads :1495-1531); each
-// batch norm + activation + mask that feeds a convolution runs inside that convolution's input loads, as
-// katago-nn-burn's `fuse_bn_act` rewrite does (crates/katago-nn-burn/build.rs:366-600, conv.rs:42-93).
+// tools/bin2onnx/bin2onnx.py (trunk :1466-1492, blocks :1243-1269 and :1357-1438, heads :1495-1531). Each
+// batch norm + activation + mask that feeds a convolution (what katago-nn-burn's `fuse_bn_act` rewrite folds into
+// the convolution's input, crates/katago-nn-burn/build.rs:366-600, conv.rs:42-93) is computed once, in the
+// epilogue of the op that produced its input, and stored in the compute type: the convolution reads half the
+// bytes of the float stream and recomputes nothing.
 #include "kgx_net.h"
 
 #include <cmath>
+#include <cstdlib>
 #include <cstring>
 #include <stdexcept>
 
@@ -27,14 +30,26 @@ uint16_t f32_to_bf16_bits(float f) {  // round to nearest even
   return (uint16_t)(u >> 16);
 }
 
-int t_pad(int B) { return round_up(B * TILES, 64); }
-
 }  // namespace
 
 Net::Net(const ModelDesc& m, int device, int max_batch, int prec) : device_(device), max_batch_(max_batch), prec_(prec) {
   KGX_HIP(hipSetDevice(device));
+  // Convolution algorithm. Float operands: Winograd F(4x4,3x3), the reference's. 16-bit operands: implicit GEMM
+  // for 1x1 and 3x3 (no transform traffic; only activations and weights are rounded). KGX_CONV=igemm|wino2|wino4
+  // overrides (igemm needs 16-bit operands; wino2 is F(2x2,3x3), whose transformed values stay small enough for
+  // 16-bit operands).
+  conv_mode_ = prec == PREC_F32 ? CONV_WINO4 : CONV_IGEMM;
+  if (const char* e = std::getenv("KGX_CONV")) {
+    const std::string v = e;
+    if (v == "wino4") conv_mode_ = CONV_WINO4;
+    else if (v == "wino2") conv_mode_ = CONV_WINO2;
+    else if (v == "igemm" && prec != PREC_F32) conv_mode_ = CONV_IGEMM;
+  }
+  wino_tm_ = conv_mode_ == CONV_WINO4 ? 4 : 2;
   build(m);
 }
+
+int Net::t_pad(int B) const { return round_up(B * wino_tiles(wino_tm_), 128); }
 
 Net::~Net() {
   (void)hipSetDevice(device_);
@@ -80,15 +95,37 @@ Prologue Net::bn_pro(const BNDesc& bn, int act, const float* prebias, int ld_pre
   return p;
 }
 
+Emit Net::bn_emit(const BNDesc& bn, int act, void* out, int ld) {
+  Emit e;
+  e.scale = upload_f(bn.scale);
+  e.bias = upload_f(bn.bias);
+  e.act = act;
+  e.mask = mask_;
+  e.out = out;
+  e.ld = ld;
+  return e;
+}
+
+void* Net::consume(int depth, const BNDesc& bn, int act) {
+  StreamState& st = ss_[depth];
+  if (!st.producer || st.producer->emit.scale) throw std::runtime_error("internal: stream activation has no producer");
+  void* buf = st.act[st.flip];
+  st.flip ^= 1;
+  st.producer->emit = bn_emit(bn, act, buf, st.c);
+  st.producer.reset();
+  return buf;
+}
+
 // Workspace needs of a block stack with `c` channels at nesting depth `depth`.
 void Net::scan(const std::vector<BlockDesc>& blocks, int c, int depth) {
   for (const BlockDesc& b : blocks) {
     switch (b.kind) {
       case BLOCK_RES:
-        tmp_c_ = std::max(tmp_c_, b.regular.oc);
+        mid_c_ = std::max(mid_c_, b.regular.oc);
         break;
       case BLOCK_GPOOL:
         tmp_c_ = std::max(tmp_c_, b.regular.oc + b.gconv.oc);
+        mid_c_ = std::max(mid_c_, b.regular.oc);
         gp_c_ = std::max(gp_c_, 3 * b.gconv.oc);
         gb_c_ = std::max(gb_c_, b.regular.oc);
         break;
@@ -111,113 +148,172 @@ void Net::scan(const std::vector<BlockDesc>& blocks, int c, int depth) {
   }
 }
 
-// y (= or +=) conv(pro(x)) + colbias. 3x3 undilated convs run as Winograd F(4x4,3x3) (transform, 36 batched MFMA
-// GEMMs, inverse transform: crates/katago-nn-burn/src/wino/ext.rs:324-437); 1x1 convs over NHWC rows as one MFMA
-// GEMM with the prologue on the A loads (wino/ext.rs:278-321); anything else as a direct convolution.
-void Net::emit_conv(const ConvDesc& c, const float* x, int ldx, bool nchw, const Prologue& pro, float* y, int ldy,
-                    bool accumulate, const float* colbias, int ld_colbias) {
+// conv(x) into `o`. 3x3 undilated convs run as Winograd (crates/katago-nn-burn/src/wino/ext.rs:324-437): with
+// F(2x2,3x3) as an input transform plus one kernel for the 16 point GEMMs and the output transform, with
+// F(4x4,3x3) as input transform, 36 batched MFMA GEMMs and output transform. 1x1 convs over NHWC rows are one MFMA
+// GEMM (wino/ext.rs:278-321); anything else is a direct convolution.
+std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ldx, bool nchw, const ConvOut& o) {
   const int prec = prec_;
   const double ts = (double)tsize();
-  if (c.ky == 3 && c.kx == 3 && c.dy == 1 && c.dx == 1) {
+  auto out = std::make_shared<ConvOut>(o);
+  const double in_bytes = (double)HW * c.ic * (nchw ? 4.0 : ts);
+  const double out_bytes = (double)HW * c.oc * ((o.y ? 4.0 : 0.0) * (o.accumulate ? 2 : 1) + (o.yt ? ts : 0.0));
+  const int ic = c.ic, oc = c.oc;
+  const bool k3 = c.ky == 3 && c.kx == 3 && c.dy == 1 && c.dx == 1, k1 = c.ky == 1 && c.kx == 1;
+  const bool strides4 = (!o.y || o.ldy % 4 == 0) && (!o.yt || o.ldyt % 4 == 0) &&
+                        (!o.colbias || o.ld_colbias % 4 == 0) && (!o.emit.scale || o.emit.ld % 4 == 0);
+  if (conv_mode_ == CONV_IGEMM && (k3 || k1) && oc % 4 == 0 && strides4 && (nchw || (ic % 8 == 0 && ldx % 8 == 0))) {
+    const int ks = k3 ? 3 : 1;
+    const void* xin = x;
+    int ldin = ldx, icin = ic;
+    if (nchw) {
+      // The network input planes are packed once into compute-type NHWC rows (0/1 planes are exact in 16 bits).
+      icin = ldin = round_up(ic, 8);
+      void* packed = alloc_bytes((size_t)max_batch_ * HW * icin * tsize());
+      const float* bin = (const float*)x;
+      Op pk;
+      pk.launch = [=](hipStream_t s, int B) { launch_pack_input(prec, bin, ic, packed, icin, B, s); };
+      pk.cls = "pack_input";
+      pk.bytes_row = (double)HW * ic * 4 + (double)HW * icin * ts;
+      ops_.push_back(pk);
+      xin = packed;
+    }
+    const int icp = conv_igemm_icp(ks, icin), taps = ks * ks;
+    std::vector<float> w((size_t)taps * oc * icp, 0.f);  // [tap][oc][icp]
+    for (int t = 0; t < taps; t++)
+      for (int oo = 0; oo < oc; oo++)
+        for (int i = 0; i < ic; i++) w[((size_t)t * oc + oo) * icp + i] = c.w[((size_t)oo * ic + i) * taps + t];
+    const void* dW = upload_t(w);
+    Op op;
+    op.launch = [=](hipStream_t s, int B) { launch_conv_igemm(prec, ks, xin, ldin, icin, dW, icp, oc, *out, B, s); };
+    op.cls = k3 ? "conv3x3" : "conv1x1";
+    op.flops_row = 2.0 * HW * ic * oc * taps;
+    op.bytes_row = (double)HW * icin * ts + out_bytes;
+    op.bytes_fixed = (double)taps * ic * oc * ts;
+    op.out = out;
+    op.out_c = oc;
+    ops_.push_back(op);
+    return out;
+  }
+  if (k3) {
+    const int tm = wino_tm_, np = wino_points(tm), nt = wino_tiles(tm);
     const int icp = round_up(c.ic, 32), ocp = round_up(c.oc, 64);
-    std::vector<float> U((size_t)36 * ocp * icp);
-    wino_filter_host(c.w.data(), c.oc, c.ic, ocp, icp, U.data());
+    std::vector<float> U((size_t)np * ocp * icp);
+    wino_filter_host(tm, c.w.data(), c.oc, c.ic, ocp, icp, U.data());
     const void* dU = upload_t(U);
-    wino_v_elems_ = std::max(wino_v_elems_, (size_t)36 * t_pad(max_batch_) * icp);
-    wino_m_elems_ = std::max(wino_m_elems_, (size_t)36 * t_pad(max_batch_) * ocp);
-    const int ic = c.ic, oc = c.oc;
+    wino_v_elems_ = std::max(wino_v_elems_, (size_t)t_pad(max_batch_) * np * icp);
     Op in;
-    in.launch = [=](hipStream_t s, int B) { launch_wino_in(prec, x, ldx, nchw, pro, wino_v_, B, ic, icp, t_pad(B), s); };
+    in.launch = [=](hipStream_t s, int B) { launch_wino_in(prec, tm, x, ldx, nchw, wino_v_, B, ic, icp, s); };
     in.cls = "wino_in";
-    in.bytes_row = (double)HW * ic * 4 + 36.0 * TILES * ic * ts;
+    in.bytes_row = in_bytes + (double)np * nt * ic * ts;
     ops_.push_back(in);
+    if (tm == 2) {
+      Op fu;
+      fu.launch = [=](hipStream_t s, int B) { launch_wino2_fused(prec, wino_v_, dU, t_pad(B), icp, ocp, oc, *out, B, s); };
+      fu.cls = "wino_gemm";
+      fu.flops_row = 2.0 * np * nt * ic * oc;
+      fu.bytes_row = (double)np * nt * ic * ts + out_bytes;
+      fu.bytes_fixed = (double)np * ic * oc * ts;
+      fu.out = out;
+      fu.out_c = oc;
+      ops_.push_back(fu);
+      return out;
+    }
+    wino_m_elems_ = std::max(wino_m_elems_, (size_t)t_pad(max_batch_) * np * ocp);
     Op gm;
     gm.launch = [=](hipStream_t s, int B) {
       GemmArgs g;
-      const int tp = t_pad(B);
-      g.A = wino_v_; g.lda = icp; g.sA = (long)tp * icp;
+      g.A = wino_v_; g.lda = (long)np * icp; g.sA = icp;
       g.Bt = dU; g.ldb = icp; g.sB = (long)ocp * icp;
-      g.C = wino_m_; g.ldc = ocp; g.sC = (long)tp * ocp;
-      g.M = tp; g.N = ocp; g.K = icp; g.Z = 36;
+      g.out.y = wino_m_; g.out.ldy = np * ocp; g.sC = ocp;
+      g.M = B * nt; g.N = ocp; g.K = icp; g.Z = np;
       launch_gemm(prec, g, s);
     };
     gm.cls = "wino_gemm";
-    gm.flops_row = 2.0 * 36 * TILES * ic * oc;
-    gm.bytes_row = 36.0 * TILES * ic * ts + 36.0 * TILES * oc * 4;
-    gm.bytes_fixed = 36.0 * ic * oc * ts;
+    gm.flops_row = 2.0 * np * nt * ic * oc;
+    gm.bytes_row = (double)np * nt * ic * ts + (double)np * nt * oc * 4;
+    gm.bytes_fixed = (double)np * ic * oc * ts;
     ops_.push_back(gm);
-    Op out;
-    out.launch = [=](hipStream_t s, int B) {
-      launch_wino_out(wino_m_, ocp, t_pad(B), y, ldy, oc, colbias, ld_colbias, accumulate, B, s);
-    };
-    out.cls = "wino_out";
-    out.bytes_row = 36.0 * TILES * oc * 4 + (double)HW * oc * 4 * (accumulate ? 2 : 1);
-    ops_.push_back(out);
-  } else if (c.ky == 1 && c.kx == 1 && !nchw && !colbias && c.ic % 8 == 0 && ldx % 8 == 0) {
+    Op wo;
+    wo.launch = [=](hipStream_t s, int B) { launch_wino_out(prec, tm, wino_m_, ocp, oc, *out, B, s); };
+    wo.cls = "wino_out";
+    wo.bytes_row = (double)np * nt * oc * 4 + out_bytes;
+    wo.out = out;
+    wo.out_c = oc;
+    ops_.push_back(wo);
+    return out;
+  }
+  const int vec = prec == PREC_F32 ? 4 : 8;
+  if (c.ky == 1 && c.kx == 1 && !nchw && c.ic % vec == 0 && ldx % vec == 0) {
     const void* dW = upload_t(c.w);  // [oc][ic] is already the B^T layout
-    const int ic = c.ic, oc = c.oc;
     Op gm;
     gm.launch = [=](hipStream_t s, int B) {
       GemmArgs g;
-      g.A = x; g.lda = ldx; g.a_float = true; g.pro = pro;
+      g.A = x; g.lda = ldx;
       g.Bt = dW; g.ldb = ic;
-      g.C = y; g.ldc = ldy;
-      if (accumulate) { g.residual = y; g.ldr = ldy; }
+      g.out = *out;
       g.M = B * HW; g.N = oc; g.K = ic;
       launch_gemm(prec, g, s);
     };
     gm.cls = "gemm_1x1";
     gm.flops_row = 2.0 * HW * ic * oc;
-    gm.bytes_row = (double)HW * ic * 4 + (double)HW * oc * 4 * (accumulate ? 2 : 1);
+    gm.bytes_row = in_bytes + out_bytes;
     gm.bytes_fixed = (double)ic * oc * ts;
+    gm.out = out;
+    gm.out_c = oc;
     ops_.push_back(gm);
-  } else {
-    // [oc][ic][ky][kx] -> [ic][ky][kx][oc]
-    std::vector<float> w((size_t)c.ic * c.ky * c.kx * c.oc);
-    for (int o = 0; o < c.oc; o++)
-      for (int i = 0; i < c.ic; i++)
-        for (int a = 0; a < c.ky; a++)
-          for (int b = 0; b < c.kx; b++)
-            w[(((size_t)i * c.ky + a) * c.kx + b) * c.oc + o] = c.w[(((size_t)o * c.ic + i) * c.ky + a) * c.kx + b];
-    const float* dW = upload_f(w);
-    const int ic = c.ic, oc = c.oc, ky = c.ky, kx = c.kx, dy = c.dy, dx = c.dx;
-    Op op;
-    op.launch = [=](hipStream_t s, int B) {
-      launch_conv_direct(x, ldx, nchw, pro, ic, dW, oc, ky, kx, dy, dx, y, ldy, colbias, ld_colbias, accumulate, B, s);
-    };
-    op.cls = "conv_direct";
-    op.flops_row = 2.0 * HW * ic * oc * ky * kx;
-    op.bytes_row = (double)HW * ic * 4 + (double)HW * oc * 4;
-    ops_.push_back(op);
+    return out;
   }
+  // [oc][ic][ky][kx] -> [ic][ky][kx][oc]
+  std::vector<float> w((size_t)c.ic * c.ky * c.kx * c.oc);
+  for (int oo = 0; oo < c.oc; oo++)
+    for (int i = 0; i < c.ic; i++)
+      for (int a = 0; a < c.ky; a++)
+        for (int b = 0; b < c.kx; b++)
+          w[(((size_t)i * c.ky + a) * c.kx + b) * c.oc + oo] = c.w[(((size_t)oo * c.ic + i) * c.ky + a) * c.kx + b];
+  const float* dW = upload_f(w);
+  const int ky = c.ky, kx = c.kx, dy = c.dy, dx = c.dx;
+  Op op;
+  op.launch = [=](hipStream_t s, int B) { launch_conv_direct(prec, x, ldx, nchw, ic, dW, oc, ky, kx, dy, dx, *out, B, s); };
+  op.cls = "conv_direct";
+  op.flops_row = 2.0 * HW * ic * oc * ky * kx;
+  op.bytes_row = in_bytes + out_bytes;
+  op.out = out;
+  op.out_c = oc;
+  ops_.push_back(op);
+  return out;
 }
 
-void Net::emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, void* C, int ldc, bool out_t,
-                          float* residual_masked, const char* cls) {
+std::shared_ptr<ConvOut> Net::emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, const ConvOut& o,
+                                              const char* cls) {
   const int prec = prec_;
-  const float* mask = mask_;
+  auto out = std::make_shared<ConvOut>(o);
   Op op;
   op.launch = [=](hipStream_t s, int B) {
     GemmArgs g;
     g.A = A; g.lda = lda;
     g.Bt = Bt; g.ldb = K;
-    g.C = C; g.ldc = ldc; g.out_t = out_t;
-    if (residual_masked) { g.residual = residual_masked; g.ldr = ldc; g.rowmask = mask; }
+    g.out = *out;
     g.M = B * HW; g.N = N; g.K = K;
     launch_gemm(prec, g, s);
   };
   op.cls = cls;
   const double ts = (double)tsize();
   op.flops_row = 2.0 * HW * K * N;
-  op.bytes_row = (double)HW * K * ts + (double)HW * N * (out_t ? ts : 4.0) * (residual_masked ? 2 : 1);
+  op.bytes_row = (double)HW * K * ts + (double)HW * N * ((o.y ? 4.0 : 0.0) * (o.accumulate ? 2 : 1) + (o.yt ? ts : 0.0));
   op.bytes_fixed = (double)K * N * ts;
+  op.out = out;
+  op.out_c = N;
   ops_.push_back(op);
+  return out;
 }
 
 // TransformerAttentionBlock (bin2onnx.py:1357-1421): RMSNorm, fused q|k|v projection (RoPE-permuted q and k
 // columns, bin2onnx.py:1369-1374), attention with RoPE on load, out projection * mask + residual.
-void Net::emit_attention(const BlockDesc& b, float* x, int c) {
+void Net::emit_attention(const BlockDesc& b, int depth) {
   const int prec = prec_;
+  float* x = ss_[depth].x;
+  const int c = ss_[depth].c;
   const int H = b.heads, KV = b.kv_heads, dq = b.dq, dv = b.dv;
   if (dq != dv) throw std::runtime_error(b.name + ": attention with qHeadDim != vHeadDim is not supported");
   const int nq = H * dq, nk = KV * dq, nv = KV * dv, nqkv = nq + nk + nv;
@@ -279,7 +375,10 @@ void Net::emit_attention(const BlockDesc& b, float* x, int c) {
   rn.cls = "rmsnorm";
   rn.bytes_row = (double)HW * c * (4 + tsize());
   ops_.push_back(rn);
-  emit_token_gemm(nrm_, c, dWqkv, nqkv, c, qkv_, nqkv, true, nullptr, "token_gemm");
+  ConvOut oq;
+  oq.yt = qkv_;
+  oq.ldyt = nqkv;
+  emit_token_gemm(nrm_, c, dWqkv, nqkv, c, oq, "token_gemm");
   void* qkv = qkv_;
   void* ao = ao_;
   const float scale = 1.0f / std::sqrt((float)dq);
@@ -296,13 +395,17 @@ void Net::emit_attention(const BlockDesc& b, float* x, int c) {
   at.flops_row = 2.0 * H * HW * HW * (dq + dv);
   at.bytes_row = (double)HW * nqkv * tsize() + (double)HW * H * dv * tsize();
   ops_.push_back(at);
-  emit_token_gemm(ao_, H * dv, dWo, c, H * dv, x, c, false, x, "token_gemm");
+  ConvOut oo;
+  oo.y = x; oo.ldy = c; oo.accumulate = true; oo.rowmask = mask;
+  ss_[depth].producer = emit_token_gemm(ao_, H * dv, dWo, c, H * dv, oo, "token_gemm");
 }
 
 // TransformerFFNBlock (bin2onnx.py:1423-1438): RMSNorm, linear1 (| gate), SiLU(l1) * gate (the plain FFN, which
 // the reference rejects, as mish(l1)), linear2 * mask + residual.
-void Net::emit_ffn(const BlockDesc& b, float* x, int c) {
+void Net::emit_ffn(const BlockDesc& b, int depth) {
   const int prec = prec_;
+  float* x = ss_[depth].x;
+  const int c = ss_[depth].c;
   const int F = b.ffn_c, Fu = b.swiglu ? 2 * F : F;
   std::vector<float> w1((size_t)Fu * c);
   for (int f = 0; f < F; f++)
@@ -324,7 +427,10 @@ void Net::emit_ffn(const BlockDesc& b, float* x, int c) {
   rn.cls = "rmsnorm";
   rn.bytes_row = (double)HW * c * (4 + tsize());
   ops_.push_back(rn);
-  emit_token_gemm(nrm_, c, dW1, Fu, c, u_, Fu, false, nullptr, "token_gemm");
+  ConvOut o1;
+  o1.y = u_;
+  o1.ldy = Fu;
+  emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm");
   float* u = u_;
   void* h = h_;
   const bool gated = b.swiglu;
@@ -333,17 +439,29 @@ void Net::emit_ffn(const BlockDesc& b, float* x, int c) {
   fa.cls = "ffn_act";
   fa.bytes_row = (double)HW * Fu * 4 + (double)HW * F * tsize();
   ops_.push_back(fa);
-  emit_token_gemm(h_, F, dW2, c, F, x, c, false, x, "token_gemm");
+  ConvOut o2;
+  o2.y = x; o2.ldy = c; o2.accumulate = true; o2.rowmask = mask;
+  ss_[depth].producer = emit_token_gemm(h_, F, dW2, c, F, o2, "token_gemm");
 }
 
-void Net::emit_stack(const std::vector<BlockDesc>& blocks, float* x, int c, int depth) {
+void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
+  const int prec = prec_;
   for (const BlockDesc& b : blocks) {
+    float* x = ss_[depth].x;
+    const int c = ss_[depth].c;
+    ConvOut res;  // the block's residual add into its stream
+    res.y = x;
+    res.ldy = c;
+    res.accumulate = true;
     switch (b.kind) {
       case BLOCK_RES: {
-        // x += conv2(bnact(conv1(bnact(x)))) (bin2onnx.py:1243-1249)
+        // x += conv2(bnact(conv1(bnact(x)))) (bin2onnx.py:1243-1249); conv1 writes only conv2's activation.
         const int cm = b.regular.oc;
-        emit_conv(b.regular, x, c, false, bn_pro(b.pre_bn, b.pre_act), tmp_, cm, false, nullptr, 0);
-        emit_conv(b.final_conv, tmp_, cm, false, bn_pro(b.mid_bn, b.mid_act), x, c, true, nullptr, 0);
+        const void* a = consume(depth, b.pre_bn, b.pre_act);
+        ConvOut o1;
+        o1.emit = bn_emit(b.mid_bn, b.mid_act, mid_, cm);
+        emit_conv(b.regular, a, c, false, o1);
+        ss_[depth].producer = emit_conv(b.final_conv, mid_, cm, false, res);
         break;
       }
       case BLOCK_GPOOL: {
@@ -354,7 +472,11 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, float* x, int c, int 
         both.w.insert(both.w.end(), b.gconv.w.begin(), b.gconv.w.end());
         if (b.regular.ky != b.gconv.ky || b.regular.kx != b.gconv.kx || b.regular.dy != b.gconv.dy || b.regular.dx != b.gconv.dx)
           throw std::runtime_error(b.name + ": regular and gpool convolutions differ in shape");
-        emit_conv(both, x, c, false, bn_pro(b.pre_bn, b.pre_act), tmp_, ct, false, nullptr, 0);
+        const void* a = consume(depth, b.pre_bn, b.pre_act);
+        ConvOut o1;
+        o1.y = tmp_;
+        o1.ldy = ct;
+        emit_conv(both, a, c, false, o1);
         const Prologue gpro = bn_pro(b.gbn, b.gact);
         float* tmp = tmp_;
         float* gp = gp_;
@@ -371,23 +493,39 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, float* x, int c, int 
         mm.cls = "small_matmul";
         mm.flops_row = 2.0 * 3 * cg * cr;
         ops_.push_back(mm);
-        emit_conv(b.final_conv, tmp_, ct, false, bn_pro(b.mid_bn, b.mid_act, gb_, cr), x, c, true, nullptr, 0);
+        // The mid activation adds the pooled bias per (row, channel) before its batch norm.
+        const Emit me = bn_emit(b.mid_bn, b.mid_act, mid_, cr);
+        Op ba;
+        ba.launch = [=](hipStream_t s, int B) {
+          launch_bias_act(prec, tmp, ct, cr, gb, cr, me.scale, me.bias, me.act, me.mask, me.out, me.ld, B * HW, s);
+        };
+        ba.cls = "bias_act";
+        ba.bytes_row = (double)HW * cr * (4 + tsize());
+        ops_.push_back(ba);
+        ss_[depth].producer = emit_conv(b.final_conv, mid_, cr, false, res);
         break;
       }
       case BLOCK_NBT: {
         // x += post(bnact(inner(pre(bnact(x))))) (bin2onnx.py:1263-1269)
         const int ci = b.regular.oc;
-        float* st = streams_[depth + 1];
-        emit_conv(b.regular, x, c, false, bn_pro(b.pre_bn, b.pre_act), st, ci, false, nullptr, 0);
-        emit_stack(b.inner, st, ci, depth + 1);
-        emit_conv(b.final_conv, st, ci, false, bn_pro(b.mid_bn, b.mid_act), x, c, true, nullptr, 0);
+        const void* a = consume(depth, b.pre_bn, b.pre_act);
+        StreamState& in = ss_[depth + 1];
+        in.c = ci;
+        in.producer.reset();
+        ConvOut o1;
+        o1.y = in.x;
+        o1.ldy = ci;
+        in.producer = emit_conv(b.regular, a, c, false, o1);
+        emit_stack(b.inner, depth + 1);
+        const void* a2 = consume(depth + 1, b.mid_bn, b.mid_act);
+        ss_[depth].producer = emit_conv(b.final_conv, a2, ci, false, res);
         break;
       }
       case BLOCK_ATTN:
-        emit_attention(b, x, c);
+        emit_attention(b, depth);
         break;
       case BLOCK_FFN:
-        emit_ffn(b, x, c);
+        emit_ffn(b, depth);
         break;
     }
   }
@@ -416,10 +554,14 @@ void Net::build(const ModelDesc& m) {
   stream_c_.assign(1, C);
   scan(m.blocks, C, 0);
   trunk_ = alloc_f(Mx * C);
-  streams_.assign(stream_c_.size(), nullptr);
-  streams_[0] = trunk_;
-  for (size_t d = 1; d < stream_c_.size(); d++) streams_[d] = alloc_f(Mx * stream_c_[d]);
+  ss_.assign(stream_c_.size(), StreamState());
+  for (size_t d = 0; d < stream_c_.size(); d++) {
+    ss_[d].c = stream_c_[d];
+    ss_[d].x = d == 0 ? trunk_ : alloc_f(Mx * stream_c_[d]);
+    for (int k = 0; k < 2; k++) ss_[d].act[k] = alloc_bytes(Mx * stream_c_[d] * tsize());
+  }
   if (tmp_c_) tmp_ = alloc_f(Mx * tmp_c_);
+  if (mid_c_) mid_ = alloc_bytes(Mx * mid_c_ * tsize());
   if (gp_c_) gp_ = alloc_f((size_t)max_batch_ * gp_c_);
   if (gb_c_) gb_ = alloc_f((size_t)max_batch_ * gb_c_);
   if (nrm_c_) nrm_ = alloc_bytes(Mx * nrm_c_ * tsize());
@@ -467,10 +609,17 @@ void Net::build(const ModelDesc& m) {
     op.flops_row = 2.0 * (192.0 * h1 + (double)h1 * h2 + (double)h2 * C);
     ops_.push_back(op);
   }
-  emit_conv(m.stem, d_bin_, 0, true, Prologue(), trunk_, C, false, gbias, C);
+  {
+    ConvOut o;
+    o.y = trunk_;
+    o.ldy = C;
+    o.colbias = gbias;
+    o.ld_colbias = C;
+    ss_[0].producer = emit_conv(m.stem, d_bin_, 0, true, o);
+  }
 
   // --- Blocks. ---
-  emit_stack(m.blocks, trunk_, C, 0);
+  emit_stack(m.blocks, 0);
 
   // --- Trunk tip and heads (bin2onnx.py:1489-1531). ---
   const float* head_in = trunk_;
@@ -500,16 +649,18 @@ void Net::build(const ModelDesc& m) {
   std::memcpy(wh.data(), m.p1.w.data(), (size_t)cp * C * 4);
   std::memcpy(wh.data() + (size_t)cp * C, m.g1.w.data(), (size_t)cg * C * 4);
   std::memcpy(wh.data() + (size_t)(cp + cg) * C, m.v1.w.data(), (size_t)cv * C * 4);
-  const void* dWh = upload_t(wh);
+  // The head GEMM runs on float operands in every precision: it is under 1% of the work, and its outputs feed
+  // the policy and ownership logits directly.
+  const float* dWh = upload_f(wh);
   float* H = alloc_f(Mx * nh);
   {
-    const int prec = prec_;
+    const int prec = PREC_F32;
     Op op;
     op.launch = [=](hipStream_t s, int B) {
       GemmArgs g;
       g.A = head_in; g.lda = C; g.a_float = true; g.pro = tip_pro;
       g.Bt = dWh; g.ldb = C;
-      g.C = H; g.ldc = nh;
+      g.out.y = H; g.out.ldy = nh;
       g.M = B * HW; g.N = nh; g.K = C;
       launch_gemm(prec, g, s);
     };
@@ -592,8 +743,15 @@ void Net::build(const ModelDesc& m) {
   }
 
   // Winograd workspace, sized by the largest convolution.
-  if (wino_v_elems_) wino_v_ = alloc_bytes(wino_v_elems_ * tsize());
-  if (wino_m_elems_) wino_m_ = alloc_f(wino_m_elems_);
+  // Zeroed once: padding tile rows are read by the GEMMs but never written.
+  if (wino_v_elems_) {
+    wino_v_ = alloc_bytes(wino_v_elems_ * tsize());
+    KGX_HIP(hipMemset(wino_v_, 0, wino_v_elems_ * tsize()));
+  }
+  if (wino_m_elems_) {
+    wino_m_ = alloc_f(wino_m_elems_);
+    KGX_HIP(hipMemset(wino_m_, 0, wino_m_elems_ * 4));
+  }
   KGX_HIP(hipDeviceSynchronize());
 }
 
@@ -618,10 +776,12 @@ void Net::run_ops(int B, hipStream_t s) {
     float ms = 0.f;
     KGX_HIP(hipEventElapsedTime(&ms, events_[2 * k], events_[2 * k + 1]));
     ProfileClass& pc = profile_[ops_[k].cls];
+    pc.name = ops_[k].cls;
     pc.launches++;
     pc.ms += ms;
     pc.flops += ops_[k].flops_row * B;
     pc.bytes += ops_[k].bytes_row * B + ops_[k].bytes_fixed;
+    if (ops_[k].out && ops_[k].out->emit.scale) pc.bytes += (double)HW * ops_[k].out_c * tsize() * B;
   }
 }
 

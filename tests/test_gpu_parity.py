@@ -63,6 +63,38 @@ def test_tiny_nets_match_oracle(kgx, synth, golden, name, prec):
     h.close()
 
 
+@pytest.mark.parametrize("conv,prec", [("wino2", "f32"), ("wino2", "f16"), ("wino2", "bf16"), ("wino4", "f16")])
+@pytest.mark.parametrize("name", ["t_res", "t_nbt", "t_v8"])
+def test_winograd_variants_match_oracle(kgx, synth, golden, monkeypatch, name, conv, prec):
+    """The Winograd kernels on every precision (16-bit handles default to the implicit GEMM, float ones to
+    F(4x4,3x3)); the algorithm is chosen when the handle builds its network."""
+    monkeypatch.setenv("KGX_CONV", conv)
+    g, _ = golden
+    net = kgx.Net(synth.write_model(synth.tiny_nets()[name], 1))
+    h = kgx.Handle(net, 8, prec)
+    out = h.forward(g[f"{name}.spatial"], g[f"{name}.glob"])
+    if conv == "wino4" and prec != "f32":
+        # F(4x4,3x3) transforms grow values up to 10x, so 16-bit operands lose about a digit (measured 3.5e-2 on
+        # these nets): the reason 16-bit handles use F(2x2,3x3) or the implicit GEMM. Held to 6e-2 here.
+        errs = errors(out, g[f"{name}.out"], net.P, net.S)
+        assert np.all(np.isfinite(out)) and all(e <= 6e-2 for e, _ in errs.values()), errs
+    else:
+        check(out, g[f"{name}.out"], net.P, net.S, prec, f"{name} {conv}")
+    h.close()
+
+
+def test_winograd_f2_benchmark_config(kgx, synth, oracle, monkeypatch):
+    monkeypatch.setenv("KGX_CONV", "wino2")
+    arch_fn, batch = synth.CONFIGS["b10c128"]
+    mb = synth.write_model(arch_fn(), synth.CONFIG_SEEDS["b10c128"])
+    sp, gl, _ = synth.make_inputs(batch, 17, board_sizes=[19, 19, 13, 9])
+    net = kgx.Net(mb)
+    h = kgx.Handle(net, batch, "f16")
+    out = h.forward(sp, gl)
+    check(out, oracle.Model(mb).forward(sp, gl), net.P, net.S, "f16", "b10c128 wino2")
+    h.close()
+
+
 CONFIG_ROWS = {"b10c128": 8, "b18c384nbt": 2, "b10c384h6": 2, "b10c512h8": 1, "tf3-b11c768": 1}
 
 
