@@ -17,16 +17,20 @@
 
 namespace kgx {
 
-template <int KS_, int BM_, int BN_, int BK_, int WM_, int WN_>
+template <int KS_, int BM_, int BN_, int BK_, int WM_, int WN_, int G_, int NBUF_>
 struct IgCfg {
   static constexpr int KS = KS_, TAPS = KS_ * KS_, HALO = KS_ == 3 ? POS + 1 : 0;
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
-  static constexpr int NT = WM * WN * 64;
+  static constexpr int G = G_;                  // wave groups splitting the taps (partial sums added in LDS)
+  static constexpr int NBUF = NBUF_;            // LDS stage buffers (2: the next stage is stored during the MFMAs)
+  static constexpr int NT = WM * WN * 64 * G_;
 };
 
 // Epilogue for four consecutive channels n..n+3 of pixel m (conv_store on a float4).
+// With `have_yacc`, `yacc` holds the residual values already loaded (instead of reading o.y).
 template <typename T>
-__device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floatx4 v) {
+__device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floatx4 v, bool have_yacc = false,
+                                            floatx4 yacc = floatx4{0.f, 0.f, 0.f, 0.f}) {
   if (o.colbias) v += *(const floatx4*)(o.colbias + (size_t)(m / HW) * o.ld_colbias + n);
   if (o.rowmask) v *= o.rowmask[m];
   if (o.yt) {
@@ -35,7 +39,7 @@ __device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floa
   }
   if (o.y) {
     floatx4* p = (floatx4*)(o.y + (size_t)m * o.ldy + n);
-    if (o.accumulate) v += *p;
+    if (o.accumulate) v += have_yacc ? yacc : *p;
     *p = v;
   }
   if (o.emit.scale) {
@@ -52,23 +56,27 @@ template <typename T, typename C>
 __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, int ldx, int IC, const T* __restrict__ W,
                                                       int icp, int OC, int M, ConvOut o) {
   constexpr int TAPS = C::TAPS, HALO = C::HALO, BM = C::BM, BN = C::BN, BK = C::BK, WM = C::WM, WN = C::WN;
-  constexpr int NT = C::NT;
+  constexpr int NT = C::NT, G = C::G;
   constexpr int LDK = BK + 8;                 // LDS row stride in elements (16-byte pad)
   constexpr int KV = BK / 8;                  // 16-byte vectors per staged row
   constexpr int AR = BM + 2 * HALO;           // staged pixel rows
   constexpr int AVT = AR * KV, BVT = TAPS * BN * KV;
   constexpr int AV = (AVT + NT - 1) / NT, BV = (BVT + NT - 1) / NT;
   constexpr int WTM = BM / WM, WTN = BN / WN, MB = WTM / 16, NB = WTN / 16;
-  static_assert(WTM % 16 == 0 && WTN % 16 == 0 && BK % 32 == 0, "bad tile");
-  constexpr int STAGE = (AR + TAPS * BN) * LDK * 2;   // bytes
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0 && BK % 32 == 0 && AV <= 32 && BV <= 32, "bad tile");
+  constexpr int STAGE = (AR + 1 + TAPS * BN) * LDK * 2;   // bytes (A rows, a zero row, B rows)
   constexpr int EPI = BM * (BN + 4) * 4;              // bytes
-  __shared__ __align__(16) char smem[STAGE > EPI ? STAGE : EPI];
+  constexpr int NBUF = C::NBUF;
+  constexpr int SE = STAGE / (int)sizeof(T);          // stage buffer size in elements
+  __shared__ __align__(16) char smem[NBUF * STAGE > EPI ? NBUF * STAGE : EPI];
   T* As = (T*)smem;
-  T* Bs = As + AR * LDK;
+  T* Bs = As + (AR + 1) * LDK;
   typedef u32x4 vec_t;
+  typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int wm = wave / WN, wn = wave % WN;
+  const int grp = wave / (WM * WN), wl = wave - grp * (WM * WN);
+  const int wm = wl / WN, wn = wl % WN;
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
   const int r16 = lane & 15, g4 = lane >> 4;
 
@@ -125,13 +133,15 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
 #pragma unroll
     for (int v = 0; v < BV; v++) rb[v] = ((b_ok >> v) & 1) ? *(const vec_t*)(W + b_goff[v] + k0) : vec_t{0, 0, 0, 0};
   };
-  auto store = [&]() {
+  auto store = [&](int buf) {
+    T* ab = As + buf * SE;
+    T* bb = Bs + buf * SE;
 #pragma unroll
     for (int v = 0; v < AV; v++)
-      if (AVT % NT == 0 || tid + NT * v < AVT) *(vec_t*)(As + a_soff[v]) = ra[v];
+      if (AVT % NT == 0 || tid + NT * v < AVT) *(vec_t*)(ab + a_soff[v]) = ra[v];
 #pragma unroll
     for (int v = 0; v < BV; v++)
-      if (BVT % NT == 0 || tid + NT * v < BVT) *(vec_t*)(Bs + b_soff[v]) = rb[v];
+      if (BVT % NT == 0 || tid + NT * v < BVT) *(vec_t*)(bb + b_soff[v]) = rb[v];
   };
 
   floatx4 acc[MB][NB];
@@ -140,65 +150,122 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
 #pragma unroll
     for (int j = 0; j < NB; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-  typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
-  const int nk = icp / BK;
-  load(0);
-  for (int kt = 0; kt < nk; kt++) {
-    store();
-    __syncthreads();
-    if (kt + 1 < nk) load((kt + 1) * BK);
-#pragma unroll
-    for (int t = 0; t < TAPS; t++) {
+  // The MFMA steps of one group over the staged stage: its share of the (tap, 32-channel slice) pairs, with the
+  // fragments of the next step read from LDS while the current step's MFMAs run.
+  auto mma = [&](auto gc, int sb) {
+    constexpr int g = decltype(gc)::value;
+    constexpr int KK = BK / 32, ST = TAPS * KK, S0 = g * ST / G, S = (g + 1) * ST / G - S0;
+    frag_t a[2][MB], b[2][NB];
+    auto fetch = [&](int s, int fb) {
+      const int t = (S0 + s) / KK, kk = ((S0 + s) % KK) * 32;
       const int shift = C::KS == 3 ? (t / 3 - 1) * POS + (t % 3 - 1) : 0;
-      const T* as = As + (wm * WTM + r16 + HALO + shift) * LDK + g4 * 8;
-      const T* bs = Bs + (t * BN + wn * WTN + r16) * LDK + g4 * 8;
+      const T* bs = Bs + sb * SE + (t * BN + wn * WTN + r16) * LDK + g4 * 8 + kk;
 #pragma unroll
-      for (int kk = 0; kk < BK; kk += 32) {
-        frag_t a[MB], b[NB];
-#pragma unroll
-        for (int i = 0; i < MB; i++) {
-          a[i] = *(const frag_t*)(as + i * 16 * LDK + kk);
-          if (!((vmask[i] >> t) & 1)) a[i] = frag_t{};
-        }
-#pragma unroll
-        for (int j = 0; j < NB; j++) b[j] = *(const frag_t*)(bs + j * 16 * LDK + kk);
-#pragma unroll
-        for (int i = 0; i < MB; i++)
-#pragma unroll
-          for (int j = 0; j < NB; j++) {
-            if constexpr (std::is_same<T, f16>::value)
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[i], b[j], acc[i][j], 0, 0, 0);
-            else
-              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[i], b[j], acc[i][j], 0, 0, 0);
-          }
+      for (int i = 0; i < MB; i++) {
+        // Rows whose neighbour is off the board read the zero row, so no loaded value needs masking.
+        const int row = ((vmask[i] >> t) & 1) ? wm * WTM + i * 16 + r16 + HALO + shift : AR;
+        a[fb][i] = *(const frag_t*)(As + sb * SE + row * LDK + g4 * 8 + kk);
       }
+#pragma unroll
+      for (int j = 0; j < NB; j++) b[fb][j] = *(const frag_t*)(bs + j * 16 * LDK);
+    };
+    fetch(0, 0);
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+      if (s + 1 < S) fetch(s + 1, (s + 1) & 1);
+#pragma unroll
+      for (int i = 0; i < MB; i++)
+#pragma unroll
+        for (int j = 0; j < NB; j++) {
+          if constexpr (std::is_same<T, f16>::value)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s & 1][i], b[s & 1][j], acc[i][j], 0, 0, 0);
+          else
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s & 1][i], b[s & 1][j], acc[i][j], 0, 0, 0);
+        }
     }
-    __syncthreads();
+  };
+
+  auto compute = [&](int buf) {
+    if constexpr (G == 1) {
+      mma(std::integral_constant<int, 0>{}, buf);
+    } else {
+      if (grp == 0) mma(std::integral_constant<int, 0>{}, buf);
+      else mma(std::integral_constant<int, G - 1>{}, buf);
+    }
+  };
+  // Residual values of this thread's epilogue vectors, read before the main loop so that the reads overlap it.
+  constexpr int NV = BM * (BN / 4), EV = (NV + NT - 1) / NT;
+  floatx4 yres[EV];
+  const bool yprefetch = o.y && o.accumulate;
+  if (yprefetch) {
+#pragma unroll
+    for (int e = 0; e < EV; e++) {
+      const int v = tid + e * NT;
+      const int row = v / (BN / 4), c4 = v - row * (BN / 4);
+      const int m = m0 + row, n = n0 + 4 * c4;
+      if (v < NV && m < M && n < OC) yres[e] = *(const floatx4*)(o.y + (size_t)m * o.ldy + n);
+    }
   }
 
-  // Accumulators to LDS as a float [BM][BN + 4] tile: element (i, j, r) is row wm*WTM + i*16 + 4*(lane/16) + r,
-  // column wn*WTN + j*16 + lane%16.
+  // The zero row of every stage buffer (never written by the stage stores).
+  for (int e = tid; e < NBUF * KV; e += NT) *(vec_t*)(As + (e / KV) * SE + AR * LDK + (e % KV) * 8) = vec_t{0, 0, 0, 0};
+  const int nk = icp / BK;
+  load(0);
+  if constexpr (NBUF == 1) {
+    // One stage buffer: store, barrier, next loads in flight during the MFMAs, barrier.
+    for (int kt = 0; kt < nk; kt++) {
+      store(0);
+      __syncthreads();
+      if (kt + 1 < nk) load((kt + 1) * BK);
+      compute(0);
+      __syncthreads();
+    }
+  } else {
+    // Two stage buffers: the next stage's loads are issued before and stored after the current MFMAs; one barrier.
+    store(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+      if (kt + 1 < nk) load((kt + 1) * BK);
+      compute(kt & 1);
+      if (kt + 1 < nk) store((kt + 1) & 1);
+      __syncthreads();
+    }
+  }
+
+  // Accumulators to LDS as a float [BM][BN + 4] tile (group 0 stores, group 1 adds): element (i, j, r) is row
+  // wm*WTM + i*16 + 4*(lane/16) + r, column wn*WTN + j*16 + lane%16.
+  static_assert(G == 1 || G == 2, "one or two wave groups");
   float* Cs = (float*)smem;
   constexpr int LDC = BN + 4;
 #pragma unroll
-  for (int i = 0; i < MB; i++)
+  for (int q = 0; q < G; q++) {
+    if (grp == q) {
 #pragma unroll
-    for (int j = 0; j < NB; j++)
+      for (int i = 0; i < MB; i++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) Cs[(wm * WTM + i * 16 + 4 * g4 + r) * LDC + wn * WTN + j * 16 + r16] = acc[i][j][r];
-  __syncthreads();
-  constexpr int NV = BM * (BN / 4);
-#pragma unroll 2
-  for (int v = tid; v < NV; v += NT) {
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            float* c = Cs + (wm * WTM + i * 16 + 4 * g4 + r) * LDC + wn * WTN + j * 16 + r16;
+            *c = q == 0 ? acc[i][j][r] : *c + acc[i][j][r];
+          }
+    }
+    __syncthreads();
+  }
+#pragma unroll
+  for (int e = 0; e < EV; e++) {
+    const int v = tid + e * NT;
     const int row = v / (BN / 4), c4 = v - row * (BN / 4);
     const int m = m0 + row, n = n0 + 4 * c4;
-    if (m < M && n < OC) conv_store4<T>(o, m, n, *(const floatx4*)(Cs + row * LDC + 4 * c4));
+    if (v < NV && m < M && n < OC)
+      conv_store4<T>(o, m, n, *(const floatx4*)(Cs + row * LDC + 4 * c4), yprefetch, yres[e]);
   }
 }
 
-// Configurations: 3x3 with 96x96 tiles (2x2 waves of 48x48), 1x1 with 96x96 tiles and 64 channels per stage.
-typedef IgCfg<3, 96, 96, 32, 2, 2> Ig3;
-typedef IgCfg<1, 96, 96, 64, 2, 2> Ig1;
+// Configurations (measured at batch 32, 192 channels): 3x3 with 96x96 tiles, 64 channels per stage and two wave
+// groups of 2x2 waves (48x48 each) splitting the taps; 1x1 with 64x64 tiles, two groups and two stage buffers.
+typedef IgCfg<3, 96, 96, 64, 2, 2, 2, 1> Ig3;
+typedef IgCfg<1, 64, 64, 64, 2, 2, 2, 2> Ig1;
 
 template <typename T, typename C>
 static void igemm_launch(const void* x, int ldx, int IC, const void* w, int icp, int OC, const ConvOut& o, int M,

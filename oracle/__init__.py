@@ -32,6 +32,8 @@ def lib():
         for fn in (L.kgo_forward_f64, L.kgo_forward_f32):
             fn.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                            ctypes.c_void_p, ctypes.c_int]
+        L.kgo_forward_f64_q.argtypes = [ctypes.c_void_p, ctypes.c_int] + [ctypes.c_void_p] * 4 + [ctypes.c_int] * 3
+        L.kgo_round_operands.argtypes = [ctypes.c_void_p, ctypes.c_long, ctypes.c_int]
         L.kgo_conv_direct_f64.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p] * 3
         L.kgo_wino_filter_f64.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
         L.kgo_conv3x3_winograd_f64.argtypes = [ctypes.c_int] * 3 + [ctypes.c_void_p] * 3
@@ -67,8 +69,12 @@ class Model:
             lib().kgo_model_free(self._h)
             self._h = None
 
-    def forward(self, spatial, glob, meta=None, dtype=np.float64, threads=None):
-        """Raw output rows [n, row_len] (policy P x 362 with pass last, value 3, score S, ownership 361)."""
+    def forward(self, spatial, glob, meta=None, dtype=np.float64, threads=None, operands=None, acts=True,
+                weights=True):
+        """Raw output rows [n, row_len] (policy P x 362 with pass last, value 3, score S, ownership 361).
+
+        operands="f16" / "bf16" evaluates in double with the trunk's GEMM operands rounded to that 16-bit type
+        (activations when `acts`, weights when `weights`), as a 16-bit handle computes them."""
         n = spatial.shape[0]
         spatial = np.ascontiguousarray(spatial, np.float32)
         glob = np.ascontiguousarray(glob, np.float32)
@@ -78,6 +84,13 @@ class Model:
             meta = None
         threads = threads or os.cpu_count() or 1
         out = np.zeros((n, self.row_len), dtype)
+        if operands is not None:
+            q = {"f16": 1, "bf16": 2}[operands]
+            out = np.zeros((n, self.row_len), np.float64)
+            if lib().kgo_forward_f64_q(self._h, n, _p(spatial), _p(glob), _p(meta), _p(out), threads,
+                                       q if acts else 0, q if weights else 0) != 0:
+                raise RuntimeError(lib().kgo_last_error().decode())
+            return out
         fn = lib().kgo_forward_f64 if dtype == np.float64 else lib().kgo_forward_f32
         if fn(self._h, n, _p(spatial), _p(glob), _p(meta), _p(out), threads) != 0:
             raise RuntimeError(lib().kgo_last_error().decode())
@@ -132,3 +145,10 @@ def copy_outputs_row(row, P, S, version, sym, optimism, want_owner=True):
     own = np.zeros(361, np.float32) if want_owner else None
     lib().kgo_copy_outputs_row(_p(row), P, S, version, sym, ctypes.c_float(optimism), _p(pol), _p(fields), _p(own))
     return pol, fields, own
+
+
+def round_operands(x, operands):
+    """Values rounded to a 16-bit operand type ("f16" / "bf16"), returned as float64."""
+    a = np.array(x, np.float64, copy=True, order="C")
+    lib().kgo_round_operands(_p(a), a.size, {"f16": 1, "bf16": 2}[operands])
+    return a

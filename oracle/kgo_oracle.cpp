@@ -370,17 +370,48 @@ R act(R a, int kind) {
   }
 }
 
+// Rounding of a value to a 16-bit floating-point operand, round-to-nearest-even: float16 (11 significant bits,
+// normal range from 2^-14, subnormal quantum 2^-24, overflow above 65504 to infinity) or bfloat16 (8 significant
+// bits, float32's exponent range). Used to emulate a forward pass whose GEMM operands are 16-bit.
+enum { Q_NONE = 0, Q_F16 = 1, Q_BF16 = 2 };
+double round_operand(double x, int q) {
+  if (q == Q_NONE || x == 0.0 || !std::isfinite(x)) return x;
+  int e;
+  std::frexp(x, &e);  // |x| = f 2^e, f in [0.5, 1)
+  const int bits = q == Q_F16 ? 11 : 8;
+  int qe = e - bits;
+  if (q == Q_F16) qe = std::max(qe, -24);
+  const double r = std::nearbyint(std::ldexp(x, -qe)) * std::ldexp(1.0, qe);  // default rounding: to even
+  if (q == Q_F16 && std::fabs(r) > 65504.0) return std::copysign(INFINITY, x);
+  return r;
+}
+
 template <typename R>
 struct Fwd {
   const Model& m;
   int n;
   std::vector<R> mask, area, s1, s2;  // mask [n][HW]
   int threads;
+  // Operand emulation (double only): the trunk's convolution and token-GEMM operands (inputs and weights), the
+  // q/k/v projections and the attention output are rounded to 16 bits; accumulation, residual streams, pooling,
+  // normalization statistics and the heads stay exact. qa / qw choose the rounding of activations / weights.
+  int qa = Q_NONE, qw = Q_NONE;
 
   Fwd(const Model& mm, int nn, int th) : m(mm), n(nn), threads(th) {}
 
-  // "same" convolution, zero padding, on [n][C][HW].
-  std::vector<R> conv(const std::vector<R>& x, const Conv& c) {
+  R ra(R v) const { return qa ? (R)round_operand((double)v, qa) : v; }
+  R rw(R v) const { return qw ? (R)round_operand((double)v, qw) : v; }
+
+  // "same" convolution, zero padding, on [n][C][HW]; `half` marks a trunk convolution (16-bit operands when
+  // emulated).
+  std::vector<R> conv(const std::vector<R>& x0, const Conv& c, bool half = false) {
+    std::vector<R> xr;
+    if (half && qa) {
+      xr = x0;
+      for (auto& v : xr) v = ra(v);
+    }
+    const std::vector<R>& x = (half && qa) ? xr : x0;
+    const bool hw = half && qw;
     std::vector<R> out((size_t)n * c.oc * HW, R(0));
     const int py = (c.ky / 2) * c.dy, px = (c.kx / 2) * c.dx;
 #pragma omp parallel for collapse(2) schedule(static) num_threads(threads)
@@ -393,7 +424,8 @@ struct Fwd {
             const int oy = ky * c.dy - py;
             for (int kx = 0; kx < c.kx; kx++) {
               const int ox = kx * c.dx - px;
-              const R w = (R)c.w[(((size_t)o * c.ic + i) * c.ky + ky) * c.kx + kx];
+              R w = (R)c.w[(((size_t)o * c.ic + i) * c.ky + ky) * c.kx + kx];
+              if (hw) w = rw(w);
               const int y0 = std::max(0, -oy), y1 = std::min(POS, POS - oy);
               const int x0 = std::max(0, -ox), x1 = std::min(POS, POS - ox);
               for (int y = y0; y < y1; y++) {
@@ -503,17 +535,19 @@ struct Fwd {
     return x;
   }
 
-  // rows [n*HW][ic] x [ic][oc]
+  // rows [n*HW][ic] x [ic][oc] (operands rounded when emulated)
   std::vector<R> tok_matmul(const std::vector<R>& t, const MatMul& mm) {
     const size_t rows = (size_t)n * HW;
     std::vector<R> out(rows * mm.oc, R(0));
+    std::vector<R> wr((size_t)mm.ic * mm.oc);
+    for (size_t k = 0; k < wr.size(); k++) wr[k] = rw((R)mm.w[k]);
 #pragma omp parallel for schedule(static) num_threads(threads)
     for (long r = 0; r < (long)rows; r++) {
       R* o = &out[r * mm.oc];
       for (int i = 0; i < mm.ic; i++) {
-        const R xv = t[r * mm.ic + i];
-        const float* w = &mm.w[(size_t)i * mm.oc];
-        for (int j = 0; j < mm.oc; j++) o[j] += xv * (R)w[j];
+        const R xv = ra(t[r * mm.ic + i]);
+        const R* w = &wr[(size_t)i * mm.oc];
+        for (int j = 0; j < mm.oc; j++) o[j] += xv * w[j];
       }
     }
     return out;
@@ -573,6 +607,11 @@ struct Fwd {
   void attention_block(std::vector<R>& t, const Block& bl, int C) {
     std::vector<R> xn = tf_rmsnorm(t, bl, C);
     std::vector<R> q = tok_matmul(xn, bl.q), k = tok_matmul(xn, bl.k), v = tok_matmul(xn, bl.v);
+    if (qa) {
+      for (auto& z : q) z = ra(z);
+      for (auto& z : k) z = ra(z);
+      for (auto& z : v) z = ra(z);
+    }
     const int H = bl.heads, KV = bl.kvh, dq = bl.dq, dv = bl.dv, g = H / KV;
     if (bl.rope) {
       std::vector<float> cs, sn; int ntab;
@@ -663,27 +702,27 @@ struct Fwd {
       const Block& bl = blocks[i];
       if (bl.kind == B_RES) {
         std::vector<R> t = bn_act_mask(x, bl.pre_bn, bl.pre_act);
-        t = conv(t, bl.regular);
+        t = conv(t, bl.regular, true);
         t = bn_act_mask(t, bl.mid_bn, bl.mid_act);
-        t = conv(t, bl.final_);
+        t = conv(t, bl.final_, true);
         add(x, t);
       } else if (bl.kind == B_GPOOL) {
         std::vector<R> t = bn_act_mask(x, bl.pre_bn, bl.pre_act);
-        std::vector<R> reg = conv(t, bl.regular);
-        std::vector<R> gg = conv(t, bl.gconv);
+        std::vector<R> reg = conv(t, bl.regular, true);
+        std::vector<R> gg = conv(t, bl.gconv, true);
         gg = bn_act_mask(gg, bl.gbn, bl.gact);
         std::vector<R> pooled = gpool(gg, bl.gconv.oc);
         std::vector<R> bias = matmul(pooled, bl.gmul);
         add_nc_bias(reg, bias, bl.regular.oc);
         reg = bn_act_mask(reg, bl.mid_bn, bl.mid_act);
-        reg = conv(reg, bl.final_);
+        reg = conv(reg, bl.final_, true);
         add(x, reg);
       } else if (bl.kind == B_NBT) {
         std::vector<R> t = bn_act_mask(x, bl.pre_bn, bl.pre_act);
-        t = conv(t, bl.regular);
+        t = conv(t, bl.regular, true);
         block_stack(t, bl.inner, bl.regular.oc);
         t = bn_act_mask(t, bl.mid_bn, bl.mid_act);
-        t = conv(t, bl.final_);
+        t = conv(t, bl.final_, true);
         add(x, t);
       }
       i++;
@@ -706,7 +745,9 @@ struct Fwd {
     }
     std::vector<R> x((size_t)n * m.nin * HW);
     for (size_t k = 0; k < x.size(); k++) x[k] = bin[k];
-    x = conv(x, m.stem);
+    // The device runs 1x1 and 3x3 stems on 16-bit operands and other stems (old nets' 5x5) on float ones.
+    const bool stem16 = m.stem.ky == m.stem.kx && (m.stem.ky == 1 || m.stem.ky == 3) && m.stem.dy == 1 && m.stem.dx == 1;
+    x = conv(x, m.stem, stem16);
     std::vector<R> g((size_t)n * m.nglob);
     for (size_t k = 0; k < g.size(); k++) g[k] = glob[k];
     add_nc_bias(x, matmul(g, m.stem_mm), C);
@@ -881,6 +922,35 @@ int kgo_forward_f64(const void* mp, int n, const float* bin, const float* glob, 
     f.run(bin, glob, meta, out);
     return 0;
   } catch (const std::exception& e) { g_err = e.what(); return 1; }
+}
+
+// kgo_forward_f64 with 16-bit operand emulation: act_q / weight_q = 0 (exact), 1 (float16), 2 (bfloat16).
+int kgo_forward_f64_q(const void* mp, int n, const float* bin, const float* glob, const float* meta, double* out,
+                      int threads, int act_q, int weight_q) {
+  try {
+    Fwd<double> f(*(const Model*)mp, n, threads < 1 ? 1 : threads);
+    f.qa = act_q;
+    f.qw = weight_q;
+    f.run(bin, glob, meta, out);
+    return 0;
+  } catch (const std::exception& e) { g_err = e.what(); return 1; }
+}
+
+// kgo_forward_f32 with 16-bit operand emulation (float accumulation, as the device accumulates).
+int kgo_forward_f32_q(const void* mp, int n, const float* bin, const float* glob, const float* meta, float* out,
+                      int threads, int act_q, int weight_q) {
+  try {
+    Fwd<float> f(*(const Model*)mp, n, threads < 1 ? 1 : threads);
+    f.qa = act_q;
+    f.qw = weight_q;
+    f.run(bin, glob, meta, out);
+    return 0;
+  } catch (const std::exception& e) { g_err = e.what(); return 1; }
+}
+
+// Rounds values to 16-bit operands in place (q as above).
+void kgo_round_operands(double* v, long n, int q) {
+  for (long k = 0; k < n; k++) v[k] = round_operand(v[k], q);
 }
 
 int kgo_forward_f32(const void* mp, int n, const float* bin, const float* glob, const float* meta, float* out, int threads) {

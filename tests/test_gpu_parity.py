@@ -2,8 +2,15 @@
 
 Tolerances, per output group (policy, value, score, ownership) of each row block:
 - f32: max |gpu - oracle| <= 1e-4 * max |oracle| over the group (the f32 tier's 1e-4 relative error);
-- f16: max |gpu - oracle| <= 2e-2 absolute;
-- bf16: max |gpu - oracle| <= 1e-1 absolute (8-bit mantissa operands; no reference tier exists).
+- f16: max |gpu - oracle| <= 2e-2 absolute, or, where the float16 format itself is farther than that from the
+  float64 network, within 1.5x of the format's own error: the distance of the "float16 network" (the oracle
+  evaluated with the kernels' operands rounded to float16 at the kernels' rounding points) from the float64 one;
+- bf16: the same with 1e-1 absolute (8-bit mantissa operands; no reference tier exists).
+16-bit handles are also held to that 16-bit network: max |gpu - emulation| <= 2 x the format's error
++ 1e-4 * max(1, max |oracle|). The deep synthetic nets amplify rounding: evaluating the float16 network with
+float32 instead of float64 accumulation alone moves b18c384nbt's outputs by about as much as the format error
+(1.8e-2 against 1.9e-2), so the emulation cannot pin the device closer than that; on the shallow nets it matches
+to 1e-6.
 Index work (symmetry, padding rows, batch buckets, tile scatter) is checked bit-exactly where the arithmetic
 is identical: a row's outputs must not depend on the batch it runs in.
 """
@@ -33,14 +40,30 @@ def errors(out, ref, P, S):
     return res
 
 
-def check(out, ref, P, S, prec, what):
+def check(out, ref, P, S, prec, what, ref_q=None):
+    """ref: the float64 oracle; ref_q (16-bit handles): the oracle with the same 16-bit operand rounding."""
     assert np.all(np.isfinite(out)), f"{what}: non-finite outputs"
     kind, tol = TOL[prec]
     errs = errors(out, ref, P, S)
     print(f"{what} [{prec}] " + " ".join(f"{k}: err {e:.2e} (|ref| {s:.2e})" for k, (e, s) in errs.items()))
+    fmt = {k: 0.0 for k in errs}
+    if ref_q is not None:
+        fmt = {k: e for k, (e, _) in errors(ref_q, ref, P, S).items()}
+        eq = errors(out, ref_q, P, S)
+        print(f"{what} [{prec}] vs {prec} network: " + " ".join(f"{k}: {e:.2e} (format {fmt[k]:.2e})" for k, (e, _) in eq.items()))
+        for k, (e, s) in eq.items():
+            bound = 2.0 * fmt[k] + 1e-4 * max(1.0, s)
+            assert e <= bound, f"{what} [{prec}] {k}: max |gpu - {prec} network| {e:.3e} > {bound:.3e}"
     for k, (e, s) in errs.items():
-        bound = tol * max(s, 1e-30) if kind == "rel" else tol
+        bound = tol * max(s, 1e-30) if kind == "rel" else max(tol, 1.5 * fmt[k])
         assert e <= bound, f"{what} [{prec}] {k}: max err {e:.3e} > {bound:.3e} (|ref| max {s:.3e})"
+
+
+def emulated(oracle, model_bytes, prec, spatial, glob, meta=None):
+    """The oracle with the 16-bit handle's operand rounding (None for f32)."""
+    if prec == "f32":
+        return None
+    return oracle.Model(model_bytes).forward(spatial, glob, meta, operands=prec)
 
 
 @pytest.fixture(scope="module")
@@ -50,27 +73,32 @@ def golden():
 
 @pytest.mark.parametrize("prec", ["f32", "f16", "bf16"])
 @pytest.mark.parametrize("name", ["t_res", "t_nbt", "t_v8", "t_tf", "t_human", "t_rms", "t_rmspos"])
-def test_tiny_nets_match_oracle(kgx, synth, golden, name, prec):
+def test_tiny_nets_match_oracle(kgx, synth, oracle, golden, name, prec):
     g, m0 = golden
     arch = synth.tiny_nets()[name]
-    net = kgx.Net(synth.write_model(arch, 1))
+    mb = synth.write_model(arch, 1)
+    net = kgx.Net(mb)
     h = kgx.Handle(net, 8, prec)
     meta = g[f"{name}.meta"] if f"{name}.meta" in g else None
     out = h.forward(g[f"{name}.spatial"], g[f"{name}.glob"], meta)
-    check(out, g[f"{name}.out"], net.P, net.S, prec, name)
-    out = h.forward(m0["spatial"], m0["glob"], m0["meta"] if arch.meta_encoder else None)
-    check(out, g[f"{name}.m0_out"], net.P, net.S, prec, name + " m0")
+    check(out, g[f"{name}.out"], net.P, net.S, prec, name,
+          emulated(oracle, mb, prec, g[f"{name}.spatial"], g[f"{name}.glob"], meta))
+    m0meta = m0["meta"] if arch.meta_encoder else None
+    out = h.forward(m0["spatial"], m0["glob"], m0meta)
+    check(out, g[f"{name}.m0_out"], net.P, net.S, prec, name + " m0",
+          emulated(oracle, mb, prec, m0["spatial"], m0["glob"], m0meta))
     h.close()
 
 
 @pytest.mark.parametrize("conv,prec", [("wino2", "f32"), ("wino2", "f16"), ("wino2", "bf16"), ("wino4", "f16")])
 @pytest.mark.parametrize("name", ["t_res", "t_nbt", "t_v8"])
-def test_winograd_variants_match_oracle(kgx, synth, golden, monkeypatch, name, conv, prec):
+def test_winograd_variants_match_oracle(kgx, synth, oracle, golden, monkeypatch, name, conv, prec):
     """The Winograd kernels on every precision (16-bit handles default to the implicit GEMM, float ones to
     F(4x4,3x3)); the algorithm is chosen when the handle builds its network."""
     monkeypatch.setenv("KGX_CONV", conv)
     g, _ = golden
-    net = kgx.Net(synth.write_model(synth.tiny_nets()[name], 1))
+    mb = synth.write_model(synth.tiny_nets()[name], 1)
+    net = kgx.Net(mb)
     h = kgx.Handle(net, 8, prec)
     out = h.forward(g[f"{name}.spatial"], g[f"{name}.glob"])
     if conv == "wino4" and prec != "f32":
@@ -79,6 +107,7 @@ def test_winograd_variants_match_oracle(kgx, synth, golden, monkeypatch, name, c
         errs = errors(out, g[f"{name}.out"], net.P, net.S)
         assert np.all(np.isfinite(out)) and all(e <= 6e-2 for e, _ in errs.values()), errs
     else:
+        # Winograd transforms round their transformed operands, not the activations: only the float64 bound.
         check(out, g[f"{name}.out"], net.P, net.S, prec, f"{name} {conv}")
     h.close()
 
@@ -109,7 +138,7 @@ def test_benchmark_configs_match_oracle(kgx, synth, oracle, name, prec):
     h = kgx.Handle(net, batch, prec)
     out = h.forward(sp, gl)
     ref = oracle.Model(mb).forward(sp[:n], gl[:n])
-    check(out[:n], ref, net.P, net.S, prec, name)
+    check(out[:n], ref, net.P, net.S, prec, name, emulated(oracle, mb, prec, sp[:n], gl[:n]))
     # The full batch stays finite, and a row's outputs do not depend on the rest of its batch.
     assert np.all(np.isfinite(out))
     again = h.forward(sp[:n], gl[:n])
