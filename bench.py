@@ -11,6 +11,9 @@ Prints one JSON line. Besides the throughput it carries
   with HIP events around every kernel launch on the library's stream during a second timed region of the same
   K steps (events need eager launches; the throughput region replays a HIP graph);
 - "cpu_baseline": the float32 CPU oracle on a bounded sample of the same workload, on this host's cores.
+- "roofline.traffic": HBM bytes per launch of the dominant kernel class, from the rocprofv3 FETCH_SIZE and
+  WRITE_SIZE passes recorded in profiles/traffic.json (each scaled by the same counter's reading for a device copy
+  of known size, `--copy-probe-mb`); null when no measurement for that class and workload is recorded.
 """
 
 import argparse
@@ -28,6 +31,39 @@ sys.path.insert(0, ROOT)
 
 PEAK_TFLOPS = {"f16": 2500.0, "bf16": 2500.0, "f32": 157.3}  # MI355X dense MFMA
 PEAK_HBM_GBS = 8000.0
+# The headline metric's name for the default workload; other workloads are named the same way.
+HEADLINE = "evals/s b18c384nbt fp16 batch 32 on 1 MI355X; MFMA util % + HBM GB/s %"
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+
+
+def copy_probe(mb):
+    """One device-to-device copy of `mb` MiB (a copy kernel of known size for counter calibration)."""
+    hip = ctypes.CDLL("libamdhip64.so")
+    hip.hipMalloc.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_size_t]
+    hip.hipMemcpy.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int]
+    hip.hipFree.argtypes = [ctypes.c_void_p]
+    hip.hipMemset.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_size_t]
+    n = mb << 20
+    a, b = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipMalloc(ctypes.byref(a), n) == 0 and hip.hipMalloc(ctypes.byref(b), n) == 0
+    assert hip.hipMemset(a, 1, n) == 0
+    for _ in range(3):
+        assert hip.hipMemcpy(b, a, n, 3) == 0  # hipMemcpyDeviceToDevice
+    assert hip.hipDeviceSynchronize() == 0
+    hip.hipFree(a)
+    hip.hipFree(b)
+    print(json.dumps({"copy_probe_bytes": n}))
+
+
+def recorded_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from the committed counter passes, or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            rec = json.load(f)
+    except (OSError, ValueError):
+        return None
+    e = rec.get(workload, {}).get(kernel)
+    return None if e is None else e.get("bytes_per_launch")
 
 
 def main():
@@ -38,10 +74,16 @@ def main():
     ap.add_argument("--config", default="b18c384nbt")
     ap.add_argument("--precision", default="f16", choices=["f16", "bf16", "f32"])
     ap.add_argument("--batch", type=int, default=0, help="override the config's batch size")
-    ap.add_argument("--cpu-rows", type=int, default=4, help="rows in the CPU-baseline sample (0: skip)")
+    ap.add_argument("--cpu-rows", type=int, default=-1,
+                    help="rows in the CPU-baseline sample (-1: the whole batch, 0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="CPU-baseline threads (0: min(16, cores))")
-    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="only run a device copy of this many MiB (counter calibration) and exit")
     args = ap.parse_args()
+
+    if args.copy_probe_mb:
+        copy_probe(args.copy_probe_mb)
+        return
 
     if args.gpus != 1:
         print(json.dumps({"error": "this path runs on one GPU; the forward pass shards by independent batches "
@@ -58,8 +100,6 @@ def main():
     model = synth.write_model(arch, synth.CONFIG_SEEDS[args.config])
     net = kgx.Net(model)
     h = kgx.Handle(net, batch, args.precision, device=0)
-    if args.no_graph:
-        kgx.lib()  # graphs are on by default; eager launches only with profiling
     sp, gl, me = synth.make_inputs(batch, 1234, meta=arch.meta_encoder)
 
     # Inputs resident in HBM: copy them into the handle's device buffers once.
@@ -128,7 +168,12 @@ def main():
                 "work_per_launch": dv["bytes"] / max(dv["launches"], 1), "avg_launch_us": per_launch_ms * 1e3}
     h.close()
 
+    workload = f"{args.config} {args.precision} batch {batch}"
+    roof["traffic"] = recorded_traffic(dname, workload)
+
     cpu = None
+    if args.cpu_rows < 0:
+        args.cpu_rows = batch
     if args.cpu_rows > 0:
         import oracle
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
@@ -143,7 +188,9 @@ def main():
                          f"{cdt:.1f} s"}
 
     res = {
-        "metric": f"evals/s {args.config} {args.precision} batch {batch} on 1 MI355X",
+        "metric": HEADLINE if (args.config, args.precision, batch) == ("b18c384nbt", "f16", 32) else
+                  f"evals/s {args.config} {'fp16' if args.precision == 'f16' else args.precision} batch {batch} "
+                  "on 1 MI355X; MFMA util % + HBM GB/s %",
         "value": evals_per_s,
         "unit": "evals/s",
         "n_gpus": 1,
