@@ -172,3 +172,29 @@ def test_model_file_variants_parse_alike(oracle, synth):
     a = oracle.Model(mb).forward(sp, gl, me)
     assert np.array_equal(a, oracle.Model(txt).forward(sp, gl, me))
     assert np.array_equal(a, oracle.Model(gzip.compress(mb)).forward(sp, gl, me))
+
+
+def test_operand_rounding_matches_float16_and_bfloat16(oracle):
+    """The 16-bit operand emulation rounds like numpy's float16 and like a float32 -> bfloat16 conversion."""
+    import torch
+    rng = np.random.default_rng(0)
+    x = rng.normal(size=100000) * np.exp(rng.uniform(-20, 12, 100000))
+    x[:5] = [0.0, -0.0, 65504.0, 65520.0, 2.0 ** -25]  # max, overflow to inf, half the smallest subnormal
+    with np.errstate(over="ignore"):
+        want = x.astype(np.float16).astype(np.float64)
+    got = oracle.round_operands(x, "f16")
+    assert np.array_equal(got, want)
+    # bfloat16 from float32 values (the device rounds float32): exact.
+    x32 = x.astype(np.float32).astype(np.float64)
+    want_bf = torch.tensor(x32, dtype=torch.float32).to(torch.bfloat16).double().numpy()
+    assert np.array_equal(oracle.round_operands(x32, "bf16"), want_bf)
+
+
+def test_operand_emulation_without_rounding_is_the_float64_forward(oracle, synth):
+    mb = synth.write_model(synth.tiny_nets()["t_nbt"], 1)
+    sp, gl, _ = synth.make_inputs(2, 3)
+    m = oracle.Model(mb)
+    ref = m.forward(sp, gl)
+    assert np.array_equal(m.forward(sp, gl, operands="f16", acts=False, weights=False), ref)
+    q = m.forward(sp, gl, operands="f16")
+    assert 0 < np.abs(q - ref).max() < 2e-2
