@@ -9,16 +9,20 @@
 //
 // A workgroup computes BM consecutive pixels x BN output channels. Per K stage (BK input channels) it stages in LDS
 // the pixel rows [m0 - HALO, m0 + BM + HALO) (HALO = 20 covers every 3x3 neighbour) and the stage's weights of all
-// taps; each wave then runs TAPS x (BK / 32) MFMA steps over the staged data, reading the A fragment of tap t from
+// taps (packed per N tile, [tile][tap][BN][icp], so a tile's weights are one contiguous block); each wave then
+// runs TAPS x (BK / 32) MFMA steps over the staged data, reading the A fragment of tap t from
 // the LDS row shifted by shift(t) and zeroing rows whose neighbour is off the board. The next stage's global loads
 // are in flight in registers during the MFMAs. The epilogue goes through LDS so that every thread finishes four
 // consecutive channels of one pixel with 16-byte loads and stores (conv_store4).
 #include "kgx_device.h"
 
+#include <vector>
+
 namespace kgx {
 
-template <int KS_, int BM_, int BN_, int BK_, int WM_, int WN_, int G_, int NBUF_>
+template <int KS_, int BM_, int BN_, int BK_, int WM_, int WN_, int G_, int NBUF_, bool INTERLEAVE_ = false>
 struct IgCfg {
+  static constexpr bool INTERLEAVE = INTERLEAVE_;  // MFMA / LDS-read interleaving hints for the scheduler
   static constexpr int KS = KS_, TAPS = KS_ * KS_, HALO = KS_ == 3 ? POS + 1 : 0;
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
   static constexpr int G = G_;                  // wave groups splitting the taps (partial sums added in LDS)
@@ -60,10 +64,10 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
   constexpr int LDK = BK + 8;                 // LDS row stride in elements (16-byte pad)
   constexpr int KV = BK / 8;                  // 16-byte vectors per staged row
   constexpr int AR = BM + 2 * HALO;           // staged pixel rows
-  constexpr int AVT = AR * KV, BVT = TAPS * BN * KV;
-  constexpr int AV = (AVT + NT - 1) / NT, BV = (BVT + NT - 1) / NT;
+  constexpr int RP = NT / KV;                 // staged rows per pass of all threads
+  constexpr int AV = (AR + RP - 1) / RP, BV = (TAPS * BN + RP - 1) / RP;
   constexpr int WTM = BM / WM, WTN = BN / WN, MB = WTM / 16, NB = WTN / 16;
-  static_assert(WTM % 16 == 0 && WTN % 16 == 0 && BK % 32 == 0 && AV <= 32 && BV <= 32, "bad tile");
+  static_assert(WTM % 16 == 0 && WTN % 16 == 0 && BK % 32 == 0 && NT % KV == 0, "bad tile");
   constexpr int STAGE = (AR + 1 + TAPS * BN) * LDK * 2;   // bytes (A rows, a zero row, B rows)
   constexpr int EPI = BM * (BN + 4) * 4;              // bytes
   constexpr int NBUF = C::NBUF;
@@ -80,31 +84,11 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
   const int r16 = lane & 15, g4 = lane >> 4;
 
-  // Staged-vector bookkeeping (thread-invariant): A row / vector, B (tap, row) / vector.
-  int a_goff[AV], a_soff[AV], b_goff[BV], b_soff[BV];
-  unsigned a_ok = 0, b_ok = 0;  // bit v: vector v is live (in the stage and in bounds)
-  int a_k[AV];
-#pragma unroll
-  for (int v = 0; v < AV; v++) {
-    const int idx = tid + NT * v;
-    const int r = idx / KV, kv = idx - r * KV;
-    const int gr = m0 - HALO + r;
-    const bool live = idx < AVT && gr >= 0 && gr < M;
-    a_goff[v] = live ? gr * ldx + kv * 8 : 0;
-    a_soff[v] = idx < AVT ? r * LDK + kv * 8 : 0;
-    a_k[v] = kv * 8;
-    if (live) a_ok |= 1u << v;
-  }
-#pragma unroll
-  for (int v = 0; v < BV; v++) {
-    const int idx = tid + NT * v;
-    const int tr = idx / KV, kv = idx - tr * KV;  // tr = tap * BN + row
-    const int t = tr / BN, row = tr - t * BN;
-    const bool live = idx < BVT && n0 + row < OC;
-    b_goff[v] = live ? ((t * OC + n0 + row) * icp + kv * 8) : 0;
-    b_soff[v] = idx < BVT ? tr * LDK + kv * 8 : 0;
-    if (live) b_ok |= 1u << v;
-  }
+  // Staging: thread tid moves the 16-byte vector kv of rows r0, r0 + RP, r0 + 2 RP, ... of the stage's A rows
+  // (pixels m0 - HALO + r) and B rows (tap * BN + output channel of this N tile, contiguous in the packed
+  // weights), so every address is a base plus a multiple of a uniform stride.
+  const int r0 = tid / KV, kv8 = (tid % KV) * 8;
+  const T* wb = W + ((size_t)blockIdx.x * TAPS * BN + r0) * icp + kv8;
 
   // Tap validity of this lane's A rows: bit t of vmask[i] is set when row m's neighbour at tap t is on the board.
   unsigned vmask[MB];
@@ -127,21 +111,25 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
   auto load = [&](int k0) {
 #pragma unroll
     for (int v = 0; v < AV; v++) {
-      const bool ok = ((a_ok >> v) & 1) && k0 + a_k[v] < IC;
-      ra[v] = ok ? *(const vec_t*)(X + a_goff[v] + k0) : vec_t{0, 0, 0, 0};
+      const int gr = m0 - HALO + r0 + v * RP;
+      const bool ok = (AR % RP == 0 || r0 + v * RP < AR) && gr >= 0 && gr < M && k0 + kv8 < IC;
+      ra[v] = ok ? *(const vec_t*)(X + (size_t)gr * ldx + kv8 + k0) : vec_t{0, 0, 0, 0};
     }
 #pragma unroll
-    for (int v = 0; v < BV; v++) rb[v] = ((b_ok >> v) & 1) ? *(const vec_t*)(W + b_goff[v] + k0) : vec_t{0, 0, 0, 0};
+    for (int v = 0; v < BV; v++) {
+      const bool ok = (TAPS * BN) % RP == 0 || r0 + v * RP < TAPS * BN;
+      rb[v] = ok ? *(const vec_t*)(wb + (size_t)v * RP * icp + k0) : vec_t{0, 0, 0, 0};
+    }
   };
   auto store = [&](int buf) {
-    T* ab = As + buf * SE;
-    T* bb = Bs + buf * SE;
+    T* ab = As + buf * SE + r0 * LDK + kv8;
+    T* bb = Bs + buf * SE + r0 * LDK + kv8;
 #pragma unroll
     for (int v = 0; v < AV; v++)
-      if (AVT % NT == 0 || tid + NT * v < AVT) *(vec_t*)(ab + a_soff[v]) = ra[v];
+      if (AR % RP == 0 || r0 + v * RP < AR) *(vec_t*)(ab + v * RP * LDK) = ra[v];
 #pragma unroll
     for (int v = 0; v < BV; v++)
-      if (BVT % NT == 0 || tid + NT * v < BVT) *(vec_t*)(bb + b_soff[v]) = rb[v];
+      if ((TAPS * BN) % RP == 0 || r0 + v * RP < TAPS * BN) *(vec_t*)(bb + v * RP * LDK) = rb[v];
   };
 
   floatx4 acc[MB][NB];
@@ -182,6 +170,14 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
           else
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s & 1][i], b[s & 1][j], acc[i][j], 0, 0, 0);
         }
+      if constexpr (C::INTERLEAVE) {
+        // Scheduling hint: alternate this step's MFMAs with the next step's LDS fragment reads.
+#pragma unroll
+        for (int k = 0; k < MB * NB; k++) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+          if (s + 1 < S && k < MB + NB) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+        }
+      }
     }
   };
 
@@ -276,6 +272,17 @@ static void igemm_launch(const void* x, int ldx, int IC, const void* w, int icp,
 }
 
 int conv_igemm_icp(int ks, int ic) { return round_up(ic, ks == 3 ? Ig3::BK : Ig1::BK); }
+
+// w [oc][ic][ks][ks] -> [oc tile][tap][BN][icp], zero padding beyond oc and ic.
+void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector<float>& out) {
+  const int bn = ks == 3 ? Ig3::BN : Ig1::BN, taps = ks * ks, icp = conv_igemm_icp(ks, ic);
+  const int tiles = (oc + bn - 1) / bn;
+  out.assign((size_t)tiles * taps * bn * icp, 0.f);
+  for (int o = 0; o < oc; o++)
+    for (int t = 0; t < taps; t++)
+      for (int i = 0; i < ic; i++)
+        out[(((size_t)(o / bn) * taps + t) * bn + o % bn) * icp + i] = w[((size_t)o * ic + i) * taps + t];
+}
 
 void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const void* w, int icp, int OC,
                        const ConvOut& o, int B, hipStream_t s) {

@@ -179,10 +179,12 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
       xin = packed;
     }
     const int icp = conv_igemm_icp(ks, icin), taps = ks * ks;
-    std::vector<float> w((size_t)taps * oc * icp, 0.f);  // [tap][oc][icp]
-    for (int t = 0; t < taps; t++)
-      for (int oo = 0; oo < oc; oo++)
-        for (int i = 0; i < ic; i++) w[((size_t)t * oc + oo) * icp + i] = c.w[((size_t)oo * ic + i) * taps + t];
+    // Filters over the (zero-padded) input channels icin, then packed per output tile.
+    std::vector<float> wi((size_t)oc * icin * taps, 0.f), w;
+    for (int oo = 0; oo < oc; oo++)
+      for (int i = 0; i < ic; i++)
+        for (int t = 0; t < taps; t++) wi[((size_t)oo * icin + i) * taps + t] = c.w[((size_t)oo * ic + i) * taps + t];
+    conv_igemm_pack_weights(ks, wi.data(), oc, icin, w);
     const void* dW = upload_t(w);
     Op op;
     op.launch = [=](hipStream_t s, int B) { launch_conv_igemm(prec, ks, xin, ldin, icin, dW, icp, oc, *out, B, s); };
