@@ -69,7 +69,7 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
   constexpr int WTM = BM / WM, WTN = BN / WN, MB = WTM / 16, NB = WTN / 16;
   static_assert(WTM % 16 == 0 && WTN % 16 == 0 && BK % 32 == 0 && NT % KV == 0, "bad tile");
   constexpr int STAGE = (AR + 1 + TAPS * BN) * LDK * 2;   // bytes (A rows, a zero row, B rows)
-  constexpr int EPI = BM * (BN + 4) * 4;              // bytes
+  constexpr int EPI = C::G * BM * (BN + 4) * 4;       // bytes: one float tile per wave group
   constexpr int NBUF = C::NBUF;
   constexpr int SE = STAGE / (int)sizeof(T);          // stage buffer size in elements
   __shared__ __align__(16) char smem[NBUF * STAGE > EPI ? NBUF * STAGE : EPI];
@@ -81,14 +81,20 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = wave / (WM * WN), wl = wave - grp * (WM * WN);
   const int wm = wl / WN, wn = wl % WN;
-  const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
+  // XCD-aware tile order: workgroup g runs on XCD g % 8, so the NTL output tiles of one pixel tile are given the
+  // ids g, g + 8, ... of one XCD: they share its L2 for the pixel rows they all read, and their halves of the
+  // cache lines they write meet in the same L2. Ids beyond the last pixel tile (grid rounded to 8) exit.
+  const int g = blockIdx.x, ntl = (OC + BN - 1) / BN;
+  const int slot = g >> 3, mt = (slot / ntl) * 8 + (g & 7), nt = slot % ntl;
+  if (mt * BM >= M) return;
+  const int n0 = nt * BN, m0 = mt * BM;
   const int r16 = lane & 15, g4 = lane >> 4;
 
   // Staging: thread tid moves the 16-byte vector kv of rows r0, r0 + RP, r0 + 2 RP, ... of the stage's A rows
   // (pixels m0 - HALO + r) and B rows (tap * BN + output channel of this N tile, contiguous in the packed
   // weights), so every address is a base plus a multiple of a uniform stride.
   const int r0 = tid / KV, kv8 = (tid % KV) * 8;
-  const T* wb = W + ((size_t)blockIdx.x * TAPS * BN + r0) * icp + kv8;
+  const T* wb = W + ((size_t)nt * TAPS * BN + r0) * icp + kv8;
 
   // Tap validity of this lane's A rows: bit t of vmask[i] is set when row m's neighbour at tap t is on the board.
   unsigned vmask[MB];
@@ -228,46 +234,45 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
     }
   }
 
-  // Accumulators to LDS as a float [BM][BN + 4] tile (group 0 stores, group 1 adds): element (i, j, r) is row
-  // wm*WTM + i*16 + 4*(lane/16) + r, column wn*WTN + j*16 + lane%16.
-  static_assert(G == 1 || G == 2, "one or two wave groups");
-  float* Cs = (float*)smem;
+  // Accumulators to LDS, one float [BM][BN + 4] tile per wave group, summed per output vector: element (i, j, r)
+  // is row wm*WTM + i*16 + 4*(lane/16) + r, column wn*WTN + j*16 + lane%16.
   constexpr int LDC = BN + 4;
+  float* Cs = (float*)smem;
+  float* Cg = Cs + grp * BM * LDC;
 #pragma unroll
-  for (int q = 0; q < G; q++) {
-    if (grp == q) {
+  for (int i = 0; i < MB; i++)
 #pragma unroll
-      for (int i = 0; i < MB; i++)
+    for (int j = 0; j < NB; j++)
 #pragma unroll
-        for (int j = 0; j < NB; j++)
-#pragma unroll
-          for (int r = 0; r < 4; r++) {
-            float* c = Cs + (wm * WTM + i * 16 + 4 * g4 + r) * LDC + wn * WTN + j * 16 + r16;
-            *c = q == 0 ? acc[i][j][r] : *c + acc[i][j][r];
-          }
-    }
-    __syncthreads();
-  }
+      for (int r = 0; r < 4; r++) Cg[(wm * WTM + i * 16 + 4 * g4 + r) * LDC + wn * WTN + j * 16 + r16] = acc[i][j][r];
+  __syncthreads();
 #pragma unroll
   for (int e = 0; e < EV; e++) {
     const int v = tid + e * NT;
     const int row = v / (BN / 4), c4 = v - row * (BN / 4);
     const int m = m0 + row, n = n0 + 4 * c4;
-    if (v < NV && m < M && n < OC)
-      conv_store4<T>(o, m, n, *(const floatx4*)(Cs + row * LDC + 4 * c4), yprefetch, yres[e]);
+    if (v < NV && m < M && n < OC) {
+      floatx4 sum = *(const floatx4*)(Cs + row * LDC + 4 * c4);
+#pragma unroll
+      for (int q = 1; q < G; q++) sum += *(const floatx4*)(Cs + q * BM * LDC + row * LDC + 4 * c4);
+      conv_store4<T>(o, m, n, sum, yprefetch, yres[e]);
+    }
   }
 }
 
-// Configurations (measured at batch 32, 192 channels): 3x3 with 96x96 tiles, 64 channels per stage and two wave
-// groups of 2x2 waves (48x48 each) splitting the taps; 1x1 with 64x64 tiles, two groups and two stage buffers.
-typedef IgCfg<3, 96, 96, 64, 2, 2, 2, 1> Ig3;
+// Configurations (measured at batch 32, 192 channels): 3x3 with 192 pixels x 48 channels per workgroup (a
+// quarter of the weights per workgroup: weight staging is what bounds this kernel), 64 channels per stage and two
+// wave groups of 4x1 waves (48x48 each) splitting the taps; 1x1 with 64x64 tiles, two groups and two stage
+// buffers.
+typedef IgCfg<3, 192, 48, 64, 4, 1, 2, 1> Ig3;
 typedef IgCfg<1, 64, 64, 64, 2, 2, 2, 2> Ig1;
 
 template <typename T, typename C>
 static void igemm_launch(const void* x, int ldx, int IC, const void* w, int icp, int OC, const ConvOut& o, int M,
                          hipStream_t s) {
   if (icp % C::BK != 0) throw std::runtime_error("conv_igemm: padded input channels must be a multiple of the stage");
-  dim3 grid((OC + C::BN - 1) / C::BN, (M + C::BM - 1) / C::BM);
+  const int mtiles = (M + C::BM - 1) / C::BM, ntiles = (OC + C::BN - 1) / C::BN;
+  dim3 grid(round_up(mtiles, 8) * ntiles);
   igemm_kernel<T, C><<<grid, C::NT, 0, s>>>((const T*)x, ldx, IC, (const T*)w, icp, OC, M, o);
 }
 
