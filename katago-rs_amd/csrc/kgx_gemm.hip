@@ -172,10 +172,12 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
 }
 
 // Tile configurations: narrow rows over all of a <= 192-wide N (1x1 convolutions, Winograd point GEMMs: the
-// prologue runs once per element), 128x128 for wide GEMMs (transformer linears), 64x64 for the rest.
+// prologue runs once per element), 64x96 for 65..96 columns (the heads), 128x128 for wide GEMMs (transformer
+// linears), 64x64 for the rest.
 typedef Cfg<32, 192, 64, 1, 4> CfgNarrow;
 typedef Cfg<128, 128, 64, 2, 2> CfgWide;
 typedef Cfg<64, 64, 32, 2, 2> CfgSmall;
+typedef Cfg<64, 96, 64, 2, 2> CfgHead;  // the heads' first convolutions: N = p1 + g1 + v1 channels <= 96
 
 template <typename T, typename C, bool AF, bool PRO, int ACT>
 static void gemm_launch(const GemmArgs& g, hipStream_t s) {
@@ -186,7 +188,8 @@ static void gemm_launch(const GemmArgs& g, hipStream_t s) {
 template <typename T, bool AF, bool PRO, int ACT>
 static void gemm_cfg(const GemmArgs& g, hipStream_t s) {
   const int bkh = 64, bk = sizeof(T) == 2 ? bkh : bkh / 2;
-  if (g.N > 128 && g.N <= 192 && g.K % bk == 0) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
+  if (g.N > 64 && g.N <= 96 && g.K % bk == 0) gemm_launch<T, CfgHead, AF, PRO, ACT>(g, s);
+  else if (g.N > 128 && g.N <= 192 && g.K % bk == 0) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
   else if (g.N > 192 && g.N <= 384 && g.K % bk == 0 && AF) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
   else if (g.N > 128 && g.K % bk == 0 && (long)((g.M + 127) / 128) * ((g.N + 127) / 128) * g.Z >= 256)
     gemm_launch<T, CfgWide, AF, PRO, ACT>(g, s);

@@ -262,10 +262,11 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
 
 // Configurations (measured at batch 32, 192 channels): 3x3 with 192 pixels x 48 channels per workgroup (a
 // quarter of the weights per workgroup: weight staging is what bounds this kernel), 64 channels per stage and two
-// wave groups of 4x1 waves (48x48 each) splitting the taps; 1x1 with 64x64 tiles, two groups and two stage
-// buffers.
+// wave groups of 4x1 waves (48x48 each) splitting the taps; 1x1 on the same 192-pixel tiles with two stage
+// buffers. Equal pixel tiles give every convolution the same tile -> XCD mapping, so a layer reads the
+// activations its producer wrote from the same XCD's L2.
 typedef IgCfg<3, 192, 48, 64, 4, 1, 2, 1> Ig3;
-typedef IgCfg<1, 64, 64, 64, 2, 2, 2, 2> Ig1;
+typedef IgCfg<1, 192, 48, 64, 4, 1, 2, 2> Ig1;
 
 template <typename T, typename C>
 static void igemm_launch(const void* x, int ldx, int IC, const void* w, int icp, int OC, const ConvOut& o, int M,

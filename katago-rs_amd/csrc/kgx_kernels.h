@@ -113,6 +113,32 @@ void launch_pool(const float* x, int ldx, int coff, int C, const Prologue& pro, 
 void launch_small_matmul(const float* in, int ldin, int IC, const float* W, int OC, const float* bias, int act,
                          float* out, long ldout, int ostride, bool accumulate, int B, hipStream_t s);
 
+// Per-row work of one batch row in one workgroup: up to two board poolings (as launch_pool) into LDS features, then
+// up to eight small matmuls chained through LDS (out = act(in W + bias), written to LDS and/or to a global row with
+// a stride, optionally accumulated). Replaces a pooling launch plus a launch per matmul.
+struct RowPool {
+  const float* x = nullptr; int ldx = 0, coff = 0, C = 0;
+  const float* scale = nullptr; const float* bias = nullptr; int act = ACT_ID;  // prologue (scale null: none)
+  bool value = false;
+  int dst = 0;  // LDS float offset of the 3C features
+};
+struct RowMM {
+  const float* gin = nullptr; int ldgin = 0;  // input row from global memory (row stride), else from LDS
+  int src = 0;                                // LDS float offset of the input
+  int IC = 0, OC = 0;
+  const float* W = nullptr;                   // [IC][OC]
+  const float* bias = nullptr; int act = ACT_ID;
+  int dst = -1;                               // LDS float offset of the output, or -1
+  float* out = nullptr; long ldout = 0; int ostride = 1; bool accumulate = false;
+};
+struct RowProg {
+  RowPool pool[2]; int npool = 0;
+  RowMM mm[8]; int nmm = 0;
+  int lds_floats = 0;  // LDS features and intermediates
+  const float* mask = nullptr; const float* area = nullptr; const float* s1 = nullptr; const float* s2 = nullptr;
+};
+void launch_row_prog(const RowProg& p, int B, hipStream_t s);
+
 // Per board point: the policy conv p2 over act(BN(p1 + gpool bias)) * mask, and the ownership conv over
 // act(BN(v1)) * mask, written into the readback rows.
 struct HeadSpatialArgs {

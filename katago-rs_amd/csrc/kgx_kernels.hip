@@ -106,54 +106,184 @@ void launch_pool(const float* x, int ldx, int coff, int C, const Prologue& pro, 
 // ---------------------------------------------------------------------------------------------------------
 // Small matmuls (global inputs, pooled features, value head)
 // ---------------------------------------------------------------------------------------------------------
-// One batch row per workgroup: the row is staged in LDS, each thread owns one output and keeps four
-// independent partial sums so that the weight loads of consecutive inputs are in flight together.
+// A workgroup computes 64 outputs for 8 batch rows: the rows are staged in LDS, the 4 waves take every fourth
+// input (so each thread has many independent weight loads in flight, coalesced across the wave's 64 outputs) and
+// their partial sums meet in LDS. Latency, not arithmetic, bounds these products; the split keeps each thread's
+// dependent chain short.
 
 template <int ACT>
 __global__ __launch_bounds__(256) void small_mm_kernel(const float* __restrict__ in, int ldin, int IC,
                                                        const float* __restrict__ W, int OC, const float* __restrict__ bias,
-                                                       float* __restrict__ out, long ldout, int ostride, int accumulate) {
-  extern __shared__ float xs[];
-  const int b = blockIdx.y, tid = threadIdx.x;
-  for (int i = tid; i < IC; i += 256) xs[i] = in[(size_t)b * ldin + i];
-  __syncthreads();
-  const int o = blockIdx.x * 256 + tid;
-  if (o >= OC) return;
-  float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
-  int i = 0;
-  for (; i + 4 <= IC; i += 4) {
-    a0 += xs[i] * W[(size_t)i * OC + o];
-    a1 += xs[i + 1] * W[(size_t)(i + 1) * OC + o];
-    a2 += xs[i + 2] * W[(size_t)(i + 2) * OC + o];
-    a3 += xs[i + 3] * W[(size_t)(i + 3) * OC + o];
+                                                       float* __restrict__ out, long ldout, int ostride, int accumulate,
+                                                       int B) {
+  extern __shared__ float xs[];  // [8][IC], then [4][8][64] partial sums
+  const int tid = threadIdx.x, lane = tid & 63, kg = tid >> 6;
+  const int o = blockIdx.x * 64 + lane, b0 = blockIdx.y * 8;
+  const int nb = min(8, B - b0);
+  for (int e = tid; e < 8 * IC; e += 256) {
+    const int r = e / IC, i = e - r * IC;
+    xs[e] = r < nb ? in[(size_t)(b0 + r) * ldin + i] : 0.f;
   }
-  for (; i < IC; i++) a0 += xs[i] * W[(size_t)i * OC + o];
-  float acc = (a0 + a1) + (a2 + a3);
-  if (bias) acc += bias[o];
-  acc = act_f<ACT>(acc);
-  float* p = out + (size_t)b * ldout + (size_t)o * ostride;
-  *p = accumulate ? *p + acc : acc;
+  __syncthreads();
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (o < OC) {
+#pragma unroll 8
+    for (int i = kg; i < IC; i += 4) {
+      const float w = W[(size_t)i * OC + o];
+#pragma unroll
+      for (int r = 0; r < 8; r++) acc[r] += xs[r * IC + i] * w;
+    }
+  }
+  float* ps = xs + 8 * IC;
+#pragma unroll
+  for (int r = 0; r < 8; r++) ps[(kg * 8 + r) * 64 + lane] = acc[r];
+  __syncthreads();
+  for (int e = tid; e < 8 * 64; e += 256) {
+    const int r = e >> 6, c = e & 63, oo = blockIdx.x * 64 + c;
+    if (r >= nb || oo >= OC) continue;
+    float v = (ps[(0 * 8 + r) * 64 + c] + ps[(1 * 8 + r) * 64 + c]) + (ps[(2 * 8 + r) * 64 + c] + ps[(3 * 8 + r) * 64 + c]);
+    if (bias) v += bias[oo];
+    v = act_f<ACT>(v);
+    float* p = out + (size_t)(b0 + r) * ldout + (size_t)oo * ostride;
+    *p = accumulate ? *p + v : v;
+  }
 }
 
 void launch_small_matmul(const float* in, int ldin, int IC, const float* W, int OC, const float* bias, int act,
                          float* out, long ldout, int ostride, bool accumulate, int B, hipStream_t s) {
-  if (IC > 16384) throw std::runtime_error("small_matmul: input too wide");
-  dim3 grid((OC + 255) / 256, B);
-  const size_t lds = (size_t)IC * sizeof(float);
+  if (IC > 4096) throw std::runtime_error("small_matmul: input too wide");
+  dim3 grid((OC + 63) / 64, (B + 7) / 8);
+  const size_t lds = ((size_t)8 * IC + 4 * 8 * 64) * sizeof(float);
   const int a = accumulate ? 1 : 0;
   switch (act) {
-    case ACT_RELU: small_mm_kernel<ACT_RELU><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a); break;
-    case ACT_MISH: small_mm_kernel<ACT_MISH><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a); break;
-    case ACT_SILU: small_mm_kernel<ACT_SILU><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a); break;
-    default: small_mm_kernel<ACT_ID><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a); break;
+    case ACT_RELU: small_mm_kernel<ACT_RELU><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
+    case ACT_MISH: small_mm_kernel<ACT_MISH><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
+    case ACT_SILU: small_mm_kernel<ACT_SILU><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
+    default: small_mm_kernel<ACT_ID><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
   }
+  KGX_CHECK_LAUNCH();
+}
+
+// ---------------------------------------------------------------------------------------------------------
+// Row programs: pooling and small matmuls of one batch row in one workgroup
+// ---------------------------------------------------------------------------------------------------------
+// The row's work is a few hundred KB of reads and tens of thousands of multiply-adds: latency, not bandwidth or
+// arithmetic, bounds it, so one launch does all of it with 1024 threads, each keeping its loads independent.
+// Pooling: 64 channels x 16 groups of board points (the row's mask staged in LDS first), partial sums and maxima
+// meeting in LDS (the pooling of launch_pool). Matmul: per chunk of 64 outputs, 16 K slices of the inputs per
+// output (weight loads coalesced across the 64 outputs), partial sums meeting in LDS.
+constexpr int RP_NT = 1024, RP_KS = RP_NT / 64;
+
+__device__ void row_pool(const RowProg& P, const RowPool& q, int b, float* feat, float* red, const float* mk) {
+  const int tid = threadIdx.x, lane = tid & 63, grp = tid >> 6;
+  const float* xb = q.x + (size_t)b * HW * q.ldx + q.coff;
+  for (int c0 = 0; c0 < q.C; c0 += 64) {
+    const int c = c0 + lane;
+    float sum = 0.f, mx = -FLT_MAX;
+    if (c < q.C) {
+      const float sc = q.scale ? q.scale[c] : 1.f, bi = q.scale ? q.bias[c] : 0.f;
+      constexpr int NPG = (HW + RP_KS - 1) / RP_KS, CH = 8;  // board points per group, loads in flight
+      for (int k0 = 0; k0 < NPG; k0 += CH) {
+        float v[CH];
+#pragma unroll
+        for (int k = 0; k < CH; k++) {
+          const int p = grp + RP_KS * (k0 + k);
+          v[k] = p < HW ? xb[(size_t)p * q.ldx + c] : 0.f;
+        }
+#pragma unroll
+        for (int k = 0; k < CH; k++) {
+          const int p = grp + RP_KS * (k0 + k);
+          if (p < HW) {
+            float x = v[k];
+            if (q.scale) x = act_rt(x * sc + bi, q.act) * mk[p];
+            sum += x;
+            mx = fmaxf(mx, x + (mk[p] * 1e4f - 1e4f));
+          }
+        }
+      }
+    }
+    red[grp * 64 + lane] = sum;
+    red[RP_NT + grp * 64 + lane] = mx;
+    __syncthreads();
+    if (grp == 0 && c < q.C) {
+      float s = 0.f, m = -FLT_MAX;
+#pragma unroll
+      for (int k = 0; k < RP_KS; k++) {
+        s += red[k * 64 + lane];
+        m = fmaxf(m, red[RP_NT + k * 64 + lane]);
+      }
+      const float mean = s / P.area[b];
+      feat[c] = mean;
+      feat[q.C + c] = mean * P.s1[b];
+      feat[2 * q.C + c] = q.value ? mean * P.s2[b] : m;
+    }
+    __syncthreads();
+  }
+}
+
+__device__ void row_mm(const RowMM& m, int b, float* lds, float* red) {
+  const int tid = threadIdx.x, lane = tid & 63, ks = tid >> 6;
+  const float* in = m.gin ? nullptr : lds + m.src;
+  for (int o0 = 0; o0 < m.OC; o0 += 64) {
+    const int o = o0 + lane;
+    float acc = 0.f;
+    if (o < m.OC) {
+      const float* wcol = m.W + o;
+      float a0 = 0.f, a1 = 0.f;
+      int i = ks;
+#pragma unroll 4
+      for (; i + RP_KS < m.IC; i += 2 * RP_KS) {
+        const float w0 = wcol[(size_t)i * m.OC], w1 = wcol[(size_t)(i + RP_KS) * m.OC];
+        const float x0 = m.gin ? m.gin[(size_t)b * m.ldgin + i] : in[i];
+        const float x1 = m.gin ? m.gin[(size_t)b * m.ldgin + i + RP_KS] : in[i + RP_KS];
+        a0 += x0 * w0;
+        a1 += x1 * w1;
+      }
+      if (i < m.IC) a0 += (m.gin ? m.gin[(size_t)b * m.ldgin + i] : in[i]) * wcol[(size_t)i * m.OC];
+      acc = a0 + a1;
+    }
+    red[ks * 64 + lane] = acc;
+    __syncthreads();
+    if (ks == 0 && o < m.OC) {
+      float v = 0.f;
+#pragma unroll
+      for (int k = 0; k < RP_KS; k++) v += red[k * 64 + lane];
+      if (m.bias) v += m.bias[o];
+      v = act_rt(v, m.act);
+      if (m.dst >= 0) lds[m.dst + o] = v;
+      if (m.out) {
+        float* p = m.out + (size_t)b * m.ldout + (size_t)o * m.ostride;
+        *p = m.accumulate ? *p + v : v;
+      }
+    }
+    __syncthreads();
+  }
+}
+
+__global__ __launch_bounds__(RP_NT) void row_prog_kernel(RowProg P) {
+  // [lds_floats] features and intermediates, [2 RP_NT] reduction scratch, [HW] the row's board mask
+  extern __shared__ float lds[];
+  float* red = lds + P.lds_floats;
+  float* mk = red + 2 * RP_NT;
+  const int b = blockIdx.x;
+  for (int p = threadIdx.x; p < HW; p += RP_NT) mk[p] = P.mask[(size_t)b * HW + p];
+  __syncthreads();
+  for (int k = 0; k < P.npool; k++) row_pool(P, P.pool[k], b, lds + P.pool[k].dst, red, mk);
+  for (int k = 0; k < P.nmm; k++) row_mm(P.mm[k], b, lds, red);
+}
+
+void launch_row_prog(const RowProg& p, int B, hipStream_t s) {
+  const size_t lds = ((size_t)p.lds_floats + 2 * RP_NT + HW) * sizeof(float);
+  if (lds > 64 * 1024) throw std::runtime_error("row program: too much LDS");
+  row_prog_kernel<<<B, RP_NT, lds, s>>>(p);
   KGX_CHECK_LAUNCH();
 }
 
 // ---------------------------------------------------------------------------------------------------------
 // Head: policy p2 conv and ownership conv per board point, written into the readback rows
 // ---------------------------------------------------------------------------------------------------------
-// 64 board points per workgroup; their rows of H are staged in LDS with coalesced loads first.
+// 64 board points per workgroup; their rows of H are staged in LDS with coalesced loads first, and so are the
+// per-channel parameters (this row's gpool bias, batch norms, p2 and ownership weights), which every thread reads.
 
 template <int PACT, int VACT>
 __global__ __launch_bounds__(64) void head_spatial_kernel(HeadSpatialArgs a) {
@@ -162,6 +292,24 @@ __global__ __launch_bounds__(64) void head_spatial_kernel(HeadSpatialArgs a) {
   const int np = min(64, HW - p0);
   const float* src = a.H + ((size_t)b * HW + p0) * a.ldh;
   for (int e = tid; e < np * a.ldh; e += 64) hs[e] = src[e];
+  float* pb = hs + 64 * a.ldh;          // [c_p1] gpool bias of this row
+  float* ps = pb + a.c_p1;              // [c_p1] scale
+  float* pt = ps + a.c_p1;              // [c_p1] shift
+  float* w2 = pt + a.c_p1;              // [c_p1][P]
+  float* vs = w2 + a.c_p1 * a.P;        // [c_v1] scale
+  float* vt = vs + a.c_v1;              // [c_v1] shift
+  float* wo = vt + a.c_v1;              // [c_v1]
+  for (int c = tid; c < a.c_p1; c += 64) {
+    pb[c] = a.p1_bias[(size_t)b * a.c_p1 + c];
+    ps[c] = a.p1_scale[c];
+    pt[c] = a.p1_shift[c];
+  }
+  for (int e = tid; e < a.c_p1 * a.P; e += 64) w2[e] = a.w_p2[e];
+  for (int c = tid; c < a.c_v1; c += 64) {
+    vs[c] = a.v1_scale[c];
+    vt[c] = a.v1_shift[c];
+    wo[c] = a.w_own[c];
+  }
   __syncthreads();
   const int pos = p0 + tid;
   if (tid >= np) return;
@@ -169,16 +317,13 @@ __global__ __launch_bounds__(64) void head_spatial_kernel(HeadSpatialArgs a) {
   const float mk = a.mask[(size_t)b * HW + pos];
   float pol[4] = {0.f, 0.f, 0.f, 0.f};
   for (int c = 0; c < a.c_p1; c++) {
-    const float v = act_f<PACT>((h[a.p1_off + c] + a.p1_bias[(size_t)b * a.c_p1 + c]) * a.p1_scale[c] + a.p1_shift[c]) * mk;
+    const float v = act_f<PACT>((h[a.p1_off + c] + pb[c]) * ps[c] + pt[c]) * mk;
 #pragma unroll
     for (int p = 0; p < 4; p++)
-      if (p < a.P) pol[p] += v * a.w_p2[c * a.P + p];
+      if (p < a.P) pol[p] += v * w2[c * a.P + p];
   }
   float own = 0.f;
-  for (int c = 0; c < a.c_v1; c++) {
-    const float v = act_f<VACT>(h[a.v1_off + c] * a.v1_scale[c] + a.v1_shift[c]) * mk;
-    own += v * a.w_own[c];
-  }
+  for (int c = 0; c < a.c_v1; c++) own += act_f<VACT>(h[a.v1_off + c] * vs[c] + vt[c]) * mk * wo[c];
   float* row = a.out + (size_t)b * a.row_len;
 #pragma unroll
   for (int p = 0; p < 4; p++)
@@ -190,7 +335,7 @@ void launch_head_spatial(const HeadSpatialArgs& a, int B, hipStream_t s) {
   if (a.P > 4) throw std::runtime_error("head: more than 4 policy channels");
   if (a.ldh > 256) throw std::runtime_error("head: too many head channels");
   dim3 grid((HW + 63) / 64, B);
-  const size_t lds = (size_t)64 * a.ldh * sizeof(float);
+  const size_t lds = ((size_t)64 * a.ldh + 3 * a.c_p1 + (size_t)a.c_p1 * a.P + 3 * a.c_v1) * sizeof(float);
   if (a.p1_act != a.v1_act) throw std::runtime_error("head: p1 and v1 activations differ");
   switch (a.p1_act) {
     case ACT_RELU: head_spatial_kernel<ACT_RELU, ACT_RELU><<<grid, 64, lds, s>>>(a); break;

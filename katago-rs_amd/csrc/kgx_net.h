@@ -105,6 +105,7 @@ class Net {
   void* consume(int depth, const BNDesc& bn, int act);
   Emit bn_emit(const BNDesc& bn, int act, void* out, int ld);
   Prologue bn_pro(const BNDesc& bn, int act, const float* prebias = nullptr, int ld_prebias = 0);
+  RowProg row_prog_base() const;  // a row program with the board statistics filled in
   void build(const ModelDesc& m);
 
   void run_ops(int B, hipStream_t s);
@@ -124,14 +125,14 @@ class Net {
   float *mask_ = nullptr, *area_ = nullptr, *s1_ = nullptr, *s2_ = nullptr;
 
   // Workspace sizes from scan(), then the buffers.
-  int tmp_c_ = 0, mid_c_ = 0, gp_c_ = 0, gb_c_ = 0;
+  int tmp_c_ = 0, mid_c_ = 0, gb_c_ = 0;
   std::vector<int> stream_c_;
   int nrm_c_ = 0, qkv_c_ = 0, ao_c_ = 0, u_c_ = 0, h_c_ = 0;
   size_t wino_v_elems_ = 0, wino_m_elems_ = 0;
   float* trunk_ = nullptr;
   std::vector<StreamState> ss_;
   void* mid_ = nullptr;  // compute-type mid activation of a residual block
-  float *tmp_ = nullptr, *gp_ = nullptr, *gb_ = nullptr;
+  float *tmp_ = nullptr, *gb_ = nullptr;
   void *nrm_ = nullptr, *qkv_ = nullptr, *ao_ = nullptr, *h_ = nullptr;
   float* u_ = nullptr;
   void* wino_v_ = nullptr;

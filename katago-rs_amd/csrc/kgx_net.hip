@@ -84,6 +84,15 @@ const void* Net::upload_t(const std::vector<float>& v) {
   return d;
 }
 
+RowProg Net::row_prog_base() const {
+  RowProg p;
+  p.mask = mask_;
+  p.area = area_;
+  p.s1 = s1_;
+  p.s2 = s2_;
+  return p;
+}
+
 Prologue Net::bn_pro(const BNDesc& bn, int act, const float* prebias, int ld_prebias) {
   Prologue p;
   p.scale = upload_f(bn.scale);
@@ -126,7 +135,6 @@ void Net::scan(const std::vector<BlockDesc>& blocks, int c, int depth) {
       case BLOCK_GPOOL:
         tmp_c_ = std::max(tmp_c_, b.regular.oc + b.gconv.oc);
         mid_c_ = std::max(mid_c_, b.regular.oc);
-        gp_c_ = std::max(gp_c_, 3 * b.gconv.oc);
         gb_c_ = std::max(gb_c_, b.regular.oc);
         break;
       case BLOCK_NBT:
@@ -479,22 +487,25 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
         o1.y = tmp_;
         o1.ldy = ct;
         emit_conv(both, a, c, false, o1);
-        const Prologue gpro = bn_pro(b.gbn, b.gact);
+        // Pooling of the gpool branch (after its batch norm and activation) and the matmul to the bias of the
+        // regular branch, one workgroup per row.
         float* tmp = tmp_;
-        float* gp = gp_;
         float* gb = gb_;
-        const float *area = area_, *s1 = s1_, *s2 = s2_;
+        RowProg rp = row_prog_base();
+        rp.npool = 1;
+        rp.pool[0].x = tmp; rp.pool[0].ldx = ct; rp.pool[0].coff = cr; rp.pool[0].C = cg;
+        rp.pool[0].scale = upload_f(b.gbn.scale); rp.pool[0].bias = upload_f(b.gbn.bias); rp.pool[0].act = b.gact;
+        rp.pool[0].dst = 0;
+        rp.nmm = 1;
+        rp.mm[0].src = 0; rp.mm[0].IC = 3 * cg; rp.mm[0].OC = cr; rp.mm[0].W = upload_f(b.gmul.w);
+        rp.mm[0].out = gb; rp.mm[0].ldout = cr;
+        rp.lds_floats = 3 * cg;
         Op pool;
-        pool.launch = [=](hipStream_t s, int B) { launch_pool(tmp, ct, cr, cg, gpro, area, s1, s2, false, gp, B, s); };
-        pool.cls = "pool";
+        pool.launch = [=](hipStream_t s, int B) { launch_row_prog(rp, B, s); };
+        pool.cls = "row_prog";
         pool.bytes_row = (double)HW * cg * 4;
+        pool.flops_row = 2.0 * 3 * cg * cr;
         ops_.push_back(pool);
-        const float* gw = upload_f(b.gmul.w);
-        Op mm;
-        mm.launch = [=](hipStream_t s, int B) { launch_small_matmul(gp, 3 * cg, 3 * cg, gw, cr, nullptr, ACT_ID, gb, cr, 1, false, B, s); };
-        mm.cls = "small_matmul";
-        mm.flops_row = 2.0 * 3 * cg * cr;
-        ops_.push_back(mm);
         // The mid activation adds the pooled bias per (row, channel) before its batch norm.
         const Emit me = bn_emit(b.mid_bn, b.mid_act, mid_, cr);
         Op ba;
@@ -564,7 +575,6 @@ void Net::build(const ModelDesc& m) {
   }
   if (tmp_c_) tmp_ = alloc_f(Mx * tmp_c_);
   if (mid_c_) mid_ = alloc_bytes(Mx * mid_c_ * tsize());
-  if (gp_c_) gp_ = alloc_f((size_t)max_batch_ * gp_c_);
   if (gb_c_) gb_ = alloc_f((size_t)max_batch_ * gb_c_);
   if (nrm_c_) nrm_ = alloc_bytes(Mx * nrm_c_ * tsize());
   if (qkv_c_) qkv_ = alloc_bytes(Mx * qkv_c_ * tsize());
@@ -582,33 +592,32 @@ void Net::build(const ModelDesc& m) {
     op.bytes_row = HW * 8.0;
     ops_.push_back(op);
   }
+  // The stem's per-row bias: global inputs through their matmul, plus the metadata encoder's output
+  // (bin2onnx.py:1477-1488), one workgroup per row.
   float* gbias = alloc_f((size_t)max_batch_ * C);
   {
-    const float* w = upload_f(m.stem_mm.w);
-    float* glob = d_glob_;
-    const int G = nglob_;
+    RowProg rp = row_prog_base();
+    RowMM& g = rp.mm[rp.nmm++];
+    g.gin = d_glob_; g.ldgin = nglob_; g.IC = nglob_; g.OC = C; g.W = upload_f(m.stem_mm.w);
+    g.out = gbias; g.ldout = C;
+    double flops = 2.0 * nglob_ * C;
+    if (m.meta_version > 0) {
+      const int h1 = m.meta1.oc, h2 = m.meta2.oc;
+      RowMM& a = rp.mm[rp.nmm++];
+      a.gin = d_meta_; a.ldgin = nmeta_; a.IC = nmeta_; a.OC = h1; a.W = upload_f(m.meta1.w);
+      a.bias = upload_f(m.meta_b1.b); a.act = m.meta_act1; a.dst = 0;
+      RowMM& c = rp.mm[rp.nmm++];
+      c.src = 0; c.IC = h1; c.OC = h2; c.W = upload_f(m.meta2.w); c.bias = upload_f(m.meta_b2.b);
+      c.act = m.meta_act2; c.dst = h1;
+      RowMM& d = rp.mm[rp.nmm++];
+      d.src = h1; d.IC = h2; d.OC = C; d.W = upload_f(m.meta3.w); d.out = gbias; d.ldout = C; d.accumulate = true;
+      rp.lds_floats = h1 + h2;
+      flops += 2.0 * ((double)nmeta_ * h1 + (double)h1 * h2 + (double)h2 * C);
+    }
     Op op;
-    op.launch = [=](hipStream_t s, int B) { launch_small_matmul(glob, G, G, w, C, nullptr, ACT_ID, gbias, C, 1, false, B, s); };
-    op.cls = "small_matmul";
-    op.flops_row = 2.0 * G * C;
-    ops_.push_back(op);
-  }
-  if (m.meta_version > 0) {
-    const int h1 = m.meta1.oc, h2 = m.meta2.oc;
-    float* t1 = alloc_f((size_t)max_batch_ * h1);
-    float* t2 = alloc_f((size_t)max_batch_ * h2);
-    const float *w1 = upload_f(m.meta1.w), *b1 = upload_f(m.meta_b1.b), *w2 = upload_f(m.meta2.w),
-                *b2 = upload_f(m.meta_b2.b), *w3 = upload_f(m.meta3.w);
-    const int a1 = m.meta_act1, a2 = m.meta_act2;
-    float* meta = d_meta_;
-    Op op;
-    op.launch = [=](hipStream_t s, int B) {
-      launch_small_matmul(meta, 192, 192, w1, h1, b1, a1, t1, h1, 1, false, B, s);
-      launch_small_matmul(t1, h1, h1, w2, h2, b2, a2, t2, h2, 1, false, B, s);
-      launch_small_matmul(t2, h2, h2, w3, C, nullptr, ACT_ID, gbias, C, 1, true, B, s);
-    };
-    op.cls = "small_matmul";
-    op.flops_row = 2.0 * (192.0 * h1 + (double)h1 * h2 + (double)h2 * C);
+    op.launch = [=](hipStream_t s, int B) { launch_row_prog(rp, B, s); };
+    op.cls = "row_prog";
+    op.flops_row = flops;
     ops_.push_back(op);
   }
   {
@@ -673,52 +682,54 @@ void Net::build(const ModelDesc& m) {
   }
   const int P = m.P, S = m.S, rl = row_len_;
   float* out = d_out_;
-  const float *area = area_, *s1 = s1_, *s2 = s2_;
-  // Policy: g1 pooling, gpool bias of p1, pass logits.
-  float* g1p = alloc_f((size_t)max_batch_ * 3 * cg);
+  // Row work of both heads in one launch (bin2onnx.py:1495-1531): g1 pooling -> gpool bias of p1 and the pass
+  // logits; value pooling -> v2 -> value and score outputs.
   float* p1b = alloc_f((size_t)max_batch_ * cp);
   {
-    const Prologue gpro = bn_pro(m.g1_bn, m.g1_act);
-    const float* wgb = upload_f(m.gpool_to_bias.w);
-    const float* wp1 = upload_f(m.pass1.w);
+    const int c2 = m.v2.oc, ph = m.pass1.oc;
     const bool v15 = m.version >= 15;
-    const float* pb = v15 ? upload_f(m.pass_bias.b) : nullptr;
-    const float* wp2 = v15 ? upload_f(m.pass2.w) : nullptr;
-    const int pact = m.pass_act, ph = m.pass1.oc;
-    float* pt = v15 ? alloc_f((size_t)max_batch_ * ph) : nullptr;
+    RowProg rp = row_prog_base();
+    int lds = 0;
+    const int fg = lds; lds += 3 * cg;     // g1 features
+    const int fv = lds; lds += 3 * cv;     // value features
+    const int fp = lds; lds += v15 ? ph : 0;  // pass hidden layer
+    const int f2 = lds; lds += c2;         // v2
+    rp.lds_floats = lds;
+    rp.npool = 2;
+    RowPool& pg = rp.pool[0];
+    pg.x = H; pg.ldx = nh; pg.coff = cp; pg.C = cg;
+    pg.scale = upload_f(m.g1_bn.scale); pg.bias = upload_f(m.g1_bn.bias); pg.act = m.g1_act; pg.dst = fg;
+    RowPool& pv = rp.pool[1];
+    pv.x = H; pv.ldx = nh; pv.coff = cp + cg; pv.C = cv;
+    pv.scale = upload_f(m.v1_bn.scale); pv.bias = upload_f(m.v1_bn.bias); pv.act = m.v1_act; pv.value = true;
+    pv.dst = fv;
+    RowMM& gbm = rp.mm[rp.nmm++];
+    gbm.src = fg; gbm.IC = 3 * cg; gbm.OC = cp; gbm.W = upload_f(m.gpool_to_bias.w); gbm.out = p1b; gbm.ldout = cp;
+    if (v15) {
+      RowMM& p1 = rp.mm[rp.nmm++];
+      p1.src = fg; p1.IC = 3 * cg; p1.OC = ph; p1.W = upload_f(m.pass1.w); p1.bias = upload_f(m.pass_bias.b);
+      p1.act = m.pass_act; p1.dst = fp;
+      RowMM& p2 = rp.mm[rp.nmm++];
+      p2.src = fp; p2.IC = ph; p2.OC = P; p2.W = upload_f(m.pass2.w);
+      p2.out = out + HW; p2.ldout = rl; p2.ostride = HW + 1;
+    } else {
+      RowMM& p1 = rp.mm[rp.nmm++];
+      p1.src = fg; p1.IC = 3 * cg; p1.OC = P; p1.W = upload_f(m.pass1.w);
+      p1.out = out + HW; p1.ldout = rl; p1.ostride = HW + 1;
+    }
+    RowMM& v2 = rp.mm[rp.nmm++];
+    v2.src = fv; v2.IC = 3 * cv; v2.OC = c2; v2.W = upload_f(m.v2.w); v2.bias = upload_f(m.v2_bias.b);
+    v2.act = m.v2_act; v2.dst = f2;
+    RowMM& v3 = rp.mm[rp.nmm++];
+    v3.src = f2; v3.IC = c2; v3.OC = 3; v3.W = upload_f(m.v3.w); v3.bias = upload_f(m.v3_bias.b);
+    v3.out = out + P * (HW + 1); v3.ldout = rl;
+    RowMM& sv = rp.mm[rp.nmm++];
+    sv.src = f2; sv.IC = c2; sv.OC = S; sv.W = upload_f(m.sv3.w); sv.bias = upload_f(m.sv3_bias.b);
+    sv.out = out + P * (HW + 1) + 3; sv.ldout = rl;
     Op op;
-    op.launch = [=](hipStream_t s, int B) {
-      launch_pool(H, nh, cp, cg, gpro, area, s1, s2, false, g1p, B, s);
-      launch_small_matmul(g1p, 3 * cg, 3 * cg, wgb, cp, nullptr, ACT_ID, p1b, cp, 1, false, B, s);
-      if (v15) {
-        launch_small_matmul(g1p, 3 * cg, 3 * cg, wp1, ph, pb, pact, pt, ph, 1, false, B, s);
-        launch_small_matmul(pt, ph, ph, wp2, P, nullptr, ACT_ID, out + HW, rl, HW + 1, false, B, s);
-      } else {
-        launch_small_matmul(g1p, 3 * cg, 3 * cg, wp1, P, nullptr, ACT_ID, out + HW, rl, HW + 1, false, B, s);
-      }
-    };
-    op.cls = "head";
-    op.bytes_row = (double)HW * cg * 4;
-    ops_.push_back(op);
-  }
-  // Value: value pooling, v2, v3, sv3.
-  {
-    const Prologue vpro = bn_pro(m.v1_bn, m.v1_act);
-    float* vp = alloc_f((size_t)max_batch_ * 3 * cv);
-    const int c2 = m.v2.oc;
-    float* v2 = alloc_f((size_t)max_batch_ * c2);
-    const float *w2 = upload_f(m.v2.w), *b2 = upload_f(m.v2_bias.b), *w3 = upload_f(m.v3.w), *b3 = upload_f(m.v3_bias.b),
-                *ws = upload_f(m.sv3.w), *bs = upload_f(m.sv3_bias.b);
-    const int a2 = m.v2_act;
-    Op op;
-    op.launch = [=](hipStream_t s, int B) {
-      launch_pool(H, nh, cp + cg, cv, vpro, area, s1, s2, true, vp, B, s);
-      launch_small_matmul(vp, 3 * cv, 3 * cv, w2, c2, b2, a2, v2, c2, 1, false, B, s);
-      launch_small_matmul(v2, c2, c2, w3, 3, b3, ACT_ID, out + P * (HW + 1), rl, 1, false, B, s);
-      launch_small_matmul(v2, c2, c2, ws, S, bs, ACT_ID, out + P * (HW + 1) + 3, rl, 1, false, B, s);
-    };
-    op.cls = "head";
-    op.bytes_row = (double)HW * cv * 4;
+    op.launch = [=](hipStream_t s, int B) { launch_row_prog(rp, B, s); };
+    op.cls = "row_prog";
+    op.bytes_row = (double)HW * (cg + cv) * 4;
     ops_.push_back(op);
   }
   // Spatial policy and ownership.
