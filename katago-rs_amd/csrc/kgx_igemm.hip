@@ -309,22 +309,53 @@ void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const v
   KGX_CHECK_LAUNCH();
 }
 
-// Network input planes, float NCHW [B][nin][361], to compute-type NHWC rows [B*361][ldo], channels nin..ldo-1 zero.
+// Network input of one batch row per workgroup (one thread per board point): the planes, float NCHW [nin][361], to
+// compute-type NHWC rows of ldo channels (zero beyond nin, 16-byte stores), and the board statistics of
+// launch_mask_prep: mask = plane 0, area = its sum, s1 = (sqrt(area) - 14) 0.1, s2 = (sqrt(area) - 14)^2 0.01 - 0.1.
 template <typename T>
-__global__ __launch_bounds__(256) void pack_input_kernel(const float* __restrict__ bin, int nin, T* __restrict__ out,
-                                                         int ldo, int rows) {
-  const int m = blockIdx.x * 256 + threadIdx.x;
-  if (m >= rows) return;
-  const int n = m / HW, p = m - n * HW;
-  T* o = out + (size_t)m * ldo;
-  for (int c = 0; c < ldo; c++) o[c] = to_t<T>(c < nin ? bin[((size_t)n * nin + c) * HW + p] : 0.f);
+__global__ __launch_bounds__(384) void input_prep_kernel(const float* __restrict__ bin, int nin, T* __restrict__ out,
+                                                         int ldo, float* __restrict__ mask, float* __restrict__ area,
+                                                         float* __restrict__ s1, float* __restrict__ s2) {
+  const int b = blockIdx.x, p = threadIdx.x;
+  __shared__ float red[6];
+  const float* src = bin + (size_t)b * nin * HW + p;
+  float mk = 0.f;
+  if (p < HW) {
+    T* o = out + ((size_t)b * HW + p) * ldo;
+    for (int c0 = 0; c0 < ldo; c0 += 8) {
+      float v[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) v[k] = c0 + k < nin ? src[(size_t)(c0 + k) * HW] : 0.f;
+      T t[8];
+#pragma unroll
+      for (int k = 0; k < 8; k++) t[k] = to_t<T>(v[k]);
+      *(u32x4*)(o + c0) = *(const u32x4*)t;
+      if (c0 == 0) mk = v[0];
+    }
+    mask[(size_t)b * HW + p] = mk;
+  }
+  float sum = mk;
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off);
+  if ((p & 63) == 0) red[p >> 6] = sum;
+  __syncthreads();
+  if (p == 0) {
+    const float a = ((red[0] + red[1]) + (red[2] + red[3])) + (red[4] + red[5]);
+    area[b] = a;
+    const float c = sqrtf(a) - 14.f;
+    s1[b] = c * 0.1f;
+    s2[b] = c * c * 0.01f - 0.1f;
+  }
 }
 
-void launch_pack_input(int prec, const float* bin, int nin, void* out, int ldo, int B, hipStream_t s) {
-  const int rows = B * HW;
-  if (prec == PREC_F16) pack_input_kernel<f16><<<(rows + 255) / 256, 256, 0, s>>>(bin, nin, (f16*)out, ldo, rows);
-  else if (prec == PREC_BF16) pack_input_kernel<bf16><<<(rows + 255) / 256, 256, 0, s>>>(bin, nin, (bf16*)out, ldo, rows);
-  else throw std::runtime_error("pack_input: 16-bit only");
+void launch_input_prep(int prec, const float* bin, int nin, void* out, int ldo, float* mask, float* area, float* s1,
+                       float* s2, int B, hipStream_t s) {
+  if (ldo % 8 != 0 || ldo < nin) throw std::runtime_error("input_prep: bad packed channel count");
+  if (prec == PREC_F16)
+    input_prep_kernel<f16><<<B, 384, 0, s>>>(bin, nin, (f16*)out, ldo, mask, area, s1, s2);
+  else if (prec == PREC_BF16)
+    input_prep_kernel<bf16><<<B, 384, 0, s>>>(bin, nin, (bf16*)out, ldo, mask, area, s1, s2);
+  else throw std::runtime_error("input_prep: 16-bit only");
   KGX_CHECK_LAUNCH();
 }
 

@@ -89,8 +89,10 @@ void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector
 void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const void* w, int icp, int OC,
                        const ConvOut& o, int B, hipStream_t s);
 
-// Network input planes, float NCHW [B][nin][361], to compute-type NHWC rows of ldo channels (zero beyond nin).
-void launch_pack_input(int prec, const float* bin, int nin, void* out, int ldo, int B, hipStream_t s);
+// Network input planes, float NCHW [B][nin][361], to compute-type NHWC rows of ldo channels (zero beyond nin,
+// ldo % 8 == 0), together with the board statistics of launch_mask_prep.
+void launch_input_prep(int prec, const float* bin, int nin, void* out, int ldo, float* mask, float* area, float* s1,
+                       float* s2, int B, hipStream_t s);
 
 // Direct odd-k "same" convolution, w as [ic][ky][kx][oc] float: x compute-type NHWC rows of ldx, or float NCHW.
 void launch_conv_direct(int prec, const void* x, int ldx, bool nchw_f32, int IC, const float* w, int OC, int ky, int kx,

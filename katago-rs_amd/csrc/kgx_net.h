@@ -94,6 +94,8 @@ class Net {
 
   // Planning.
   void scan(const std::vector<BlockDesc>& blocks, int c, int depth);
+  // Whether conv c runs as an implicit GEMM (16-bit handles, 1x1 / 3x3, channel and stride alignment).
+  bool igemm_eligible(const ConvDesc& c, bool nchw, int ldx, const ConvOut& o) const;
   // conv(x) into `o`; x is a compute-type activation [rows][ldx], or the float NCHW network input.
   std::shared_ptr<ConvOut> emit_conv(const ConvDesc& c, const void* x, int ldx, bool nchw, const ConvOut& o);
   void emit_stack(const std::vector<BlockDesc>& blocks, int depth);

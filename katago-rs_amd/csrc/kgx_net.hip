@@ -160,6 +160,14 @@ void Net::scan(const std::vector<BlockDesc>& blocks, int c, int depth) {
 // F(2x2,3x3) as an input transform plus one kernel for the 16 point GEMMs and the output transform, with
 // F(4x4,3x3) as input transform, 36 batched MFMA GEMMs and output transform. 1x1 convs over NHWC rows are one MFMA
 // GEMM (wino/ext.rs:278-321); anything else is a direct convolution.
+bool Net::igemm_eligible(const ConvDesc& c, bool nchw, int ldx, const ConvOut& o) const {
+  const bool k3 = c.ky == 3 && c.kx == 3 && c.dy == 1 && c.dx == 1, k1 = c.ky == 1 && c.kx == 1;
+  const bool strides4 = (!o.y || o.ldy % 4 == 0) && (!o.yt || o.ldyt % 4 == 0) &&
+                        (!o.colbias || o.ld_colbias % 4 == 0) && (!o.emit.scale || o.emit.ld % 4 == 0);
+  return conv_mode_ == CONV_IGEMM && (k3 || k1) && c.oc % 4 == 0 && strides4 &&
+         (nchw || (c.ic % 8 == 0 && ldx % 8 == 0));
+}
+
 std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ldx, bool nchw, const ConvOut& o) {
   const int prec = prec_;
   const double ts = (double)tsize();
@@ -167,22 +175,22 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
   const double in_bytes = (double)HW * c.ic * (nchw ? 4.0 : ts);
   const double out_bytes = (double)HW * c.oc * ((o.y ? 4.0 : 0.0) * (o.accumulate ? 2 : 1) + (o.yt ? ts : 0.0));
   const int ic = c.ic, oc = c.oc;
-  const bool k3 = c.ky == 3 && c.kx == 3 && c.dy == 1 && c.dx == 1, k1 = c.ky == 1 && c.kx == 1;
-  const bool strides4 = (!o.y || o.ldy % 4 == 0) && (!o.yt || o.ldyt % 4 == 0) &&
-                        (!o.colbias || o.ld_colbias % 4 == 0) && (!o.emit.scale || o.emit.ld % 4 == 0);
-  if (conv_mode_ == CONV_IGEMM && (k3 || k1) && oc % 4 == 0 && strides4 && (nchw || (ic % 8 == 0 && ldx % 8 == 0))) {
+  const bool k3 = c.ky == 3 && c.kx == 3 && c.dy == 1 && c.dx == 1;
+  if (igemm_eligible(c, nchw, ldx, o)) {
     const int ks = k3 ? 3 : 1;
     const void* xin = x;
     int ldin = ldx, icin = ic;
     if (nchw) {
-      // The network input planes are packed once into compute-type NHWC rows (0/1 planes are exact in 16 bits).
+      // The network input planes are packed once into compute-type NHWC rows (0/1 planes are exact in 16 bits),
+      // with the board statistics in the same launch.
       icin = ldin = round_up(ic, 8);
       void* packed = alloc_bytes((size_t)max_batch_ * HW * icin * tsize());
       const float* bin = (const float*)x;
+      float *mask = mask_, *area = area_, *s1 = s1_, *s2 = s2_;
       Op pk;
-      pk.launch = [=](hipStream_t s, int B) { launch_pack_input(prec, bin, ic, packed, icin, B, s); };
-      pk.cls = "pack_input";
-      pk.bytes_row = (double)HW * ic * 4 + (double)HW * icin * ts;
+      pk.launch = [=](hipStream_t s, int B) { launch_input_prep(prec, bin, ic, packed, icin, mask, area, s1, s2, B, s); };
+      pk.cls = "input_prep";
+      pk.bytes_row = (double)HW * ic * 4 + (double)HW * icin * ts + HW * 4.0;
       ops_.push_back(pk);
       xin = packed;
     }
@@ -583,7 +591,11 @@ void Net::build(const ModelDesc& m) {
   if (h_c_) h_ = alloc_bytes(Mx * h_c_ * tsize());
 
   // --- Trunk input (bin2onnx.py:1466-1492): mask, stem conv + global (and metadata) bias. ---
-  {
+  ConvOut stem_out;
+  stem_out.y = trunk_;
+  stem_out.ldy = C;
+  stem_out.ld_colbias = C;
+  if (!igemm_eligible(m.stem, true, 0, stem_out)) {  // else the stem's input packing computes the board statistics
     float *bin = d_bin_, *mask = mask_, *area = area_, *s1 = s1_, *s2 = s2_;
     const int nin = nin_;
     Op op;
@@ -620,14 +632,8 @@ void Net::build(const ModelDesc& m) {
     op.flops_row = flops;
     ops_.push_back(op);
   }
-  {
-    ConvOut o;
-    o.y = trunk_;
-    o.ldy = C;
-    o.colbias = gbias;
-    o.ld_colbias = C;
-    ss_[0].producer = emit_conv(m.stem, d_bin_, 0, true, o);
-  }
+  stem_out.colbias = gbias;
+  ss_[0].producer = emit_conv(m.stem, d_bin_, 0, true, stem_out);
 
   // --- Blocks. ---
   emit_stack(m.blocks, 0);
