@@ -61,7 +61,9 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
                                                       int icp, int OC, int M, ConvOut o) {
   constexpr int TAPS = C::TAPS, HALO = C::HALO, BM = C::BM, BN = C::BN, BK = C::BK, WM = C::WM, WN = C::WN;
   constexpr int NT = C::NT, G = C::G;
-  constexpr int LDK = BK + 8;                 // LDS row stride in elements (16-byte pad)
+  // LDS row stride in elements: a 32-byte pad makes the 16-row fragment reads conflict-free (80 dwords apart rows
+  // of a 16x16x32 fragment hit distinct banks; a 16-byte pad serialises them two-way on gfx950).
+  constexpr int LDK = BK + 16;
   constexpr int KV = BK / 8;                  // 16-byte vectors per staged row
   constexpr int AR = BM + 2 * HALO;           // staged pixel rows
   constexpr int RP = NT / KV;                 // staged rows per pass of all threads
