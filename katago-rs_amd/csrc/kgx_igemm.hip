@@ -169,6 +169,9 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
 #pragma unroll
     for (int s = 0; s < S; s++) {
       if (s + 1 < S) fetch(s + 1, (s + 1) & 1);
+      // Keep the order: all of the next step's LDS reads are issued before this step's MFMAs (the scheduler
+      // would otherwise move each read next to its first use and expose the LDS latency on every step).
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < MB; i++)
 #pragma unroll
@@ -178,6 +181,7 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
           else
             acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s & 1][i], b[s & 1][j], acc[i][j], 0, 0, 0);
         }
+      __builtin_amdgcn_sched_barrier(0);
       if constexpr (C::INTERLEAVE) {
         // Scheduling hint: alternate this step's MFMAs with the next step's LDS fragment reads.
 #pragma unroll
