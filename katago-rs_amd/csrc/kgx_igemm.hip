@@ -20,8 +20,10 @@
 
 namespace kgx {
 
-template <int KS_, int BM_, int BN_, int BK_, int WM_, int WN_, int G_, int NBUF_, bool INTERLEAVE_ = false>
+template <int KS_, int BM_, int BN_, int BK_, int WM_, int WN_, int G_, int NBUF_, int MINW_ = 2,
+          bool INTERLEAVE_ = false>
 struct IgCfg {
+  static constexpr int MINW = MINW_;            // waves per SIMD the register allocation must allow
   static constexpr bool INTERLEAVE = INTERLEAVE_;  // MFMA / LDS-read interleaving hints for the scheduler
   static constexpr int KS = KS_, TAPS = KS_ * KS_, HALO = KS_ == 3 ? POS + 1 : 0;
   static constexpr int BM = BM_, BN = BN_, BK = BK_, WM = WM_, WN = WN_;
@@ -30,34 +32,34 @@ struct IgCfg {
   static constexpr int NT = WM * WN * 64 * G_;
 };
 
-// Epilogue for four consecutive channels n..n+3 of pixel m (conv_store on a float4).
-// With `have_yacc`, `yacc` holds the residual values already loaded (instead of reading o.y).
+// Epilogue for four consecutive channels n..n+3 of pixel m (conv_store on a float4). The per-pixel inputs come
+// preloaded: the residual `yacc` (when o.accumulate), the row mask `rm`, the emit scale/bias `es`/`eb` of the
+// four channels and the emit mask `mk` (the epilogue's stores may alias them as far as the compiler knows, so a
+// load placed between stores would wait a full round trip). The column bias (the stem's global input bias, one
+// launch per forward) is read inline.
 template <typename T>
-__device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floatx4 v, bool have_yacc = false,
-                                            floatx4 yacc = floatx4{0.f, 0.f, 0.f, 0.f}) {
+__device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floatx4 v, floatx4 yacc, float rm,
+                                            floatx4 es, floatx4 eb, float mk) {
   if (o.colbias) v += *(const floatx4*)(o.colbias + (size_t)(m / HW) * o.ld_colbias + n);
-  if (o.rowmask) v *= o.rowmask[m];
+  if (o.rowmask) v *= rm;
   if (o.yt) {
     T t[4] = {to_t<T>(v[0]), to_t<T>(v[1]), to_t<T>(v[2]), to_t<T>(v[3])};
     *(uint2*)((T*)o.yt + (size_t)m * o.ldyt + n) = *(const uint2*)t;
   }
   if (o.y) {
-    floatx4* p = (floatx4*)(o.y + (size_t)m * o.ldy + n);
-    if (o.accumulate) v += have_yacc ? yacc : *p;
-    *p = v;
+    if (o.accumulate) v += yacc;
+    *(floatx4*)(o.y + (size_t)m * o.ldy + n) = v;
   }
   if (o.emit.scale) {
-    const floatx4 s = *(const floatx4*)(o.emit.scale + n), b = *(const floatx4*)(o.emit.bias + n);
-    const float mk = o.emit.mask[m];
     T t[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) t[e] = to_t<T>(act_rt(v[e] * s[e] + b[e], o.emit.act) * mk);
+    for (int e = 0; e < 4; e++) t[e] = to_t<T>(act_rt(v[e] * es[e] + eb[e], o.emit.act) * mk);
     *(uint2*)((T*)o.emit.out + (size_t)m * o.emit.ld + n) = *(const uint2*)t;
   }
 }
 
 template <typename T, typename C>
-__global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, int ldx, int IC, const T* __restrict__ W,
+__global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restrict__ X, int ldx, int IC, const T* __restrict__ W,
                                                       int icp, int OC, int M, ConvOut o) {
   constexpr int TAPS = C::TAPS, HALO = C::HALO, BM = C::BM, BN = C::BN, BK = C::BK, WM = C::WM, WN = C::WN;
   constexpr int NT = C::NT, G = C::G;
@@ -201,19 +203,28 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
       else mma(std::integral_constant<int, G - 1>{}, buf);
     }
   };
-  // Residual values of this thread's epilogue vectors, read before the main loop so that the reads overlap it.
-  constexpr int NV = BM * (BN / 4), EV = (NV + NT - 1) / NT;
+  // Epilogue mapping: thread tid finishes the four channels 4 * (tid % G4) of rows tid / G4 + e * RPE, so its
+  // emit scale and bias are loaded once. The 3x3 kernel reads the residual values before the main loop so that
+  // the reads overlap it; the 1x1 kernel reads them after (its registers stay within two workgroups per CU).
+  constexpr int G4 = BN / 4, RPE = NT / G4, EV = (BM + RPE - 1) / RPE;
+  constexpr bool YEARLY = C::KS == 3;
+  const int ec4 = tid % G4, er0 = tid / G4, en = n0 + 4 * ec4;
+  const bool eon = er0 < RPE && en < OC;
+  // Loads use clamped pixel and channel indices (always in range, no branches, so they issue back to back);
+  // the stores below skip what lies outside the tile.
+  const int enc = min(en, OC - 4);
+  auto epix = [&](int e) { return min(m0 + min(er0 + e * RPE, BM - 1), M - 1); };
+  const bool yacc = o.y && o.accumulate;
+  // Each input is loaded under one uniform branch and left undefined otherwise (no per-element control flow,
+  // so the loads issue back to back).
   floatx4 yres[EV];
-  const bool yprefetch = o.y && o.accumulate;
-  if (yprefetch) {
+  auto load_y = [&]() {
+    if (yacc) {
 #pragma unroll
-    for (int e = 0; e < EV; e++) {
-      const int v = tid + e * NT;
-      const int row = v / (BN / 4), c4 = v - row * (BN / 4);
-      const int m = m0 + row, n = n0 + 4 * c4;
-      if (v < NV && m < M && n < OC) yres[e] = *(const floatx4*)(o.y + (size_t)m * o.ldy + n);
+      for (int e = 0; e < EV; e++) yres[e] = *(const floatx4*)(o.y + (size_t)epix(e) * o.ldy + enc);
     }
-  }
+  };
+  if constexpr (YEARLY) load_y();
 
   // The zero row of every stage buffer (never written by the stage stores).
   for (int e = tid; e < NBUF * KV; e += NT) *(vec_t*)(As + (e / KV) * SE + AR * LDK + (e % KV) * 8) = vec_t{0, 0, 0, 0};
@@ -252,16 +263,29 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
 #pragma unroll
       for (int r = 0; r < 4; r++) Cg[(wm * WTM + i * 16 + 4 * g4 + r) * LDC + wn * WTN + j * 16 + r16] = acc[i][j][r];
   __syncthreads();
+  // The other epilogue inputs, loaded after the accumulator exchange and before the first store.
+  if constexpr (!YEARLY) load_y();
+  float rmv[EV], mkv[EV];
+  floatx4 es, eb;
+  if (o.emit.scale) {
+    es = *(const floatx4*)(o.emit.scale + enc);
+    eb = *(const floatx4*)(o.emit.bias + enc);
+#pragma unroll
+    for (int e = 0; e < EV; e++) mkv[e] = o.emit.mask[epix(e)];
+  }
+  if (o.rowmask) {
+#pragma unroll
+    for (int e = 0; e < EV; e++) rmv[e] = o.rowmask[epix(e)];
+  }
+
 #pragma unroll
   for (int e = 0; e < EV; e++) {
-    const int v = tid + e * NT;
-    const int row = v / (BN / 4), c4 = v - row * (BN / 4);
-    const int m = m0 + row, n = n0 + 4 * c4;
-    if (v < NV && m < M && n < OC) {
-      floatx4 sum = *(const floatx4*)(Cs + row * LDC + 4 * c4);
+    const int row = er0 + e * RPE, m = m0 + row;
+    if (eon && row < BM && m < M) {
+      floatx4 sum = *(const floatx4*)(Cs + row * LDC + 4 * ec4);
 #pragma unroll
-      for (int q = 1; q < G; q++) sum += *(const floatx4*)(Cs + q * BM * LDC + row * LDC + 4 * c4);
-      conv_store4<T>(o, m, n, sum, yprefetch, yres[e]);
+      for (int q = 1; q < G; q++) sum += *(const floatx4*)(Cs + q * BM * LDC + row * LDC + 4 * ec4);
+      conv_store4<T>(o, m, en, sum, yres[e], rmv[e], es, eb, mkv[e]);
     }
   }
 }
@@ -270,9 +294,10 @@ __global__ __launch_bounds__(C::NT) void igemm_kernel(const T* __restrict__ X, i
 // quarter of the weights per workgroup: weight staging is what bounds this kernel), 64 channels per stage and two
 // wave groups of 4x1 waves (48x48 each) splitting the taps; 1x1 on the same 192-pixel tiles with two stage
 // buffers. Equal pixel tiles give every convolution the same tile -> XCD mapping, so a layer reads the
-// activations its producer wrote from the same XCD's L2.
+// activations its producer wrote from the same XCD's L2. The 1x1 kernel keeps two workgroups per CU (four waves
+// per SIMD, at most 128 registers): its 384-channel outputs are 512 workgroups.
 typedef IgCfg<3, 192, 48, 64, 4, 1, 2, 1> Ig3;
-typedef IgCfg<1, 192, 48, 64, 4, 1, 2, 2> Ig1;
+typedef IgCfg<1, 192, 48, 64, 4, 1, 2, 2, 4> Ig1;
 
 template <typename T, typename C>
 static void igemm_launch(const void* x, int ldx, int IC, const void* w, int icp, int OC, const ConvOut& o, int M,
