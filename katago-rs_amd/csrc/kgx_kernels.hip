@@ -282,67 +282,80 @@ void launch_row_prog(const RowProg& p, int B, hipStream_t s) {
 // ---------------------------------------------------------------------------------------------------------
 // Head: policy p2 conv and ownership conv per board point, written into the readback rows
 // ---------------------------------------------------------------------------------------------------------
-// 64 board points per workgroup; their rows of H are staged in LDS with coalesced loads first, and so are the
-// per-channel parameters (this row's gpool bias, batch norms, p2 and ownership weights), which every thread reads.
+// Sixteen lanes per board point: lane l of a point takes channels l, l + 16, ... of p1 and of v1 (at most 16 HK of
+// each), so the point's 16 lanes read contiguous 64-byte runs of its row of H, and each lane keeps the parameters of
+// its channels (this row's gpool bias, the batch norms, p2 and ownership weights) in registers for every point it
+// visits. Partial sums are added over the 16 lanes. HS_PTS points of one batch row per workgroup.
+constexpr int HS_PTS = 48;
 
-template <int PACT, int VACT>
-__global__ __launch_bounds__(64) void head_spatial_kernel(HeadSpatialArgs a) {
-  extern __shared__ float hs[];
-  const int b = blockIdx.y, p0 = blockIdx.x * 64, tid = threadIdx.x;
-  const int np = min(64, HW - p0);
-  const float* src = a.H + ((size_t)b * HW + p0) * a.ldh;
-  for (int e = tid; e < np * a.ldh; e += 64) hs[e] = src[e];
-  float* pb = hs + 64 * a.ldh;          // [c_p1] gpool bias of this row
-  float* ps = pb + a.c_p1;              // [c_p1] scale
-  float* pt = ps + a.c_p1;              // [c_p1] shift
-  float* w2 = pt + a.c_p1;              // [c_p1][P]
-  float* vs = w2 + a.c_p1 * a.P;        // [c_v1] scale
-  float* vt = vs + a.c_v1;              // [c_v1] shift
-  float* wo = vt + a.c_v1;              // [c_v1]
-  for (int c = tid; c < a.c_p1; c += 64) {
-    pb[c] = a.p1_bias[(size_t)b * a.c_p1 + c];
-    ps[c] = a.p1_scale[c];
-    pt[c] = a.p1_shift[c];
-  }
-  for (int e = tid; e < a.c_p1 * a.P; e += 64) w2[e] = a.w_p2[e];
-  for (int c = tid; c < a.c_v1; c += 64) {
-    vs[c] = a.v1_scale[c];
-    vt[c] = a.v1_shift[c];
-    wo[c] = a.w_own[c];
-  }
-  __syncthreads();
-  const int pos = p0 + tid;
-  if (tid >= np) return;
-  const float* h = hs + (size_t)tid * a.ldh;
-  const float mk = a.mask[(size_t)b * HW + pos];
-  float pol[4] = {0.f, 0.f, 0.f, 0.f};
-  for (int c = 0; c < a.c_p1; c++) {
-    const float v = act_f<PACT>((h[a.p1_off + c] + pb[c]) * ps[c] + pt[c]) * mk;
+template <int ACT, int HK>
+__global__ __launch_bounds__(256) void head_spatial_kernel(HeadSpatialArgs a) {
+  const int b = blockIdx.y, tid = threadIdx.x, l16 = tid & 15, slot = tid >> 4;
+  float pb[HK], ps[HK], pt[HK], w2[HK][4], vs[HK], vt[HK], wo[HK];
 #pragma unroll
-    for (int p = 0; p < 4; p++)
-      if (p < a.P) pol[p] += v * w2[c * a.P + p];
-  }
-  float own = 0.f;
-  for (int c = 0; c < a.c_v1; c++) own += act_f<VACT>(h[a.v1_off + c] * vs[c] + vt[c]) * mk * wo[c];
-  float* row = a.out + (size_t)b * a.row_len;
+  for (int k = 0; k < HK; k++) {
+    const int c = l16 + 16 * k;
+    const bool okp = c < a.c_p1, okv = c < a.c_v1;
+    pb[k] = okp ? a.p1_bias[(size_t)b * a.c_p1 + c] : 0.f;
+    ps[k] = okp ? a.p1_scale[c] : 0.f;
+    pt[k] = okp ? a.p1_shift[c] : 0.f;
 #pragma unroll
-  for (int p = 0; p < 4; p++)
-    if (p < a.P) row[p * (HW + 1) + pos] = pol[p];
-  row[a.own_off + pos] = own;
+    for (int p = 0; p < 4; p++) w2[k][p] = (okp && p < a.P) ? a.w_p2[c * a.P + p] : 0.f;
+    vs[k] = okv ? a.v1_scale[c] : 0.f;
+    vt[k] = okv ? a.v1_shift[c] : 0.f;
+    wo[k] = okv ? a.w_own[c] : 0.f;
+  }
+  const int p_end = min(HW, ((int)blockIdx.x + 1) * HS_PTS);
+  for (int pos = blockIdx.x * HS_PTS + slot; pos < p_end; pos += 16) {
+    const float* h = a.H + ((size_t)b * HW + pos) * a.ldh;
+    const float mk = a.mask[(size_t)b * HW + pos];
+    float pol[4] = {0.f, 0.f, 0.f, 0.f}, own = 0.f;
+#pragma unroll
+    for (int k = 0; k < HK; k++) {
+      const int c = l16 + 16 * k;
+      if (c < a.c_p1) {
+        const float v = act_f<ACT>((h[a.p1_off + c] + pb[k]) * ps[k] + pt[k]) * mk;
+#pragma unroll
+        for (int p = 0; p < 4; p++) pol[p] += v * w2[k][p];
+      }
+      if (c < a.c_v1) own += act_f<ACT>(h[a.v1_off + c] * vs[k] + vt[k]) * mk * wo[k];
+    }
+    // The 16 lanes of a point share its trip count, so the exchanges stay within active lanes.
+#pragma unroll
+    for (int off = 8; off > 0; off >>= 1) {
+#pragma unroll
+      for (int p = 0; p < 4; p++) pol[p] += __shfl_xor(pol[p], off);
+      own += __shfl_xor(own, off);
+    }
+    if (l16 == 0) {
+      float* row = a.out + (size_t)b * a.row_len;
+#pragma unroll
+      for (int p = 0; p < 4; p++)
+        if (p < a.P) row[p * (HW + 1) + pos] = pol[p];
+      row[a.own_off + pos] = own;
+    }
+  }
+}
+
+template <int HK>
+static void head_spatial_launch(const HeadSpatialArgs& a, int B, hipStream_t s) {
+  dim3 grid((HW + HS_PTS - 1) / HS_PTS, B);
+  switch (a.p1_act) {
+    case ACT_RELU: head_spatial_kernel<ACT_RELU, HK><<<grid, 256, 0, s>>>(a); break;
+    case ACT_MISH: head_spatial_kernel<ACT_MISH, HK><<<grid, 256, 0, s>>>(a); break;
+    case ACT_SILU: head_spatial_kernel<ACT_SILU, HK><<<grid, 256, 0, s>>>(a); break;
+    default: head_spatial_kernel<ACT_ID, HK><<<grid, 256, 0, s>>>(a); break;
+  }
 }
 
 void launch_head_spatial(const HeadSpatialArgs& a, int B, hipStream_t s) {
   if (a.P > 4) throw std::runtime_error("head: more than 4 policy channels");
-  if (a.ldh > 256) throw std::runtime_error("head: too many head channels");
-  dim3 grid((HW + 63) / 64, B);
-  const size_t lds = ((size_t)64 * a.ldh + 3 * a.c_p1 + (size_t)a.c_p1 * a.P + 3 * a.c_v1) * sizeof(float);
   if (a.p1_act != a.v1_act) throw std::runtime_error("head: p1 and v1 activations differ");
-  switch (a.p1_act) {
-    case ACT_RELU: head_spatial_kernel<ACT_RELU, ACT_RELU><<<grid, 64, lds, s>>>(a); break;
-    case ACT_MISH: head_spatial_kernel<ACT_MISH, ACT_MISH><<<grid, 64, lds, s>>>(a); break;
-    case ACT_SILU: head_spatial_kernel<ACT_SILU, ACT_SILU><<<grid, 64, lds, s>>>(a); break;
-    default: head_spatial_kernel<ACT_ID, ACT_ID><<<grid, 64, lds, s>>>(a); break;
-  }
+  const int c = std::max(a.c_p1, a.c_v1);
+  if (c <= 32) head_spatial_launch<2>(a, B, s);
+  else if (c <= 64) head_spatial_launch<4>(a, B, s);
+  else if (c <= 128) head_spatial_launch<8>(a, B, s);
+  else throw std::runtime_error("head: more than 128 p1 or v1 channels");
   KGX_CHECK_LAUNCH();
 }
 
