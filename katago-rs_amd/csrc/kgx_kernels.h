@@ -137,6 +137,7 @@ struct RowProg {
   RowPool pool[2]; int npool = 0;
   RowMM mm[8]; int nmm = 0;
   int lds_floats = 0;  // LDS features and intermediates
+  int splits = 1;      // workgroups per row sharing the outputs of the (single) matmul
   const float* mask = nullptr; const float* area = nullptr; const float* s1 = nullptr; const float* s2 = nullptr;
 };
 void launch_row_prog(const RowProg& p, int B, hipStream_t s);

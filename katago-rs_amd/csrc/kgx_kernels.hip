@@ -168,86 +168,121 @@ void launch_small_matmul(const float* in, int ldin, int IC, const float* W, int 
 // Row programs: pooling and small matmuls of one batch row in one workgroup
 // ---------------------------------------------------------------------------------------------------------
 // The row's work is a few hundred KB of reads and tens of thousands of multiply-adds: latency, not bandwidth or
-// arithmetic, bounds it, so one launch does all of it with 1024 threads, each keeping its loads independent.
-// Pooling: 64 channels x 16 groups of board points (the row's mask staged in LDS first), partial sums and maxima
-// meeting in LDS (the pooling of launch_pool). Matmul: per chunk of 64 outputs, 16 K slices of the inputs per
-// output (weight loads coalesced across the 64 outputs), partial sums meeting in LDS.
-constexpr int RP_NT = 1024, RP_KS = RP_NT / 64;
+// arithmetic, bounds it, so one launch does all of it with 1024 threads, and every stage issues all of its loads
+// before using any (one round trip per stage).
+// Pooling: four channels per thread (16-byte loads), C/4 threads per board point, so one wave covers 64 / (C/4)
+// points per load and each thread loads all of its (at most RP_PPT) points at once. Per-thread partial sums and
+// maxima are combined over the lanes of a wave that share channels, then over the waves in LDS (the pooling of
+// launch_pool). The row's mask is staged in LDS first.
+// Matmul: each wave takes a chunk of 64 outputs (weight loads coalesced across them) and a slice of the inputs;
+// partial sums meet in LDS. A program with a single matmul may split its outputs over gridDim.y workgroups per
+// row, so that each streams only its share of the weights.
+constexpr int RP_NT = 1024, RP_PPT = 6;  // chunks of <= 64 channels: at least 64 point slots, 6 passes cover 361
 
-__device__ void row_pool(const RowProg& P, const RowPool& q, int b, float* feat, float* red, const float* mk) {
-  const int tid = threadIdx.x, lane = tid & 63, grp = tid >> 6;
-  const float* xb = q.x + (size_t)b * HW * q.ldx + q.coff;
-  for (int c0 = 0; c0 < q.C; c0 += 64) {
-    const int c = c0 + lane;
-    float sum = 0.f, mx = -FLT_MAX;
-    if (c < q.C) {
-      const float sc = q.scale ? q.scale[c] : 1.f, bi = q.scale ? q.bias[c] : 0.f;
-      constexpr int NPG = (HW + RP_KS - 1) / RP_KS, CH = 8;  // board points per group, loads in flight
-      for (int k0 = 0; k0 < NPG; k0 += CH) {
-        float v[CH];
+// Channels [c0, c0 + C) of one pooling, C <= 64.
+__device__ void row_pool_chunk(const RowProg& P, const RowPool& q, int c0, int C, int b, float* feat, float* red,
+                               const float* mk) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tpp = C / 4, pslots = RP_NT / tpp;  // threads per point, point slots per pass of all threads
+  const int cg4 = tid % tpp, slot = tid / tpp, c = c0 + 4 * cg4;
+  const float* xb = q.x + (size_t)b * HW * q.ldx + q.coff + c;
+  floatx4 v[RP_PPT];
 #pragma unroll
-        for (int k = 0; k < CH; k++) {
-          const int p = grp + RP_KS * (k0 + k);
-          v[k] = p < HW ? xb[(size_t)p * q.ldx + c] : 0.f;
-        }
-#pragma unroll
-        for (int k = 0; k < CH; k++) {
-          const int p = grp + RP_KS * (k0 + k);
-          if (p < HW) {
-            float x = v[k];
-            if (q.scale) x = act_rt(x * sc + bi, q.act) * mk[p];
-            sum += x;
-            mx = fmaxf(mx, x + (mk[p] * 1e4f - 1e4f));
-          }
-        }
-      }
-    }
-    red[grp * 64 + lane] = sum;
-    red[RP_NT + grp * 64 + lane] = mx;
-    __syncthreads();
-    if (grp == 0 && c < q.C) {
-      float s = 0.f, m = -FLT_MAX;
-#pragma unroll
-      for (int k = 0; k < RP_KS; k++) {
-        s += red[k * 64 + lane];
-        m = fmaxf(m, red[RP_NT + k * 64 + lane]);
-      }
-      const float mean = s / P.area[b];
-      feat[c] = mean;
-      feat[q.C + c] = mean * P.s1[b];
-      feat[2 * q.C + c] = q.value ? mean * P.s2[b] : m;
-    }
-    __syncthreads();
+  for (int k = 0; k < RP_PPT; k++) {
+    const int p = slot + pslots * k;
+    v[k] = p < HW ? *(const floatx4*)(xb + (size_t)p * q.ldx) : floatx4{0.f, 0.f, 0.f, 0.f};
   }
+  floatx4 sc = {1.f, 1.f, 1.f, 1.f}, bi = {0.f, 0.f, 0.f, 0.f};
+  if (q.scale) {
+    sc = *(const floatx4*)(q.scale + c);
+    bi = *(const floatx4*)(q.bias + c);
+  }
+  __syncthreads();  // the staged mask
+  floatx4 sum = {0.f, 0.f, 0.f, 0.f}, mx = {-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
+  auto accum = [&](auto actc) {  // straight-line per activation (no switch inside the unrolled loop)
+    constexpr int A = decltype(actc)::value;
+#pragma unroll
+    for (int k = 0; k < RP_PPT; k++) {
+      const int p = slot + pslots * k;
+      if (p < HW) {
+        const float m = mk[p], pen = m * 1e4f - 1e4f;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float x = v[k][e];
+          if (A >= 0) x = act_f<A < 0 ? ACT_ID : A>(x * sc[e] + bi[e]) * m;
+          sum[e] += x;
+          mx[e] = fmaxf(mx[e], x + pen);
+        }
+      }
+    }
+  };
+  if (!q.scale) accum(std::integral_constant<int, -1>{});
+  else if (q.act == ACT_RELU) accum(std::integral_constant<int, ACT_RELU>{});
+  else if (q.act == ACT_MISH) accum(std::integral_constant<int, ACT_MISH>{});
+  else if (q.act == ACT_SILU) accum(std::integral_constant<int, ACT_SILU>{});
+  else accum(std::integral_constant<int, ACT_ID>{});
+  // Lanes l and l ^ (tpp << j) of a wave hold the same channels.
+  for (int off = tpp; off < 64; off <<= 1) {
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      sum[e] += __shfl_xor(sum[e], off);
+      mx[e] = fmaxf(mx[e], __shfl_xor(mx[e], off));
+    }
+  }
+  if (lane < tpp) {
+    *(floatx4*)(red + wave * C + 4 * cg4) = sum;
+    *(floatx4*)(red + RP_NT + wave * C + 4 * cg4) = mx;
+  }
+  __syncthreads();
+  if (tid < C) {
+    float s = 0.f, m = -FLT_MAX;
+    for (int w = 0; w < RP_NT / 64; w++) {
+      s += red[w * C + tid];
+      m = fmaxf(m, red[RP_NT + w * C + tid]);
+    }
+    const float mean = s / P.area[b];
+    feat[c0 + tid] = mean;
+    feat[q.C + c0 + tid] = mean * P.s1[b];
+    feat[2 * q.C + c0 + tid] = q.value ? mean * P.s2[b] : m;
+  }
+  __syncthreads();
 }
 
-__device__ void row_mm(const RowMM& m, int b, float* lds, float* red) {
-  const int tid = threadIdx.x, lane = tid & 63, ks = tid >> 6;
-  const float* in = m.gin ? nullptr : lds + m.src;
-  for (int o0 = 0; o0 < m.OC; o0 += 64) {
-    const int o = o0 + lane;
+__device__ void row_pool(const RowProg& P, const RowPool& q, int b, float* feat, float* red, const float* mk) {
+  for (int c0 = 0; c0 < q.C; c0 += 64) row_pool_chunk(P, q, c0, min(64, q.C - c0), b, feat, red, mk);
+}
+
+// Outputs [o_begin, o_end) of one matmul for row b.
+__device__ void row_mm(const RowMM& m, int b, float* lds, float* red, int o_begin, int o_end) {
+  constexpr int NW = RP_NT / 64, KB = 16;  // waves, loads in flight per batch
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform
+  const float* gin = m.gin ? m.gin + (size_t)b * m.ldgin : nullptr;
+  const float* lin = lds + m.src;
+  const int nch = (o_end - o_begin + 63) / 64;
+  for (int ch0 = 0; ch0 < nch; ch0 += NW) {
+    const int nc = min(NW, nch - ch0), nks = NW / nc;  // chunks this round, K slices per chunk
+    const int ch = ch0 + w % nc, ks = w / nc;
+    const int o = o_begin + ch * 64 + lane;
     float acc = 0.f;
-    if (o < m.OC) {
+    if (ks < nks && o < o_end) {
       const float* wcol = m.W + o;
-      float a0 = 0.f, a1 = 0.f;
-      int i = ks;
-#pragma unroll 4
-      for (; i + RP_KS < m.IC; i += 2 * RP_KS) {
-        const float w0 = wcol[(size_t)i * m.OC], w1 = wcol[(size_t)(i + RP_KS) * m.OC];
-        const float x0 = m.gin ? m.gin[(size_t)b * m.ldgin + i] : in[i];
-        const float x1 = m.gin ? m.gin[(size_t)b * m.ldgin + i + RP_KS] : in[i + RP_KS];
-        a0 += x0 * w0;
-        a1 += x1 * w1;
-      }
-      if (i < m.IC) a0 += (m.gin ? m.gin[(size_t)b * m.ldgin + i] : in[i]) * wcol[(size_t)i * m.OC];
-      acc = a0 + a1;
-    }
-    red[ks * 64 + lane] = acc;
-    __syncthreads();
-    if (ks == 0 && o < m.OC) {
-      float v = 0.f;
+      for (int i0 = ks; i0 < m.IC; i0 += KB * nks) {
+        float wv[KB], xv[KB];
 #pragma unroll
-      for (int k = 0; k < RP_KS; k++) v += red[k * 64 + lane];
+        for (int j = 0; j < KB; j++) {
+          const int i = i0 + j * nks;
+          wv[j] = i < m.IC ? wcol[(size_t)i * m.OC] : 0.f;
+          xv[j] = i < m.IC ? (gin ? gin[i] : lin[i]) : 0.f;
+        }
+#pragma unroll
+        for (int j = 0; j < KB; j++) acc += xv[j] * wv[j];
+      }
+    }
+    red[w * 64 + lane] = acc;
+    __syncthreads();
+    if (w < nc && o < o_end) {
+      float v = 0.f;
+      for (int k = 0; k < nks; k++) v += red[(k * nc + w) * 64 + lane];
       if (m.bias) v += m.bias[o];
       v = act_rt(v, m.act);
       if (m.dst >= 0) lds[m.dst + o] = v;
@@ -266,16 +301,34 @@ __global__ __launch_bounds__(RP_NT) void row_prog_kernel(RowProg P) {
   float* red = lds + P.lds_floats;
   float* mk = red + 2 * RP_NT;
   const int b = blockIdx.x;
-  for (int p = threadIdx.x; p < HW; p += RP_NT) mk[p] = P.mask[(size_t)b * HW + p];
-  __syncthreads();
+  if (P.npool > 0)
+    for (int p = threadIdx.x; p < HW; p += RP_NT) mk[p] = P.mask[(size_t)b * HW + p];
   for (int k = 0; k < P.npool; k++) row_pool(P, P.pool[k], b, lds + P.pool[k].dst, red, mk);
-  for (int k = 0; k < P.nmm; k++) row_mm(P.mm[k], b, lds, red);
+  for (int k = 0; k < P.nmm; k++) {
+    const RowMM& m = P.mm[k];
+    int o0 = 0, o1 = m.OC;
+    if (k == P.nmm - 1 && gridDim.y > 1) {  // this workgroup's share of the last matmul's outputs
+      const int per = (m.OC + gridDim.y - 1) / gridDim.y;
+      o0 = min(m.OC, (int)blockIdx.y * per);
+      o1 = min(m.OC, o0 + per);
+    }
+    row_mm(m, b, lds, red, o0, o1);
+  }
 }
 
 void launch_row_prog(const RowProg& p, int B, hipStream_t s) {
   const size_t lds = ((size_t)p.lds_floats + 2 * RP_NT + HW) * sizeof(float);
   if (lds > 64 * 1024) throw std::runtime_error("row program: too much LDS");
-  row_prog_kernel<<<B, RP_NT, lds, s>>>(p);
+  if (p.splits < 1 || (p.splits > 1 && p.nmm != 1))
+    throw std::runtime_error("row program: output splits need exactly one matmul");
+  for (int k = 0; k < p.npool; k++) {
+    // Pooled in chunks of 64 channels: every chunk's C/4 threads per point must divide 64 (16-byte loads).
+    const RowPool& q = p.pool[k];
+    const int last = q.C % 64 ? q.C % 64 : 64;
+    if (q.C < 4 || last % 4 || 64 % (last / 4) || q.ldx % 4 || q.coff % 4)
+      throw std::runtime_error("row program: unsupported pooled channel count or layout");
+  }
+  row_prog_kernel<<<dim3(B, p.splits), RP_NT, lds, s>>>(p);
   KGX_CHECK_LAUNCH();
 }
 

@@ -508,6 +508,7 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
         rp.mm[0].src = 0; rp.mm[0].IC = 3 * cg; rp.mm[0].OC = cr; rp.mm[0].W = upload_f(b.gmul.w);
         rp.mm[0].out = gb; rp.mm[0].ldout = cr;
         rp.lds_floats = 3 * cg;
+        rp.splits = std::max(1, std::min(8, cr / 64));
         Op pool;
         pool.launch = [=](hipStream_t s, int B) { launch_row_prog(rp, B, s); };
         pool.cls = "row_prog";
@@ -625,6 +626,8 @@ void Net::build(const ModelDesc& m) {
       d.src = h1; d.IC = h2; d.OC = C; d.W = upload_f(m.meta3.w); d.out = gbias; d.ldout = C; d.accumulate = true;
       rp.lds_floats = h1 + h2;
       flops += 2.0 * ((double)nmeta_ * h1 + (double)h1 * h2 + (double)h2 * C);
+    } else {
+      rp.splits = std::max(1, std::min(8, C / 64));
     }
     Op op;
     op.launch = [=](hipStream_t s, int B) { launch_row_prog(rp, B, s); };
