@@ -132,6 +132,7 @@ struct RowMM {
   const float* bias = nullptr; int act = ACT_ID;
   int dst = -1;                               // LDS float offset of the output, or -1
   float* out = nullptr; long ldout = 0; int ostride = 1; bool accumulate = false;
+  int wlds = -1;                              // LDS float offset of a staged copy of W, or -1 (read from memory)
 };
 struct RowProg {
   RowPool pool[2]; int npool = 0;
@@ -140,7 +141,17 @@ struct RowProg {
   int splits = 1;      // workgroups per row sharing the outputs of the (single) matmul
   const float* mask = nullptr; const float* area = nullptr; const float* s1 = nullptr; const float* s2 = nullptr;
 };
+// Independent row programs of one launch (blockIdx.y picks the program).
+struct RowProgs {
+  static constexpr int MAX = 3;
+  RowProg p[MAX];
+  int n = 0;
+};
 void launch_row_prog(const RowProg& p, int B, hipStream_t s);
+void launch_row_progs(const RowProgs& ps, int B, hipStream_t s);
+// Gives each matmul of `p` whose weights fit a staged copy in LDS (after the program's features), as long as the
+// program's LDS stays within `max_bytes`.
+void row_prog_stage_weights(RowProg& p, size_t max_bytes);
 
 // Per board point: the policy conv p2 over act(BN(p1 + gpool bias)) * mask, and the ownership conv over
 // act(BN(v1)) * mask, written into the readback rows.

@@ -176,7 +176,8 @@ void launch_small_matmul(const float* in, int ldin, int IC, const float* W, int 
 // launch_pool). The row's mask is staged in LDS first.
 // Matmul: each wave takes a chunk of 64 outputs (weight loads coalesced across them) and a slice of the inputs;
 // partial sums meet in LDS. A program with a single matmul may split its outputs over gridDim.y workgroups per
-// row, so that each streams only its share of the weights.
+// row, so that each streams only its share of the weights. Weights that fit are staged in LDS at the start, all
+// loads of all staged matrices in flight together, so that a chain of small matmuls waits for memory once.
 constexpr int RP_NT = 1024, RP_PPT = 6;  // chunks of <= 64 channels: at least 64 point slots, 6 passes cover 361
 
 // Channels [c0, c0 + C) of one pooling, C <= 64.
@@ -197,6 +198,8 @@ __device__ void row_pool_chunk(const RowProg& P, const RowPool& q, int c0, int C
     sc = *(const floatx4*)(q.scale + c);
     bi = *(const floatx4*)(q.bias + c);
   }
+  // Every global load of the stage is issued before its first barrier (a load after one costs a round trip).
+  const float area = P.area[b], s1 = P.s1[b], s2 = P.s2[b];
   __syncthreads();  // the staged mask
   floatx4 sum = {0.f, 0.f, 0.f, 0.f}, mx = {-FLT_MAX, -FLT_MAX, -FLT_MAX, -FLT_MAX};
   auto accum = [&](auto actc) {  // straight-line per activation (no switch inside the unrolled loop)
@@ -240,10 +243,10 @@ __device__ void row_pool_chunk(const RowProg& P, const RowPool& q, int c0, int C
       s += red[w * C + tid];
       m = fmaxf(m, red[RP_NT + w * C + tid]);
     }
-    const float mean = s / P.area[b];
+    const float mean = s / area;
     feat[c0 + tid] = mean;
-    feat[q.C + c0 + tid] = mean * P.s1[b];
-    feat[2 * q.C + c0 + tid] = q.value ? mean * P.s2[b] : m;
+    feat[q.C + c0 + tid] = mean * s1;
+    feat[2 * q.C + c0 + tid] = q.value ? mean * s2 : m;
   }
   __syncthreads();
 }
@@ -263,9 +266,14 @@ __device__ void row_mm(const RowMM& m, int b, float* lds, float* red, int o_begi
     const int nc = min(NW, nch - ch0), nks = NW / nc;  // chunks this round, K slices per chunk
     const int ch = ch0 + w % nc, ks = w / nc;
     const int o = o_begin + ch * 64 + lane;
+    const bool fin = w < nc && o < o_end;  // this thread finishes output o
+    // Every global load of the stage is issued before its first barrier (a load after one costs a round trip).
+    const float bo = fin && m.bias ? m.bias[o] : 0.f;
+    float* op = fin && m.out ? m.out + (size_t)b * m.ldout + (size_t)o * m.ostride : nullptr;
+    const float prev = op && m.accumulate ? *op : 0.f;
     float acc = 0.f;
     if (ks < nks && o < o_end) {
-      const float* wcol = m.W + o;
+      const float* wcol = (m.wlds >= 0 ? lds + m.wlds : m.W) + o;
       for (int i0 = ks; i0 < m.IC; i0 += KB * nks) {
         float wv[KB], xv[KB];
 #pragma unroll
@@ -280,44 +288,81 @@ __device__ void row_mm(const RowMM& m, int b, float* lds, float* red, int o_begi
     }
     red[w * 64 + lane] = acc;
     __syncthreads();
-    if (w < nc && o < o_end) {
+    if (fin) {
       float v = 0.f;
       for (int k = 0; k < nks; k++) v += red[(k * nc + w) * 64 + lane];
-      if (m.bias) v += m.bias[o];
-      v = act_rt(v, m.act);
+      v = act_rt(v + bo, m.act);
       if (m.dst >= 0) lds[m.dst + o] = v;
-      if (m.out) {
-        float* p = m.out + (size_t)b * m.ldout + (size_t)o * m.ostride;
-        *p = m.accumulate ? *p + v : v;
-      }
+      if (op) *op = prev + v;
     }
     __syncthreads();
   }
 }
 
-__global__ __launch_bounds__(RP_NT) void row_prog_kernel(RowProg P) {
-  // [lds_floats] features and intermediates, [2 RP_NT] reduction scratch, [HW] the row's board mask
-  extern __shared__ float lds[];
+// One row program for row b; with nsplit > 1 this workgroup computes share `split` of the last matmul's outputs.
+__device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, float* lds) {
+  // [lds_floats] features, intermediates and staged weights, [2 RP_NT] reduction scratch, [HW] the row's mask
   float* red = lds + P.lds_floats;
   float* mk = red + 2 * RP_NT;
-  const int b = blockIdx.x;
   if (P.npool > 0)
     for (int p = threadIdx.x; p < HW; p += RP_NT) mk[p] = P.mask[(size_t)b * HW + p];
+  {
+    // Staged weights: the whole set as one list of 16-byte vectors, RP_WB loads per thread in flight.
+    constexpr int RP_WB = 8;
+    int total = 0;
+    for (int k = 0; k < P.nmm; k++)
+      if (P.mm[k].wlds >= 0) total += P.mm[k].IC * P.mm[k].OC / 4;
+    for (int v0 = 0; v0 < total; v0 += RP_NT * RP_WB) {
+      floatx4 buf[RP_WB];
+      float* dst[RP_WB];
+#pragma unroll
+      for (int j = 0; j < RP_WB; j++) {
+        int v = v0 + j * RP_NT + threadIdx.x, k = 0;
+        dst[j] = nullptr;
+        if (v < total) {
+          for (; k < P.nmm; k++) {
+            if (P.mm[k].wlds < 0) continue;
+            const int n4 = P.mm[k].IC * P.mm[k].OC / 4;
+            if (v < n4) break;
+            v -= n4;
+          }
+          buf[j] = *(const floatx4*)(P.mm[k].W + 4 * v);
+          dst[j] = lds + P.mm[k].wlds + 4 * v;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < RP_WB; j++)
+        if (dst[j]) *(floatx4*)dst[j] = buf[j];
+    }
+    __syncthreads();
+  }
   for (int k = 0; k < P.npool; k++) row_pool(P, P.pool[k], b, lds + P.pool[k].dst, red, mk);
   for (int k = 0; k < P.nmm; k++) {
     const RowMM& m = P.mm[k];
     int o0 = 0, o1 = m.OC;
-    if (k == P.nmm - 1 && gridDim.y > 1) {  // this workgroup's share of the last matmul's outputs
-      const int per = (m.OC + gridDim.y - 1) / gridDim.y;
-      o0 = min(m.OC, (int)blockIdx.y * per);
+    if (k == P.nmm - 1 && nsplit > 1) {
+      const int per = (m.OC + nsplit - 1) / nsplit;
+      o0 = min(m.OC, split * per);
       o1 = min(m.OC, o0 + per);
     }
     row_mm(m, b, lds, red, o0, o1);
   }
 }
 
-void launch_row_prog(const RowProg& p, int B, hipStream_t s) {
+// blockIdx.x: the batch row; blockIdx.y: the program (several independent programs), or the output share of the
+// single program's last matmul.
+__global__ __launch_bounds__(RP_NT) void row_prog_kernel(RowProgs PS) {
+  extern __shared__ float lds[];
+  if (PS.n > 1) run_row_prog(PS.p[blockIdx.y], blockIdx.x, 0, 1, lds);
+  else run_row_prog(PS.p[0], blockIdx.x, blockIdx.y, gridDim.y, lds);
+}
+
+static size_t row_prog_check(const RowProg& p) {
   const size_t lds = ((size_t)p.lds_floats + 2 * RP_NT + HW) * sizeof(float);
+  for (int k = 0; k < p.nmm; k++)
+    if (p.mm[k].wlds >= 0 && ((p.mm[k].IC * p.mm[k].OC) % 4 || p.mm[k].wlds % 4 ||
+                              p.mm[k].wlds + p.mm[k].IC * p.mm[k].OC > p.lds_floats))
+      throw std::runtime_error("row program: bad staged weight layout");
   if (lds > 64 * 1024) throw std::runtime_error("row program: too much LDS");
   if (p.splits < 1 || (p.splits > 1 && p.nmm != 1))
     throw std::runtime_error("row program: output splits need exactly one matmul");
@@ -328,8 +373,37 @@ void launch_row_prog(const RowProg& p, int B, hipStream_t s) {
     if (q.C < 4 || last % 4 || 64 % (last / 4) || q.ldx % 4 || q.coff % 4)
       throw std::runtime_error("row program: unsupported pooled channel count or layout");
   }
-  row_prog_kernel<<<dim3(B, p.splits), RP_NT, lds, s>>>(p);
+  return lds;
+}
+
+void launch_row_progs(const RowProgs& ps, int B, hipStream_t s) {
+  if (ps.n < 1 || ps.n > RowProgs::MAX) throw std::runtime_error("row programs: bad count");
+  size_t lds = 0;
+  for (int k = 0; k < ps.n; k++) lds = std::max(lds, row_prog_check(ps.p[k]));
+  if (ps.n > 1)
+    for (int k = 0; k < ps.n; k++)
+      if (ps.p[k].splits != 1) throw std::runtime_error("row programs: output splits need a single program");
+  row_prog_kernel<<<dim3(B, ps.n > 1 ? ps.n : ps.p[0].splits), RP_NT, lds, s>>>(ps);
   KGX_CHECK_LAUNCH();
+}
+
+void row_prog_stage_weights(RowProg& p, size_t max_bytes) {
+  int off = (p.lds_floats + 3) / 4 * 4;
+  for (int k = 0; k < p.nmm; k++) {
+    const int n = p.mm[k].IC * p.mm[k].OC;
+    if (n % 4 == 0 && ((size_t)off + n + 2 * RP_NT + HW) * sizeof(float) <= max_bytes) {
+      p.mm[k].wlds = off;
+      off += n;
+    }
+  }
+  p.lds_floats = off;
+}
+
+void launch_row_prog(const RowProg& p, int B, hipStream_t s) {
+  RowProgs ps;
+  ps.p[0] = p;
+  ps.n = 1;
+  launch_row_progs(ps, B, s);
 }
 
 // ---------------------------------------------------------------------------------------------------------

@@ -691,54 +691,67 @@ void Net::build(const ModelDesc& m) {
   }
   const int P = m.P, S = m.S, rl = row_len_;
   float* out = d_out_;
-  // Row work of both heads in one launch (bin2onnx.py:1495-1531): g1 pooling -> gpool bias of p1 and the pass
-  // logits; value pooling -> v2 -> value and score outputs.
+  // Row work of both heads in one launch (bin2onnx.py:1495-1531), as three independent programs that run side by
+  // side: g1 pooling -> gpool bias of p1; g1 pooling -> the pass logits; value pooling -> v2 -> value and score
+  // outputs. Their small matrices are staged in LDS.
   float* p1b = alloc_f((size_t)max_batch_ * cp);
   {
     const int c2 = m.v2.oc, ph = m.pass1.oc;
     const bool v15 = m.version >= 15;
-    RowProg rp = row_prog_base();
-    int lds = 0;
-    const int fg = lds; lds += 3 * cg;     // g1 features
-    const int fv = lds; lds += 3 * cv;     // value features
-    const int fp = lds; lds += v15 ? ph : 0;  // pass hidden layer
-    const int f2 = lds; lds += c2;         // v2
-    rp.lds_floats = lds;
-    rp.npool = 2;
-    RowPool& pg = rp.pool[0];
+    RowPool pg;
     pg.x = H; pg.ldx = nh; pg.coff = cp; pg.C = cg;
-    pg.scale = upload_f(m.g1_bn.scale); pg.bias = upload_f(m.g1_bn.bias); pg.act = m.g1_act; pg.dst = fg;
-    RowPool& pv = rp.pool[1];
+    pg.scale = upload_f(m.g1_bn.scale); pg.bias = upload_f(m.g1_bn.bias); pg.act = m.g1_act; pg.dst = 0;
+    RowPool pv;
     pv.x = H; pv.ldx = nh; pv.coff = cp + cg; pv.C = cv;
     pv.scale = upload_f(m.v1_bn.scale); pv.bias = upload_f(m.v1_bn.bias); pv.act = m.v1_act; pv.value = true;
-    pv.dst = fv;
-    RowMM& gbm = rp.mm[rp.nmm++];
-    gbm.src = fg; gbm.IC = 3 * cg; gbm.OC = cp; gbm.W = upload_f(m.gpool_to_bias.w); gbm.out = p1b; gbm.ldout = cp;
-    if (v15) {
-      RowMM& p1 = rp.mm[rp.nmm++];
-      p1.src = fg; p1.IC = 3 * cg; p1.OC = ph; p1.W = upload_f(m.pass1.w); p1.bias = upload_f(m.pass_bias.b);
-      p1.act = m.pass_act; p1.dst = fp;
-      RowMM& p2 = rp.mm[rp.nmm++];
-      p2.src = fp; p2.IC = ph; p2.OC = P; p2.W = upload_f(m.pass2.w);
-      p2.out = out + HW; p2.ldout = rl; p2.ostride = HW + 1;
-    } else {
-      RowMM& p1 = rp.mm[rp.nmm++];
-      p1.src = fg; p1.IC = 3 * cg; p1.OC = P; p1.W = upload_f(m.pass1.w);
-      p1.out = out + HW; p1.ldout = rl; p1.ostride = HW + 1;
+    pv.dst = 0;
+    RowProgs ps;
+    ps.n = 3;
+    {  // gpool bias of p1
+      RowProg& rp = ps.p[0];
+      rp = row_prog_base();
+      rp.npool = 1; rp.pool[0] = pg; rp.lds_floats = 3 * cg;
+      RowMM& gbm = rp.mm[rp.nmm++];
+      gbm.src = 0; gbm.IC = 3 * cg; gbm.OC = cp; gbm.W = upload_f(m.gpool_to_bias.w); gbm.out = p1b; gbm.ldout = cp;
     }
-    RowMM& v2 = rp.mm[rp.nmm++];
-    v2.src = fv; v2.IC = 3 * cv; v2.OC = c2; v2.W = upload_f(m.v2.w); v2.bias = upload_f(m.v2_bias.b);
-    v2.act = m.v2_act; v2.dst = f2;
-    RowMM& v3 = rp.mm[rp.nmm++];
-    v3.src = f2; v3.IC = c2; v3.OC = 3; v3.W = upload_f(m.v3.w); v3.bias = upload_f(m.v3_bias.b);
-    v3.out = out + P * (HW + 1); v3.ldout = rl;
-    RowMM& sv = rp.mm[rp.nmm++];
-    sv.src = f2; sv.IC = c2; sv.OC = S; sv.W = upload_f(m.sv3.w); sv.bias = upload_f(m.sv3_bias.b);
-    sv.out = out + P * (HW + 1) + 3; sv.ldout = rl;
+    {  // pass logits
+      RowProg& rp = ps.p[1];
+      rp = row_prog_base();
+      rp.npool = 1; rp.pool[0] = pg; rp.lds_floats = 3 * cg;
+      if (v15) {
+        const int fp = rp.lds_floats; rp.lds_floats += ph;  // pass hidden layer
+        RowMM& p1 = rp.mm[rp.nmm++];
+        p1.src = 0; p1.IC = 3 * cg; p1.OC = ph; p1.W = upload_f(m.pass1.w); p1.bias = upload_f(m.pass_bias.b);
+        p1.act = m.pass_act; p1.dst = fp;
+        RowMM& p2 = rp.mm[rp.nmm++];
+        p2.src = fp; p2.IC = ph; p2.OC = P; p2.W = upload_f(m.pass2.w);
+        p2.out = out + HW; p2.ldout = rl; p2.ostride = HW + 1;
+      } else {
+        RowMM& p1 = rp.mm[rp.nmm++];
+        p1.src = 0; p1.IC = 3 * cg; p1.OC = P; p1.W = upload_f(m.pass1.w);
+        p1.out = out + HW; p1.ldout = rl; p1.ostride = HW + 1;
+      }
+    }
+    {  // value and score outputs
+      RowProg& rp = ps.p[2];
+      rp = row_prog_base();
+      rp.npool = 1; rp.pool[0] = pv; rp.lds_floats = 3 * cv;
+      const int f2 = rp.lds_floats; rp.lds_floats += c2;  // v2
+      RowMM& v2 = rp.mm[rp.nmm++];
+      v2.src = 0; v2.IC = 3 * cv; v2.OC = c2; v2.W = upload_f(m.v2.w); v2.bias = upload_f(m.v2_bias.b);
+      v2.act = m.v2_act; v2.dst = f2;
+      RowMM& v3 = rp.mm[rp.nmm++];
+      v3.src = f2; v3.IC = c2; v3.OC = 3; v3.W = upload_f(m.v3.w); v3.bias = upload_f(m.v3_bias.b);
+      v3.out = out + P * (HW + 1); v3.ldout = rl;
+      RowMM& sv = rp.mm[rp.nmm++];
+      sv.src = f2; sv.IC = c2; sv.OC = S; sv.W = upload_f(m.sv3.w); sv.bias = upload_f(m.sv3_bias.b);
+      sv.out = out + P * (HW + 1) + 3; sv.ldout = rl;
+    }
+    for (int k = 0; k < ps.n; k++) row_prog_stage_weights(ps.p[k], 60 * 1024);
     Op op;
-    op.launch = [=](hipStream_t s, int B) { launch_row_prog(rp, B, s); };
+    op.launch = [=](hipStream_t s, int B) { launch_row_progs(ps, B, s); };
     op.cls = "row_prog";
-    op.bytes_row = (double)HW * (cg + cv) * 4;
+    op.bytes_row = (double)HW * (2 * cg + cv) * 4;
     ops_.push_back(op);
   }
   // Spatial policy and ownership.
