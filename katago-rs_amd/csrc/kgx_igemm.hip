@@ -298,6 +298,28 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
 // per SIMD, at most 128 registers): its 384-channel outputs are 512 workgroups.
 typedef IgCfg<3, 192, 48, 64, 4, 1, 2, 1> Ig3;
 typedef IgCfg<1, 192, 48, 64, 4, 1, 2, 2, 4> Ig1;
+// Wider output tiles keep a 3x3 convolution with more than 192 output channels at four column tiles (one wave
+// of workgroups on 256 CUs at batch 32): 64 channels for up to 256 (a global-pooling block's first conv), 96 for
+// up to 384 (the stem), the latter on 32-channel stages with all eight waves on every tap (its weights for all
+// taps of 96 channels would not fit LDS at 64 channels per stage).
+typedef IgCfg<3, 192, 64, 64, 4, 1, 2, 1> Ig3n64;
+typedef IgCfg<3, 192, 96, 32, 4, 2, 1, 1> Ig3n96;
+
+enum { IG3_48, IG3_64, IG3_96, IG1_48 };
+static int igemm_kind(int ks, int oc) {
+  if (ks == 1) return IG1_48;
+  if (oc <= 4 * Ig3::BN) return IG3_48;
+  if (oc <= 4 * Ig3n64::BN) return IG3_64;
+  return IG3_96;
+}
+static void igemm_tile(int kind, int& bn, int& bk) {
+  switch (kind) {
+    case IG3_48: bn = Ig3::BN; bk = Ig3::BK; break;
+    case IG3_64: bn = Ig3n64::BN; bk = Ig3n64::BK; break;
+    case IG3_96: bn = Ig3n96::BN; bk = Ig3n96::BK; break;
+    default: bn = Ig1::BN; bk = Ig1::BK; break;
+  }
+}
 
 template <typename T, typename C>
 static void igemm_launch(const void* x, int ldx, int IC, const void* w, int icp, int OC, const ConvOut& o, int M,
@@ -308,11 +330,29 @@ static void igemm_launch(const void* x, int ldx, int IC, const void* w, int icp,
   igemm_kernel<T, C><<<grid, C::NT, 0, s>>>((const T*)x, ldx, IC, (const T*)w, icp, OC, M, o);
 }
 
-int conv_igemm_icp(int ks, int ic) { return round_up(ic, ks == 3 ? Ig3::BK : Ig1::BK); }
+template <typename T>
+static void igemm_dispatch(int kind, const void* x, int ldx, int IC, const void* w, int icp, int OC,
+                           const ConvOut& o, int M, hipStream_t s) {
+  switch (kind) {
+    case IG3_48: igemm_launch<T, Ig3>(x, ldx, IC, w, icp, OC, o, M, s); break;
+    case IG3_64: igemm_launch<T, Ig3n64>(x, ldx, IC, w, icp, OC, o, M, s); break;
+    case IG3_96: igemm_launch<T, Ig3n96>(x, ldx, IC, w, icp, OC, o, M, s); break;
+    default: igemm_launch<T, Ig1>(x, ldx, IC, w, icp, OC, o, M, s); break;
+  }
+}
 
-// w [oc][ic][ks][ks] -> [oc tile][tap][BN][icp], zero padding beyond oc and ic.
+int conv_igemm_icp(int ks, int ic, int oc) {
+  int bn, bk;
+  igemm_tile(igemm_kind(ks, oc), bn, bk);
+  return round_up(ic, bk);
+}
+
+// w [oc][ic][ks][ks] -> [oc tile][tap][BN][icp], zero padding beyond oc and ic (BN and icp of the configuration
+// launch_conv_igemm picks for these channel counts).
 void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector<float>& out) {
-  const int bn = ks == 3 ? Ig3::BN : Ig1::BN, taps = ks * ks, icp = conv_igemm_icp(ks, ic);
+  int bn, bk;
+  igemm_tile(igemm_kind(ks, oc), bn, bk);
+  const int taps = ks * ks, icp = round_up(ic, bk);
   const int tiles = (oc + bn - 1) / bn;
   out.assign((size_t)tiles * taps * bn * icp, 0.f);
   for (int o = 0; o < oc; o++)
@@ -325,18 +365,13 @@ void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const v
                        const ConvOut& o, int B, hipStream_t s) {
   if (prec != PREC_F16 && prec != PREC_BF16) throw std::runtime_error("conv_igemm: 16-bit operands only");
   if (ks != 1 && ks != 3) throw std::runtime_error("conv_igemm: 1x1 or 3x3 kernels only");
-  if (IC % 8 != 0 || ldx % 8 != 0 || OC % 4 != 0 || icp != conv_igemm_icp(ks, IC))
+  if (IC % 8 != 0 || ldx % 8 != 0 || OC % 4 != 0 || icp != conv_igemm_icp(ks, IC, OC))
     throw std::runtime_error("conv_igemm: channel counts must be multiples of 8 (inputs) and 4 (outputs)");
   if ((o.y && o.ldy % 4) || (o.yt && o.ldyt % 4) || (o.colbias && o.ld_colbias % 4) || (o.emit.scale && o.emit.ld % 4))
     throw std::runtime_error("conv_igemm: output strides must be multiples of 4");
-  const int M = B * HW;
-  if (prec == PREC_F16) {
-    if (ks == 3) igemm_launch<f16, Ig3>(x, ldx, IC, w, icp, OC, o, M, s);
-    else igemm_launch<f16, Ig1>(x, ldx, IC, w, icp, OC, o, M, s);
-  } else {
-    if (ks == 3) igemm_launch<bf16, Ig3>(x, ldx, IC, w, icp, OC, o, M, s);
-    else igemm_launch<bf16, Ig1>(x, ldx, IC, w, icp, OC, o, M, s);
-  }
+  const int M = B * HW, kind = igemm_kind(ks, OC);
+  if (prec == PREC_F16) igemm_dispatch<f16>(kind, x, ldx, IC, w, icp, OC, o, M, s);
+  else igemm_dispatch<bf16>(kind, x, ldx, IC, w, icp, OC, o, M, s);
   KGX_CHECK_LAUNCH();
 }
 

@@ -84,7 +84,7 @@ void launch_gemm(int prec, const GemmArgs& g, hipStream_t s);
 // Implicit-GEMM 1x1 / 3x3 "same" convolution on 16-bit operands: x compute-type NHWC rows of ldx (IC channels,
 // IC % 8 == 0), w the compute-type conversion of conv_igemm_pack_weights' layout (icp = conv_igemm_icp(ks, IC)),
 // OC % 4 == 0.
-int conv_igemm_icp(int ks, int ic);
+int conv_igemm_icp(int ks, int ic, int oc);
 void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector<float>& out);
 void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const void* w, int icp, int OC,
                        const ConvOut& o, int B, hipStream_t s);

@@ -194,7 +194,7 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
       ops_.push_back(pk);
       xin = packed;
     }
-    const int icp = conv_igemm_icp(ks, icin), taps = ks * ks;
+    const int icp = conv_igemm_icp(ks, icin, oc), taps = ks * ks;
     // Filters over the (zero-padded) input channels icin, then packed per output tile.
     std::vector<float> wi((size_t)oc * icin * taps, 0.f), w;
     for (int oo = 0; oo < oc; oo++)
