@@ -468,8 +468,64 @@ __global__ __launch_bounds__(256) void bias_act_kernel(const float* __restrict__
   out[(size_t)m * ldo + c] = to_t<T>(act_rt(a * scale[c] + bias[c], act) * mask[m]);
 }
 
+// Eight channels per thread: two 16-byte loads of x (and of the per-row bias), one 16-byte store of the result.
+template <typename T, int ACT>
+__global__ __launch_bounds__(256) void bias_act8_kernel(const float* __restrict__ x, int ldx, int C,
+                                                        const float* __restrict__ prebias, int ldpb,
+                                                        const float* __restrict__ scale,
+                                                        const float* __restrict__ bias,
+                                                        const float* __restrict__ mask, T* __restrict__ out, int ldo,
+                                                        int rows) {
+  const int vpr = C / 8;  // vectors per row
+  const long v = (long)blockIdx.x * 256 + threadIdx.x;
+  if (v >= (long)rows * vpr) return;
+  const int m = (int)(v / vpr), c = (int)(v - (long)m * vpr) * 8;
+  const float* xp = x + (size_t)m * ldx + c;
+  floatx4 a0 = *(const floatx4*)xp, a1 = *(const floatx4*)(xp + 4);
+  if (prebias) {
+    const float* pp = prebias + (size_t)(m / HW) * ldpb + c;
+    a0 += *(const floatx4*)pp;
+    a1 += *(const floatx4*)(pp + 4);
+  }
+  const floatx4 s0 = *(const floatx4*)(scale + c), s1 = *(const floatx4*)(scale + c + 4);
+  const floatx4 b0 = *(const floatx4*)(bias + c), b1 = *(const floatx4*)(bias + c + 4);
+  const float mk = mask[m];
+  T t[8];
+#pragma unroll
+  for (int e = 0; e < 4; e++) {
+    t[e] = to_t<T>(act_f<ACT>(a0[e] * s0[e] + b0[e]) * mk);
+    t[4 + e] = to_t<T>(act_f<ACT>(a1[e] * s1[e] + b1[e]) * mk);
+  }
+  *(u32x4*)(out + (size_t)m * ldo + c) = *(const u32x4*)t;
+}
+
+template <typename T>
+static void bias_act8_launch(const float* x, int ldx, int C, const float* prebias, int ld_prebias, const float* scale,
+                             const float* bias, int act, const float* mask, T* out, int ldo, int rows, hipStream_t s) {
+  const long n = (long)rows * (C / 8);
+  const dim3 grid((unsigned)((n + 255) / 256));
+  switch (act) {
+    case ACT_RELU: bias_act8_kernel<T, ACT_RELU><<<grid, 256, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
+    case ACT_MISH: bias_act8_kernel<T, ACT_MISH><<<grid, 256, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
+    case ACT_SILU: bias_act8_kernel<T, ACT_SILU><<<grid, 256, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
+    default: bias_act8_kernel<T, ACT_ID><<<grid, 256, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
+  }
+}
+
 void launch_bias_act(int prec, const float* x, int ldx, int C, const float* prebias, int ld_prebias, const float* scale,
                      const float* bias, int act, const float* mask, void* out, int ldo, int rows, hipStream_t s) {
+  // 16-byte path for 16-bit outputs when every row and channel group is 16-byte aligned.
+  const bool vec = (prec == PREC_F16 || prec == PREC_BF16) && C % 8 == 0 && ldx % 4 == 0 && ldo % 8 == 0 &&
+                   (!prebias || ld_prebias % 4 == 0) && ((uintptr_t)x | (uintptr_t)out | (uintptr_t)scale |
+                                                          (uintptr_t)bias | (uintptr_t)prebias) % 16 == 0;
+  if (vec) {
+    if (prec == PREC_F16)
+      bias_act8_launch<f16>(x, ldx, C, prebias, ld_prebias, scale, bias, act, mask, (f16*)out, ldo, rows, s);
+    else
+      bias_act8_launch<bf16>(x, ldx, C, prebias, ld_prebias, scale, bias, act, mask, (bf16*)out, ldo, rows, s);
+    KGX_CHECK_LAUNCH();
+    return;
+  }
   dim3 block(64, 4), grid((C + 63) / 64, (rows + 3) / 4);
   if (prec == PREC_F16)
     bias_act_kernel<f16><<<grid, block, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, act, mask, (f16*)out, ldo, rows);
