@@ -16,6 +16,7 @@
 // consecutive channels of one pixel with 16-byte loads and stores (conv_store4).
 #include "kgx_device.h"
 
+#include <hip/hip_ext.h>
 #include <vector>
 
 namespace kgx {
@@ -327,7 +328,13 @@ static void igemm_launch(const void* x, int ldx, int IC, const void* w, int icp,
   if (icp % C::BK != 0) throw std::runtime_error("conv_igemm: padded input channels must be a multiple of the stage");
   const int mtiles = (M + C::BM - 1) / C::BM, ntiles = (OC + C::BN - 1) / C::BN;
   dim3 grid(round_up(mtiles, 8) * ntiles);
-  igemm_kernel<T, C><<<grid, C::NT, 0, s>>>((const T*)x, ldx, IC, (const T*)w, icp, OC, M, o);
+  if (g_launch_timing.start) {
+    hipExtLaunchKernelGGL(igemm_kernel<T, C>, grid, dim3(C::NT), 0, s, g_launch_timing.start, g_launch_timing.stop,
+                          0, (const T*)x, ldx, IC, (const T*)w, icp, OC, M, o);
+    g_launch_timing.used = true;
+  } else {
+    igemm_kernel<T, C><<<grid, C::NT, 0, s>>>((const T*)x, ldx, IC, (const T*)w, icp, OC, M, o);
+  }
 }
 
 template <typename T>
@@ -340,6 +347,8 @@ static void igemm_dispatch(int kind, const void* x, int ldx, int IC, const void*
     default: igemm_launch<T, Ig1>(x, ldx, IC, w, icp, OC, o, M, s); break;
   }
 }
+
+thread_local LaunchTiming g_launch_timing;
 
 int conv_igemm_icp(int ks, int ic, int oc) {
   int bn, bk;

@@ -84,6 +84,15 @@ void launch_gemm(int prec, const GemmArgs& g, hipStream_t s);
 // Implicit-GEMM 1x1 / 3x3 "same" convolution on 16-bit operands: x compute-type NHWC rows of ldx (IC channels,
 // IC % 8 == 0), w the compute-type conversion of conv_igemm_pack_weights' layout (icp = conv_igemm_icp(ks, IC)),
 // OC % 4 == 0.
+// Kernel-timing events for the next launch (set by a profiled forward): a launch site that supports them
+// launches through hipExtLaunchKernel, whose dispatch records `start` and `stop` around the kernel itself, and sets
+// `used`. Others leave them alone and are timed by events around their launch.
+struct LaunchTiming {
+  hipEvent_t start = nullptr, stop = nullptr;
+  bool used = false;
+};
+extern thread_local LaunchTiming g_launch_timing;
+
 int conv_igemm_icp(int ks, int ic, int oc);
 void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector<float>& out);
 void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const void* w, int icp, int OC,

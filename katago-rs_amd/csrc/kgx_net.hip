@@ -795,21 +795,33 @@ void Net::run_ops(int B, hipStream_t s) {
     for (const Op& op : ops_) op.launch(s, B);
     return;
   }
-  const size_t need = 2 * ops_.size();
+  // Events around every launch, plus a pair for launch sites that time their kernel itself (LaunchTiming: the
+  // implicit-GEMM convolutions), whose time then excludes the dispatch latency of an eager launch.
+  const size_t need = 4 * ops_.size();
   while (events_.size() < need) {
     hipEvent_t e;
     KGX_HIP(hipEventCreate(&e));
     events_.push_back(e);
   }
+  std::vector<char> kernel_timed(ops_.size(), 0);
   for (size_t k = 0; k < ops_.size(); k++) {
-    KGX_HIP(hipEventRecord(events_[2 * k], s));
-    ops_[k].launch(s, B);
-    KGX_HIP(hipEventRecord(events_[2 * k + 1], s));
+    KGX_HIP(hipEventRecord(events_[4 * k], s));
+    g_launch_timing = LaunchTiming{events_[4 * k + 2], events_[4 * k + 3], false};
+    try {
+      ops_[k].launch(s, B);
+    } catch (...) {
+      g_launch_timing = LaunchTiming{};
+      throw;
+    }
+    kernel_timed[k] = g_launch_timing.used;
+    g_launch_timing = LaunchTiming{};
+    KGX_HIP(hipEventRecord(events_[4 * k + 1], s));
   }
   KGX_HIP(hipStreamSynchronize(s));
   for (size_t k = 0; k < ops_.size(); k++) {
     float ms = 0.f;
-    KGX_HIP(hipEventElapsedTime(&ms, events_[2 * k], events_[2 * k + 1]));
+    if (kernel_timed[k]) KGX_HIP(hipEventElapsedTime(&ms, events_[4 * k + 2], events_[4 * k + 3]));
+    else KGX_HIP(hipEventElapsedTime(&ms, events_[4 * k], events_[4 * k + 1]));
     ProfileClass& pc = profile_[ops_[k].cls];
     pc.name = ops_[k].cls;
     pc.launches++;
