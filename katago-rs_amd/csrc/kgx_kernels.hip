@@ -672,6 +672,285 @@ __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
   }
 }
 
+// Attention on the matrix cores (16-bit handles). A workgroup of four waves takes 128 queries of one (batch row,
+// head); the three query blocks of a head are launched 8 workgroup ids apart, which puts them on one XCD, so its
+// K/V rows come from that XCD's L2 after the first read. Keys go in tiles of 64, double-buffered in LDS: K with
+// RoPE applied ([key][d]) and V transposed ([d][key], keys permuted as below), each tile loaded into registers one
+// tile ahead of its use. Each wave computes S^T = K Q^T for its 32 queries (keys as rows: a lane holds four
+// consecutive keys of one query, so the reductions over keys stay in the lane but for two cross-lane steps), with
+// the key mask bias as the accumulator's initial value, then O^T += V^T P^T. P needs no data movement: for a
+// 32-key block the B operand of a lane is its own eight probabilities (keys 4g..4g+3 of the block's first 16 and
+// of its second 16, g = lane / 16), so V^T holds its keys in that order. The softmax runs online over 32-key
+// blocks (running maximum per query, accumulators rescaled every block). Q carries RoPE and the 1/sqrt(d) scale
+// and is held in registers as B fragments. The output goes through LDS for 16-byte stores.
+constexpr int ATT_QW = 32, ATT_NW = 4, ATT_QB = ATT_QW * ATT_NW, ATT_NQB = (HW + ATT_QB - 1) / ATT_QB;
+constexpr int ATT_KT = 64, ATT_NKT = (HW + ATT_KT - 1) / ATT_KT;
+
+// Position of key kk (0..31) of a 32-key block in the permuted V^T rows.
+__device__ __forceinline__ int att_kpos(int kk) {
+  return kk < 16 ? 8 * (kk >> 2) + (kk & 3) : 8 * ((kk - 16) >> 2) + 4 + ((kk - 16) & 3);
+}
+
+template <typename T>
+__device__ __forceinline__ unsigned att_pack2(float lo, float hi) {
+  return (unsigned)__builtin_bit_cast(unsigned short, to_t<T>(lo)) |
+         ((unsigned)__builtin_bit_cast(unsigned short, to_t<T>(hi)) << 16);
+}
+
+template <typename T, int D, bool ROPE>
+__global__ __launch_bounds__(ATT_NW * 64, 3) void attn_mfma_kernel(AttnArgs a, int nheads_total) {
+  static_assert(D == 16 || D == 32 || D == 64, "head dim");
+  typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
+  constexpr int NT = ATT_NW * 64;
+  constexpr int DP = D < 32 ? 32 : D;  // contraction length of S (zero-padded to an MFMA K)
+  constexpr int KC = DP / 32, DT = D / 16, QT = ATT_QW / 16, KB = ATT_KT / 32;
+  constexpr int HALF = D / 2, NCH = HALF / 8;
+  constexpr int KLD = DP + 16, VLD = ATT_KT + 16;  // LDS row strides (160 / 96-byte rows: conflict-free fragments)
+  constexpr int KS_SZ = ATT_KT * KLD, VS_SZ = D * VLD;
+  constexpr int BUF = (KS_SZ + VS_SZ) * (int)sizeof(T) + ATT_KT * 4;  // bytes per buffer: K, V^T, key bias
+  constexpr int OLD = D + 8, OUT = ATT_NW * ATT_QW * OLD * (int)sizeof(T);
+  constexpr int LDS = 2 * BUF > OUT ? 2 * BUF : OUT;
+  constexpr int KU = ATT_KT * NCH, VU = (ATT_KT / 2) * (D / 8);  // staging units: (key, chunk pair), (key pair, chunk)
+  static_assert(KU <= NT && VU <= NT && BUF % 16 == 0, "staging layout");
+  constexpr float L2E = 1.4426950408889634f;
+  __shared__ __align__(16) char smem[LDS];
+
+  const int g0 = blockIdx.x, slot = g0 >> 3, qb = slot % ATT_NQB, nh = (slot / ATT_NQB) * 8 + (g0 & 7);
+  if (nh >= nheads_total) return;
+  const int h = nh % a.H, n = nh / a.H;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g = lane >> 4;
+  const int kvh = h / (a.H / a.KV);
+  const int qtab = a.q_tables == 1 ? 0 : kvh, ktab = a.k_tables == 1 ? 0 : kvh;
+  const T* qkv = (const T*)a.qkv;
+  const T* kbase = qkv + (size_t)n * HW * a.ldq + a.k_off + kvh * D;
+  const T* vbase = qkv + (size_t)n * HW * a.ldq + a.v_off + kvh * D;
+  const float* mrow = a.mask + (size_t)n * HW;
+
+  // Zero K's padding columns (head dim 16) in both buffers; staging never writes them.
+  if constexpr (DP > D) {
+    for (int i = tid; i < 2 * ATT_KT; i += NT) {
+      T* Ks = (T*)(smem + (i / ATT_KT) * BUF) + (i % ATT_KT) * KLD + D;
+      *(u32x4*)Ks = u32x4{0, 0, 0, 0};
+      *(u32x4*)(Ks + 8) = u32x4{0, 0, 0, 0};
+    }
+  }
+
+  // Q fragments: query qbase + qt*16 + l16, dims kc*32 + 8g .. +8 (zero beyond the head dim and the board).
+  const int qbase = qb * ATT_QB + wave * ATT_QW;
+  frag_t qf[QT][KC];
+#pragma unroll
+  for (int qt = 0; qt < QT; qt++) {
+    const int qi = qbase + qt * 16 + l16;
+#pragma unroll
+    for (int kc = 0; kc < KC; kc++) {
+      const int d0 = kc * 32 + 8 * g;
+      frag_t r;
+#pragma unroll
+      for (int e = 0; e < 8; e++) r[e] = to_t<T>(0.f);
+      if (qi < HW && d0 < D) {
+        const T* qp = qkv + ((size_t)n * HW + qi) * a.ldq + a.q_off + h * D;
+        if constexpr (ROPE) {
+          const bool lo = d0 < HALF;
+          const int p0 = lo ? d0 : d0 - HALF;
+          const frag_t x0 = *(const frag_t*)(qp + p0), x1 = *(const frag_t*)(qp + p0 + HALF);
+          const float* ct = a.cos_t + ((size_t)qtab * HW + qi) * HALF + p0;
+          const float* st = a.sin_t + ((size_t)qtab * HW + qi) * HALF + p0;
+          const floatx4 c0 = *(const floatx4*)ct, c1 = *(const floatx4*)(ct + 4);
+          const floatx4 s0 = *(const floatx4*)st, s1 = *(const floatx4*)(st + 4);
+#pragma unroll
+          for (int e = 0; e < 8; e++) {
+            const float c = e < 4 ? c0[e & 3] : c1[e & 3], sn = e < 4 ? s0[e & 3] : s1[e & 3];
+            const float v0 = (float)x0[e], v1 = (float)x1[e];
+            r[e] = to_t<T>((lo ? v0 * c - v1 * sn : v0 * sn + v1 * c) * a.scale);
+          }
+        } else {
+          const frag_t x = *(const frag_t*)(qp + d0);
+#pragma unroll
+          for (int e = 0; e < 8; e++) r[e] = to_t<T>((float)x[e] * a.scale);
+        }
+      }
+      qf[qt][kc] = r;
+    }
+  }
+
+  // Staging of one key tile: registers (fetch) then LDS (stash).
+  const int ku_key = tid / NCH, ku_c = (tid % NCH) * 8;            // K unit: key, first dim of the low chunk
+  const int vu_pair = tid / (D / 8), vu_c = (tid % (D / 8)) * 8;  // V unit: key pair, first dim of the chunk
+  frag_t kx0, kx1, vx0, vx1;
+  floatx4 c0, c1, s0, s1;
+  float mk = 0.f;
+  auto fetch = [&](int t) {
+    const int k0 = t * ATT_KT;
+    const frag_t z = __builtin_bit_cast(frag_t, u32x4{0, 0, 0, 0});
+    kx0 = kx1 = vx0 = vx1 = z;
+    c0 = c1 = s0 = s1 = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (tid < KU) {
+      const int key = k0 + ku_key;
+      if (key < HW) {
+        const T* kp = kbase + (size_t)key * a.ldq + ku_c;
+        kx0 = *(const frag_t*)kp;
+        kx1 = *(const frag_t*)(kp + HALF);
+        if constexpr (ROPE) {
+          const float* ct = a.cos_t + ((size_t)ktab * HW + key) * HALF + ku_c;
+          const float* st = a.sin_t + ((size_t)ktab * HW + key) * HALF + ku_c;
+          c0 = *(const floatx4*)ct;
+          c1 = *(const floatx4*)(ct + 4);
+          s0 = *(const floatx4*)st;
+          s1 = *(const floatx4*)(st + 4);
+        }
+      }
+    }
+    if (tid < VU) {
+      const int key = k0 + 2 * vu_pair;
+      if (key < HW) vx0 = *(const frag_t*)(vbase + (size_t)key * a.ldq + vu_c);
+      if (key + 1 < HW) vx1 = *(const frag_t*)(vbase + (size_t)(key + 1) * a.ldq + vu_c);
+    }
+    if (tid < ATT_KT) {
+      const int key = k0 + tid;
+      mk = key < HW ? mrow[key] * 3e4f - 3e4f : -1e30f;
+    }
+  };
+  auto stash = [&](int b) {
+    T* Ks = (T*)(smem + b * BUF);
+    T* Vs = Ks + KS_SZ;
+    float* kbias = (float*)(Vs + VS_SZ);
+    if (tid < KU) {
+      frag_t lo = kx0, hi = kx1;
+      if constexpr (ROPE) {
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float c = e < 4 ? c0[e & 3] : c1[e & 3], sn = e < 4 ? s0[e & 3] : s1[e & 3];
+          const float v0 = (float)kx0[e], v1 = (float)kx1[e];
+          lo[e] = to_t<T>(v0 * c - v1 * sn);
+          hi[e] = to_t<T>(v0 * sn + v1 * c);
+        }
+      }
+      *(frag_t*)(Ks + ku_key * KLD + ku_c) = lo;
+      *(frag_t*)(Ks + ku_key * KLD + ku_c + HALF) = hi;
+    }
+    if (tid < VU) {
+      const int kk = 2 * vu_pair, pos = (kk & ~31) + att_kpos(kk & 31);
+#pragma unroll
+      for (int e = 0; e < 8; e++) *(unsigned*)(Vs + (vu_c + e) * VLD + pos) = att_pack2<T>((float)vx0[e], (float)vx1[e]);
+    }
+    if (tid < ATT_KT) kbias[tid] = mk;
+  };
+
+  floatx4 o[DT][QT];
+  float mref[QT], lsum[QT];
+#pragma unroll
+  for (int qt = 0; qt < QT; qt++) {
+    mref[qt] = -FLT_MAX;
+    lsum[qt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++) o[dt][qt] = floatx4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  fetch(0);
+  stash(0);
+  __syncthreads();
+  for (int t = 0; t < ATT_NKT; t++) {
+    if (t + 1 < ATT_NKT) fetch(t + 1);
+    const T* Ks = (const T*)(smem + (t & 1) * BUF);
+    const T* Vs = Ks + KS_SZ;
+    const float* kbias = (const float*)(Vs + VS_SZ);
+    // Per 32-key block: S^T tiles [key tile][query tile] with the key bias as initial accumulator, softmax
+    // numerators (exp2 of log2(e)-scaled differences) as B fragments, O^T += V^T P^T.
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++) {
+      floatx4 sc[2][QT];
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int kt = 2 * kb + j;
+        frag_t kf[KC];
+#pragma unroll
+        for (int kc = 0; kc < KC; kc++) kf[kc] = *(const frag_t*)(Ks + (kt * 16 + l16) * KLD + kc * 32 + 8 * g);
+        const floatx4 bias = *(const floatx4*)(kbias + kt * 16 + 4 * g);
+#pragma unroll
+        for (int qt = 0; qt < QT; qt++) {
+          floatx4 c = bias;
+#pragma unroll
+          for (int kc = 0; kc < KC; kc++) {
+            if constexpr (std::is_same<T, f16>::value)
+              c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kc], qf[qt][kc], c, 0, 0, 0);
+            else
+              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kc], qf[qt][kc], c, 0, 0, 0);
+          }
+          sc[j][qt] = c;
+        }
+      }
+      frag_t pf[QT];
+#pragma unroll
+      for (int qt = 0; qt < QT; qt++) {
+        float mx = fmaxf(sc[0][qt][0], sc[1][qt][0]);
+#pragma unroll
+        for (int r = 1; r < 4; r++) mx = fmaxf(mx, fmaxf(sc[0][qt][r], sc[1][qt][r]));
+        mx = fmaxf(mx, __shfl_xor(mx, 16));
+        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        const float mnew = fmaxf(mref[qt], mx);
+        const float alpha = __builtin_amdgcn_exp2f((mref[qt] - mnew) * L2E);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[dt][qt] *= alpha;
+        mref[qt] = mnew;
+        const float ml = mnew * L2E;
+        float ps = 0.f;
+        frag_t pr;
+#pragma unroll
+        for (int j = 0; j < 2; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++) {
+            const float pv = __builtin_amdgcn_exp2f(fmaf(sc[j][qt][r], L2E, -ml));
+            ps += pv;
+            pr[4 * j + r] = to_t<T>(pv);
+          }
+        lsum[qt] = lsum[qt] * alpha + ps;
+        pf[qt] = pr;
+      }
+#pragma unroll
+      for (int dt = 0; dt < DT; dt++) {
+        const frag_t vf = *(const frag_t*)(Vs + (dt * 16 + l16) * VLD + kb * 32 + 8 * g);
+#pragma unroll
+        for (int qt = 0; qt < QT; qt++) {
+          if constexpr (std::is_same<T, f16>::value)
+            o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[qt], o[dt][qt], 0, 0, 0);
+          else
+            o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qt], o[dt][qt], 0, 0, 0);
+        }
+      }
+    }
+    if (t + 1 < ATT_NKT) stash((t + 1) & 1);
+    __syncthreads();
+  }
+
+  // Normalize (each lane's sum covers its own keys: add the four lane groups), transpose through LDS
+  // ([wave][query][d]) and store 16-byte vectors of the queries on the board.
+  T* Os = (T*)smem + wave * ATT_QW * OLD;
+#pragma unroll
+  for (int qt = 0; qt < QT; qt++) {
+    float l = lsum[qt];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const float inv = l > 0.f ? 1.f / l : 0.f;
+#pragma unroll
+    for (int dt = 0; dt < DT; dt++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) Os[(qt * 16 + l16) * OLD + dt * 16 + 4 * g + r] = to_t<T>(o[dt][qt][r] * inv);
+  }
+  __syncthreads();
+  for (int e = lane; e < ATT_QW * (D / 8); e += 64) {
+    const int qq = e / (D / 8), d0 = (e % (D / 8)) * 8, qi = qbase + qq;
+    if (qi < HW) *(u32x4*)((T*)a.out + ((size_t)n * HW + qi) * a.ldo + h * D + d0) = *(const u32x4*)(Os + qq * OLD + d0);
+  }
+}
+
+template <typename T, int D>
+static void attn_mfma_d(const AttnArgs& a, int B, hipStream_t s) {
+  const int nh = B * a.H;
+  dim3 grid((nh + 7) / 8 * 8 * ATT_NQB);
+  if (a.q_tables > 0) attn_mfma_kernel<T, D, true><<<grid, ATT_NW * 64, 0, s>>>(a, nh);
+  else attn_mfma_kernel<T, D, false><<<grid, ATT_NW * 64, 0, s>>>(a, nh);
+}
+
 template <typename T, int D>
 static void attn_d(const AttnArgs& a, int B, hipStream_t s) {
   dim3 grid((HW + 63) / 64, a.H, B);
@@ -690,9 +969,23 @@ static void attn_t(const AttnArgs& a, int B, hipStream_t s) {
   }
 }
 
+template <typename T>
+static void attn_mfma_t(const AttnArgs& a, int B, hipStream_t s) {
+  if (a.dq != a.dv) throw std::runtime_error("attention: dq != dv unsupported");
+  // 16-byte rows of q/k/v and of the output.
+  if (a.ldq % 8 || a.q_off % 8 || a.k_off % 8 || a.v_off % 8 || a.ldo % 8)
+    throw std::runtime_error("attention: q/k/v and output offsets must be multiples of 8 elements");
+  switch (a.dq) {
+    case 16: attn_mfma_d<T, 16>(a, B, s); break;
+    case 32: attn_mfma_d<T, 32>(a, B, s); break;
+    case 64: attn_mfma_d<T, 64>(a, B, s); break;
+    default: throw std::runtime_error("attention: head dim must be 16, 32 or 64");
+  }
+}
+
 void launch_attention(int prec, const AttnArgs& a, int B, hipStream_t s) {
-  if (prec == PREC_F16) attn_t<f16>(a, B, s);
-  else if (prec == PREC_BF16) attn_t<bf16>(a, B, s);
+  if (prec == PREC_F16) attn_mfma_t<f16>(a, B, s);
+  else if (prec == PREC_BF16) attn_mfma_t<bf16>(a, B, s);
   else attn_t<float>(a, B, s);
   KGX_CHECK_LAUNCH();
 }

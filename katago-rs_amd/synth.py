@@ -134,6 +134,9 @@ def tiny_nets() -> dict:
         "t_tf": Arch("t-tf", 15, 64, [("attn", 2, 2, 32, 32, "fixed"), ("ffn", 128, True),
                                       ("attn", 4, 2, 16, 16, "learnable"), ("ffn", 96, False)],
                      p1_c=16, g1_c=16, v1_c=16, v2_c=24),
+        "t_tf64": Arch("t-tf64", 15, 96, [("attn", 2, 1, 64, 64, "fixed"), ("ffn", 128, True),
+                                          ("attn", 2, 2, 64, 64, "none"), ("ffn", 96, True)],
+                       p1_c=16, g1_c=16, v1_c=16, v2_c=24),
         "t_human": Arch("t-human", 15, 32, [("res", 32), ("gpool", 32, 16)], meta_encoder=1, meta_c=32,
                         gpool_c=16, p1_c=16, g1_c=16, v1_c=16, v2_c=24),
         "t_rms": Arch("t-rms", 17, 64, [("nbt", 32, [("attn", 2, 2, 16, 16, "fixed"), ("ffn", 64, True)]),

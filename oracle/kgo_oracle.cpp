@@ -635,7 +635,13 @@ struct Fwd {
       rot(q, H, true);
       rot(k, KV, false);
     }
-    const R scale = (R)(1.0f / std::sqrt((float)dq));
+    R scale = (R)(1.0f / std::sqrt((float)dq));
+    if (qa) {
+      // 16-bit storage feeds the matrix cores: the scaled, rotated queries and the rotated keys are operands.
+      for (auto& z : q) z = ra(z * scale);
+      for (auto& z : k) z = ra(z);
+      scale = R(1);
+    }
     std::vector<R> o((size_t)n * HW * H * dv, R(0));
 #pragma omp parallel for collapse(2) schedule(static) num_threads(threads)
     for (int b = 0; b < n; b++)
@@ -656,8 +662,10 @@ struct Fwd {
           R den = 0;
           for (int j = 0; j < HW; j++) { sc[j] = std::exp(sc[j] - mx); den += sc[j]; }
           R* oi = &o[((size_t)b * HW + i) * H * dv + (size_t)h * dv];
+          // With 16-bit storage the unnormalized probabilities are operands too; the denominator stays exact.
+          const R inv = R(1) / den;
           for (int j = 0; j < HW; j++) {
-            const R pj = sc[j] / den;
+            const R pj = ra(sc[j]) * inv;
             const R* vj = &v[((size_t)b * HW + j) * KV * dv + (size_t)kh * dv];
             for (int d = 0; d < dv; d++) oi[d] += pj * vj[d];
           }

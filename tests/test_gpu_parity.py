@@ -72,7 +72,7 @@ def golden():
 
 
 @pytest.mark.parametrize("prec", ["f32", "f16", "bf16"])
-@pytest.mark.parametrize("name", ["t_res", "t_nbt", "t_v8", "t_tf", "t_human", "t_rms", "t_rmspos"])
+@pytest.mark.parametrize("name", ["t_res", "t_nbt", "t_v8", "t_tf", "t_tf64", "t_human", "t_rms", "t_rmspos"])
 def test_tiny_nets_match_oracle(kgx, synth, oracle, golden, name, prec):
     g, m0 = golden
     arch = synth.tiny_nets()[name]

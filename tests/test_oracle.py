@@ -64,7 +64,7 @@ def _tiny(synth):
     return synth.tiny_nets()
 
 
-@pytest.mark.parametrize("name", ["t_res", "t_nbt", "t_v8", "t_tf", "t_human", "t_rms", "t_rmspos"])
+@pytest.mark.parametrize("name", ["t_res", "t_nbt", "t_v8", "t_tf", "t_tf64", "t_human", "t_rms", "t_rmspos"])
 def test_oracle_matches_independent_torch_forward(oracle, synth, name):
     arch = _tiny(synth)[name]
     mb, tree = synth.write_model_tree(arch, 11)
