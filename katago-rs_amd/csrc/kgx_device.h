@@ -91,6 +91,40 @@ __device__ __forceinline__ void conv_store(const ConvOut& o, int m, int n, float
         to_t<T>(act_rt(v * o.emit.scale[n] + o.emit.bias[n], o.emit.act) * o.emit.mask[m]);
 }
 
+// Epilogue for four consecutive channels n..n+3 of pixel m (conv_store on a float4). The per-pixel inputs come
+// preloaded: the residual `yacc` (when o.accumulate), the row mask `rm`, the emit scale/bias `es`/`eb` of the
+// four channels and the emit mask `mk` (the epilogue's stores may alias them as far as the compiler knows, so a
+// load placed between stores would wait a full round trip). The column bias (the stem's global input bias, one
+// launch per forward) is read inline.
+// Four consecutive compute-type values in one store (8 bytes for 16-bit types, 16 for float).
+template <typename T>
+__device__ __forceinline__ void store4(T* p, float a, float b, float c, float d) {
+  if constexpr (sizeof(T) == 4) {
+    *(floatx4*)p = floatx4{a, b, c, d};
+  } else {
+    T t[4] = {to_t<T>(a), to_t<T>(b), to_t<T>(c), to_t<T>(d)};
+    *(uint2*)p = *(const uint2*)t;
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floatx4 v, floatx4 yacc, float rm,
+                                            floatx4 es, floatx4 eb, float mk) {
+  if (o.colbias) v += *(const floatx4*)(o.colbias + (size_t)(m / HW) * o.ld_colbias + n);
+  if (o.rowmask) v *= rm;
+  if (o.yt) store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, v[0], v[1], v[2], v[3]);
+  if (o.y) {
+    if (o.accumulate) v += yacc;
+    *(floatx4*)(o.y + (size_t)m * o.ldy + n) = v;
+  }
+  if (o.emit.scale) {
+    float t[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) t[e] = act_rt(v[e] * es[e] + eb[e], o.emit.act) * mk;
+    store4<T>((T*)o.emit.out + (size_t)m * o.emit.ld + n, t[0], t[1], t[2], t[3]);
+  }
+}
+
 // Winograd F(TM x TM, 3x3) geometry on the 19x19 board.
 template <int TM>
 struct Wino {

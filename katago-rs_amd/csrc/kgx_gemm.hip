@@ -22,15 +22,21 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN;
   constexpr int VEC = Tile<T>::VEC;
   constexpr int BK = sizeof(T) == 2 ? C::BKH : C::BKH / 2;
-  constexpr int LDK = BK + VEC;
+  // 128-byte rows (16-bit, BK = 64) are stored unpadded with their 16-byte chunks swizzled (chunk ^ (row/2 % 8)):
+  // the 16 rows x 4 chunks of a fragment read then hit distinct banks. Other widths pad rows by 16 bytes.
+  constexpr bool SWZ = sizeof(T) == 2 && BK == 64;
+  constexpr int LDK = SWZ ? BK : BK + VEC;
   constexpr int KV = BK / VEC;                       // 16-byte vectors per tile row
   constexpr int AV = BM * KV / 256, BV = BN * KV / 256;
   static_assert(AV * 256 == BM * KV && BV * 256 == BN * KV, "tile not divisible over 256 threads");
   constexpr int WTM = BM / WM, WTN = BN / WN;        // wave tile
   constexpr int MB = WTM / 16, NB = WTN / 16;        // MFMA blocks per wave
   constexpr int KS = sizeof(T) == 2 ? 32 : 4;        // K per MFMA
-  __shared__ __align__(16) T As[2][BM * LDK];
-  __shared__ __align__(16) T Bs[2][BN * LDK];
+  constexpr int ELD = BN + 4;                        // epilogue float tile row stride
+  constexpr int STAGE = 2 * (BM + BN) * LDK * (int)sizeof(T), EPI = BM * ELD * 4;
+  __shared__ __align__(16) char smem[STAGE > EPI ? STAGE : EPI];
+  T (*As)[BM * LDK] = (T (*)[BM * LDK])smem;
+  T (*Bs)[BN * LDK] = (T (*)[BN * LDK])(smem + 2 * BM * LDK * sizeof(T));
   typedef u32x4 vec_t;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -50,14 +56,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     const int idx = tid + 256 * v;
     a_row[v] = idx / KV;
     a_kk[v] = (idx % KV) * VEC;
-    a_s[v] = a_row[v] * LDK + a_kk[v];
+    a_s[v] = a_row[v] * LDK + (SWZ ? ((a_kk[v] / VEC) ^ ((a_row[v] >> 1) & 7)) * VEC : a_kk[v]);
   }
 #pragma unroll
   for (int v = 0; v < BV; v++) {
     const int idx = tid + 256 * v;
     b_row[v] = idx / KV;
     b_kk[v] = (idx % KV) * VEC;
-    b_s[v] = b_row[v] * LDK + b_kk[v];
+    b_s[v] = b_row[v] * LDK + (SWZ ? ((b_kk[v] / VEC) ^ ((b_row[v] >> 1) & 7)) * VEC : b_kk[v]);
   }
   const T* At0 = At + (size_t)m0 * g.lda;
   const float* Af0 = Af + (size_t)m0 * g.lda;
@@ -138,17 +144,21 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   __syncthreads();
   const int r16 = lane & 15, g4 = lane >> 4;
   const int koff = sizeof(T) == 2 ? g4 * 8 : g4;
+  // Swizzled chunk of this lane's fragment reads: (kk/8 + g4) ^ sw = (kk/8) ^ (g4 ^ sw), kk/8 in {0, 4}.
+  const int sw = SWZ ? (g4 ^ ((r16 >> 1) & 7)) : 0;
   for (int kt = 0; kt < nk; kt++) {
     const int cur = kt & 1;
     if (kt + 1 < nk) load((kt + 1) * BK);
-    const T* as = As[cur] + (wm * WTM + r16) * LDK + koff;
-    const T* bs = Bs[cur] + (wn * WTN + r16) * LDK + koff;
+    const T* as = As[cur] + (wm * WTM + r16) * LDK + (SWZ ? 0 : koff);
+    const T* bs = Bs[cur] + (wn * WTN + r16) * LDK + (SWZ ? 0 : koff);
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += KS)
+    for (int kk = 0; kk < BK; kk += KS) {
+      const int ko = SWZ ? ((kk / 8) ^ sw) * 8 : kk;
 #pragma unroll
       for (int i = 0; i < MB; i++)
 #pragma unroll
-        for (int j = 0; j < NB; j++) acc[i][j] = mfma16<T>(as + i * 16 * LDK + kk, bs + j * 16 * LDK + kk, acc[i][j]);
+        for (int j = 0; j < NB; j++) acc[i][j] = mfma16<T>(as + i * 16 * LDK + ko, bs + j * 16 * LDK + ko, acc[i][j]);
+    }
     if (kt + 1 < nk) store(cur ^ 1, (kt + 1) * BK);
     __syncthreads();
   }
@@ -158,17 +168,67 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
     if (o.y) o.y += (size_t)z * g.sC;
     if (o.yt) o.yt = (T*)o.yt + (size_t)z * g.sC;
   }
-  // Output element (i, j, r) of this lane: row wm*WTM + i*16 + 4*(lane/16) + r, column wn*WTN + j*16 + lane%16.
+  if (!g.vec_epi) {
+    // Output element (i, j, r) of this lane: row wm*WTM + i*16 + 4*(lane/16) + r, column wn*WTN + j*16 + lane%16.
+#pragma unroll
+    for (int i = 0; i < MB; i++)
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          const int m = m0 + wm * WTM + i * 16 + 4 * (lane >> 4) + r;
+          const int nn = n0 + wn * WTN + j * 16 + (lane & 15);
+          if (m < M && nn < N) conv_store<T>(o, m, nn, acc[i][j][r]);
+        }
+    return;
+  }
+  // Epilogue through LDS (the stage buffers are free after the loop's last barrier): the float tile, then four
+  // consecutive columns of one row per thread with 16-byte accesses, the per-row and per-column inputs loaded
+  // ahead of the stores.
+  float* Et = (float*)smem;
 #pragma unroll
   for (int i = 0; i < MB; i++)
 #pragma unroll
     for (int j = 0; j < NB; j++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) {
-        const int m = m0 + wm * WTM + i * 16 + 4 * (lane >> 4) + r;
-        const int nn = n0 + wn * WTN + j * 16 + (lane & 15);
-        if (m < M && nn < N) conv_store<T>(o, m, nn, acc[i][j][r]);
+      for (int r = 0; r < 4; r++) Et[(wm * WTM + i * 16 + 4 * g4 + r) * ELD + wn * WTN + j * 16 + r16] = acc[i][j][r];
+  __syncthreads();
+  if (g.glu) {
+    constexpr int HV = BN / 8;  // 4-wide vectors of gated outputs per tile row
+    for (int e = tid; e < BM * HV; e += 256) {
+      const int r = e / HV, hc = (e % HV) * 4, lc = (hc / 16) * 32 + hc % 16;
+      const int m = m0 + r, f = n0 / 2 + hc;
+      if (m < M && f < N / 2) {
+        const floatx4 a = *(const floatx4*)(Et + r * ELD + lc), b = *(const floatx4*)(Et + r * ELD + lc + 16);
+        store4<T>((T*)o.yt + (size_t)m * o.ldyt + f, act_f<ACT_SILU>(a[0]) * b[0], act_f<ACT_SILU>(a[1]) * b[1],
+                  act_f<ACT_SILU>(a[2]) * b[2], act_f<ACT_SILU>(a[3]) * b[3]);
       }
+    }
+    return;
+  }
+  constexpr int CV = BN / 4, EV = BM * CV / 256;
+  static_assert(EV * 256 == BM * CV, "epilogue vectors not divisible over 256 threads");
+  floatx4 yres[EV];
+  float rmv[EV], mkv[EV];
+#pragma unroll
+  for (int v = 0; v < EV; v++) {
+    const int e = tid + 256 * v, m = min(m0 + e / CV, M - 1), n = min(n0 + (e % CV) * 4, N - 4);
+    yres[v] = o.y && o.accumulate ? *(const floatx4*)(o.y + (size_t)m * o.ldy + n) : floatx4{0.f, 0.f, 0.f, 0.f};
+    rmv[v] = o.rowmask ? o.rowmask[m] : 1.f;
+    mkv[v] = o.emit.scale ? o.emit.mask[m] : 1.f;
+  }
+#pragma unroll
+  for (int v = 0; v < EV; v++) {
+    const int e = tid + 256 * v, r = e / CV, c = (e % CV) * 4, m = m0 + r, n = n0 + c;
+    if (m < M && n < N) {
+      floatx4 es = {1.f, 1.f, 1.f, 1.f}, eb = {0.f, 0.f, 0.f, 0.f};
+      if (o.emit.scale) {
+        es = *(const floatx4*)(o.emit.scale + n);
+        eb = *(const floatx4*)(o.emit.bias + n);
+      }
+      conv_store4<T>(o, m, n, *(const floatx4*)(Et + r * ELD + c), yres[v], rmv[v], es, eb, mkv[v]);
+    }
+  }
 }
 
 // Tile configurations: narrow rows over all of a <= 192-wide N (1x1 convolutions, Winograd point GEMMs: the
@@ -212,12 +272,35 @@ static void gemm_t(const GemmArgs& g, hipStream_t s) {
   }
 }
 
-void launch_gemm(int prec, const GemmArgs& g, hipStream_t s) {
-  if (g.M <= 0 || g.N <= 0 || g.K <= 0) return;
+static bool aligned(const void* p, size_t a) { return ((uintptr_t)p & (a - 1)) == 0; }
+
+// Whether the four-column vector epilogue applies: every output row and column block it touches is 16-byte
+// (float) / 8-byte (16-bit) aligned.
+static bool vector_epilogue_ok(const GemmArgs& g, int tsize) {
+  const ConvOut& o = g.out;
+  if (g.N % 4 || (g.Z > 1 && g.sC % 4)) return false;
+  if (o.y && (o.ldy % 4 || !aligned(o.y, 16))) return false;
+  if (o.yt && (o.ldyt % 4 || !aligned(o.yt, 4 * tsize))) return false;
+  if (o.colbias && (o.ld_colbias % 4 || !aligned(o.colbias, 16))) return false;
+  if (o.emit.scale && (o.emit.ld % 4 || !aligned(o.emit.out, 4 * tsize) || !aligned(o.emit.scale, 16) ||
+                       !aligned(o.emit.bias, 16)))
+    return false;
+  return true;
+}
+
+void launch_gemm(int prec, const GemmArgs& g0, hipStream_t s) {
+  if (g0.M <= 0 || g0.N <= 0 || g0.K <= 0) return;
   const int vec = prec == PREC_F32 ? 4 : 8;
-  if (g.K % vec != 0 || g.lda % vec != 0 || g.ldb % vec != 0)
+  if (g0.K % vec != 0 || g0.lda % vec != 0 || g0.ldb % vec != 0)
     throw std::runtime_error("gemm: K and strides must be multiples of the vector width");
-  if (g.Z > 1 && g.out.emit.scale) throw std::runtime_error("gemm: batched GEMMs carry no emission");
+  if (g0.Z > 1 && g0.out.emit.scale) throw std::runtime_error("gemm: batched GEMMs carry no emission");
+  GemmArgs g = g0;
+  g.vec_epi = vector_epilogue_ok(g, prec == PREC_F32 ? 4 : 2);
+  if (g.glu) {
+    const ConvOut& o = g.out;
+    if (!g.vec_epi || g.N % 32 || g.Z != 1 || !o.yt || o.y || o.emit.scale || o.colbias || o.rowmask)
+      throw std::runtime_error("gemm: the gated output needs N % 32 == 0, one GEMM and only a compute-type store");
+  }
   if (prec == PREC_F16) gemm_t<f16>(g, s);
   else if (prec == PREC_BF16) gemm_t<bf16>(g, s);
   else gemm_t<float>(g, s);

@@ -33,32 +33,6 @@ struct IgCfg {
   static constexpr int NT = WM * WN * 64 * G_;
 };
 
-// Epilogue for four consecutive channels n..n+3 of pixel m (conv_store on a float4). The per-pixel inputs come
-// preloaded: the residual `yacc` (when o.accumulate), the row mask `rm`, the emit scale/bias `es`/`eb` of the
-// four channels and the emit mask `mk` (the epilogue's stores may alias them as far as the compiler knows, so a
-// load placed between stores would wait a full round trip). The column bias (the stem's global input bias, one
-// launch per forward) is read inline.
-template <typename T>
-__device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floatx4 v, floatx4 yacc, float rm,
-                                            floatx4 es, floatx4 eb, float mk) {
-  if (o.colbias) v += *(const floatx4*)(o.colbias + (size_t)(m / HW) * o.ld_colbias + n);
-  if (o.rowmask) v *= rm;
-  if (o.yt) {
-    T t[4] = {to_t<T>(v[0]), to_t<T>(v[1]), to_t<T>(v[2]), to_t<T>(v[3])};
-    *(uint2*)((T*)o.yt + (size_t)m * o.ldyt + n) = *(const uint2*)t;
-  }
-  if (o.y) {
-    if (o.accumulate) v += yacc;
-    *(floatx4*)(o.y + (size_t)m * o.ldy + n) = v;
-  }
-  if (o.emit.scale) {
-    T t[4];
-#pragma unroll
-    for (int e = 0; e < 4; e++) t[e] = to_t<T>(act_rt(v[e] * es[e] + eb[e], o.emit.act) * mk);
-    *(uint2*)((T*)o.emit.out + (size_t)m * o.emit.ld + n) = *(const uint2*)t;
-  }
-}
-
 template <typename T, typename C>
 __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restrict__ X, int ldx, int IC, const T* __restrict__ W,
                                                       int icp, int OC, int M, ConvOut o) {

@@ -78,6 +78,10 @@ struct GemmArgs {
   bool a_float = false;        // A holds float (converted, with `pro` applied when pro.scale)
   Prologue pro;
   ConvOut out;
+  // Gated output (SwiGLU): the columns come in 16-wide pairs of blocks (value block, gate block) and the GEMM
+  // writes only out.yt[m][f] = silu(C[m][32 (f / 16) + f % 16]) * C[m][32 (f / 16) + 16 + f % 16], f < N / 2.
+  bool glu = false;
+  bool vec_epi = false;  // set by launch_gemm: the four-column vector epilogue applies
 };
 void launch_gemm(int prec, const GemmArgs& g, hipStream_t s);
 

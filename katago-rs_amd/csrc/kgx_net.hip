@@ -149,7 +149,7 @@ void Net::scan(const std::vector<BlockDesc>& blocks, int c, int depth) {
         break;
       case BLOCK_FFN:
         nrm_c_ = std::max(nrm_c_, c);
-        u_c_ = std::max(u_c_, b.swiglu ? 2 * b.ffn_c : b.ffn_c);
+        if (b.swiglu && b.ffn_c % 16) u_c_ = std::max(u_c_, 2 * b.ffn_c);  // the unfused SwiGLU's float u
         h_c_ = std::max(h_c_, b.ffn_c);
         break;
     }
@@ -303,7 +303,7 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
 }
 
 std::shared_ptr<ConvOut> Net::emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, const ConvOut& o,
-                                              const char* cls) {
+                                              const char* cls, bool glu) {
   const int prec = prec_;
   auto out = std::make_shared<ConvOut>(o);
   Op op;
@@ -313,12 +313,15 @@ std::shared_ptr<ConvOut> Net::emit_token_gemm(const void* A, int lda, const void
     g.Bt = Bt; g.ldb = K;
     g.out = *out;
     g.M = B * HW; g.N = N; g.K = K;
+    g.glu = glu;
     launch_gemm(prec, g, s);
   };
   op.cls = cls;
   const double ts = (double)tsize();
   op.flops_row = 2.0 * HW * K * N;
-  op.bytes_row = (double)HW * K * ts + (double)HW * N * ((o.y ? 4.0 : 0.0) * (o.accumulate ? 2 : 1) + (o.yt ? ts : 0.0));
+  op.bytes_row = (double)HW * K * ts +
+                 (double)HW * N * ((o.y ? 4.0 : 0.0) * (o.accumulate ? 2 : 1) + (o.yt ? (glu ? ts / 2 : ts) : 0.0) +
+                                   (o.emit.scale ? ts : 0.0));
   op.bytes_fixed = (double)K * N * ts;
   op.out = out;
   op.out_c = N;
@@ -425,11 +428,21 @@ void Net::emit_ffn(const BlockDesc& b, int depth) {
   float* x = ss_[depth].x;
   const int c = ss_[depth].c;
   const int F = b.ffn_c, Fu = b.swiglu ? 2 * F : F;
+  // The activation runs in the first GEMM's epilogue: SwiGLU through its gated output, whose B^T rows alternate
+  // 16 value features and the 16 matching gate features (F % 16 == 0; otherwise u = [value | gate] goes through
+  // the separate activation kernel); mish through the emission (unit scale, zero bias, board mask: masked rows of
+  // h only reach output rows that the second GEMM masks).
+  const bool fused = !b.swiglu || F % 16 == 0;
+  auto row_of = [&](int f, bool gate) {
+    if (!b.swiglu) return f;
+    if (!fused) return gate ? F + f : f;
+    return (f / 16) * 32 + (gate ? 16 : 0) + f % 16;
+  };
   std::vector<float> w1((size_t)Fu * c);
   for (int f = 0; f < F; f++)
     for (int k = 0; k < c; k++) {
-      w1[(size_t)f * c + k] = b.l1.w[(size_t)k * F + f];
-      if (b.swiglu) w1[(size_t)(F + f) * c + k] = b.lg.w[(size_t)k * F + f];
+      w1[(size_t)row_of(f, false) * c + k] = b.l1.w[(size_t)k * F + f];
+      if (b.swiglu) w1[(size_t)row_of(f, true) * c + k] = b.lg.w[(size_t)k * F + f];
     }
   const void* dW1 = upload_t(w1);
   std::vector<float> w2((size_t)c * F);
@@ -446,17 +459,31 @@ void Net::emit_ffn(const BlockDesc& b, int depth) {
   rn.bytes_row = (double)HW * c * (4 + tsize());
   ops_.push_back(rn);
   ConvOut o1;
-  o1.y = u_;
-  o1.ldy = Fu;
-  emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm");
-  float* u = u_;
-  void* h = h_;
-  const bool gated = b.swiglu;
-  Op fa;
-  fa.launch = [=](hipStream_t s, int B) { launch_ffn_act(prec, u, Fu, F, gated, h, F, B * HW, s); };
-  fa.cls = "ffn_act";
-  fa.bytes_row = (double)HW * Fu * 4 + (double)HW * F * tsize();
-  ops_.push_back(fa);
+  if (fused && b.swiglu) {
+    o1.yt = h_;
+    o1.ldyt = F;
+    emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm", true);
+  } else if (fused) {
+    o1.emit.scale = upload_f(std::vector<float>(F, 1.f));
+    o1.emit.bias = upload_f(std::vector<float>(F, 0.f));
+    o1.emit.act = ACT_MISH;
+    o1.emit.mask = mask_;
+    o1.emit.out = h_;
+    o1.emit.ld = F;
+    emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm");
+  } else {
+    o1.y = u_;
+    o1.ldy = Fu;
+    emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm");
+    float* u = u_;
+    void* h = h_;
+    const bool gated = b.swiglu;
+    Op fa;
+    fa.launch = [=](hipStream_t s, int B) { launch_ffn_act(prec, u, Fu, F, gated, h, F, B * HW, s); };
+    fa.cls = "ffn_act";
+    fa.bytes_row = (double)HW * Fu * 4 + (double)HW * F * tsize();
+    ops_.push_back(fa);
+  }
   ConvOut o2;
   o2.y = x; o2.ldy = c; o2.accumulate = true; o2.rowmask = mask;
   ss_[depth].producer = emit_token_gemm(h_, F, dW2, c, F, o2, "token_gemm");
