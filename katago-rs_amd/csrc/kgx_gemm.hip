@@ -6,7 +6,7 @@
 
 namespace kgx {
 
-// Cfg: BM x BN output tile per 256-thread workgroup, waves in WM x WN, each wave (BM/WM) x (BN/WN) built from
+// Cfg: BM x BN output tile per workgroup of WM x WN waves, each wave (BM/WM) x (BN/WN) built from
 // 16x16 MFMA blocks. K advances BK at a time (several MFMA K steps), so each stage moves tens of KB: the next
 // stage's global loads are in flight in registers while the current stage, double-buffered in LDS with a 16-byte
 // row pad, feeds the MFMAs; one barrier per stage. A may be float (the head's f32 trunk): a BN + activation + mask
@@ -18,8 +18,8 @@ struct Cfg {
 };
 
 template <typename T, typename C, bool AF, bool PRO, int ACT>
-__global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
-  constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN;
+__global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
+  constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, NT = WM * WN * 64;
   constexpr int VEC = Tile<T>::VEC;
   constexpr int BK = sizeof(T) == 2 ? C::BKH : C::BKH / 2;
   // 128-byte rows (16-bit, BK = 64) are stored unpadded with their 16-byte chunks swizzled (chunk ^ (row/2 % 8)):
@@ -27,13 +27,17 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   constexpr bool SWZ = sizeof(T) == 2 && BK == 64;
   constexpr int LDK = SWZ ? BK : BK + VEC;
   constexpr int KV = BK / VEC;                       // 16-byte vectors per tile row
-  constexpr int AV = BM * KV / 256, BV = BN * KV / 256;
-  static_assert(AV * 256 == BM * KV && BV * 256 == BN * KV, "tile not divisible over 256 threads");
+  constexpr int AV = BM * KV / NT, BV = BN * KV / NT;
+  static_assert(AV * NT == BM * KV && BV * NT == BN * KV, "tile not divisible over the threads");
   constexpr int WTM = BM / WM, WTN = BN / WN;        // wave tile
   constexpr int MB = WTM / 16, NB = WTN / 16;        // MFMA blocks per wave
   constexpr int KS = sizeof(T) == 2 ? 32 : 4;        // K per MFMA
   constexpr int ELD = BN + 4;                        // epilogue float tile row stride
-  constexpr int STAGE = 2 * (BM + BN) * LDK * (int)sizeof(T), EPI = BM * ELD * 4;
+  constexpr int STAGE = 2 * (BM + BN) * LDK * (int)sizeof(T);
+  // The epilogue's float tile goes through LDS in EP passes of PR rows (whole wave rows) that fit the stage space.
+  constexpr int EP = BM * ELD * 4 <= STAGE || WM == 1 ? 1 : ((BM / 2) * ELD * 4 <= STAGE || WM == 2 ? 2 : 4);
+  constexpr int PR = BM / EP, EPI = PR * ELD * 4;
+  static_assert(WM % EP == 0, "epilogue passes split the wave rows");
   __shared__ __align__(16) char smem[STAGE > EPI ? STAGE : EPI];
   T (*As)[BM * LDK] = (T (*)[BM * LDK])smem;
   T (*Bs)[BN * LDK] = (T (*)[BN * LDK])(smem + 2 * BM * LDK * sizeof(T));
@@ -53,14 +57,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
   int a_row[AV], a_kk[AV], a_s[AV], b_row[BV], b_kk[BV], b_s[BV];
 #pragma unroll
   for (int v = 0; v < AV; v++) {
-    const int idx = tid + 256 * v;
+    const int idx = tid + NT * v;
     a_row[v] = idx / KV;
     a_kk[v] = (idx % KV) * VEC;
     a_s[v] = a_row[v] * LDK + (SWZ ? ((a_kk[v] / VEC) ^ ((a_row[v] >> 1) & 7)) * VEC : a_kk[v]);
   }
 #pragma unroll
   for (int v = 0; v < BV; v++) {
-    const int idx = tid + 256 * v;
+    const int idx = tid + NT * v;
     b_row[v] = idx / KV;
     b_kk[v] = (idx % KV) * VEC;
     b_s[v] = b_row[v] * LDK + (SWZ ? ((b_kk[v] / VEC) ^ ((b_row[v] >> 1) & 7)) * VEC : b_kk[v]);
@@ -182,51 +186,59 @@ __global__ __launch_bounds__(256) void gemm_kernel(GemmArgs g) {
         }
     return;
   }
-  // Epilogue through LDS (the stage buffers are free after the loop's last barrier): the float tile, then four
-  // consecutive columns of one row per thread with 16-byte accesses, the per-row and per-column inputs loaded
-  // ahead of the stores.
+  // Epilogue through LDS (the stage buffers are free after the loop's last barrier), in passes of PR rows: the
+  // float tile, then four consecutive columns of one row per thread with 16-byte accesses, the per-row and
+  // per-column inputs loaded ahead of the stores.
   float* Et = (float*)smem;
 #pragma unroll
-  for (int i = 0; i < MB; i++)
+  for (int p = 0; p < EP; p++) {
+    if (p) __syncthreads();
+    if (wm / (WM / EP) == p) {
 #pragma unroll
-    for (int j = 0; j < NB; j++)
+      for (int i = 0; i < MB; i++)
 #pragma unroll
-      for (int r = 0; r < 4; r++) Et[(wm * WTM + i * 16 + 4 * g4 + r) * ELD + wn * WTN + j * 16 + r16] = acc[i][j][r];
-  __syncthreads();
-  if (g.glu) {
-    constexpr int HV = BN / 8;  // 4-wide vectors of gated outputs per tile row
-    for (int e = tid; e < BM * HV; e += 256) {
-      const int r = e / HV, hc = (e % HV) * 4, lc = (hc / 16) * 32 + hc % 16;
-      const int m = m0 + r, f = n0 / 2 + hc;
-      if (m < M && f < N / 2) {
-        const floatx4 a = *(const floatx4*)(Et + r * ELD + lc), b = *(const floatx4*)(Et + r * ELD + lc + 16);
-        store4<T>((T*)o.yt + (size_t)m * o.ldyt + f, act_f<ACT_SILU>(a[0]) * b[0], act_f<ACT_SILU>(a[1]) * b[1],
-                  act_f<ACT_SILU>(a[2]) * b[2], act_f<ACT_SILU>(a[3]) * b[3]);
-      }
+        for (int j = 0; j < NB; j++)
+#pragma unroll
+          for (int r = 0; r < 4; r++)
+            Et[(wm * WTM - p * PR + i * 16 + 4 * g4 + r) * ELD + wn * WTN + j * 16 + r16] = acc[i][j][r];
     }
-    return;
-  }
-  constexpr int CV = BN / 4, EV = BM * CV / 256;
-  static_assert(EV * 256 == BM * CV, "epilogue vectors not divisible over 256 threads");
-  floatx4 yres[EV];
-  float rmv[EV], mkv[EV];
-#pragma unroll
-  for (int v = 0; v < EV; v++) {
-    const int e = tid + 256 * v, m = min(m0 + e / CV, M - 1), n = min(n0 + (e % CV) * 4, N - 4);
-    yres[v] = o.y && o.accumulate ? *(const floatx4*)(o.y + (size_t)m * o.ldy + n) : floatx4{0.f, 0.f, 0.f, 0.f};
-    rmv[v] = o.rowmask ? o.rowmask[m] : 1.f;
-    mkv[v] = o.emit.scale ? o.emit.mask[m] : 1.f;
-  }
-#pragma unroll
-  for (int v = 0; v < EV; v++) {
-    const int e = tid + 256 * v, r = e / CV, c = (e % CV) * 4, m = m0 + r, n = n0 + c;
-    if (m < M && n < N) {
-      floatx4 es = {1.f, 1.f, 1.f, 1.f}, eb = {0.f, 0.f, 0.f, 0.f};
-      if (o.emit.scale) {
-        es = *(const floatx4*)(o.emit.scale + n);
-        eb = *(const floatx4*)(o.emit.bias + n);
+    __syncthreads();
+    const int mp = m0 + p * PR;
+    if (g.glu) {
+      constexpr int HV = BN / 8;  // 4-wide vectors of gated outputs per tile row
+      for (int e = tid; e < PR * HV; e += NT) {
+        const int r = e / HV, hc = (e % HV) * 4, lc = (hc / 16) * 32 + hc % 16;
+        const int m = mp + r, f = n0 / 2 + hc;
+        if (m < M && f < N / 2) {
+          const floatx4 a = *(const floatx4*)(Et + r * ELD + lc), b = *(const floatx4*)(Et + r * ELD + lc + 16);
+          store4<T>((T*)o.yt + (size_t)m * o.ldyt + f, act_f<ACT_SILU>(a[0]) * b[0], act_f<ACT_SILU>(a[1]) * b[1],
+                    act_f<ACT_SILU>(a[2]) * b[2], act_f<ACT_SILU>(a[3]) * b[3]);
+        }
       }
-      conv_store4<T>(o, m, n, *(const floatx4*)(Et + r * ELD + c), yres[v], rmv[v], es, eb, mkv[v]);
+      continue;
+    }
+    constexpr int CV = BN / 4, EV = PR * CV / NT;
+    static_assert(EV * NT == PR * CV, "epilogue vectors not divisible over the threads");
+    floatx4 yres[EV];
+    float rmv[EV], mkv[EV];
+#pragma unroll
+    for (int v = 0; v < EV; v++) {
+      const int e = tid + NT * v, m = min(mp + e / CV, M - 1), n = min(n0 + (e % CV) * 4, N - 4);
+      yres[v] = o.y && o.accumulate ? *(const floatx4*)(o.y + (size_t)m * o.ldy + n) : floatx4{0.f, 0.f, 0.f, 0.f};
+      rmv[v] = o.rowmask ? o.rowmask[m] : 1.f;
+      mkv[v] = o.emit.scale ? o.emit.mask[m] : 1.f;
+    }
+#pragma unroll
+    for (int v = 0; v < EV; v++) {
+      const int e = tid + NT * v, r = e / CV, c = (e % CV) * 4, m = mp + r, n = n0 + c;
+      if (m < M && n < N) {
+        floatx4 es = {1.f, 1.f, 1.f, 1.f}, eb = {0.f, 0.f, 0.f, 0.f};
+        if (o.emit.scale) {
+          es = *(const floatx4*)(o.emit.scale + n);
+          eb = *(const floatx4*)(o.emit.bias + n);
+        }
+        conv_store4<T>(o, m, n, *(const floatx4*)(Et + r * ELD + c), yres[v], rmv[v], es, eb, mkv[v]);
+      }
     }
   }
 }
@@ -242,7 +254,7 @@ typedef Cfg<64, 96, 64, 2, 2> CfgHead;  // the heads' first convolutions: N = p1
 template <typename T, typename C, bool AF, bool PRO, int ACT>
 static void gemm_launch(const GemmArgs& g, hipStream_t s) {
   dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM, g.Z);
-  gemm_kernel<T, C, AF, PRO, ACT><<<grid, 256, 0, s>>>(g);
+  gemm_kernel<T, C, AF, PRO, ACT><<<grid, C::WM * C::WN * 64, 0, s>>>(g);
 }
 
 template <typename T, bool AF, bool PRO, int ACT>

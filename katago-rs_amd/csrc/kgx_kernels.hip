@@ -508,8 +508,80 @@ __global__ __launch_bounds__(256) void rmsnorm_tok_kernel(const float* __restric
   for (int c = lane; c < C; c += 64) o[c] = to_t<T>(xr[c] * rs * w[c] * mk);
 }
 
+// Vector form: each lane holds eight consecutive channels per 512-channel chunk of RPW rows, so a row is read
+// once with 16-byte loads (a wave reads 2 KB contiguous per chunk), the loads of all RPW rows are in flight before
+// the first reduction, and the outputs go out as 16-byte (8 x 16-bit) or 2 x 16-byte (float) stores.
+constexpr int RMS_RPW = 2;
+
+template <typename T, int CH>
+__global__ __launch_bounds__(256) void rmsnorm_tok8_kernel(const float* __restrict__ x, int ldx, int C,
+                                                           const float* __restrict__ w, float eps,
+                                                           const float* __restrict__ mask, T* __restrict__ out,
+                                                           int ldo, int rows) {
+  const int lane = threadIdx.x & 63, row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RMS_RPW;
+  floatx4 v[RMS_RPW][CH][2];
+#pragma unroll
+  for (int r = 0; r < RMS_RPW; r++) {
+    const int row = min(row0 + r, rows - 1);
+#pragma unroll
+    for (int ch = 0; ch < CH; ch++) {
+      const int c = ch * 512 + lane * 8;
+      v[r][ch][0] = v[r][ch][1] = floatx4{0.f, 0.f, 0.f, 0.f};
+      if (c < C) {
+        const float* xp = x + (size_t)row * ldx + c;
+        v[r][ch][0] = *(const floatx4*)xp;
+        v[r][ch][1] = *(const floatx4*)(xp + 4);
+      }
+    }
+  }
+#pragma unroll
+  for (int r = 0; r < RMS_RPW; r++) {
+    const int row = row0 + r;
+    float ss = 0.f;
+#pragma unroll
+    for (int ch = 0; ch < CH; ch++)
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) ss += v[r][ch][h][e] * v[r][ch][h][e];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    if (row >= rows) continue;
+    const float rs = 1.f / sqrtf(ss / (float)C + eps), mk = mask[row];
+#pragma unroll
+    for (int ch = 0; ch < CH; ch++) {
+      const int c = ch * 512 + lane * 8;
+      if (c < C) {
+        const floatx4 w0 = *(const floatx4*)(w + c), w1 = *(const floatx4*)(w + c + 4);
+        const floatx4 a = v[r][ch][0] * rs * w0 * mk, b = v[r][ch][1] * rs * w1 * mk;
+        T* op = out + (size_t)row * ldo + c;
+        store4<T>(op, a[0], a[1], a[2], a[3]);
+        store4<T>(op + 4, b[0], b[1], b[2], b[3]);
+      }
+    }
+  }
+}
+
+template <typename T>
+static void rmsnorm_tok8(const float* x, int ldx, int C, const float* w, float eps, const float* mask, T* out, int ldo,
+                         int rows, hipStream_t s) {
+  dim3 grid((rows + 4 * RMS_RPW - 1) / (4 * RMS_RPW));
+  if (C <= 512) rmsnorm_tok8_kernel<T, 1><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, out, ldo, rows);
+  else if (C <= 1024) rmsnorm_tok8_kernel<T, 2><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, out, ldo, rows);
+  else rmsnorm_tok8_kernel<T, 4><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, out, ldo, rows);
+}
+
 void launch_rmsnorm_tok(int prec, const float* x, int ldx, int C, const float* w, float eps, const float* mask,
                         void* out, int ldo, int rows, hipStream_t s) {
+  const int tsz = prec == PREC_F32 ? 4 : 2;
+  if (rows > 0 && C % 8 == 0 && C <= 2048 && ldx % 4 == 0 && ldo % (16 / tsz) == 0 &&
+      ((uintptr_t)x | (uintptr_t)w) % 16 == 0 && (uintptr_t)out % 16 == 0) {
+    if (prec == PREC_F16) rmsnorm_tok8<f16>(x, ldx, C, w, eps, mask, (f16*)out, ldo, rows, s);
+    else if (prec == PREC_BF16) rmsnorm_tok8<bf16>(x, ldx, C, w, eps, mask, (bf16*)out, ldo, rows, s);
+    else rmsnorm_tok8<float>(x, ldx, C, w, eps, mask, (float*)out, ldo, rows, s);
+    KGX_CHECK_LAUNCH();
+    return;
+  }
   dim3 grid((rows + 3) / 4);
   if (prec == PREC_F16) rmsnorm_tok_kernel<f16><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, (f16*)out, ldo, rows);
   else if (prec == PREC_BF16) rmsnorm_tok_kernel<bf16><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, (bf16*)out, ldo, rows);
