@@ -11,10 +11,13 @@ namespace kgx {
 // stage's global loads are in flight in registers while the current stage, double-buffered in LDS with a 16-byte
 // row pad, feeds the MFMAs; one barrier per stage. A may be float (the head's f32 trunk): a BN + activation + mask
 // prologue then runs as the stage is written to LDS and values are converted to T there.
-template <int BM_, int BN_, int BKH_, int WM_, int WN_>
+template <int BM_, int BN_, int BKH_, int WM_, int WN_, bool KFULL_ = false>
 struct Cfg {
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
   static constexpr int BKH = BKH_;  // K per stage for 16-bit types (float uses half as many)
+  // K is a multiple of the stage depth (the dispatcher checks): loads need no K bound, and rows past M or N are
+  // clamped to the last one instead of zeroed, since they only feed outputs that are not stored.
+  static constexpr bool KFULL = KFULL_;
 };
 
 template <typename T, typename C, bool AF, bool PRO, int ACT>
@@ -73,6 +76,11 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
   const float* Af0 = Af + (size_t)m0 * g.lda;
   const T* Bt0 = Bt + (size_t)n0 * g.ldb;
   const int lda = (int)g.lda, ldb = (int)g.ldb;
+  int a_off[AV], b_off[BV];  // clamped-row offsets (KFULL)
+#pragma unroll
+  for (int v = 0; v < AV; v++) a_off[v] = min(a_row[v], M - 1 - m0) * lda + a_kk[v];
+#pragma unroll
+  for (int v = 0; v < BV; v++) b_off[v] = min(b_row[v], N - 1 - n0) * ldb + b_kk[v];
 
   vec_t ra[AF ? 1 : AV];
   float rf[AF ? AV * VEC : 1];
@@ -81,6 +89,10 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
   auto load = [&](int k0) {
 #pragma unroll
     for (int v = 0; v < AV; v++) {
+      if constexpr (!AF && C::KFULL) {
+        ra[v] = *(const vec_t*)(At0 + a_off[v] + k0);
+        continue;
+      }
       const bool ok = m0 + a_row[v] < M && k0 + a_kk[v] < K;
       const int off = ok ? a_row[v] * lda + k0 + a_kk[v] : 0;
       if constexpr (!AF) {
@@ -97,6 +109,10 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
     }
 #pragma unroll
     for (int v = 0; v < BV; v++) {
+      if constexpr (C::KFULL) {
+        rb[v] = *(const vec_t*)(Bt0 + b_off[v] + k0);
+        continue;
+      }
       const bool ok = n0 + b_row[v] < N && k0 + b_kk[v] < K;
       const int off = ok ? b_row[v] * ldb + k0 + b_kk[v] : 0;
       rb[v] = *(const vec_t*)(Bt0 + off);
@@ -155,13 +171,39 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
     if (kt + 1 < nk) load((kt + 1) * BK);
     const T* as = As[cur] + (wm * WTM + r16) * LDK + (SWZ ? 0 : koff);
     const T* bs = Bs[cur] + (wn * WTN + r16) * LDK + (SWZ ? 0 : koff);
+    if constexpr (sizeof(T) == 2) {
+      // All fragments of the stage are read before its first MFMA, so the later K steps' reads land while the
+      // earlier steps compute.
+      typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
+      constexpr int KST = BK / KS;
+      frag_t fa[KST][MB], fb[KST][NB];
 #pragma unroll
-    for (int kk = 0; kk < BK; kk += KS) {
-      const int ko = SWZ ? ((kk / 8) ^ sw) * 8 : kk;
+      for (int q = 0; q < KST; q++) {
+        const int ko = SWZ ? ((q * KS / 8) ^ sw) * 8 : q * KS;
 #pragma unroll
-      for (int i = 0; i < MB; i++)
+        for (int i = 0; i < MB; i++) fa[q][i] = *(const frag_t*)(as + i * 16 * LDK + ko);
 #pragma unroll
-        for (int j = 0; j < NB; j++) acc[i][j] = mfma16<T>(as + i * 16 * LDK + ko, bs + j * 16 * LDK + ko, acc[i][j]);
+        for (int j = 0; j < NB; j++) fb[q][j] = *(const frag_t*)(bs + j * 16 * LDK + ko);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int q = 0; q < KST; q++)
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+          for (int j = 0; j < NB; j++) {
+            if constexpr (std::is_same<T, f16>::value)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[q][i], fb[q][j], acc[i][j], 0, 0, 0);
+            else
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[q][i], fb[q][j], acc[i][j], 0, 0, 0);
+          }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < BK; kk += KS)
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+          for (int j = 0; j < NB; j++) acc[i][j] = mfma16<T>(as + i * 16 * LDK + kk, bs + j * 16 * LDK + kk, acc[i][j]);
     }
     if (kt + 1 < nk) store(cur ^ 1, (kt + 1) * BK);
     __syncthreads();
@@ -246,10 +288,10 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
 // Tile configurations: narrow rows over all of a <= 192-wide N (1x1 convolutions, Winograd point GEMMs: the
 // prologue runs once per element), 64x96 for 65..96 columns (the heads), 128x128 for wide GEMMs (transformer
 // linears), 64x64 for the rest.
-typedef Cfg<32, 192, 64, 1, 4> CfgNarrow;
-typedef Cfg<128, 128, 64, 2, 2> CfgWide;
+typedef Cfg<32, 192, 64, 1, 4, true> CfgNarrow;
+typedef Cfg<128, 128, 64, 2, 2, true> CfgWide;
 typedef Cfg<64, 64, 32, 2, 2> CfgSmall;
-typedef Cfg<64, 96, 64, 2, 2> CfgHead;  // the heads' first convolutions: N = p1 + g1 + v1 channels <= 96
+typedef Cfg<64, 96, 64, 2, 2, true> CfgHead;  // the heads' first convolutions: N = p1 + g1 + v1 channels <= 96
 
 template <typename T, typename C, bool AF, bool PRO, int ACT>
 static void gemm_launch(const GemmArgs& g, hipStream_t s) {
