@@ -752,8 +752,8 @@ __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
 // consecutive keys of one query, so the reductions over keys stay in the lane but for two cross-lane steps), with
 // the key mask bias as the accumulator's initial value, then O^T += V^T P^T. P needs no data movement: for a
 // 32-key block the B operand of a lane is its own eight probabilities (keys 4g..4g+3 of the block's first 16 and
-// of its second 16, g = lane / 16), so V^T holds its keys in that order. The softmax runs online over 32-key
-// blocks (running maximum per query, accumulators rescaled every block). Q carries RoPE and the 1/sqrt(d) scale
+// of its second 16, g = lane / 16), so V^T holds its keys in that order. The softmax runs online over the 64-key
+// tiles (running maximum per query, accumulators rescaled once per tile). Q carries RoPE and the 1/sqrt(d) scale
 // and is held in registers as B fragments. The output goes through LDS for 16-byte stores.
 constexpr int ATT_QW = 32, ATT_NW = 4, ATT_QB = ATT_QW * ATT_NW, ATT_NQB = (HW + ATT_QB - 1) / ATT_QB;
 constexpr int ATT_KT = 64, ATT_NKT = (HW + ATT_KT - 1) / ATT_KT;
@@ -761,12 +761,6 @@ constexpr int ATT_KT = 64, ATT_NKT = (HW + ATT_KT - 1) / ATT_KT;
 // Position of key kk (0..31) of a 32-key block in the permuted V^T rows.
 __device__ __forceinline__ int att_kpos(int kk) {
   return kk < 16 ? 8 * (kk >> 2) + (kk & 3) : 8 * ((kk - 16) >> 2) + 4 + ((kk - 16) & 3);
-}
-
-template <typename T>
-__device__ __forceinline__ unsigned att_pack2(float lo, float hi) {
-  return (unsigned)__builtin_bit_cast(unsigned short, to_t<T>(lo)) |
-         ((unsigned)__builtin_bit_cast(unsigned short, to_t<T>(hi)) << 16);
 }
 
 template <typename T, int D, bool ROPE>
@@ -851,31 +845,27 @@ __global__ __launch_bounds__(ATT_NW * 64, 3) void attn_mfma_kernel(AttnArgs a, i
   frag_t kx0, kx1, vx0, vx1;
   floatx4 c0, c1, s0, s1;
   float mk = 0.f;
+  // Keys past the board read the last key's rows (finite values): their bias of -1e30 gives them probability 0.
   auto fetch = [&](int t) {
     const int k0 = t * ATT_KT;
-    const frag_t z = __builtin_bit_cast(frag_t, u32x4{0, 0, 0, 0});
-    kx0 = kx1 = vx0 = vx1 = z;
-    c0 = c1 = s0 = s1 = floatx4{0.f, 0.f, 0.f, 0.f};
     if (tid < KU) {
-      const int key = k0 + ku_key;
-      if (key < HW) {
-        const T* kp = kbase + (size_t)key * a.ldq + ku_c;
-        kx0 = *(const frag_t*)kp;
-        kx1 = *(const frag_t*)(kp + HALF);
-        if constexpr (ROPE) {
-          const float* ct = a.cos_t + ((size_t)ktab * HW + key) * HALF + ku_c;
-          const float* st = a.sin_t + ((size_t)ktab * HW + key) * HALF + ku_c;
-          c0 = *(const floatx4*)ct;
-          c1 = *(const floatx4*)(ct + 4);
-          s0 = *(const floatx4*)st;
-          s1 = *(const floatx4*)(st + 4);
-        }
+      const int key = min(k0 + ku_key, HW - 1);
+      const T* kp = kbase + (size_t)key * a.ldq + ku_c;
+      kx0 = *(const frag_t*)kp;
+      kx1 = *(const frag_t*)(kp + HALF);
+      if constexpr (ROPE) {
+        const float* ct = a.cos_t + ((size_t)ktab * HW + key) * HALF + ku_c;
+        const float* st = a.sin_t + ((size_t)ktab * HW + key) * HALF + ku_c;
+        c0 = *(const floatx4*)ct;
+        c1 = *(const floatx4*)(ct + 4);
+        s0 = *(const floatx4*)st;
+        s1 = *(const floatx4*)(st + 4);
       }
     }
     if (tid < VU) {
-      const int key = k0 + 2 * vu_pair;
-      if (key < HW) vx0 = *(const frag_t*)(vbase + (size_t)key * a.ldq + vu_c);
-      if (key + 1 < HW) vx1 = *(const frag_t*)(vbase + (size_t)(key + 1) * a.ldq + vu_c);
+      const int key = min(k0 + 2 * vu_pair, HW - 1), key1 = min(k0 + 2 * vu_pair + 1, HW - 1);
+      vx0 = *(const frag_t*)(vbase + (size_t)key * a.ldq + vu_c);
+      vx1 = *(const frag_t*)(vbase + (size_t)key1 * a.ldq + vu_c);
     }
     if (tid < ATT_KT) {
       const int key = k0 + tid;
@@ -902,8 +892,14 @@ __global__ __launch_bounds__(ATT_NW * 64, 3) void attn_mfma_kernel(AttnArgs a, i
     }
     if (tid < VU) {
       const int kk = 2 * vu_pair, pos = (kk & ~31) + att_kpos(kk & 31);
+      const u32x4 w0 = __builtin_bit_cast(u32x4, vx0), w1 = __builtin_bit_cast(u32x4, vx1);
 #pragma unroll
-      for (int e = 0; e < 8; e++) *(unsigned*)(Vs + (vu_c + e) * VLD + pos) = att_pack2<T>((float)vx0[e], (float)vx1[e]);
+      for (int e = 0; e < 8; e++) {
+        // Element e of both keys: the 16-bit halves of word e / 2.
+        const unsigned a0 = w0[e >> 1], a1 = w1[e >> 1];
+        *(unsigned*)(Vs + (vu_c + e) * VLD + pos) =
+            (e & 1) ? (a0 >> 16) | (a1 & 0xffff0000u) : (a0 & 0xffffu) | (a1 << 16);
+      }
     }
     if (tid < ATT_KT) kbias[tid] = mk;
   };
@@ -926,67 +922,71 @@ __global__ __launch_bounds__(ATT_NW * 64, 3) void attn_mfma_kernel(AttnArgs a, i
     const T* Ks = (const T*)(smem + (t & 1) * BUF);
     const T* Vs = Ks + KS_SZ;
     const float* kbias = (const float*)(Vs + VS_SZ);
-    // Per 32-key block: S^T tiles [key tile][query tile] with the key bias as initial accumulator, softmax
-    // numerators (exp2 of log2(e)-scaled differences) as B fragments, O^T += V^T P^T.
+    // S^T tiles [key tile][query tile] of the whole 64-key tile with the key bias as initial accumulator; one
+    // maximum and one rescale per tile; numerators as B fragments of the two 32-key blocks; O^T += V^T P^T.
+    floatx4 sc[2 * KB][QT];
 #pragma unroll
-    for (int kb = 0; kb < KB; kb++) {
-      floatx4 sc[2][QT];
+    for (int kt = 0; kt < 2 * KB; kt++) {
+      frag_t kf[KC];
 #pragma unroll
-      for (int j = 0; j < 2; j++) {
-        const int kt = 2 * kb + j;
-        frag_t kf[KC];
-#pragma unroll
-        for (int kc = 0; kc < KC; kc++) kf[kc] = *(const frag_t*)(Ks + (kt * 16 + l16) * KLD + kc * 32 + 8 * g);
-        const floatx4 bias = *(const floatx4*)(kbias + kt * 16 + 4 * g);
-#pragma unroll
-        for (int qt = 0; qt < QT; qt++) {
-          floatx4 c = bias;
-#pragma unroll
-          for (int kc = 0; kc < KC; kc++) {
-            if constexpr (std::is_same<T, f16>::value)
-              c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kc], qf[qt][kc], c, 0, 0, 0);
-            else
-              c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kc], qf[qt][kc], c, 0, 0, 0);
-          }
-          sc[j][qt] = c;
-        }
-      }
-      frag_t pf[QT];
+      for (int kc = 0; kc < KC; kc++) kf[kc] = *(const frag_t*)(Ks + (kt * 16 + l16) * KLD + kc * 32 + 8 * g);
+      const floatx4 bias = *(const floatx4*)(kbias + kt * 16 + 4 * g);
 #pragma unroll
       for (int qt = 0; qt < QT; qt++) {
-        float mx = fmaxf(sc[0][qt][0], sc[1][qt][0]);
+        floatx4 c = bias;
 #pragma unroll
-        for (int r = 1; r < 4; r++) mx = fmaxf(mx, fmaxf(sc[0][qt][r], sc[1][qt][r]));
-        mx = fmaxf(mx, __shfl_xor(mx, 16));
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float mnew = fmaxf(mref[qt], mx);
-        const float alpha = __builtin_amdgcn_exp2f((mref[qt] - mnew) * L2E);
+        for (int kc = 0; kc < KC; kc++) {
+          if constexpr (std::is_same<T, f16>::value)
+            c = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[kc], qf[qt][kc], c, 0, 0, 0);
+          else
+            c = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[kc], qf[qt][kc], c, 0, 0, 0);
+        }
+        sc[kt][qt] = c;
+      }
+    }
+    frag_t pf[KB][QT];
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) o[dt][qt] *= alpha;
-        mref[qt] = mnew;
-        const float ml = mnew * L2E;
-        float ps = 0.f;
+    for (int qt = 0; qt < QT; qt++) {
+      float mx = sc[0][qt][0];
+#pragma unroll
+      for (int kt = 0; kt < 2 * KB; kt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) mx = fmaxf(mx, sc[kt][qt][r]);
+      mx = fmaxf(mx, __shfl_xor(mx, 16));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(mref[qt], mx);
+      const float alpha = __builtin_amdgcn_exp2f((mref[qt] - mnew) * L2E);
+#pragma unroll
+      for (int dt = 0; dt < DT; dt++) o[dt][qt] *= alpha;
+      mref[qt] = mnew;
+      const float ml = mnew * L2E;
+      float ps = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < KB; kb++) {
         frag_t pr;
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
           for (int r = 0; r < 4; r++) {
-            const float pv = __builtin_amdgcn_exp2f(fmaf(sc[j][qt][r], L2E, -ml));
+            const float pv = __builtin_amdgcn_exp2f(fmaf(sc[2 * kb + j][qt][r], L2E, -ml));
             ps += pv;
             pr[4 * j + r] = to_t<T>(pv);
           }
-        lsum[qt] = lsum[qt] * alpha + ps;
-        pf[qt] = pr;
+        pf[kb][qt] = pr;
       }
+      lsum[qt] = lsum[qt] * alpha + ps;
+    }
 #pragma unroll
-      for (int dt = 0; dt < DT; dt++) {
+    for (int dt = 0; dt < DT; dt++) {
+#pragma unroll
+      for (int kb = 0; kb < KB; kb++) {
         const frag_t vf = *(const frag_t*)(Vs + (dt * 16 + l16) * VLD + kb * 32 + 8 * g);
 #pragma unroll
         for (int qt = 0; qt < QT; qt++) {
           if constexpr (std::is_same<T, f16>::value)
-            o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[qt], o[dt][qt], 0, 0, 0);
+            o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf, pf[kb][qt], o[dt][qt], 0, 0, 0);
           else
-            o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[qt], o[dt][qt], 0, 0, 0);
+            o[dt][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vf, pf[kb][qt], o[dt][qt], 0, 0, 0);
         }
       }
     }
