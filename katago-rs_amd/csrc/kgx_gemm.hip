@@ -261,6 +261,34 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
     }
     constexpr int CV = BN / 4, EV = PR * CV / NT;
     static_assert(EV * NT == PR * CV, "epilogue vectors not divisible over the threads");
+    if (g.qkv.dq) {
+      // q|k|v projection: each head lies inside the tile, so the rotation partner of column n (n +- dq/2) is
+      // in LDS too.
+      const QkvEpi& q = g.qkv;
+      const int half = q.dq / 2;
+#pragma unroll
+      for (int v = 0; v < EV; v++) {
+        const int e = tid + NT * v, r = e / CV, c = (e % CV) * 4, m = mp + r, n = n0 + c;
+        if (m < M && n < N) {
+          floatx4 x = *(const floatx4*)(Et + r * ELD + c);
+          if (n < q.nq + q.nk) {
+            const bool isq = n < q.nq;
+            const int hh = (n - (isq ? 0 : q.nq)) / q.dq, rr = (n - (isq ? 0 : q.nq)) - hh * q.dq;
+            if (q.cos) {
+              const bool lo = rr < half;
+              const int p = lo ? rr : rr - half, tab = q.tables == 1 ? 0 : (isq ? hh / (q.H / q.KV) : hh);
+              const floatx4 y = *(const floatx4*)(Et + r * ELD + c + (lo ? half : -half));
+              const size_t ti = ((size_t)tab * HW + m % HW) * half + p;
+              const floatx4 cs = *(const floatx4*)(q.cos + ti), sn = *(const floatx4*)(q.sin + ti);
+              x = lo ? x * cs - y * sn : y * sn + x * cs;
+            }
+            if (isq) x *= q.qscale;
+          }
+          store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, x[0], x[1], x[2], x[3]);
+        }
+      }
+      continue;
+    }
     floatx4 yres[EV];
     float rmv[EV], mkv[EV];
 #pragma unroll
@@ -295,6 +323,8 @@ typedef Cfg<64, 96, 64, 2, 2, true> CfgHead;  // the heads' first convolutions: 
 
 template <typename T, typename C, bool AF, bool PRO, int ACT>
 static void gemm_launch(const GemmArgs& g, hipStream_t s) {
+  if (g.qkv.dq && C::BN % g.qkv.dq)
+    throw std::runtime_error("gemm: the q|k|v epilogue needs the column tile to hold whole heads");
   dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM, g.Z);
   gemm_kernel<T, C, AF, PRO, ACT><<<grid, C::WM * C::WN * 64, 0, s>>>(g);
 }
@@ -350,6 +380,14 @@ void launch_gemm(int prec, const GemmArgs& g0, hipStream_t s) {
   if (g0.Z > 1 && g0.out.emit.scale) throw std::runtime_error("gemm: batched GEMMs carry no emission");
   GemmArgs g = g0;
   g.vec_epi = vector_epilogue_ok(g, prec == PREC_F32 ? 4 : 2);
+  if (g.qkv.dq) {
+    const ConvOut& o = g.out;
+    const QkvEpi& q = g.qkv;
+    if (!g.vec_epi || g.glu || g.Z != 1 || !o.yt || o.y || o.emit.scale || o.colbias || o.rowmask || q.dq % 8 ||
+        q.nq % q.dq || q.nk % q.dq || q.H < 1 || q.KV < 1 || q.H % q.KV ||
+        (q.cos && (!q.sin || !aligned(q.cos, 16) || !aligned(q.sin, 16))))
+      throw std::runtime_error("gemm: bad q|k|v epilogue arguments");
+  }
   if (g.glu) {
     const ConvOut& o = g.out;
     if (!g.vec_epi || g.N % 32 || g.Z != 1 || !o.yt || o.y || o.emit.scale || o.colbias || o.rowmask)

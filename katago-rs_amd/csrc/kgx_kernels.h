@@ -70,6 +70,17 @@ void wino_filter_host(int tm, const float* w, int oc, int ic, int oc_pad, int ic
 
 // C[z] = A[z] * Bt[z]^T on MFMA: A [M][K] (row stride lda; T, or float with a prologue), Bt [N][K].
 // Batch z offsets: A sA, Bt sB, outputs sC (elements, applied to out.y / out.yt).
+// Epilogue of the fused q|k|v projection (active when dq > 0): columns [0, nq) are H query heads and
+// [nq, nq + nk) KV key heads of dq dims each. Query and key heads are rotated on their pairs (p, p + dq/2) with
+// the tables cos/sin [tables][HW][dq/2] of the row's board point (query head h uses its kv head's table; tables
+// == 1 shares one; cos == nullptr: no rotation), and query columns are scaled by qscale.
+struct QkvEpi {
+  const float* cos = nullptr;
+  const float* sin = nullptr;
+  int dq = 0, nq = 0, nk = 0, H = 1, KV = 1, tables = 1;
+  float qscale = 1.f;
+};
+
 struct GemmArgs {
   const void* A = nullptr; long lda = 0; long sA = 0;
   const void* Bt = nullptr; long ldb = 0; long sB = 0;
@@ -81,6 +92,7 @@ struct GemmArgs {
   // Gated output (SwiGLU): the columns come in 16-wide pairs of blocks (value block, gate block) and the GEMM
   // writes only out.yt[m][f] = silu(C[m][32 (f / 16) + f % 16]) * C[m][32 (f / 16) + 16 + f % 16], f < N / 2.
   bool glu = false;
+  QkvEpi qkv;
   bool vec_epi = false;  // set by launch_gemm: the four-column vector epilogue applies
 };
 void launch_gemm(int prec, const GemmArgs& g, hipStream_t s);

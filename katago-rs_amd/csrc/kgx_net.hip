@@ -303,7 +303,7 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
 }
 
 std::shared_ptr<ConvOut> Net::emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, const ConvOut& o,
-                                              const char* cls, bool glu) {
+                                              const char* cls, bool glu, const QkvEpi& qkv) {
   const int prec = prec_;
   auto out = std::make_shared<ConvOut>(o);
   Op op;
@@ -314,6 +314,7 @@ std::shared_ptr<ConvOut> Net::emit_token_gemm(const void* A, int lda, const void
     g.out = *out;
     g.M = B * HW; g.N = N; g.K = K;
     g.glu = glu;
+    g.qkv = qkv;
     launch_gemm(prec, g, s);
   };
   op.cls = cls;
@@ -396,20 +397,24 @@ void Net::emit_attention(const BlockDesc& b, int depth) {
   rn.cls = "rmsnorm";
   rn.bytes_row = (double)HW * c * (4 + tsize());
   ops_.push_back(rn);
+  // The projection's epilogue applies RoPE to the query and key heads and the 1/sqrt(dq) scale to the queries,
+  // so attention reads them ready to use.
   ConvOut oq;
   oq.yt = qkv_;
   oq.ldyt = nqkv;
-  emit_token_gemm(nrm_, c, dWqkv, nqkv, c, oq, "token_gemm");
+  QkvEpi qe;
+  qe.cos = dcos; qe.sin = dsin; qe.dq = dq; qe.nq = nq; qe.nk = nk; qe.H = H; qe.KV = KV; qe.tables = ntab;
+  qe.qscale = 1.0f / std::sqrt((float)dq);
+  emit_token_gemm(nrm_, c, dWqkv, nqkv, c, oq, "token_gemm", false, qe);
   void* qkv = qkv_;
   void* ao = ao_;
-  const float scale = 1.0f / std::sqrt((float)dq);
   Op at;
   at.launch = [=](hipStream_t s, int B) {
     AttnArgs a;
     a.qkv = qkv; a.ldq = nqkv; a.q_off = 0; a.k_off = nq; a.v_off = nq + nk;
     a.H = H; a.KV = KV; a.dq = dq; a.dv = dv;
-    a.cos_t = dcos; a.sin_t = dsin; a.q_tables = ntab; a.k_tables = ntab;
-    a.scale = scale; a.mask = mask; a.out = ao; a.ldo = H * dv;
+    a.q_tables = 0; a.k_tables = 0;
+    a.scale = 1.f; a.mask = mask; a.out = ao; a.ldo = H * dv;
     launch_attention(prec, a, B, s);
   };
   at.cls = "attention";

@@ -607,11 +607,9 @@ struct Fwd {
   void attention_block(std::vector<R>& t, const Block& bl, int C) {
     std::vector<R> xn = tf_rmsnorm(t, bl, C);
     std::vector<R> q = tok_matmul(xn, bl.q), k = tok_matmul(xn, bl.k), v = tok_matmul(xn, bl.v);
-    if (qa) {
-      for (auto& z : q) z = ra(z);
-      for (auto& z : k) z = ra(z);
+    // With 16-bit storage: v is stored as projected; q and k are stored once, after rotation and scaling below.
+    if (qa)
       for (auto& z : v) z = ra(z);
-    }
     const int H = bl.heads, KV = bl.kvh, dq = bl.dq, dv = bl.dv, g = H / KV;
     if (bl.rope) {
       std::vector<float> cs, sn; int ntab;
