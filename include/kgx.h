@@ -84,6 +84,13 @@ void kg_handle_free(kg_handle* handle);
 int kg_handle_set_batch_buckets(kg_handle* handle, const int* buckets, int count);
 int kg_padded_batch_size(const int* buckets, int count, int n, int max_batch);
 
+/* Symmetry copy of one row of `channels` planes of h x w floats, NCHW (copy_with_symmetry,
+ * crates/katago-core/src/neuralnet/nninputs.rs:756-850): symmetry bit 0 flips y, bit 1 flips x, bit 2
+ * transposes (square planes only). reverse = 0 is copy_inputs_with_symmetry (nninputs.rs:872-874: a transpose
+ * swaps the flips), reverse = 1 copy_outputs_with_symmetry (nninputs.rs:877-879). kg_get_output applies it to
+ * the rows it stages and reads back. Host only; src and dst must not overlap. */
+int kg_copy_with_symmetry(const float* src, float* dst, int channels, int h, int w, int symmetry, int reverse);
+
 /* Whether the handle computes its GEMMs in a 16-bit type (NeuralNet::is_using_fp16, backend.rs:400-404). */
 int kg_handle_is_using_fp16(const kg_handle* handle);
 

@@ -32,6 +32,7 @@ MAX_POLICY = 362
 EXPORTS = [
     "kg_version", "kg_last_error", "kg_device_count", "kg_device_open", "kg_net_load", "kg_net_free", "kg_net_desc",
     "kg_handle_create", "kg_handle_free", "kg_handle_set_batch_buckets", "kg_padded_batch_size",
+    "kg_copy_with_symmetry",
     "kg_handle_is_using_fp16", "kg_forward", "kg_handle_device_buffers", "kg_run", "kg_sync", "kg_handle_stream",
     "kg_get_output", "kg_profile_enable", "kg_profile_reset", "kg_profile_read",
 ]
@@ -112,6 +113,7 @@ def lib():
         L.kg_handle_free.argtypes = [vp]
         L.kg_handle_set_batch_buckets.argtypes = [vp, vp, ci]
         L.kg_padded_batch_size.argtypes = [vp, ci, ci, ci]
+        L.kg_copy_with_symmetry.argtypes = [vp, vp, ci, ci, ci, ci, ci]
         L.kg_handle_is_using_fp16.argtypes = [vp]
         L.kg_forward.argtypes = [vp, ci, vp, vp, vp, vp]
         L.kg_handle_device_buffers.argtypes = [vp, ctypes.POINTER(vp), ctypes.POINTER(vp), ctypes.POINTER(vp),
@@ -153,6 +155,18 @@ def device_count() -> int:
 def padded_batch_size(buckets, n, max_batch) -> int:
     b = np.ascontiguousarray(buckets, np.int32)
     return lib().kg_padded_batch_size(_ptr(b), len(b), n, max_batch)
+
+
+def copy_with_symmetry(src, symmetry: int, reverse: bool = False) -> np.ndarray:
+    """copy_inputs_with_symmetry (reverse False) / copy_outputs_with_symmetry (reverse True) of one row of
+    [C, H, W] float planes (crates/katago-core/src/neuralnet/nninputs.rs:756-879), through the library."""
+    a = np.ascontiguousarray(src, np.float32)
+    if a.ndim != 3:
+        raise ValueError("copy_with_symmetry: src must be [C, H, W]")
+    out = np.empty_like(a)
+    _check(lib().kg_copy_with_symmetry(_ptr(a), _ptr(out), a.shape[0], a.shape[1], a.shape[2], int(symmetry),
+                                       int(bool(reverse))))
+    return out
 
 
 class Net:

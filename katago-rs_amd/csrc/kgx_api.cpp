@@ -231,6 +231,15 @@ int kg_padded_batch_size(const int* buckets, int count, int n, int max_batch) {
   return padded_batch_size(b, n, max_batch);
 }
 
+int kg_copy_with_symmetry(const float* src, float* dst, int channels, int h, int w, int symmetry, int reverse) {
+  return guarded([&] {
+    if (!src || !dst) throw std::runtime_error("null buffer");
+    if (channels < 1 || h < 1 || w < 1) throw std::runtime_error("bad plane shape");
+    if (symmetry < 0 || symmetry > 7) throw std::runtime_error("symmetry must be in [0, 8)");
+    copy_with_symmetry(src, dst, channels, h, w, symmetry, reverse != 0);
+  });
+}
+
 int kg_handle_is_using_fp16(const kg_handle* h) { return h && h->precision != KG_PRECISION_F32 ? 1 : 0; }
 
 int kg_forward(kg_handle* h, int n, const float* bin, const float* global, const float* meta, float* out) {

@@ -68,6 +68,43 @@ def test_parser_rejections(kgx, synth):
         kgx.Net(mb.replace(b"t-res", b"t.res", 1))
 
 
+def _fnv1a(a) -> int:
+    """FNV-1a 64 over the little-endian bytes of float32 values (nninputs.cpp:43-45 of the reference's
+    fixtures)."""
+    h = 0xCBF29CE484222325
+    for b in np.ascontiguousarray(a, "<f4").tobytes():
+        h = ((h ^ b) * 0x100000001B3) & 0xFFFFFFFFFFFFFFFF
+    return h
+
+
+def test_symmetry_copies_match_reference_fixtures(kgx):
+    """copy_inputs_with_symmetry / copy_outputs_with_symmetry against the reference's own oracle fixtures
+    (fixtures/upstream-v1.18.2/unit/oracle/nninputs_expected.txt, via tests/golden/gen_nninputs_sym.py): 57
+    featurized rows on square and non-square boards over all eight symmetries, bit-exact by FNV-1a."""
+    g = np.load(os.path.join(ROOT, "tests", "golden", "nninputs_sym.npz"))
+    syms = set()
+    for ci, (pid, ei, sym, nx, ny) in enumerate(g["meta"]):
+        bits = np.zeros(22 * nx * ny, np.uint32)
+        sel = g["nz_case"] == ci
+        bits[g["nz_index"][sel]] = g["nz_bits"][sel]
+        row = bits.view(np.float32).reshape(22, ny, nx)
+        fnv_nchw, fnv_in, fnv_out = (int(v) for v in g["hashes"][ci])
+        assert _fnv1a(row) == fnv_nchw, (pid, ei)
+        s = int(sym) if sym >= 0 else 0
+        syms.add(s)
+        assert _fnv1a(kgx.copy_with_symmetry(row, s)) == fnv_in, (pid, ei, s, nx, ny)
+        assert _fnv1a(kgx.copy_with_symmetry(row[:1], s, reverse=True)) == fnv_out, (pid, ei, s, nx, ny)
+    assert syms == set(range(8))
+
+
+def test_symmetry_copy_rejects_bad_arguments(kgx):
+    x = np.zeros((1, 3, 3), np.float32)
+    with pytest.raises(kgx.KgError):
+        kgx.copy_with_symmetry(x, 8)
+    with pytest.raises(kgx.KgError):
+        kgx.copy_with_symmetry(x, -1)
+
+
 def test_padded_batch_size_reference_cases(kgx):
     # crates/katago-nn-burn/tests/batch_buckets.rs:27-35
     b = [1, 2, 4, 8, 16, 32]
