@@ -20,8 +20,28 @@ struct Cfg {
   static constexpr bool KFULL = KFULL_;
 };
 
-template <typename T, typename C, bool AF, bool PRO, int ACT>
-__global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
+// One 16-byte-per-lane load straight into LDS (buffer_load ... lds): lane i's bytes [off, off + 16) of the
+// range [base, base + nbytes) land at lds + 16 i; offsets past the range read as zero. The buffer resource is
+// built here so that kernels never hold its type.
+__device__ __forceinline__ void lds_load16(const void* base, int nbytes, void* lds, int off) {
+  typedef __attribute__((address_space(3))) void* lds_ptr_t;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(__builtin_amdgcn_make_buffer_rsrc((void*)base, 0, nbytes, 0x00020000),
+                                           (lds_ptr_t)lds, 16, off, 0, 0, 0);
+}
+
+// Epilogue variants, chosen at launch so that a kernel carries only its own epilogue code (a kernel holding all
+// of them ran 15-25 % slower on the token GEMMs, its main loop unchanged).
+enum GemmEpi {
+  EPI_SCALAR,  // per-element conv_store (rows or columns not 16-byte aligned)
+  EPI_GEN,     // conv_store4: any of colbias, rowmask, yt, y (+ residual), emission
+  EPI_YT,      // compute-type store only
+  EPI_ACC,     // float store or residual add (+ row mask) only
+  EPI_GLU,     // gated output
+  EPI_QKV,     // q|k|v projection
+};
+
+template <typename T, typename C, bool AF, bool PRO, int ACT, int EPI>
+__global__ __launch_bounds__(C::WM * C::WN * 64, 2) void gemm_kernel(GemmArgs g) {
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, NT = WM * WN * 64;
   constexpr int VEC = Tile<T>::VEC;
   constexpr int BK = sizeof(T) == 2 ? C::BKH : C::BKH / 2;
@@ -39,9 +59,9 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
   constexpr int STAGE = 2 * (BM + BN) * LDK * (int)sizeof(T);
   // The epilogue's float tile goes through LDS in EP passes of PR rows (whole wave rows) that fit the stage space.
   constexpr int EP = BM * ELD * 4 <= STAGE || WM == 1 ? 1 : ((BM / 2) * ELD * 4 <= STAGE || WM == 2 ? 2 : 4);
-  constexpr int PR = BM / EP, EPI = PR * ELD * 4;
+  constexpr int PR = BM / EP, EPIB = PR * ELD * 4;
   static_assert(WM % EP == 0, "epilogue passes split the wave rows");
-  __shared__ __align__(16) char smem[STAGE > EPI ? STAGE : EPI];
+  __shared__ __align__(1024) char smem[STAGE > EPIB ? STAGE : EPIB];  // 1 KB: each direct-to-LDS load fills one aligned KB
   T (*As)[BM * LDK] = (T (*)[BM * LDK])smem;
   T (*Bs)[BN * LDK] = (T (*)[BN * LDK])(smem + 2 * BM * LDK * sizeof(T));
   typedef u32x4 vec_t;
@@ -159,16 +179,12 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
     for (int j = 0; j < NB; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
 
   const int nk = (K + BK - 1) / BK;
-  load(0);
-  store(0, 0);
-  __syncthreads();
   const int r16 = lane & 15, g4 = lane >> 4;
   const int koff = sizeof(T) == 2 ? g4 * 8 : g4;
   // Swizzled chunk of this lane's fragment reads: (kk/8 + g4) ^ sw = (kk/8) ^ (g4 ^ sw), kk/8 in {0, 4}.
   const int sw = SWZ ? (g4 ^ ((r16 >> 1) & 7)) : 0;
-  for (int kt = 0; kt < nk; kt++) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) load((kt + 1) * BK);
+  // The MFMAs of one stage buffer.
+  auto mma = [&](int cur) {
     const T* as = As[cur] + (wm * WTM + r16) * LDK + (SWZ ? 0 : koff);
     const T* bs = Bs[cur] + (wn * WTN + r16) * LDK + (SWZ ? 0 : koff);
     if constexpr (sizeof(T) == 2) {
@@ -205,8 +221,101 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
 #pragma unroll
           for (int j = 0; j < NB; j++) acc[i][j] = mfma16<T>(as + i * 16 * LDK + kk, bs + j * 16 * LDK + kk, acc[i][j]);
     }
-    if (kt + 1 < nk) store(cur ^ 1, (kt + 1) * BK);
+  };
+
+  // 16-bit operands with K a multiple of the stage: stages go straight from memory into LDS
+  // (buffer_load ... lds, 16 bytes per lane). One instruction fills 8 swizzled 128-byte rows (lane i: row i / 8,
+  // stored chunk i % 8, loaded chunk (i % 8) ^ (row / 2 % 8)); the instructions of A and B are dealt round-robin
+  // to the waves. Rows past M or N lie beyond the buffer range and read as zero.
+  constexpr bool DMA = sizeof(T) == 2 && !AF && C::KFULL && SWZ;
+  if constexpr (DMA) {
+    constexpr int NW = WM * WN, AI = BM / 8 / NW, BI = BN / 8 / NW;
+    static_assert(AI * 8 * NW == BM && BI * 8 * NW == BN, "stage rows not divisible over the waves");
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
+    const long arb = (long)lda * 2, brb = (long)ldb * 2;
+    const int abytes = (int)(min(BM, M - m0) * arb), bbytes = (int)(min(BN, N - n0) * brb);
+    int aoff[AI], boff[BI];
+#pragma unroll
+    for (int q = 0; q < AI; q++) {
+      const int row = (q * NW + wv) * 8 + (lane >> 3);
+      aoff[q] = (int)(row * arb) + (((lane & 7) ^ ((row >> 1) & 7)) * 16);
+    }
+#pragma unroll
+    for (int q = 0; q < BI; q++) {
+      const int row = (q * NW + wv) * 8 + (lane >> 3);
+      boff[q] = (int)(row * brb) + (((lane & 7) ^ ((row >> 1) & 7)) * 16);
+    }
+    auto issue = [&](int buf, int k0) {
+#pragma unroll
+      for (int q = 0; q < AI; q++) lds_load16(At0, abytes, As[buf] + (q * NW + wv) * 8 * LDK, aoff[q] + k0 * 2);
+#pragma unroll
+      for (int q = 0; q < BI; q++) lds_load16(Bt0, bbytes, Bs[buf] + (q * NW + wv) * 8 * LDK, boff[q] + k0 * 2);
+    };
+    // Software pipeline over two stage buffers and two fragment register sets: at step kt the fragments of
+    // stage kt + 1 are read from LDS while stage kt's MFMAs run, and stage kt + 2 streams into the buffer that
+    // stage kt occupied. The compiler does not count these loads, so each wave waits for its own before the
+    // barrier (which also waits for the wave's outstanding LDS reads: no buffer is overwritten while read).
+    typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
+    constexpr int KST = BK / KS;
+    frag_t fa[2][KST][MB], fb[2][KST][NB];
+    auto rd = [&](int buf, auto setc) {
+      constexpr int set = decltype(setc)::value;
+      const T* as = As[buf] + (wm * WTM + r16) * LDK;
+      const T* bs = Bs[buf] + (wn * WTN + r16) * LDK;
+#pragma unroll
+      for (int q = 0; q < KST; q++) {
+        const int ko = ((q * KS / 8) ^ sw) * 8;
+#pragma unroll
+        for (int i = 0; i < MB; i++) fa[set][q][i] = *(const frag_t*)(as + i * 16 * LDK + ko);
+#pragma unroll
+        for (int j = 0; j < NB; j++) fb[set][q][j] = *(const frag_t*)(bs + j * 16 * LDK + ko);
+      }
+    };
+    auto mf = [&](auto setc) {
+      constexpr int set = decltype(setc)::value;
+#pragma unroll
+      for (int q = 0; q < KST; q++)
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+          for (int j = 0; j < NB; j++) {
+            if constexpr (std::is_same<T, f16>::value)
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(fa[set][q][i], fb[set][q][j], acc[i][j], 0, 0, 0);
+            else
+              acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fa[set][q][i], fb[set][q][j], acc[i][j], 0, 0, 0);
+          }
+    };
+    // Step kt uses register set kt % 2 and stage buffer kt % 2; the loop runs two steps per trip so that both
+    // are compile-time indices (a runtime index would put the register arrays in scratch memory).
+    auto step = [&](int kt, auto setc) {
+      constexpr int set = decltype(setc)::value;
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (kt + 2 < nk) issue(set, (kt + 2) * BK);
+      if (kt + 1 < nk) rd(set ^ 1, std::integral_constant<int, set ^ 1>{});
+      mf(setc);
+    };
+    issue(0, 0);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
+    rd(0, std::integral_constant<int, 0>{});
+    if (nk > 1) issue(1, BK);
+    for (int kt = 0; kt < nk; kt += 2) {
+      step(kt, std::integral_constant<int, 0>{});
+      if (kt + 1 < nk) step(kt + 1, std::integral_constant<int, 1>{});
+    }
+  } else {
+    load(0);
+    store(0, 0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) load((kt + 1) * BK);
+      mma(cur);
+      if (kt + 1 < nk) store(cur ^ 1, (kt + 1) * BK);
+      __syncthreads();
+    }
   }
 
   ConvOut o = g.out;
@@ -214,7 +323,7 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
     if (o.y) o.y += (size_t)z * g.sC;
     if (o.yt) o.yt = (T*)o.yt + (size_t)z * g.sC;
   }
-  if (!g.vec_epi) {
+  if constexpr (EPI == EPI_SCALAR) {
     // Output element (i, j, r) of this lane: row wm*WTM + i*16 + 4*(lane/16) + r, column wn*WTN + j*16 + lane%16.
 #pragma unroll
     for (int i = 0; i < MB; i++)
@@ -232,6 +341,8 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
   // float tile, then four consecutive columns of one row per thread with 16-byte accesses, the per-row and
   // per-column inputs loaded ahead of the stores.
   float* Et = (float*)smem;
+  constexpr int CV = BN / 4, EV = PR * CV / NT;
+  static_assert(EV * NT == PR * CV, "epilogue vectors not divisible over the threads");
 #pragma unroll
   for (int p = 0; p < EP; p++) {
     if (p) __syncthreads();
@@ -246,7 +357,7 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
     }
     __syncthreads();
     const int mp = m0 + p * PR;
-    if (g.glu) {
+    if constexpr (EPI == EPI_GLU) {
       constexpr int HV = BN / 8;  // 4-wide vectors of gated outputs per tile row
       for (int e = tid; e < PR * HV; e += NT) {
         const int r = e / HV, hc = (e % HV) * 4, lc = (hc / 16) * 32 + hc % 16;
@@ -257,11 +368,7 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
                     act_f<ACT_SILU>(a[2]) * b[2], act_f<ACT_SILU>(a[3]) * b[3]);
         }
       }
-      continue;
-    }
-    constexpr int CV = BN / 4, EV = PR * CV / NT;
-    static_assert(EV * NT == PR * CV, "epilogue vectors not divisible over the threads");
-    if (g.qkv.dq) {
+    } else if constexpr (EPI == EPI_QKV) {
       // q|k|v projection: each head lies inside the tile, so the rotation partner of column n (n +- dq/2) is
       // in LDS too.
       const QkvEpi& q = g.qkv;
@@ -276,9 +383,9 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
             const int hh = (n - (isq ? 0 : q.nq)) / q.dq, rr = (n - (isq ? 0 : q.nq)) - hh * q.dq;
             if (q.cos) {
               const bool lo = rr < half;
-              const int p = lo ? rr : rr - half, tab = q.tables == 1 ? 0 : (isq ? hh / (q.H / q.KV) : hh);
+              const int pp = lo ? rr : rr - half, tab = q.tables == 1 ? 0 : (isq ? hh / (q.H / q.KV) : hh);
               const floatx4 y = *(const floatx4*)(Et + r * ELD + c + (lo ? half : -half));
-              const size_t ti = ((size_t)tab * HW + m % HW) * half + p;
+              const size_t ti = ((size_t)tab * HW + m % HW) * half + pp;
               const floatx4 cs = *(const floatx4*)(q.cos + ti), sn = *(const floatx4*)(q.sin + ti);
               x = lo ? x * cs - y * sn : y * sn + x * cs;
             }
@@ -287,27 +394,49 @@ __global__ __launch_bounds__(C::WM * C::WN * 64) void gemm_kernel(GemmArgs g) {
           store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, x[0], x[1], x[2], x[3]);
         }
       }
-      continue;
-    }
-    floatx4 yres[EV];
-    float rmv[EV], mkv[EV];
+    } else if constexpr (EPI == EPI_YT) {
 #pragma unroll
-    for (int v = 0; v < EV; v++) {
-      const int e = tid + NT * v, m = min(mp + e / CV, M - 1), n = min(n0 + (e % CV) * 4, N - 4);
-      yres[v] = o.y && o.accumulate ? *(const floatx4*)(o.y + (size_t)m * o.ldy + n) : floatx4{0.f, 0.f, 0.f, 0.f};
-      rmv[v] = o.rowmask ? o.rowmask[m] : 1.f;
-      mkv[v] = o.emit.scale ? o.emit.mask[m] : 1.f;
-    }
-#pragma unroll
-    for (int v = 0; v < EV; v++) {
-      const int e = tid + NT * v, r = e / CV, c = (e % CV) * 4, m = mp + r, n = n0 + c;
-      if (m < M && n < N) {
-        floatx4 es = {1.f, 1.f, 1.f, 1.f}, eb = {0.f, 0.f, 0.f, 0.f};
-        if (o.emit.scale) {
-          es = *(const floatx4*)(o.emit.scale + n);
-          eb = *(const floatx4*)(o.emit.bias + n);
+      for (int v = 0; v < EV; v++) {
+        const int e = tid + NT * v, r = e / CV, c = (e % CV) * 4, m = mp + r, n = n0 + c;
+        if (m < M && n < N) {
+          const floatx4 x = *(const floatx4*)(Et + r * ELD + c);
+          store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, x[0], x[1], x[2], x[3]);
         }
-        conv_store4<T>(o, m, n, *(const floatx4*)(Et + r * ELD + c), yres[v], rmv[v], es, eb, mkv[v]);
+      }
+    } else if constexpr (EPI == EPI_ACC) {
+      // Float output, the residual and row mask loaded ahead of the stores.
+      floatx4 yres[EV];
+      float rmv[EV];
+#pragma unroll
+      for (int v = 0; v < EV; v++) {
+        const int e = tid + NT * v, m = min(mp + e / CV, M - 1), n = min(n0 + (e % CV) * 4, N - 4);
+        yres[v] = o.accumulate ? *(const floatx4*)(o.y + (size_t)m * o.ldy + n) : floatx4{0.f, 0.f, 0.f, 0.f};
+        rmv[v] = o.rowmask ? o.rowmask[m] : 1.f;
+      }
+#pragma unroll
+      for (int v = 0; v < EV; v++) {
+        const int e = tid + NT * v, r = e / CV, c = (e % CV) * 4, m = mp + r, n = n0 + c;
+        if (m < M && n < N)
+          *(floatx4*)(o.y + (size_t)m * o.ldy + n) = *(const floatx4*)(Et + r * ELD + c) * rmv[v] + yres[v];
+      }
+    } else {
+      // Generic (EPI_GEN): one vector at a time, not unrolled, to keep the code small.
+#pragma unroll 1
+      for (int v = 0; v < EV; v++) {
+        const int e = tid + NT * v, r = e / CV, c = (e % CV) * 4, m = mp + r, n = n0 + c;
+        if (m < M && n < N) {
+          const floatx4 yres = o.y && o.accumulate ? *(const floatx4*)(o.y + (size_t)m * o.ldy + n)
+                                                   : floatx4{0.f, 0.f, 0.f, 0.f};
+          floatx4 es = {1.f, 1.f, 1.f, 1.f}, eb = {0.f, 0.f, 0.f, 0.f};
+          float mk = 1.f;
+          if (o.emit.scale) {
+            es = *(const floatx4*)(o.emit.scale + n);
+            eb = *(const floatx4*)(o.emit.bias + n);
+            mk = o.emit.mask[m];
+          }
+          conv_store4<T>(o, m, n, *(const floatx4*)(Et + r * ELD + c), yres, o.rowmask ? o.rowmask[m] : 1.f, es,
+                         eb, mk);
+        }
       }
     }
   }
@@ -321,12 +450,32 @@ typedef Cfg<128, 128, 64, 2, 2, true> CfgWide;
 typedef Cfg<64, 64, 32, 2, 2> CfgSmall;
 typedef Cfg<64, 96, 64, 2, 2, true> CfgHead;  // the heads' first convolutions: N = p1 + g1 + v1 channels <= 96
 
+// The epilogue a GEMM's outputs need (launch_gemm has set vec_epi and validated glu / qkv).
+static int gemm_epi(const GemmArgs& g) {
+  const ConvOut& o = g.out;
+  if (!g.vec_epi) return EPI_SCALAR;
+  if (g.glu) return EPI_GLU;
+  if (g.qkv.dq) return EPI_QKV;
+  if (o.colbias || o.emit.scale) return EPI_GEN;
+  if (o.yt && !o.y && !o.rowmask) return EPI_YT;
+  if (o.y && !o.yt) return EPI_ACC;
+  return EPI_GEN;
+}
+
 template <typename T, typename C, bool AF, bool PRO, int ACT>
 static void gemm_launch(const GemmArgs& g, hipStream_t s) {
+  const int epi = gemm_epi(g);
   if (g.qkv.dq && C::BN % g.qkv.dq)
     throw std::runtime_error("gemm: the q|k|v epilogue needs the column tile to hold whole heads");
   dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM, g.Z);
-  gemm_kernel<T, C, AF, PRO, ACT><<<grid, C::WM * C::WN * 64, 0, s>>>(g);
+  switch (epi) {
+    case EPI_SCALAR: gemm_kernel<T, C, AF, PRO, ACT, EPI_SCALAR><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
+    case EPI_YT: gemm_kernel<T, C, AF, PRO, ACT, EPI_YT><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
+    case EPI_ACC: gemm_kernel<T, C, AF, PRO, ACT, EPI_ACC><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
+    case EPI_GLU: gemm_kernel<T, C, AF, PRO, ACT, EPI_GLU><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
+    case EPI_QKV: gemm_kernel<T, C, AF, PRO, ACT, EPI_QKV><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
+    default: gemm_kernel<T, C, AF, PRO, ACT, EPI_GEN><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
+  }
 }
 
 template <typename T, bool AF, bool PRO, int ACT>

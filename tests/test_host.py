@@ -22,6 +22,19 @@ def test_library_exports_every_declared_symbol(kgx):
     assert sorted(kgx.EXPORTS) == declared
 
 
+def test_library_defines_every_kernel_stub(kgx):
+    """A kernel template whose host-side instantiation fails is dropped silently, leaving its launch stub
+    undefined in the shared library (it would fail only when loaded with lazy binding resolved)."""
+    import shutil
+    import subprocess
+    nm = shutil.which("nm")
+    if nm is None:
+        pytest.skip("nm not available")
+    so = os.path.join(ROOT, "katago-rs_amd", "libkgx.so")
+    out = subprocess.run([nm, "-D", "--undefined-only", so], capture_output=True, text=True, check=True).stdout
+    assert "__device_stub__" not in out, [l for l in out.splitlines() if "__device_stub__" in l][:5]
+
+
 def _nets(synth):
     nets = dict(synth.tiny_nets())
     for name in ("b10c128", "b18c384nbt", "b10c384h6"):
