@@ -38,6 +38,7 @@ enum GemmEpi {
   EPI_ACC,     // float store or residual add (+ row mask) only
   EPI_GLU,     // gated output
   EPI_QKV,     // q|k|v projection
+  EPI_YTMISH,  // compute-type store of mish(C)
 };
 
 template <typename T, typename C, bool AF, bool PRO, int ACT, int EPI>
@@ -394,12 +395,16 @@ __global__ __launch_bounds__(C::WM * C::WN * 64, 2) void gemm_kernel(GemmArgs g)
           store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, x[0], x[1], x[2], x[3]);
         }
       }
-    } else if constexpr (EPI == EPI_YT) {
+    } else if constexpr (EPI == EPI_YT || EPI == EPI_YTMISH) {
 #pragma unroll
       for (int v = 0; v < EV; v++) {
         const int e = tid + NT * v, r = e / CV, c = (e % CV) * 4, m = mp + r, n = n0 + c;
         if (m < M && n < N) {
-          const floatx4 x = *(const floatx4*)(Et + r * ELD + c);
+          floatx4 x = *(const floatx4*)(Et + r * ELD + c);
+          if constexpr (EPI == EPI_YTMISH) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) x[q] = act_f<ACT_MISH>(x[q]);
+          }
           store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, x[0], x[1], x[2], x[3]);
         }
       }
@@ -456,6 +461,7 @@ static int gemm_epi(const GemmArgs& g) {
   if (!g.vec_epi) return EPI_SCALAR;
   if (g.glu) return EPI_GLU;
   if (g.qkv.dq) return EPI_QKV;
+  if (g.yt_act == ACT_MISH) return EPI_YTMISH;
   if (o.colbias || o.emit.scale) return EPI_GEN;
   if (o.yt && !o.y && !o.rowmask) return EPI_YT;
   if (o.y && !o.yt) return EPI_ACC;
@@ -474,6 +480,7 @@ static void gemm_launch(const GemmArgs& g, hipStream_t s) {
     case EPI_ACC: gemm_kernel<T, C, AF, PRO, ACT, EPI_ACC><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
     case EPI_GLU: gemm_kernel<T, C, AF, PRO, ACT, EPI_GLU><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
     case EPI_QKV: gemm_kernel<T, C, AF, PRO, ACT, EPI_QKV><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
+    case EPI_YTMISH: gemm_kernel<T, C, AF, PRO, ACT, EPI_YTMISH><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
     default: gemm_kernel<T, C, AF, PRO, ACT, EPI_GEN><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
   }
 }
@@ -529,6 +536,12 @@ void launch_gemm(int prec, const GemmArgs& g0, hipStream_t s) {
   if (g0.Z > 1 && g0.out.emit.scale) throw std::runtime_error("gemm: batched GEMMs carry no emission");
   GemmArgs g = g0;
   g.vec_epi = vector_epilogue_ok(g, prec == PREC_F32 ? 4 : 2);
+  if (g.yt_act != ACT_ID) {
+    const ConvOut& o = g.out;
+    if (g.yt_act != ACT_MISH || !g.vec_epi || g.glu || g.qkv.dq || !o.yt || o.y || o.emit.scale || o.colbias ||
+        o.rowmask)
+      throw std::runtime_error("gemm: an output activation needs only a compute-type store (mish)");
+  }
   if (g.qkv.dq) {
     const ConvOut& o = g.out;
     const QkvEpi& q = g.qkv;

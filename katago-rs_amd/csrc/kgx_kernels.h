@@ -92,6 +92,8 @@ struct GemmArgs {
   // Gated output (SwiGLU): the columns come in 16-wide pairs of blocks (value block, gate block) and the GEMM
   // writes only out.yt[m][f] = silu(C[m][32 (f / 16) + f % 16]) * C[m][32 (f / 16) + 16 + f % 16], f < N / 2.
   bool glu = false;
+  // Activation of the compute-type output alone (ACT_ID or ACT_MISH): out.yt = act(C), as the mish FFN's h.
+  int yt_act = ACT_ID;
   QkvEpi qkv;
   bool vec_epi = false;  // set by launch_gemm: the four-column vector epilogue applies
 };

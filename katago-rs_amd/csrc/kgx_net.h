@@ -102,7 +102,8 @@ class Net {
   void emit_attention(const BlockDesc& b, int depth);
   void emit_ffn(const BlockDesc& b, int depth);
   std::shared_ptr<ConvOut> emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, const ConvOut& o,
-                                           const char* cls, bool glu = false, const QkvEpi& qkv = QkvEpi());
+                                           const char* cls, bool glu = false, const QkvEpi& qkv = QkvEpi(),
+                                           int yt_act = ACT_ID);
   // The activation act(bn(x)) * mask of stream `depth`, emitted by the stream's last producer.
   void* consume(int depth, const BNDesc& bn, int act);
   Emit bn_emit(const BNDesc& bn, int act, void* out, int ld);

@@ -303,7 +303,7 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
 }
 
 std::shared_ptr<ConvOut> Net::emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, const ConvOut& o,
-                                              const char* cls, bool glu, const QkvEpi& qkv) {
+                                              const char* cls, bool glu, const QkvEpi& qkv, int yt_act) {
   const int prec = prec_;
   auto out = std::make_shared<ConvOut>(o);
   Op op;
@@ -315,6 +315,7 @@ std::shared_ptr<ConvOut> Net::emit_token_gemm(const void* A, int lda, const void
     g.M = B * HW; g.N = N; g.K = K;
     g.glu = glu;
     g.qkv = qkv;
+    g.yt_act = yt_act;
     launch_gemm(prec, g, s);
   };
   op.cls = cls;
@@ -435,8 +436,7 @@ void Net::emit_ffn(const BlockDesc& b, int depth) {
   const int F = b.ffn_c, Fu = b.swiglu ? 2 * F : F;
   // The activation runs in the first GEMM's epilogue: SwiGLU through its gated output, whose B^T rows alternate
   // 16 value features and the 16 matching gate features (F % 16 == 0; otherwise u = [value | gate] goes through
-  // the separate activation kernel); mish through the emission (unit scale, zero bias, board mask: masked rows of
-  // h only reach output rows that the second GEMM masks).
+  // the separate activation kernel); mish as the activation of its compute-type output.
   const bool fused = !b.swiglu || F % 16 == 0;
   auto row_of = [&](int f, bool gate) {
     if (!b.swiglu) return f;
@@ -469,13 +469,9 @@ void Net::emit_ffn(const BlockDesc& b, int depth) {
     o1.ldyt = F;
     emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm", true);
   } else if (fused) {
-    o1.emit.scale = upload_f(std::vector<float>(F, 1.f));
-    o1.emit.bias = upload_f(std::vector<float>(F, 0.f));
-    o1.emit.act = ACT_MISH;
-    o1.emit.mask = mask_;
-    o1.emit.out = h_;
-    o1.emit.ld = F;
-    emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm");
+    o1.yt = h_;
+    o1.ldyt = F;
+    emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm", false, QkvEpi(), ACT_MISH);
   } else {
     o1.y = u_;
     o1.ldy = Fu;
