@@ -84,7 +84,7 @@ __device__ __forceinline__ void conv_store(const ConvOut& o, int m, int n, float
   if (o.y) {
     float* p = o.y + (size_t)m * o.ldy + n;
     if (o.accumulate) v += *p;
-    *p = v;
+    if (!o.y_dead) *p = v;
   }
   if (o.emit.scale)
     ((T*)o.emit.out)[(size_t)m * o.emit.ld + n] =
@@ -115,7 +115,7 @@ __device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floa
   if (o.yt) store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, v[0], v[1], v[2], v[3]);
   if (o.y) {
     if (o.accumulate) v += yacc;
-    *(floatx4*)(o.y + (size_t)m * o.ldy + n) = v;
+    if (!o.y_dead) *(floatx4*)(o.y + (size_t)m * o.ldy + n) = v;
   }
   if (o.emit.scale) {
     float t[4];

@@ -464,7 +464,7 @@ static int gemm_epi(const GemmArgs& g) {
   if (g.yt_act == ACT_MISH) return EPI_YTMISH;
   if (o.colbias || o.emit.scale) return EPI_GEN;
   if (o.yt && !o.y && !o.rowmask) return EPI_YT;
-  if (o.y && !o.yt) return EPI_ACC;
+  if (o.y && !o.yt && !o.y_dead) return EPI_ACC;
   return EPI_GEN;
 }
 

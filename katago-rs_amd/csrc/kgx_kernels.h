@@ -42,6 +42,8 @@ struct Emit {
 struct ConvOut {
   float* y = nullptr; int ldy = 0;
   bool accumulate = false;
+  bool y_dead = false;  // y (and the residual, when accumulating) is read but the result is not stored: the
+                        // stream ends here and only the emission consumes it
   const float* colbias = nullptr; int ld_colbias = 0;
   const float* rowmask = nullptr;
   void* yt = nullptr; int ldyt = 0;

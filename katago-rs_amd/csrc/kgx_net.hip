@@ -567,7 +567,11 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
         o1.ldy = ci;
         in.producer = emit_conv(b.regular, a, c, false, o1);
         emit_stack(b.inner, depth + 1);
+        // The inner stream ends with this activation: its last producer computes the stream's final value only
+        // for the emission, so that sum is not stored.
+        const std::shared_ptr<ConvOut> last = ss_[depth + 1].producer;
         const void* a2 = consume(depth + 1, b.mid_bn, b.mid_act);
+        if (last) last->y_dead = true;
         ss_[depth].producer = emit_conv(b.final_conv, a2, ci, false, res);
         break;
       }
