@@ -77,6 +77,8 @@ def main():
     ap.add_argument("--cpu-rows", type=int, default=-1,
                     help="rows in the CPU-baseline sample (-1: the whole batch, 0: skip)")
     ap.add_argument("--cpu-threads", type=int, default=0, help="CPU-baseline threads (0: min(16, cores))")
+    ap.add_argument("--handles", type=int, default=2,
+                    help="also time this many handles in flight, one thread each (reported as 'pipelined'; 1: skip)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="only run a device copy of this many MiB (counter calibration) and exit")
     args = ap.parse_args()
@@ -166,6 +168,38 @@ def main():
         roof = {"bound": "hbm", "kernel": dname, "achieved": achieved, "peak": PEAK_HBM_GBS, "unit": "GB/s",
                 "frac": achieved / PEAK_HBM_GBS, "traffic": None,
                 "work_per_launch": dv["bytes"] / max(dv["launches"], 1), "avg_launch_us": per_launch_ms * 1e3}
+    # Several handles in flight (one engine thread per handle, as the reference's serve tasks, docs/M9-report.md):
+    # each step is still one batch's forward + readback, on its handle's own stream; the handles' kernels fill
+    # each other's gaps. Reported beside the single-forward value, not as it.
+    pipelined = None
+    if args.handles > 1:
+        import threading
+        hs = [h] + [kgx.Handle(net, batch, args.precision, device=0) for _ in range(args.handles - 1)]
+        for hh in hs[1:]:
+            db, dg, dm, _ = hh.device_buffers()
+            assert hip.hipMemcpy(db, sp.ctypes.data, sp.nbytes, 1) == 0
+            assert hip.hipMemcpy(dg, gl.ctypes.data, gl.nbytes, 1) == 0
+            if me is not None:
+                assert hip.hipMemcpy(dm, me.ctypes.data, me.nbytes, 1) == 0
+
+        def loop(hh, k):
+            o = np.empty((batch, net.row_len), np.float32)
+            for _ in range(k):
+                hh.run(batch, o)
+
+        for hh in hs:
+            loop(hh, args.warmup)
+        ths = [threading.Thread(target=loop, args=(hh, args.steps)) for hh in hs]
+        t2 = time.perf_counter()
+        for t in ths:
+            t.start()
+        for t in ths:
+            t.join()
+        pdt = time.perf_counter() - t2
+        pipelined = {"handles": args.handles, "value": args.handles * batch * args.steps / pdt, "unit": "evals/s",
+                     "steps_per_handle": args.steps}
+        for hh in hs[1:]:
+            hh.close()
     h.close()
 
     workload = f"{args.config} {args.precision} batch {batch}"
@@ -210,6 +244,7 @@ def main():
         "kernels": classes,
         "profiled_ms_per_step": prof_ms_per_step,
         "checksum": checksum,
+        "pipelined": pipelined,
     }
     print(json.dumps(res))
 

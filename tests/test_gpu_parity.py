@@ -173,6 +173,35 @@ def test_graph_replays_are_deterministic(kgx, synth):
     h.close()
 
 
+def test_handles_in_flight_match_sequential(kgx, synth):
+    """Several handles of one net, each driven by its own thread (the reference's serve tasks in flight,
+    backend.rs:598-605): every handle's outputs equal the same handle's outputs run alone."""
+    import threading
+    arch = synth.tiny_nets()["t_nbt"]
+    net = kgx.Net(synth.write_model(arch, 4))
+    hs = [kgx.Handle(net, 8, "f16") for _ in range(3)]
+    inputs = [synth.make_inputs(8, 20 + i) for i in range(3)]
+    alone = [h.forward(sp, gl) for h, (sp, gl, _) in zip(hs, inputs)]
+    got = [[] for _ in hs]
+
+    def drive(i):
+        sp, gl, _ = inputs[i]
+        for _ in range(20):
+            got[i].append(hs[i].forward(sp, gl))
+
+    ths = [threading.Thread(target=drive, args=(i,)) for i in range(3)]
+    for t in ths:
+        t.start()
+    for t in ths:
+        t.join()
+    for i in range(3):
+        assert len(got[i]) == 20
+        for out in got[i]:
+            assert np.array_equal(out, alone[i]), i
+    for h in hs:
+        h.close()
+
+
 def test_get_output_applies_symmetry_and_optimism(kgx, synth, oracle):
     arch = synth.tiny_nets()["t_rms"]  # P = 4 at model version 17: the optimism mix uses channels 0 and 1
     mb = synth.write_model(arch, 8)
