@@ -179,8 +179,9 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     }
   };
   // Epilogue mapping: thread tid finishes the four channels 4 * (tid % G4) of rows tid / G4 + e * RPE, so its
-  // emit scale and bias are loaded once. The 3x3 kernel reads the residual values before the main loop so that
-  // the reads overlap it; the 1x1 kernel reads them after (its registers stay within two workgroups per CU).
+  // emit scale and bias are loaded once. The 3x3 kernel reads the residual values, masks and emit parameters
+  // before the main loop so that the reads overlap it (0.4-1 us less per conv than after the loop); the 1x1
+  // kernel reads them after (read early they spill at its 128-register bound of two workgroups per CU).
   constexpr int G4 = BN / 4, RPE = NT / G4, EV = (BM + RPE - 1) / RPE;
   constexpr bool YEARLY = C::KS == 3;
   const int ec4 = tid % G4, er0 = tid / G4, en = n0 + 4 * ec4;
@@ -199,7 +200,21 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
       for (int e = 0; e < EV; e++) yres[e] = *(const floatx4*)(o.y + (size_t)epix(e) * o.ldy + enc);
     }
   };
-  if constexpr (YEARLY) load_y();
+  float rmv[EV], mkv[EV];
+  floatx4 es, eb;
+  auto load_side = [&]() {
+    if (o.emit.scale) {
+      es = *(const floatx4*)(o.emit.scale + enc);
+      eb = *(const floatx4*)(o.emit.bias + enc);
+#pragma unroll
+      for (int e = 0; e < EV; e++) mkv[e] = o.emit.mask[epix(e)];
+    }
+    if (o.rowmask) {
+#pragma unroll
+      for (int e = 0; e < EV; e++) rmv[e] = o.rowmask[epix(e)];
+    }
+  };
+  if constexpr (YEARLY) { load_y(); load_side(); }
 
   // The zero row of every stage buffer (never written by the stage stores).
   for (int e = tid; e < NBUF * KV; e += NT) *(vec_t*)(As + (e / KV) * SE + AR * LDK + (e % KV) * 8) = vec_t{0, 0, 0, 0};
@@ -239,19 +254,7 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
       for (int r = 0; r < 4; r++) Cg[(wm * WTM + i * 16 + 4 * g4 + r) * LDC + wn * WTN + j * 16 + r16] = acc[i][j][r];
   __syncthreads();
   // The other epilogue inputs, loaded after the accumulator exchange and before the first store.
-  if constexpr (!YEARLY) load_y();
-  float rmv[EV], mkv[EV];
-  floatx4 es, eb;
-  if (o.emit.scale) {
-    es = *(const floatx4*)(o.emit.scale + enc);
-    eb = *(const floatx4*)(o.emit.bias + enc);
-#pragma unroll
-    for (int e = 0; e < EV; e++) mkv[e] = o.emit.mask[epix(e)];
-  }
-  if (o.rowmask) {
-#pragma unroll
-    for (int e = 0; e < EV; e++) rmv[e] = o.rowmask[epix(e)];
-  }
+  if constexpr (!YEARLY) { load_y(); load_side(); }
 
 #pragma unroll
   for (int e = 0; e < EV; e++) {
