@@ -163,13 +163,26 @@ struct RowMM {
   float* out = nullptr; long ldout = 0; int ostride = 1; bool accumulate = false;
   int wlds = -1;                              // LDS float offset of a staged copy of W, or -1 (read from memory)
 };
+// Optional last stage: the workgroup's share [o0, o1) of the last matmul's outputs (kept in LDS at its dst) is a
+// per-row channel bias, and out[m][c] = T(act((x[m][c] + bias_row[c]) * scale[c] + bias[c]) * mask[m]) for the
+// row's HW points and c in [o0, o1) (launch_bias_act's arithmetic; 16-bit compute types only). Its loads of x are
+// issued before the pooling, so they overlap it.
+struct RowEmit {
+  const float* x = nullptr; int ldx = 0;  // null: no emission
+  const float* scale = nullptr; const float* bias = nullptr; int act = ACT_ID;
+  void* out = nullptr; int ldo = 0; int prec = PREC_F16;
+};
+constexpr int RE_MAX = 4;  // emitted 8-channel vectors per thread: (o1 - o0) / 8 * HW <= RE_MAX * 1024
 struct RowProg {
   RowPool pool[2]; int npool = 0;
   RowMM mm[8]; int nmm = 0;
   int lds_floats = 0;  // LDS features and intermediates
   int splits = 1;      // workgroups per row sharing the outputs of the (single) matmul
   const float* mask = nullptr; const float* area = nullptr; const float* s1 = nullptr; const float* s2 = nullptr;
+  RowEmit emit;
 };
+// Whether a row program with `splits` output shares of an OC-output last matmul can carry an emission.
+bool row_emit_fits(int OC, int splits);
 // Independent row programs of one launch (blockIdx.y picks the program).
 struct RowProgs {
   static constexpr int MAX = 3;

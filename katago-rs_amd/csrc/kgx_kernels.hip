@@ -306,6 +306,28 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
   float* mk = red + 2 * RP_NT;
   if (P.npool > 0)
     for (int p = threadIdx.x; p < HW; p += RP_NT) mk[p] = P.mask[(size_t)b * HW + p];
+  // The emission's inputs come first: this thread's x vectors into registers, the share's batch-norm scale and
+  // bias into LDS after the mask (the barrier after the weight staging publishes them).
+  const RowEmit& E = P.emit;
+  floatx4 ex[RE_MAX][2];
+  int e_o0 = 0, e_n8 = 0;
+  float* esb = mk + HW;
+  if (E.x) {
+    const int per = P.mm[P.nmm - 1].OC / nsplit;
+    e_o0 = split * per;
+    e_n8 = per / 8;
+#pragma unroll
+    for (int k = 0; k < RE_MAX; k++) {
+      const int v = threadIdx.x + k * RP_NT;
+      if (v < HW * e_n8) {
+        const int p = v / e_n8, c = e_o0 + (v - p * e_n8) * 8;
+        const float* xp = E.x + ((size_t)b * HW + p) * E.ldx + c;
+        ex[k][0] = *(const floatx4*)xp;
+        ex[k][1] = *(const floatx4*)(xp + 4);
+      }
+    }
+    for (int i = threadIdx.x; i < 2 * per; i += RP_NT) esb[i] = i < per ? E.scale[e_o0 + i] : E.bias[e_o0 + i - per];
+  }
   {
     // Staged weights: the whole set as one list of 16-byte vectors, RP_WB loads per thread in flight.
     constexpr int RP_WB = 8;
@@ -347,6 +369,41 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
     }
     row_mm(m, b, lds, red, o0, o1);
   }
+  if (E.x) {
+    // row_mm ends with a barrier: the share's per-row bias is in LDS at the last matmul's dst.
+    const float* rb = lds + P.mm[P.nmm - 1].dst;
+    const int per = e_n8 * 8;
+#pragma unroll
+    for (int k = 0; k < RE_MAX; k++) {
+      const int v = threadIdx.x + k * RP_NT;
+      if (v < HW * e_n8) {
+        const int p = v / e_n8, cl = (v - p * e_n8) * 8, c = e_o0 + cl;
+        const float m = mk[p];
+        float t[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+          const float a = ex[k][e >> 2][e & 3] + rb[c + e];
+          t[e] = act_rt(a * esb[cl + e] + esb[per + cl + e], E.act) * m;
+        }
+        u32x4 w;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          unsigned short lo, hi;
+          if (E.prec == PREC_F16) {
+            const f16 l = to_t<f16>(t[2 * e]), h = to_t<f16>(t[2 * e + 1]);
+            lo = __builtin_bit_cast(unsigned short, l);
+            hi = __builtin_bit_cast(unsigned short, h);
+          } else {
+            const bf16 l = to_t<bf16>(t[2 * e]), h = to_t<bf16>(t[2 * e + 1]);
+            lo = __builtin_bit_cast(unsigned short, l);
+            hi = __builtin_bit_cast(unsigned short, h);
+          }
+          w[e] = lo | ((unsigned)hi << 16);
+        }
+        *(u32x4*)((unsigned short*)E.out + ((size_t)b * HW + p) * E.ldo + c) = w;
+      }
+    }
+  }
 }
 
 // blockIdx.x: the batch row; blockIdx.y: the program (several independent programs), or the output share of the
@@ -357,8 +414,21 @@ __global__ __launch_bounds__(RP_NT) void row_prog_kernel(RowProgs PS) {
   else run_row_prog(PS.p[0], blockIdx.x, blockIdx.y, gridDim.y, lds);
 }
 
+bool row_emit_fits(int OC, int splits) {
+  return splits >= 1 && OC % splits == 0 && (OC / splits) % 8 == 0 && (OC / splits) / 8 * HW <= RE_MAX * RP_NT;
+}
+
 static size_t row_prog_check(const RowProg& p) {
-  const size_t lds = ((size_t)p.lds_floats + 2 * RP_NT + HW) * sizeof(float);
+  const RowEmit& e = p.emit;
+  const size_t lds = ((size_t)p.lds_floats + 2 * RP_NT + HW + (e.x ? 2 * p.mm[p.nmm > 0 ? p.nmm - 1 : 0].OC : 0)) *
+                     sizeof(float);
+  if (e.x) {
+    const RowMM& lm = p.mm[p.nmm > 0 ? p.nmm - 1 : 0];
+    if (p.nmm < 1 || p.npool < 1 || lm.dst < 0 || lm.dst + lm.OC > p.lds_floats || !row_emit_fits(lm.OC, p.splits) ||
+        (e.prec != PREC_F16 && e.prec != PREC_BF16) || e.ldx % 4 || e.ldo % 8 || !e.scale || !e.bias || !e.out ||
+        ((uintptr_t)e.x | (uintptr_t)e.out) % 16)
+      throw std::runtime_error("row program: unsupported emission layout");
+  }
   for (int k = 0; k < p.nmm; k++)
     if (p.mm[k].wlds >= 0 && ((p.mm[k].IC * p.mm[k].OC) % 4 || p.mm[k].wlds % 4 ||
                               p.mm[k].wlds + p.mm[k].IC * p.mm[k].OC > p.lds_floats))
