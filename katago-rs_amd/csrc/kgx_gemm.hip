@@ -106,6 +106,10 @@ __global__ __launch_bounds__(C::WM * C::WN * 64, 2) void gemm_kernel(GemmArgs g)
   vec_t ra[AF ? 1 : AV];
   float rf[AF ? AV * VEC : 1];
   vec_t rb[BV];
+  // The float-A prologue's per-element parameters travel with the stage's loads (loaded where the A values are,
+  // so the stores after the MFMAs wait for no memory).
+  constexpr int PV = AF && PRO ? AV : 1;
+  float rsc[PV * VEC], rbi[PV * VEC], rpb[PV * VEC], rmk[PV];
 
   auto load = [&](int k0) {
 #pragma unroll
@@ -125,6 +129,20 @@ __global__ __launch_bounds__(C::WM * C::WN * 64, 2) void gemm_kernel(GemmArgs g)
           float4 q = *(const float4*)(Af0 + off + e);
           if (!ok) q = float4{0.f, 0.f, 0.f, 0.f};
           rf[v * VEC + e] = q.x; rf[v * VEC + e + 1] = q.y; rf[v * VEC + e + 2] = q.z; rf[v * VEC + e + 3] = q.w;
+        }
+        if constexpr (PRO) {
+          const int mm = ok ? m0 + a_row[v] : 0, kc = ok ? k0 + a_kk[v] : 0;
+          rmk[v] = g.pro.mask[mm];
+#pragma unroll
+          for (int e = 0; e < VEC; e++) {
+            rsc[v * VEC + e] = g.pro.scale[kc + e];
+            rbi[v * VEC + e] = g.pro.bias[kc + e];
+          }
+          if (g.pro.prebias) {
+            const float* pb = g.pro.prebias + (size_t)(mm / HW) * g.pro.ld_prebias + kc;
+#pragma unroll
+            for (int e = 0; e < VEC; e++) rpb[v * VEC + e] = pb[e];
+          }
         }
       }
     }
@@ -148,18 +166,12 @@ __global__ __launch_bounds__(C::WM * C::WN * 64, 2) void gemm_kernel(GemmArgs g)
       } else {
         T t[VEC];
         if constexpr (PRO) {
-          const int m = m0 + a_row[v], k = k0 + a_kk[v];
-          const bool ok = m < M && k < K;
-          const int mm = ok ? m : 0, kc = ok ? k : 0;
-          const float mk = g.pro.mask[mm];
-          const float* pb = g.pro.prebias ? g.pro.prebias + (size_t)(mm / HW) * g.pro.ld_prebias + kc : nullptr;
-          const float* sc = g.pro.scale + kc;
-          const float* bi = g.pro.bias + kc;
+          const bool ok = m0 + a_row[v] < M && k0 + a_kk[v] < K;
 #pragma unroll
           for (int e = 0; e < VEC; e++) {
             float a = rf[v * VEC + e];
-            if (pb) a += pb[e];
-            const float y = act_f<ACT>(a * sc[e] + bi[e]) * mk;
+            if (g.pro.prebias) a += rpb[v * VEC + e];
+            const float y = act_f<ACT>(a * rsc[v * VEC + e] + rbi[v * VEC + e]) * rmk[v];
             t[e] = to_t<T>(ok ? y : 0.f);
           }
         } else {

@@ -179,11 +179,13 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     }
   };
   // Epilogue mapping: thread tid finishes the four channels 4 * (tid % G4) of rows tid / G4 + e * RPE, so its
-  // emit scale and bias are loaded once. The 3x3 kernel reads the residual values, masks and emit parameters
-  // before the main loop so that the reads overlap it (0.4-1 us less per conv than after the loop); the 1x1
-  // kernel reads them after (read early they spill at its 128-register bound of two workgroups per CU).
+  // emit scale and bias are loaded once. The 3x3 kernel reads the residual values before the main loop so that
+  // the reads overlap it, and on 48-column tiles also the masks and emit parameters (0.4-1 us less per conv than
+  // after the loop); the wider 3x3 tiles and the 1x1 kernel read those after (read early they spill: the 1x1 is
+  // held to 128 registers for two workgroups per CU).
   constexpr int G4 = BN / 4, RPE = NT / G4, EV = (BM + RPE - 1) / RPE;
   constexpr bool YEARLY = C::KS == 3;
+  constexpr bool SEARLY = YEARLY && C::BN <= 48;  // wider column tiles would spill with these registers live
   const int ec4 = tid % G4, er0 = tid / G4, en = n0 + 4 * ec4;
   const bool eon = er0 < RPE && en < OC;
   // Loads use clamped pixel and channel indices (always in range, no branches, so they issue back to back);
@@ -214,7 +216,8 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
       for (int e = 0; e < EV; e++) rmv[e] = o.rowmask[epix(e)];
     }
   };
-  if constexpr (YEARLY) { load_y(); load_side(); }
+  if constexpr (YEARLY) load_y();
+  if constexpr (SEARLY) load_side();
 
   // The zero row of every stage buffer (never written by the stage stores).
   for (int e = tid; e < NBUF * KV; e += NT) *(vec_t*)(As + (e / KV) * SE + AR * LDK + (e % KV) * 8) = vec_t{0, 0, 0, 0};
@@ -254,7 +257,8 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
       for (int r = 0; r < 4; r++) Cg[(wm * WTM + i * 16 + 4 * g4 + r) * LDC + wn * WTN + j * 16 + r16] = acc[i][j][r];
   __syncthreads();
   // The other epilogue inputs, loaded after the accumulator exchange and before the first store.
-  if constexpr (!YEARLY) { load_y(); load_side(); }
+  if constexpr (!YEARLY) load_y();
+  if constexpr (!SEARLY) load_side();
 
 #pragma unroll
   for (int e = 0; e < EV; e++) {
