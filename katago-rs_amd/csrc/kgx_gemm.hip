@@ -503,9 +503,12 @@ static void gemm_cfg(const GemmArgs& g, hipStream_t s) {
   if (g.N > 64 && g.N <= 96 && g.K % bk == 0) gemm_launch<T, CfgHead, AF, PRO, ACT>(g, s);
   else if (g.N > 128 && g.N <= 192 && g.K % bk == 0) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
   else if (g.N > 192 && g.N <= 384 && g.K % bk == 0 && AF) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
-  else if (g.N > 128 && g.K % bk == 0 && (long)((g.M + 127) / 128) * ((g.N + 127) / 128) * g.Z >= 256)
-    gemm_launch<T, CfgWide, AF, PRO, ACT>(g, s);
-  else gemm_launch<T, CfgSmall, AF, PRO, ACT>(g, s);
+  else if constexpr (!AF) {
+    // (Float-A prologue kernels are not built on the wide tile: their staging registers spill there.)
+    if (g.N > 128 && g.K % bk == 0 && (long)((g.M + 127) / 128) * ((g.N + 127) / 128) * g.Z >= 256)
+      gemm_launch<T, CfgWide, AF, PRO, ACT>(g, s);
+    else gemm_launch<T, CfgSmall, AF, PRO, ACT>(g, s);
+  } else gemm_launch<T, CfgSmall, AF, PRO, ACT>(g, s);
 }
 
 template <typename T>

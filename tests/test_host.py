@@ -35,6 +35,45 @@ def test_library_defines_every_kernel_stub(kgx):
     assert "__device_stub__" not in out, [l for l in out.splitlines() if "__device_stub__" in l][:5]
 
 
+def _device_kernels(obj, tmp):
+    """(name, scratch bytes per lane, spilled VGPRs) of every gfx950 kernel in one object of the library build,
+    from the code object's metadata notes."""
+    import subprocess
+    llvm = "/opt/rocm/llvm/bin"
+    fat, co = os.path.join(tmp, "fatbin"), os.path.join(tmp, "gfx950.co")
+    subprocess.run([f"{llvm}/llvm-objcopy", f"--dump-section=.hip_fatbin={fat}", obj, os.path.join(tmp, "o")],
+                   check=True, capture_output=True)
+    subprocess.run([f"{llvm}/clang-offload-bundler", "--unbundle", "--type=o", f"--input={fat}",
+                    "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", f"--output={co}"], check=True, capture_output=True)
+    notes = subprocess.run([f"{llvm}/llvm-readelf", "--notes", co], check=True, capture_output=True,
+                           text=True).stdout
+    names = re.findall(r"^\s+\.name:\s+(\S+)", notes, re.M)
+    scratch = [int(v) for v in re.findall(r"\.private_segment_fixed_size:\s+(\d+)", notes)]
+    spills = [int(v) for v in re.findall(r"\.vgpr_spill_count:\s+(\d+)", notes)]
+    assert len(names) == len(scratch) == len(spills), obj
+    return list(zip(names, scratch, spills))
+
+
+def test_kernels_use_no_scratch(tmp_path):
+    """No kernel of the library spills registers to scratch memory (a spill in a hot loop costs more than the
+    occupancy or tile choice that caused it)."""
+    import glob
+    objs = sorted(glob.glob(os.path.join(ROOT, "katago-rs_amd", "csrc", "build", "*.o")))
+    if not objs or not os.path.exists("/opt/rocm/llvm/bin/clang-offload-bundler"):
+        pytest.skip("library objects or ROCm LLVM tools not available")
+    bad, n = [], 0
+    for obj in objs:
+        with open(obj, "rb") as f:
+            if b"__CLANG_OFFLOAD_BUNDLE__" not in f.read():
+                continue  # host-only object
+        for name, scratch, spills in _device_kernels(obj, str(tmp_path)):
+            n += 1
+            if scratch or spills:
+                bad.append((os.path.basename(obj), name, scratch, spills))
+    assert n > 50, n
+    assert not bad, bad[:5]
+
+
 def _nets(synth):
     nets = dict(synth.tiny_nets())
     for name in ("b10c128", "b18c384nbt", "b10c384h6"):
