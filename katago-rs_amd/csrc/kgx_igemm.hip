@@ -368,11 +368,21 @@ void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const v
 // Network input of one batch row per workgroup (one thread per board point): the planes, float NCHW [nin][361], to
 // compute-type NHWC rows of ldo channels (zero beyond nin, 16-byte stores), and the board statistics of
 // launch_mask_prep: mask = plane 0, area = its sum, s1 = (sqrt(area) - 14) 0.1, s2 = (sqrt(area) - 14)^2 0.01 - 0.1.
+// Workgroups (b, 1) compute the row's global-input bias of the stem instead (when `gl.W` is set).
 template <typename T>
 __global__ __launch_bounds__(384) void input_prep_kernel(const float* __restrict__ bin, int nin, T* __restrict__ out,
                                                          int ldo, float* __restrict__ mask, float* __restrict__ area,
-                                                         float* __restrict__ s1, float* __restrict__ s2) {
+                                                         float* __restrict__ s1, float* __restrict__ s2,
+                                                         InputGlobal gl) {
   const int b = blockIdx.x, p = threadIdx.x;
+  if (blockIdx.y == 1) {
+    for (int o = p; o < gl.C; o += 384) {
+      float acc = 0.f;
+      for (int i = 0; i < gl.nglob; i++) acc += gl.glob[(size_t)b * gl.nglob + i] * gl.W[(size_t)i * gl.C + o];
+      gl.out[(size_t)b * gl.C + o] = acc;
+    }
+    return;
+  }
   __shared__ float red[6];
   const float* src = bin + (size_t)b * nin * HW + p;
   float mk = 0.f;
@@ -405,12 +415,15 @@ __global__ __launch_bounds__(384) void input_prep_kernel(const float* __restrict
 }
 
 void launch_input_prep(int prec, const float* bin, int nin, void* out, int ldo, float* mask, float* area, float* s1,
-                       float* s2, int B, hipStream_t s) {
+                       float* s2, int B, hipStream_t s, const InputGlobal& gl) {
   if (ldo % 8 != 0 || ldo < nin) throw std::runtime_error("input_prep: bad packed channel count");
+  if (gl.W && (!gl.glob || !gl.out || gl.C < 1 || gl.nglob < 0))
+    throw std::runtime_error("input_prep: bad global-input bias arguments");
+  const dim3 grid(B, gl.W ? 2 : 1);
   if (prec == PREC_F16)
-    input_prep_kernel<f16><<<B, 384, 0, s>>>(bin, nin, (f16*)out, ldo, mask, area, s1, s2);
+    input_prep_kernel<f16><<<grid, 384, 0, s>>>(bin, nin, (f16*)out, ldo, mask, area, s1, s2, gl);
   else if (prec == PREC_BF16)
-    input_prep_kernel<bf16><<<B, 384, 0, s>>>(bin, nin, (bf16*)out, ldo, mask, area, s1, s2);
+    input_prep_kernel<bf16><<<grid, 384, 0, s>>>(bin, nin, (bf16*)out, ldo, mask, area, s1, s2, gl);
   else throw std::runtime_error("input_prep: 16-bit only");
   KGX_CHECK_LAUNCH();
 }

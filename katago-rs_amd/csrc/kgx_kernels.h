@@ -119,9 +119,15 @@ void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const v
                        const ConvOut& o, int B, hipStream_t s);
 
 // Network input planes, float NCHW [B][nin][361], to compute-type NHWC rows of ldo channels (zero beyond nin,
-// ldo % 8 == 0), together with the board statistics of launch_mask_prep.
+// ldo % 8 == 0), together with the board statistics of launch_mask_prep; with `gl.W` set, the same launch also
+// computes the stem's per-row bias from the global inputs: out[b][o] = sum_i glob[b][i] * W[i][o] (W [nglob][C]).
+struct InputGlobal {
+  const float* glob = nullptr; int nglob = 0;
+  const float* W = nullptr; int C = 0;
+  float* out = nullptr;
+};
 void launch_input_prep(int prec, const float* bin, int nin, void* out, int ldo, float* mask, float* area, float* s1,
-                       float* s2, int B, hipStream_t s);
+                       float* s2, int B, hipStream_t s, const InputGlobal& gl = InputGlobal());
 
 // Direct odd-k "same" convolution, w as [ic][ky][kx][oc] float: x compute-type NHWC rows of ldx, or float NCHW.
 void launch_conv_direct(int prec, const void* x, int ldx, bool nchw_f32, int IC, const float* w, int OC, int ky, int kx,

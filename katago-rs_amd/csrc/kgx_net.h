@@ -125,6 +125,7 @@ class Net {
 
   // Inputs / outputs and per-row board data.
   float *d_bin_ = nullptr, *d_glob_ = nullptr, *d_meta_ = nullptr, *d_out_ = nullptr;
+  InputGlobal stem_glob_;  // the stem's global-input bias, computed in the input packing launch when set
   float *mask_ = nullptr, *area_ = nullptr, *s1_ = nullptr, *s2_ = nullptr;
 
   // Workspace sizes from scan(), then the buffers.

@@ -188,7 +188,10 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
       const float* bin = (const float*)x;
       float *mask = mask_, *area = area_, *s1 = s1_, *s2 = s2_;
       Op pk;
-      pk.launch = [=](hipStream_t s, int B) { launch_input_prep(prec, bin, ic, packed, icin, mask, area, s1, s2, B, s); };
+      const InputGlobal gl = stem_glob_;
+      pk.launch = [=](hipStream_t s, int B) {
+        launch_input_prep(prec, bin, ic, packed, icin, mask, area, s1, s2, B, s, gl);
+      };
       pk.cls = "input_prep";
       pk.bytes_row = (double)HW * ic * 4 + (double)HW * icin * ts + HW * 4.0;
       ops_.push_back(pk);
@@ -656,9 +659,14 @@ void Net::build(const ModelDesc& m) {
     ops_.push_back(op);
   }
   // The stem's per-row bias: global inputs through their matmul, plus the metadata encoder's output
-  // (bin2onnx.py:1477-1488), one workgroup per row.
+  // (bin2onnx.py:1477-1488), one workgroup per row. Without a metadata encoder, and when the stem packs its
+  // input planes (implicit GEMM), the input packing launch computes it (one launch less).
   float* gbias = alloc_f((size_t)max_batch_ * C);
-  {
+  if (m.meta_version == 0 && igemm_eligible(m.stem, true, 0, stem_out)) {
+    stem_glob_.glob = d_glob_; stem_glob_.nglob = nglob_;
+    stem_glob_.W = upload_f(m.stem_mm.w); stem_glob_.C = C;
+    stem_glob_.out = gbias;
+  } else {
     RowProg rp = row_prog_base();
     RowMM& g = rp.mm[rp.nmm++];
     g.gin = d_glob_; g.ldgin = nglob_; g.IC = nglob_; g.OC = C; g.W = upload_f(m.stem_mm.w);
