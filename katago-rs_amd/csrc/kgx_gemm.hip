@@ -11,8 +11,9 @@ namespace kgx {
 // stage's global loads are in flight in registers while the current stage, double-buffered in LDS with a 16-byte
 // row pad, feeds the MFMAs; one barrier per stage. A may be float (the head's f32 trunk): a BN + activation + mask
 // prologue then runs as the stage is written to LDS and values are converted to T there.
-template <int BM_, int BN_, int BKH_, int WM_, int WN_, bool KFULL_ = false>
+template <int BM_, int BN_, int BKH_, int WM_, int WN_, bool KFULL_ = false, int MINW_ = 2>
 struct Cfg {
+  static constexpr int MINW = MINW_;  // waves per SIMD the register allocation must allow
   static constexpr int BM = BM_, BN = BN_, WM = WM_, WN = WN_;
   static constexpr int BKH = BKH_;  // K per stage for 16-bit types (float uses half as many)
   // K is a multiple of the stage depth (the dispatcher checks): loads need no K bound, and rows past M or N are
@@ -42,7 +43,7 @@ enum GemmEpi {
 };
 
 template <typename T, typename C, bool AF, bool PRO, int ACT, int EPI>
-__global__ __launch_bounds__(C::WM * C::WN * 64, 2) void gemm_kernel(GemmArgs g) {
+__global__ __launch_bounds__(C::WM * C::WN * 64, C::MINW) void gemm_kernel(GemmArgs g) {
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, NT = WM * WN * 64;
   constexpr int VEC = Tile<T>::VEC;
   constexpr int BK = sizeof(T) == 2 ? C::BKH : C::BKH / 2;
@@ -467,8 +468,8 @@ typedef Cfg<128, 128, 64, 2, 2, true> CfgWide;
 typedef Cfg<64, 64, 32, 2, 2> CfgSmall;
 typedef Cfg<64, 96, 64, 2, 2, true> CfgHead;  // the heads' first convolutions: N = p1 + g1 + v1 channels <= 96
 // Float operands on the head tile take 64 channels per stage (six stages at 384 channels): 20.8 against 21.8 us
-// with 32 at b18c384nbt batch 32.
-typedef Cfg<64, 96, 128, 2, 2, true> CfgHeadF;
+// with 32 at b18c384nbt batch 32. Its 87 KB of LDS allow one workgroup per CU.
+typedef Cfg<64, 96, 128, 2, 2, true, 1> CfgHeadF;
 
 // The epilogue a GEMM's outputs need (launch_gemm has set vec_epi and validated glu / qkv).
 static int gemm_epi(const GemmArgs& g) {
@@ -503,8 +504,9 @@ static void gemm_launch(const GemmArgs& g, hipStream_t s) {
 template <typename T, bool AF, bool PRO, int ACT>
 static void gemm_cfg(const GemmArgs& g, hipStream_t s) {
   const int bkh = 64, bk = sizeof(T) == 2 ? bkh : bkh / 2;
-  if (sizeof(T) == 4 && g.N > 64 && g.N <= 96 && g.K % 64 == 0) gemm_launch<T, CfgHeadF, AF, PRO, ACT>(g, s);
-  else if (g.N > 64 && g.N <= 96 && g.K % bk == 0) gemm_launch<T, CfgHead, AF, PRO, ACT>(g, s);
+  if (g.N > 64 && g.N <= 96 && g.K % 64 == 0 && sizeof(T) == 4) {
+    if constexpr (sizeof(T) == 4) gemm_launch<T, CfgHeadF, AF, PRO, ACT>(g, s);  // (built for float only)
+  } else if (g.N > 64 && g.N <= 96 && g.K % bk == 0) gemm_launch<T, CfgHead, AF, PRO, ACT>(g, s);
   else if (g.N > 128 && g.N <= 192 && g.K % bk == 0) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
   else if (g.N > 192 && g.N <= 384 && g.K % bk == 0 && AF) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
   else if constexpr (!AF) {
