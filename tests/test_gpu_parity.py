@@ -127,8 +127,11 @@ def test_winograd_f2_benchmark_config(kgx, synth, oracle, monkeypatch):
 CONFIG_ROWS = {"b10c128": 8, "b18c384nbt": 2, "b10c384h6": 2, "b10c512h8": 1, "tf3-b11c768": 1}
 
 
-@pytest.mark.parametrize("prec", ["f32", "f16"])
-@pytest.mark.parametrize("name", list(CONFIG_ROWS))
+# bf16 handles run the f16 kernels' bf16 instantiations; the headline net covers those of its shapes.
+CONFIG_CASES = [(n, p) for n in CONFIG_ROWS for p in ("f32", "f16")] + [("b18c384nbt", "bf16")]
+
+
+@pytest.mark.parametrize("name,prec", CONFIG_CASES)
 def test_benchmark_configs_match_oracle(kgx, synth, oracle, name, prec):
     arch_fn, batch = synth.CONFIGS[name]
     mb = synth.write_model(arch_fn(), synth.CONFIG_SEEDS[name])
