@@ -662,7 +662,7 @@ void Net::build(const ModelDesc& m) {
   // (bin2onnx.py:1477-1488), one workgroup per row. Without a metadata encoder, and when the stem packs its
   // input planes (implicit GEMM), the input packing launch computes it (one launch less).
   float* gbias = alloc_f((size_t)max_batch_ * C);
-  if (m.meta_version == 0 && igemm_eligible(m.stem, true, 0, stem_out)) {
+  if (m.meta_version == 0 && nglob_ > 0 && igemm_eligible(m.stem, true, 0, stem_out)) {
     stem_glob_.glob = d_glob_; stem_glob_.nglob = nglob_;
     stem_glob_.W = upload_f(m.stem_mm.w); stem_glob_.C = C;
     stem_glob_.out = gbias;
