@@ -149,6 +149,21 @@ def test_benchmark_configs_match_oracle(kgx, synth, oracle, name, prec):
     h.close()
 
 
+@pytest.mark.parametrize("prec", ["f16", "bf16"])
+def test_gpool_widths_the_row_emission_does_not_fit(kgx, synth, oracle, prec):
+    """A global-pooling block whose regular width has no share of a multiple of 8 channels (20): 16-bit handles
+    then emit the biased mid activation with a separate bias_act launch instead of in the row program."""
+    arch = synth.Arch("t-gp20", 14, 32, [("res", 32), ("gpool", 20, 16), ("res", 32)], gpool_c=16,
+                      p1_c=16, g1_c=16, v1_c=16, v2_c=24)
+    mb = synth.write_model(arch, 3)
+    sp, gl, _ = synth.make_inputs(4, 11, board_sizes=[19, 13, 9, 19])
+    net = kgx.Net(mb)
+    h = kgx.Handle(net, 4, prec)
+    out = h.forward(sp, gl)
+    check(out, oracle.Model(mb).forward(sp, gl), net.P, net.S, prec, "t-gp20", emulated(oracle, mb, prec, sp, gl))
+    h.close()
+
+
 def test_rows_do_not_depend_on_batch_or_bucket(kgx, synth):
     arch = synth.tiny_nets()["t_nbt"]
     net = kgx.Net(synth.write_model(arch, 3))
