@@ -70,10 +70,22 @@ typedef struct {
 } kg_model_desc;
 int kg_net_desc(const kg_net* net, kg_model_desc* out);
 
+/* NNModelVersion::getInputsVersion / getNumSpatialFeatures / getNumGlobalFeatures
+ * (crates/katago-core/src/neuralnet/modelversion.rs:40-110): the input layout of a model version (3..17).
+ * Other versions fail with "NNModelVersion: Model version not currently implemented or supported: <v>".
+ * Any output pointer may be NULL. */
+int kg_model_version_features(int model_version, int* inputs_version, int* num_spatial, int* num_global);
+
+/* NNModelVersion::getNumInputMetaChannels (modelversion.rs): 0 for meta encoder version 0, 192 for 1; other
+ * versions fail with "NNModelVersion: metaEncoderVersion not currently implemented or supported: <v>". */
+int kg_meta_encoder_channels(int meta_encoder_version, int* num_meta);
+
 /* A device replica of the network with its own stream and workspace for up to max_batch rows.
  * Replaces create_compute_context + create_compute_handle (backend.rs:300-390) with their checks:
  * nn_x_len and nn_y_len must be 19 ("nnXLen and nnYLen must equal the network's posLen 19"), and
- * inputs_use_nhwc must be 0 ("inputsUseNHWC = true unsupported"). precision is a KG_PRECISION_*. */
+ * inputs_use_nhwc must be 0 ("inputsUseNHWC = true unsupported"); and the input buffers' check
+ * (BurnInputBuffers::new, backend.rs:184-188): the model's input channel counts must be its version's.
+ * precision is a KG_PRECISION_*. */
 int kg_handle_create(const kg_net* net, int device, int max_batch, int precision, int nn_x_len, int nn_y_len,
                      int inputs_use_nhwc, kg_handle** out);
 void kg_handle_free(kg_handle* handle);
@@ -135,6 +147,12 @@ typedef struct {
  * bucket), one readback, copy_outputs (policy optimism mix, inverse symmetry, value / score unpacking by model
  * version). n must be in [1, max_batch]. */
 int kg_get_output(kg_handle* handle, int n, const kg_row_input* rows, kg_nn_output* outputs);
+
+/* copy_outputs alone (backend.rs:622-731), on the host: n raw rows of P*362 + 3 + S + 361 floats (kg_forward /
+ * kg_run output) to NNOutput fields, with each row's symmetry (0..7) and policy optimism. For callers that run
+ * the forward pass with kg_run on device-filled inputs. S must be the model version's score channel count. */
+int kg_copy_outputs(const float* raw, int n, int num_policy_channels, int num_score_value_channels,
+                    int model_version, const int* symmetry, const float* policy_optimism, kg_nn_output* outputs);
 
 /* Kernel timing, for benchmarks: while enabled, kg_run / kg_forward launch eagerly and bracket every kernel
  * with events on the handle's stream. kg_profile_read reports, per kernel class, the launch count, the

@@ -35,6 +35,7 @@ EXPORTS = [
     "kg_copy_with_symmetry",
     "kg_handle_is_using_fp16", "kg_forward", "kg_handle_device_buffers", "kg_run", "kg_sync", "kg_handle_stream",
     "kg_get_output", "kg_profile_enable", "kg_profile_reset", "kg_profile_read",
+    "kg_model_version_features", "kg_meta_encoder_channels", "kg_copy_outputs",
 ]
 
 _lib = None
@@ -128,6 +129,9 @@ def lib():
         L.kg_profile_read.argtypes = [vp, ctypes.POINTER(ctypes.c_char_p), ctypes.POINTER(ctypes.c_long),
                                       ctypes.POINTER(ctypes.c_double), ctypes.POINTER(ctypes.c_double),
                                       ctypes.POINTER(ctypes.c_double), ci]
+        L.kg_model_version_features.argtypes = [ci, ctypes.POINTER(ci), ctypes.POINTER(ci), ctypes.POINTER(ci)]
+        L.kg_meta_encoder_channels.argtypes = [ci, ctypes.POINTER(ci)]
+        L.kg_copy_outputs.argtypes = [vp, ci, ci, ci, ci, vp, vp, ctypes.POINTER(NNOutput)]
         _ = cf
         _lib = L
     return _lib
@@ -167,6 +171,47 @@ def copy_with_symmetry(src, symmetry: int, reverse: bool = False) -> np.ndarray:
     _check(lib().kg_copy_with_symmetry(_ptr(a), _ptr(out), a.shape[0], a.shape[1], a.shape[2], int(symmetry),
                                        int(bool(reverse))))
     return out
+
+
+def model_version_features(model_version: int):
+    """(inputs version, spatial features, global features) of a model version (NNModelVersion)."""
+    iv, sp, gl = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    _check(lib().kg_model_version_features(int(model_version), ctypes.byref(iv), ctypes.byref(sp), ctypes.byref(gl)))
+    return iv.value, sp.value, gl.value
+
+
+def meta_encoder_channels(meta_encoder_version: int) -> int:
+    c = ctypes.c_int()
+    _check(lib().kg_meta_encoder_channels(int(meta_encoder_version), ctypes.byref(c)))
+    return c.value
+
+
+def _output_dict(o, own):
+    return {
+        "policy": np.ctypeslib.as_array(o.policy_probs).copy(),
+        "white_win_prob": o.white_win_prob, "white_loss_prob": o.white_loss_prob,
+        "white_no_result_prob": o.white_no_result_prob, "white_score_mean": o.white_score_mean,
+        "white_score_mean_sq": o.white_score_mean_sq, "white_lead": o.white_lead,
+        "var_time_left": o.var_time_left, "shortterm_winloss_error": o.shortterm_winloss_error,
+        "shortterm_score_error": o.shortterm_score_error, "ownership": own,
+    }
+
+
+def copy_outputs(raw, P: int, S: int, model_version: int, symmetry, policy_optimism, want_ownership=True):
+    """copy_outputs (crates/katago-nn-burn/src/backend.rs:622-731) on the host: raw rows [n, P*362 + 3 + S + 361]
+    to a list of dicts of NNOutput fields."""
+    raw = np.ascontiguousarray(raw, np.float32)
+    n = raw.shape[0]
+    if raw.shape != (n, P * 362 + 3 + S + HW):
+        raise ValueError(f"raw rows must be [n, {P * 362 + 3 + S + HW}], got {raw.shape}")
+    sym = np.ascontiguousarray(np.broadcast_to(symmetry, (n,)), np.int32)
+    opt = np.ascontiguousarray(np.broadcast_to(policy_optimism, (n,)), np.float32)
+    outs = (NNOutput * n)()
+    owners = [np.zeros(HW, np.float32) if want_ownership else None for _ in range(n)]
+    for i in range(n):
+        outs[i].white_owner_map = None if owners[i] is None else _ptr(owners[i]).value
+    _check(lib().kg_copy_outputs(_ptr(raw), n, P, S, model_version, _ptr(sym), _ptr(opt), outs))
+    return [_output_dict(outs[i], owners[i]) for i in range(n)]
 
 
 class Net:
@@ -232,6 +277,14 @@ class Handle:
         spatial = np.ascontiguousarray(spatial, np.float32)
         glob = np.ascontiguousarray(glob, np.float32)
         meta = None if meta is None else np.ascontiguousarray(meta, np.float32)
+        # kg_forward reads n rows of each input: shapes are checked here, where the arrays' sizes are known.
+        net = self.net
+        if spatial.shape != (n, net.num_input_channels, 19, 19):
+            raise ValueError(f"spatial must be [n, {net.num_input_channels}, 19, 19], got {spatial.shape}")
+        if glob.shape != (n, net.num_global):
+            raise ValueError(f"glob must be [n, {net.num_global}], got {glob.shape}")
+        if meta is not None and meta.shape != (n, net.num_meta):
+            raise ValueError(f"meta must be [n, {net.num_meta}], got {meta.shape}")
         out = np.empty((n, self.net.row_len), np.float32)
         _check(lib().kg_forward(self._h, n, _ptr(spatial), _ptr(glob), _ptr(meta), _ptr(out)))
         return out
@@ -244,6 +297,9 @@ class Handle:
 
     def run(self, n: int, out: np.ndarray = None):
         """Forward pass on the inputs already in the device buffers; reads back into `out` when given."""
+        if out is not None and (out.dtype != np.float32 or not out.flags.c_contiguous or
+                                out.size < n * self.net.row_len):
+            raise ValueError(f"out must be contiguous float32 with room for {n} rows of {self.net.row_len}")
         _check(lib().kg_run(self._h, n, _ptr(out)))
 
     def sync(self):
@@ -261,11 +317,17 @@ class Handle:
         arr = (RowInput * n)()
         outs = (NNOutput * n)()
         owners = []
+        net = self.net
         for i, r in enumerate(rows):
             sp = np.ascontiguousarray(r["spatial"], np.float32)
             gl = np.ascontiguousarray(r["glob"], np.float32)
             me = r.get("meta")
             me = None if me is None else np.ascontiguousarray(me, np.float32)
+            if sp.shape != (net.num_input_channels, 19, 19) or gl.shape != (net.num_global,):
+                raise ValueError(f"row {i}: spatial must be [{net.num_input_channels}, 19, 19] and glob "
+                                 f"[{net.num_global}], got {sp.shape} and {gl.shape}")
+            if me is not None and me.shape != (net.num_meta,):
+                raise ValueError(f"row {i}: meta must be [{net.num_meta}], got {me.shape}")
             keep += [sp, gl, me]
             arr[i].row_spatial = _ptr(sp).value
             arr[i].row_global = _ptr(gl).value
@@ -276,18 +338,7 @@ class Handle:
             owners.append(own)
             outs[i].white_owner_map = None if own is None else _ptr(own).value
         _check(lib().kg_get_output(self._h, n, arr, outs))
-        res = []
-        for i in range(n):
-            o = outs[i]
-            res.append({
-                "policy": np.ctypeslib.as_array(o.policy_probs).copy(),
-                "white_win_prob": o.white_win_prob, "white_loss_prob": o.white_loss_prob,
-                "white_no_result_prob": o.white_no_result_prob, "white_score_mean": o.white_score_mean,
-                "white_score_mean_sq": o.white_score_mean_sq, "white_lead": o.white_lead,
-                "var_time_left": o.var_time_left, "shortterm_winloss_error": o.shortterm_winloss_error,
-                "shortterm_score_error": o.shortterm_score_error, "ownership": owners[i],
-            })
-        return res
+        return [_output_dict(outs[i], owners[i]) for i in range(n)]
 
     # --- kernel timing ---
     def profile(self, enable: bool):

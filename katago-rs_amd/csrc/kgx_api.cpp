@@ -85,6 +85,72 @@ void copy_with_symmetry(const float* src, float* dst, int c_size, int h_size, in
   }
 }
 
+// NNModelVersion's input layout per model version (crates/katago-core/src/neuralnet/modelversion.rs:40-110):
+// the inputs version, spatial and global feature counts; versions outside 3..17 fail with the reference's text.
+void model_version_features(int v, int& inputs_version, int& spatial, int& global) {
+  if (v < 3 || v > 17)
+    throw std::runtime_error("NNModelVersion: Model version not currently implemented or supported: " + std::to_string(v));
+  static const int iv[5] = {3, 4, 5, 6, 7}, sp[5] = {22, 22, 13, 22, 22}, gl[5] = {14, 14, 12, 16, 19};
+  const int k = v <= 4 ? 0 : v >= 8 ? 4 : v - 4;  // inputs versions 3 (v3-4), 4 (v5), 5 (v6), 6 (v7), 7 (v8+)
+  inputs_version = iv[k];
+  spatial = sp[k];
+  global = gl[k];
+}
+
+// NNModelVersion::getNumInputMetaChannels (modelversion.rs): 0 without an SGF metadata encoder, 192 with one.
+int meta_encoder_channels(int meta_version) {
+  if (meta_version == 0) return 0;
+  if (meta_version == 1) return 192;
+  throw std::runtime_error("NNModelVersion: metaEncoderVersion not currently implemented or supported: " +
+                           std::to_string(meta_version));
+}
+
+// copy_outputs (crates/katago-nn-burn/src/backend.rs:622-731): one readback row of P*362 + 3 + S + 361 floats to
+// NNOutput fields. The policy mixes channel 1 (optimistic) into channel 0 by the row's optimism for P == 2 or for
+// P == 4 from model version 16; policy and ownership are mapped back through the row's symmetry; the score fields
+// are unpacked by model version.
+void copy_outputs_row(const float* row, int P, int S, int v, int sym, float optimism, kg_nn_output& o) {
+  float tmp[HW];
+  const float* pol = row;
+  if (P == 2 || (P == 4 && v >= 16)) {
+    for (int i = 0; i < HW; i++) {
+      const float p = pol[i], po = pol[(HW + 1) + i];
+      tmp[i] = p + (po - p) * optimism;
+    }
+    copy_with_symmetry(tmp, o.policy_probs, 1, POS, POS, sym, true);
+    const float p0 = pol[HW], p1 = pol[(HW + 1) + HW];
+    o.policy_probs[HW] = p0 + (p1 - p0) * optimism;
+  } else {
+    copy_with_symmetry(pol, o.policy_probs, 1, POS, POS, sym, true);
+    o.policy_probs[HW] = pol[HW];
+  }
+  const float* val = row + P * (HW + 1);
+  const float* sc = val + 3;
+  const float* own = sc + S;
+  o.white_win_prob = val[0];
+  o.white_loss_prob = val[1];
+  o.white_no_result_prob = val[2];
+  if (o.white_owner_map) copy_with_symmetry(own, o.white_owner_map, 1, POS, POS, sym, true);
+  if (v >= 9) {
+    o.white_score_mean = sc[0]; o.white_score_mean_sq = sc[1]; o.white_lead = sc[2]; o.var_time_left = sc[3];
+    o.shortterm_winloss_error = sc[4]; o.shortterm_score_error = sc[5];
+  } else if (v >= 8) {
+    o.white_score_mean = sc[0]; o.white_score_mean_sq = sc[1]; o.white_lead = sc[2]; o.var_time_left = sc[3];
+    o.shortterm_winloss_error = 0.f; o.shortterm_score_error = 0.f;
+  } else if (v >= 4) {
+    o.white_score_mean = sc[0]; o.white_score_mean_sq = sc[1]; o.white_lead = o.white_score_mean;
+    o.var_time_left = 0.f; o.shortterm_winloss_error = 0.f; o.shortterm_score_error = 0.f;
+  } else {
+    // Version 3 nets have no second moment output: the mean squared stands in for it.
+    o.white_score_mean = sc[0]; o.white_score_mean_sq = o.white_score_mean * o.white_score_mean;
+    o.white_lead = o.white_score_mean; o.var_time_left = 0.f; o.shortterm_winloss_error = 0.f;
+    o.shortterm_score_error = 0.f;
+  }
+}
+
+// The score-value channel count each model version's value head has (bin2onnx.py:849-856).
+int score_channels_for_version(int v) { return v >= 9 ? 6 : v >= 8 ? 4 : v >= 4 ? 2 : 1; }
+
 int padded_batch_size(const std::vector<int>& buckets, int n, int max_batch) {
   int best = -1;
   for (int b : buckets)
@@ -182,6 +248,16 @@ int kg_handle_create(const kg_net* net, int device, int max_batch, int precision
     h->max_batch = max_batch;
     h->precision = precision;
     const kgx::ModelDesc& m = net->model;
+    // The input buffers' layout must be the model version's (BurnInputBuffers::new, backend.rs:184-188).
+    int iv = 0, nsp = 0, ngl = 0;
+    model_version_features(m.version, iv, nsp, ngl);
+    if (m.num_input_channels != nsp || m.num_global != ngl)
+      throw std::runtime_error("kgx backend: model version " + std::to_string(m.version) + " takes " +
+                               std::to_string(nsp) + " spatial and " + std::to_string(ngl) +
+                               " global input features, the model has " + std::to_string(m.num_input_channels) +
+                               " and " + std::to_string(m.num_global));
+    if (m.num_meta != meta_encoder_channels(m.meta_version))
+      throw std::runtime_error("kgx backend: SGF metadata input must have 192 channels");
     h->model_version = m.version;
     h->P = m.P;
     h->S = m.S;
@@ -217,6 +293,8 @@ void kg_handle_free(kg_handle* h) {
 
 int kg_handle_set_batch_buckets(kg_handle* h, const int* buckets, int count) {
   return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    if (count > 0 && !buckets) throw std::runtime_error("null buckets");
     std::lock_guard<std::mutex> lock(h->mu);
     h->buckets.clear();
     for (int k = 0; k < count; k++)
@@ -245,6 +323,7 @@ int kg_handle_is_using_fp16(const kg_handle* h) { return h && h->precision != KG
 int kg_forward(kg_handle* h, int n, const float* bin, const float* global, const float* meta, float* out) {
   return guarded([&] {
     if (!h) throw std::runtime_error("null handle");
+    if (!bin || (h->nglob && !global) || !out) throw std::runtime_error("kgx backend: null input or output buffer");
     std::lock_guard<std::mutex> lock(h->mu);
     if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
     if (h->nmeta && !meta) throw std::runtime_error("kgx backend: the network needs a meta_input");
@@ -262,6 +341,7 @@ int kg_forward(kg_handle* h, int n, const float* bin, const float* global, const
 int kg_handle_device_buffers(kg_handle* h, float** bin, float** global, float** meta, float** out) {
   return guarded([&] {
     if (!h) throw std::runtime_error("null handle");
+    std::lock_guard<std::mutex> lock(h->mu);
     if (bin) *bin = h->net->d_bin();
     if (global) *global = h->net->d_global();
     if (meta) *meta = h->net->d_meta();
@@ -282,7 +362,10 @@ int kg_run(kg_handle* h, int n, float* out) {
 }
 
 int kg_sync(kg_handle* h) {
-  return guarded([&] { KGX_HIP(hipStreamSynchronize(h->stream)); });
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    KGX_HIP(hipStreamSynchronize(h->stream));
+  });
 }
 
 void* kg_handle_stream(kg_handle* h) { return h ? (void*)h->stream : nullptr; }
@@ -290,11 +373,13 @@ void* kg_handle_stream(kg_handle* h) { return h ? (void*)h->stream : nullptr; }
 int kg_get_output(kg_handle* h, int n, const kg_row_input* rows, kg_nn_output* outputs) {
   return guarded([&] {
     if (!h) throw std::runtime_error("null handle");
+    if (!rows || !outputs) throw std::runtime_error("null rows or outputs");
     std::lock_guard<std::mutex> lock(h->mu);
     if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
     // copy_inputs (backend.rs:497-546).
     for (int r = 0; r < n; r++) {
       const kg_row_input& in = rows[r];
+      if (in.symmetry < 0 || in.symmetry > 7) throw std::runtime_error("kgx backend: symmetry must be in [0, 8)");
       std::memcpy(h->h_glob + (size_t)r * h->nglob, in.row_global, (size_t)h->nglob * 4);
       if (h->nmeta) {
         if (!in.row_meta) throw std::runtime_error("kgx backend: the network needs a meta row");
@@ -311,53 +396,50 @@ int kg_get_output(kg_handle* h, int n, const kg_row_input* rows, kg_nn_output* o
     run_and_read(h, n_run, n, nullptr);
     // copy_outputs (backend.rs:622-731).
     const int rl = h->net->row_len();
-    const int P = h->P, S = h->S, v = h->model_version;
-    float tmp[HW];
+    for (int r = 0; r < n; r++)
+      copy_outputs_row(h->h_out + (size_t)r * rl, h->P, h->S, h->model_version, rows[r].symmetry,
+                       rows[r].policy_optimism, outputs[r]);
+  });
+}
+
+int kg_copy_outputs(const float* raw, int n, int P, int S, int model_version, const int* symmetry,
+                    const float* policy_optimism, kg_nn_output* outputs) {
+  return guarded([&] {
+    if (!raw || !symmetry || !policy_optimism || !outputs) throw std::runtime_error("null argument");
+    if (n < 0) throw std::runtime_error("negative row count");
+    int iv, sp, gl;
+    model_version_features(model_version, iv, sp, gl);
+    if (!(P == 1 || P == 2 || P == 4)) throw std::runtime_error("policy channels must be 1, 2 or 4");
+    if (S != score_channels_for_version(model_version))
+      throw std::runtime_error("score value channels do not match the model version");
+    const size_t rl = (size_t)P * (HW + 1) + 3 + S + HW;
     for (int r = 0; r < n; r++) {
-      const float* row = h->h_out + (size_t)r * rl;
-      kg_nn_output& o = outputs[r];
-      const float optimism = rows[r].policy_optimism;
-      const int sym = rows[r].symmetry;
-      const float* pol = row;
-      if (P == 2 || (P == 4 && v >= 16)) {
-        for (int i = 0; i < HW; i++) {
-          const float p = pol[i], po = pol[(HW + 1) + i];
-          tmp[i] = p + (po - p) * optimism;
-        }
-        copy_with_symmetry(tmp, o.policy_probs, 1, POS, POS, sym, true);
-        const float p0 = pol[HW], p1 = pol[(HW + 1) + HW];
-        o.policy_probs[HW] = p0 + (p1 - p0) * optimism;
-      } else {
-        copy_with_symmetry(pol, o.policy_probs, 1, POS, POS, sym, true);
-        o.policy_probs[HW] = pol[HW];
-      }
-      const float* val = row + P * (HW + 1);
-      const float* sc = val + 3;
-      const float* own = sc + S;
-      o.white_win_prob = val[0];
-      o.white_loss_prob = val[1];
-      o.white_no_result_prob = val[2];
-      if (o.white_owner_map) copy_with_symmetry(own, o.white_owner_map, 1, POS, POS, sym, true);
-      if (v >= 9) {
-        o.white_score_mean = sc[0]; o.white_score_mean_sq = sc[1]; o.white_lead = sc[2]; o.var_time_left = sc[3];
-        o.shortterm_winloss_error = sc[4]; o.shortterm_score_error = sc[5];
-      } else if (v >= 8) {
-        o.white_score_mean = sc[0]; o.white_score_mean_sq = sc[1]; o.white_lead = sc[2]; o.var_time_left = sc[3];
-        o.shortterm_winloss_error = 0.f; o.shortterm_score_error = 0.f;
-      } else if (v >= 4) {
-        o.white_score_mean = sc[0]; o.white_score_mean_sq = sc[1]; o.white_lead = o.white_score_mean;
-        o.var_time_left = 0.f; o.shortterm_winloss_error = 0.f; o.shortterm_score_error = 0.f;
-      } else {
-        o.white_score_mean = sc[0]; o.white_score_mean_sq = o.white_score_mean * o.white_score_mean;
-        o.white_lead = o.white_score_mean; o.var_time_left = 0.f; o.shortterm_winloss_error = 0.f;
-        o.shortterm_score_error = 0.f;
-      }
+      if (symmetry[r] < 0 || symmetry[r] > 7) throw std::runtime_error("symmetry must be in [0, 8)");
+      copy_outputs_row(raw + r * rl, P, S, model_version, symmetry[r], policy_optimism[r], outputs[r]);
     }
+  });
+}
+
+int kg_model_version_features(int model_version, int* inputs_version, int* num_spatial, int* num_global) {
+  return guarded([&] {
+    int iv, sp, gl;
+    model_version_features(model_version, iv, sp, gl);
+    if (inputs_version) *inputs_version = iv;
+    if (num_spatial) *num_spatial = sp;
+    if (num_global) *num_global = gl;
+  });
+}
+
+int kg_meta_encoder_channels(int meta_encoder_version, int* num_meta) {
+  return guarded([&] {
+    const int c = meta_encoder_channels(meta_encoder_version);
+    if (num_meta) *num_meta = c;
   });
 }
 
 int kg_profile_enable(kg_handle* h, int enable) {
   return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
     std::lock_guard<std::mutex> lock(h->mu);
     h->net->set_profiling(enable != 0);
   });
@@ -365,6 +447,7 @@ int kg_profile_enable(kg_handle* h, int enable) {
 
 int kg_profile_reset(kg_handle* h) {
   return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
     std::lock_guard<std::mutex> lock(h->mu);
     h->net->reset_profile();
   });

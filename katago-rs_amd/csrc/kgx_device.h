@@ -86,9 +86,12 @@ __device__ __forceinline__ void conv_store(const ConvOut& o, int m, int n, float
     if (o.accumulate) v += *p;
     if (!o.y_dead) *p = v;
   }
-  if (o.emit.scale)
-    ((T*)o.emit.out)[(size_t)m * o.emit.ld + n] =
-        to_t<T>(act_rt(v * o.emit.scale[n] + o.emit.bias[n], o.emit.act) * o.emit.mask[m]);
+  if (o.emit.scale) {
+    const float a = act_rt(v * o.emit.scale[n] + o.emit.bias[n], o.emit.act) * o.emit.mask[m];
+    const T hi = to_t<T>(a);
+    ((T*)o.emit.out)[(size_t)m * o.emit.ld + n] = hi;
+    if (o.emit.out_lo) ((T*)o.emit.out_lo)[(size_t)m * o.emit.ld + n] = to_t<T>(a - (float)hi);
+  }
 }
 
 // Epilogue for four consecutive channels n..n+3 of pixel m (conv_store on a float4). The per-pixel inputs come
@@ -122,6 +125,13 @@ __device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floa
 #pragma unroll
     for (int e = 0; e < 4; e++) t[e] = act_rt(v[e] * es[e] + eb[e], o.emit.act) * mk;
     store4<T>((T*)o.emit.out + (size_t)m * o.emit.ld + n, t[0], t[1], t[2], t[3]);
+    if (o.emit.out_lo) {
+      // Split operands: the low part is what the 16-bit high part leaves of the float activation (exact in float).
+      float l[4];
+#pragma unroll
+      for (int e = 0; e < 4; e++) l[e] = t[e] - (float)to_t<T>(t[e]);
+      store4<T>((T*)o.emit.out_lo + (size_t)m * o.emit.ld + n, l[0], l[1], l[2], l[3]);
+    }
   }
 }
 

@@ -17,13 +17,18 @@
 #include "kgx_device.h"
 
 #include <hip/hip_ext.h>
+#include <cstring>
 #include <vector>
 
 namespace kgx {
 
 template <int KS_, int BM_, int BN_, int BK_, int WM_, int WN_, int G_, int NBUF_, int MINW_ = 2,
-          bool INTERLEAVE_ = false>
+          bool INTERLEAVE_ = false, bool SPLIT_ = false>
 struct IgCfg {
+  // Split operands (1x1): the stage holds the high and the low plane of both operands, and each step takes
+  // hi*hi + lo*hi + hi*lo (three MFMAs), a product of about 22 significant bits per operand.
+  static constexpr bool SPLIT = SPLIT_;
+  static constexpr int PL = SPLIT_ ? 2 : 1;     // operand planes per stage
   static constexpr int MINW = MINW_;            // waves per SIMD the register allocation must allow
   static constexpr bool INTERLEAVE = INTERLEAVE_;  // MFMA / LDS-read interleaving hints for the scheduler
   static constexpr int KS = KS_, TAPS = KS_ * KS_, HALO = KS_ == 3 ? POS + 1 : 0;
@@ -34,26 +39,30 @@ struct IgCfg {
 };
 
 template <typename T, typename C>
-__global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restrict__ X, int ldx, int IC, const T* __restrict__ W,
-                                                      int icp, int OC, int M, ConvOut o) {
+__global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restrict__ X, const T* __restrict__ Xlo,
+                                                               int ldx, int IC, const T* __restrict__ W, int icp,
+                                                               int OC, int M, ConvOut o) {
   constexpr int TAPS = C::TAPS, HALO = C::HALO, BM = C::BM, BN = C::BN, BK = C::BK, WM = C::WM, WN = C::WN;
-  constexpr int NT = C::NT, G = C::G;
+  constexpr int NT = C::NT, G = C::G, PL = C::PL;
+  static_assert(!C::SPLIT || C::KS == 1, "split operands: 1x1 only");
   // LDS row stride in elements: a 32-byte pad makes the 16-row fragment reads conflict-free (80 dwords apart rows
   // of a 16x16x32 fragment hit distinct banks; a 16-byte pad serialises them two-way on gfx950).
   constexpr int LDK = BK + 16;
   constexpr int KV = BK / 8;                  // 16-byte vectors per staged row
-  constexpr int AR = BM + 2 * HALO;           // staged pixel rows
+  constexpr int AR = BM + 2 * HALO;           // staged pixel rows (per operand plane)
+  constexpr int TB = TAPS * BN;               // staged weight rows (per operand plane)
+  constexpr int ZR = PL * AR;                 // the zero row
   constexpr int RP = NT / KV;                 // staged rows per pass of all threads
-  constexpr int AV = (AR + RP - 1) / RP, BV = (TAPS * BN + RP - 1) / RP;
+  constexpr int AV = (PL * AR + RP - 1) / RP, BV = (PL * TB + RP - 1) / RP;
   constexpr int WTM = BM / WM, WTN = BN / WN, MB = WTM / 16, NB = WTN / 16;
   static_assert(WTM % 16 == 0 && WTN % 16 == 0 && BK % 32 == 0 && NT % KV == 0, "bad tile");
-  constexpr int STAGE = (AR + 1 + TAPS * BN) * LDK * 2;   // bytes (A rows, a zero row, B rows)
+  constexpr int STAGE = (PL * AR + 1 + PL * TB) * LDK * 2;  // bytes (A rows, a zero row, B rows)
   constexpr int EPI = C::G * BM * (BN + 4) * 4;       // bytes: one float tile per wave group
   constexpr int NBUF = C::NBUF;
   constexpr int SE = STAGE / (int)sizeof(T);          // stage buffer size in elements
   __shared__ __align__(16) char smem[NBUF * STAGE > EPI ? NBUF * STAGE : EPI];
   T* As = (T*)smem;
-  T* Bs = As + (AR + 1) * LDK;
+  T* Bs = As + (ZR + 1) * LDK;
   typedef u32x4 vec_t;
   typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
 
@@ -70,10 +79,11 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   const int r16 = lane & 15, g4 = lane >> 4;
 
   // Staging: thread tid moves the 16-byte vector kv of rows r0, r0 + RP, r0 + 2 RP, ... of the stage's A rows
-  // (pixels m0 - HALO + r) and B rows (tap * BN + output channel of this N tile, contiguous in the packed
-  // weights), so every address is a base plus a multiple of a uniform stride.
+  // (pixels m0 - HALO + r; split: rows AR + r hold the low plane) and B rows (tap * BN + output channel of this N
+  // tile, then the low plane, contiguous in the packed weights), so every address is a base plus a multiple of a
+  // uniform stride.
   const int r0 = tid / KV, kv8 = (tid % KV) * 8;
-  const T* wb = W + ((size_t)nt * TAPS * BN + r0) * icp + kv8;
+  const T* wb = W + ((size_t)nt * PL * TB + r0) * icp + kv8;
 
   // Tap validity of this lane's A rows: bit t of vmask[i] is set when row m's neighbour at tap t is on the board.
   unsigned vmask[MB];
@@ -96,13 +106,15 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   auto load = [&](int k0) {
 #pragma unroll
     for (int v = 0; v < AV; v++) {
-      const int gr = m0 - HALO + r0 + v * RP;
-      const bool ok = (AR % RP == 0 || r0 + v * RP < AR) && gr >= 0 && gr < M && k0 + kv8 < IC;
-      ra[v] = ok ? *(const vec_t*)(X + (size_t)gr * ldx + kv8 + k0) : vec_t{0, 0, 0, 0};
+      const int r = r0 + v * RP;
+      const bool lo = C::SPLIT && r >= AR;
+      const int gr = m0 - HALO + (lo ? r - AR : r);
+      const bool ok = ((PL * AR) % RP == 0 || r < PL * AR) && gr >= 0 && gr < M && k0 + kv8 < IC;
+      ra[v] = ok ? *(const vec_t*)((lo ? Xlo : X) + (size_t)gr * ldx + kv8 + k0) : vec_t{0, 0, 0, 0};
     }
 #pragma unroll
     for (int v = 0; v < BV; v++) {
-      const bool ok = (TAPS * BN) % RP == 0 || r0 + v * RP < TAPS * BN;
+      const bool ok = (PL * TB) % RP == 0 || r0 + v * RP < PL * TB;
       rb[v] = ok ? *(const vec_t*)(wb + (size_t)v * RP * icp + k0) : vec_t{0, 0, 0, 0};
     }
   };
@@ -111,10 +123,10 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     T* bb = Bs + buf * SE + r0 * LDK + kv8;
 #pragma unroll
     for (int v = 0; v < AV; v++)
-      if (AR % RP == 0 || r0 + v * RP < AR) *(vec_t*)(ab + v * RP * LDK) = ra[v];
+      if ((PL * AR) % RP == 0 || r0 + v * RP < PL * AR) *(vec_t*)(ab + v * RP * LDK) = ra[v];
 #pragma unroll
     for (int v = 0; v < BV; v++)
-      if ((TAPS * BN) % RP == 0 || r0 + v * RP < TAPS * BN) *(vec_t*)(bb + v * RP * LDK) = rb[v];
+      if ((PL * TB) % RP == 0 || r0 + v * RP < PL * TB) *(vec_t*)(bb + v * RP * LDK) = rb[v];
   };
 
   floatx4 acc[MB][NB];
@@ -129,6 +141,7 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     constexpr int g = decltype(gc)::value;
     constexpr int KK = BK / 32, ST = TAPS * KK, S0 = g * ST / G, S = (g + 1) * ST / G - S0;
     frag_t a[2][MB], b[2][NB];
+    frag_t al[C::SPLIT ? 2 : 1][MB], bl[C::SPLIT ? 2 : 1][NB];  // low planes (split)
     auto fetch = [&](int s, int fb) {
       const int t = (S0 + s) / KK, kk = ((S0 + s) % KK) * 32;
       const int shift = C::KS == 3 ? (t / 3 - 1) * POS + (t % 3 - 1) : 0;
@@ -136,11 +149,20 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
 #pragma unroll
       for (int i = 0; i < MB; i++) {
         // Rows whose neighbour is off the board read the zero row, so no loaded value needs masking.
-        const int row = ((vmask[i] >> t) & 1) ? wm * WTM + i * 16 + r16 + HALO + shift : AR;
+        const bool on = (vmask[i] >> t) & 1;
+        const int row = on ? wm * WTM + i * 16 + r16 + HALO + shift : ZR;
         a[fb][i] = *(const frag_t*)(As + sb * SE + row * LDK + g4 * 8 + kk);
+        if constexpr (C::SPLIT) al[fb][i] = *(const frag_t*)(As + sb * SE + (on ? row + AR : ZR) * LDK + g4 * 8 + kk);
       }
 #pragma unroll
-      for (int j = 0; j < NB; j++) b[fb][j] = *(const frag_t*)(bs + j * 16 * LDK);
+      for (int j = 0; j < NB; j++) {
+        b[fb][j] = *(const frag_t*)(bs + j * 16 * LDK);
+        if constexpr (C::SPLIT) bl[fb][j] = *(const frag_t*)(bs + (TB + j * 16) * LDK);
+      }
+    };
+    auto mfma = [&](const frag_t& x, const frag_t& y, floatx4 c) {
+      if constexpr (std::is_same<T, f16>::value) return __builtin_amdgcn_mfma_f32_16x16x32_f16(x, y, c, 0, 0, 0);
+      else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(x, y, c, 0, 0, 0);
     };
     fetch(0, 0);
 #pragma unroll
@@ -149,15 +171,21 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
       // Keep the order: all of the next step's LDS reads are issued before this step's MFMAs (the scheduler
       // would otherwise move each read next to its first use and expose the LDS latency on every step).
       __builtin_amdgcn_sched_barrier(0);
+      if constexpr (C::SPLIT) {
+        // The two correction terms first (independent accumulators back to back), then the main product.
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+          for (int j = 0; j < NB; j++) acc[i][j] = mfma(al[s & 1][i], b[s & 1][j], acc[i][j]);
+#pragma unroll
+        for (int i = 0; i < MB; i++)
+#pragma unroll
+          for (int j = 0; j < NB; j++) acc[i][j] = mfma(a[s & 1][i], bl[s & 1][j], acc[i][j]);
+      }
 #pragma unroll
       for (int i = 0; i < MB; i++)
 #pragma unroll
-        for (int j = 0; j < NB; j++) {
-          if constexpr (std::is_same<T, f16>::value)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[s & 1][i], b[s & 1][j], acc[i][j], 0, 0, 0);
-          else
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[s & 1][i], b[s & 1][j], acc[i][j], 0, 0, 0);
-        }
+        for (int j = 0; j < NB; j++) acc[i][j] = mfma(a[s & 1][i], b[s & 1][j], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (C::INTERLEAVE) {
         // Scheduling hint: alternate this step's MFMAs with the next step's LDS fragment reads.
@@ -220,7 +248,7 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   if constexpr (SEARLY) load_side();
 
   // The zero row of every stage buffer (never written by the stage stores).
-  for (int e = tid; e < NBUF * KV; e += NT) *(vec_t*)(As + (e / KV) * SE + AR * LDK + (e % KV) * 8) = vec_t{0, 0, 0, 0};
+  for (int e = tid; e < NBUF * KV; e += NT) *(vec_t*)(As + (e / KV) * SE + ZR * LDK + (e % KV) * 8) = vec_t{0, 0, 0, 0};
   const int nk = icp / BK;
   load(0);
   if constexpr (NBUF == 1) {
@@ -290,9 +318,14 @@ typedef IgCfg<3, 192, 96, 32, 4, 2, 1, 1> Ig3n96;
 // one wave of workgroups at batch 32) takes 128 channels per stage, one stage buffer: half the stages, 10.2-10.7
 // against 11.3-12.0 us at 384 -> 192.
 typedef IgCfg<1, 192, 48, 128, 4, 1, 2, 1, 2> Ig1k128;
+// Split-operand 1x1 (float-accurate): the same tiles with both operand planes staged, one workgroup per CU
+// (138.5 KB of LDS at 128 channels per stage; 154 KB for two 64-channel stage buffers).
+typedef IgCfg<1, 192, 48, 128, 4, 1, 2, 1, 2, false, true> Ig1k128s;
+typedef IgCfg<1, 192, 48, 64, 4, 1, 2, 2, 2, false, true> Ig1s;
 
-enum { IG3_48, IG3_64, IG3_96, IG1_48, IG1_128 };
-static int igemm_kind(int ks, int ic, int oc) {
+enum { IG3_48, IG3_64, IG3_96, IG1_48, IG1_128, IG1_48S, IG1_128S };
+static int igemm_kind(int ks, int ic, int oc, bool split) {
+  if (ks == 1 && split) return ic % Ig1k128s::BK == 0 && oc <= 4 * Ig1k128s::BN ? IG1_128S : IG1_48S;
   if (ks == 1) return ic % Ig1k128::BK == 0 && oc <= 4 * Ig1k128::BN ? IG1_128 : IG1_48;
   if (oc <= 4 * Ig3::BN) return IG3_48;
   if (oc <= 4 * Ig3n64::BN) return IG3_64;
@@ -304,70 +337,97 @@ static void igemm_tile(int kind, int& bn, int& bk) {
     case IG3_64: bn = Ig3n64::BN; bk = Ig3n64::BK; break;
     case IG3_96: bn = Ig3n96::BN; bk = Ig3n96::BK; break;
     case IG1_128: bn = Ig1k128::BN; bk = Ig1k128::BK; break;
+    case IG1_128S: bn = Ig1k128s::BN; bk = Ig1k128s::BK; break;
+    case IG1_48S: bn = Ig1s::BN; bk = Ig1s::BK; break;
     default: bn = Ig1::BN; bk = Ig1::BK; break;
   }
 }
 
 template <typename T, typename C>
-static void igemm_launch(const void* x, int ldx, int IC, const void* w, int icp, int OC, const ConvOut& o, int M,
-                         hipStream_t s) {
+static void igemm_launch(const void* x, const void* xlo, int ldx, int IC, const void* w, int icp, int OC,
+                         const ConvOut& o, int M, hipStream_t s) {
   if (icp % C::BK != 0) throw std::runtime_error("conv_igemm: padded input channels must be a multiple of the stage");
   const int mtiles = (M + C::BM - 1) / C::BM, ntiles = (OC + C::BN - 1) / C::BN;
   dim3 grid(round_up(mtiles, 8) * ntiles);
   if (g_launch_timing.start) {
     hipExtLaunchKernelGGL(igemm_kernel<T, C>, grid, dim3(C::NT), 0, s, g_launch_timing.start, g_launch_timing.stop,
-                          0, (const T*)x, ldx, IC, (const T*)w, icp, OC, M, o);
+                          0, (const T*)x, (const T*)xlo, ldx, IC, (const T*)w, icp, OC, M, o);
     g_launch_timing.used = true;
   } else {
-    igemm_kernel<T, C><<<grid, C::NT, 0, s>>>((const T*)x, ldx, IC, (const T*)w, icp, OC, M, o);
+    igemm_kernel<T, C><<<grid, C::NT, 0, s>>>((const T*)x, (const T*)xlo, ldx, IC, (const T*)w, icp, OC, M, o);
   }
 }
 
 template <typename T>
-static void igemm_dispatch(int kind, const void* x, int ldx, int IC, const void* w, int icp, int OC,
+static void igemm_dispatch(int kind, const void* x, const void* xlo, int ldx, int IC, const void* w, int icp, int OC,
                            const ConvOut& o, int M, hipStream_t s) {
   switch (kind) {
-    case IG3_48: igemm_launch<T, Ig3>(x, ldx, IC, w, icp, OC, o, M, s); break;
-    case IG3_64: igemm_launch<T, Ig3n64>(x, ldx, IC, w, icp, OC, o, M, s); break;
-    case IG3_96: igemm_launch<T, Ig3n96>(x, ldx, IC, w, icp, OC, o, M, s); break;
-    case IG1_128: igemm_launch<T, Ig1k128>(x, ldx, IC, w, icp, OC, o, M, s); break;
-    default: igemm_launch<T, Ig1>(x, ldx, IC, w, icp, OC, o, M, s); break;
+    case IG3_48: igemm_launch<T, Ig3>(x, xlo, ldx, IC, w, icp, OC, o, M, s); break;
+    case IG3_64: igemm_launch<T, Ig3n64>(x, xlo, ldx, IC, w, icp, OC, o, M, s); break;
+    case IG3_96: igemm_launch<T, Ig3n96>(x, xlo, ldx, IC, w, icp, OC, o, M, s); break;
+    case IG1_128: igemm_launch<T, Ig1k128>(x, xlo, ldx, IC, w, icp, OC, o, M, s); break;
+    case IG1_128S: igemm_launch<T, Ig1k128s>(x, xlo, ldx, IC, w, icp, OC, o, M, s); break;
+    case IG1_48S: igemm_launch<T, Ig1s>(x, xlo, ldx, IC, w, icp, OC, o, M, s); break;
+    default: igemm_launch<T, Ig1>(x, xlo, ldx, IC, w, icp, OC, o, M, s); break;
   }
 }
 
 thread_local LaunchTiming g_launch_timing;
 
-int conv_igemm_icp(int ks, int ic, int oc) {
+int conv_igemm_icp(int ks, int ic, int oc, bool split) {
   int bn, bk;
-  igemm_tile(igemm_kind(ks, ic, oc), bn, bk);
+  igemm_tile(igemm_kind(ks, ic, oc, split), bn, bk);
   return round_up(ic, bk);
 }
 
-// w [oc][ic][ks][ks] -> [oc tile][tap][BN][icp], zero padding beyond oc and ic (BN and icp of the configuration
-// launch_conv_igemm picks for these channel counts).
-void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector<float>& out) {
+// The value a float becomes as a compute-type operand (round to nearest even), as a float.
+static float round_operand(float v, int prec) {
+  if (prec == PREC_BF16) {
+    uint32_t u;
+    std::memcpy(&u, &v, 4);
+    if ((u & 0x7f800000u) == 0x7f800000u) return v;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    u &= 0xffff0000u;
+    float r;
+    std::memcpy(&r, &u, 4);
+    return r;
+  }
+  return (float)(_Float16)v;
+}
+
+// w [oc][ic][ks][ks] -> [oc tile][plane][tap][BN][icp], zero padding beyond oc and ic (BN and icp of the
+// configuration launch_conv_igemm picks for these channel counts); one plane, or with `split` the high plane and
+// the low plane w - round(w).
+void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector<float>& out, bool split, int prec) {
+  if (split && ks != 1) throw std::runtime_error("conv_igemm: split operands for 1x1 convolutions only");
   int bn, bk;
-  igemm_tile(igemm_kind(ks, ic, oc), bn, bk);
-  const int taps = ks * ks, icp = round_up(ic, bk);
+  igemm_tile(igemm_kind(ks, ic, oc, split), bn, bk);
+  const int taps = ks * ks, icp = round_up(ic, bk), pl = split ? 2 : 1;
   const int tiles = (oc + bn - 1) / bn;
-  out.assign((size_t)tiles * taps * bn * icp, 0.f);
+  out.assign((size_t)tiles * pl * taps * bn * icp, 0.f);
   for (int o = 0; o < oc; o++)
     for (int t = 0; t < taps; t++)
-      for (int i = 0; i < ic; i++)
-        out[(((size_t)(o / bn) * taps + t) * bn + o % bn) * icp + i] = w[((size_t)o * ic + i) * taps + t];
+      for (int i = 0; i < ic; i++) {
+        const float v = w[((size_t)o * ic + i) * taps + t];
+        const size_t hi = ((((size_t)(o / bn) * pl) * taps + t) * bn + o % bn) * icp + i;
+        out[hi] = v;
+        if (split) out[hi + (size_t)taps * bn * icp] = v - round_operand(v, prec);
+      }
 }
 
 void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const void* w, int icp, int OC,
-                       const ConvOut& o, int B, hipStream_t s) {
+                       const ConvOut& o, int B, hipStream_t s, const void* x_lo) {
   if (prec != PREC_F16 && prec != PREC_BF16) throw std::runtime_error("conv_igemm: 16-bit operands only");
   if (ks != 1 && ks != 3) throw std::runtime_error("conv_igemm: 1x1 or 3x3 kernels only");
-  if (IC % 8 != 0 || ldx % 8 != 0 || OC % 4 != 0 || icp != conv_igemm_icp(ks, IC, OC))
+  if (x_lo && ks != 1) throw std::runtime_error("conv_igemm: split operands for 1x1 convolutions only");
+  const bool split = x_lo != nullptr;
+  if (IC % 8 != 0 || ldx % 8 != 0 || OC % 4 != 0 || icp != conv_igemm_icp(ks, IC, OC, split))
     throw std::runtime_error("conv_igemm: channel counts must be multiples of 8 (inputs) and 4 (outputs)");
   if ((o.y && o.ldy % 4) || (o.yt && o.ldyt % 4) || (o.colbias && o.ld_colbias % 4) || (o.emit.scale && o.emit.ld % 4))
     throw std::runtime_error("conv_igemm: output strides must be multiples of 4");
-  const int M = B * HW, kind = igemm_kind(ks, IC, OC);
-  if (prec == PREC_F16) igemm_dispatch<f16>(kind, x, ldx, IC, w, icp, OC, o, M, s);
-  else igemm_dispatch<bf16>(kind, x, ldx, IC, w, icp, OC, o, M, s);
+  const int M = B * HW, kind = igemm_kind(ks, IC, OC, split);
+  if (prec == PREC_F16) igemm_dispatch<f16>(kind, x, x_lo, ldx, IC, w, icp, OC, o, M, s);
+  else igemm_dispatch<bf16>(kind, x, x_lo, ldx, IC, w, icp, OC, o, M, s);
   KGX_CHECK_LAUNCH();
 }
 

@@ -27,13 +27,16 @@ struct Prologue {
 };
 
 // Activation of a consumer layer, written by the producer's epilogue from its final float output y[m][n]:
-// out[m][n] = T(act(y * scale[n] + bias[n]) * mask[m]). scale == nullptr disables it.
+// out[m][n] = T(act(y * scale[n] + bias[n]) * mask[m]). scale == nullptr disables it. With out_lo set the
+// activation a is written as two compute-type operands, out = T(a) and out_lo = T(a - T(a)) (same layout), for a
+// consumer that multiplies with split operands (a float-accurate convolution on 16-bit matrix cores).
 struct Emit {
   const float* scale = nullptr;
   const float* bias = nullptr;
   int act = ACT_ID;
   const float* mask = nullptr;
   void* out = nullptr;
+  void* out_lo = nullptr;
   int ld = 0;
 };
 
@@ -103,7 +106,9 @@ void launch_gemm(int prec, const GemmArgs& g, hipStream_t s);
 
 // Implicit-GEMM 1x1 / 3x3 "same" convolution on 16-bit operands: x compute-type NHWC rows of ldx (IC channels,
 // IC % 8 == 0), w the compute-type conversion of conv_igemm_pack_weights' layout (icp = conv_igemm_icp(ks, IC)),
-// OC % 4 == 0.
+// OC % 4 == 0. Split (1x1 only): x_lo holds the low parts of the activation (Emit::out_lo, same layout) and w
+// packs each output tile's high weight rows followed by their low parts; every product is then taken as
+// hi*hi + lo*hi + hi*lo, which carries about 22 significant bits of each operand (a float-accurate convolution).
 // Kernel-timing events for the next launch (set by a profiled forward): a launch site that supports them
 // launches through hipExtLaunchKernel, whose dispatch records `start` and `stop` around the kernel itself, and sets
 // `used`. Others leave them alone and are timed by events around their launch.
@@ -113,10 +118,13 @@ struct LaunchTiming {
 };
 extern thread_local LaunchTiming g_launch_timing;
 
-int conv_igemm_icp(int ks, int ic, int oc);
-void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector<float>& out);
+int conv_igemm_icp(int ks, int ic, int oc, bool split = false);
+// w [oc][ic][ks][ks] -> [oc tile][tap][BN][icp] float; with `split` -> [oc tile][hi, lo][tap][BN][icp], the low
+// plane holding w - round(w) for the compute type `prec`.
+void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector<float>& out, bool split = false,
+                             int prec = PREC_F16);
 void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const void* w, int icp, int OC,
-                       const ConvOut& o, int B, hipStream_t s);
+                       const ConvOut& o, int B, hipStream_t s, const void* x_lo = nullptr);
 
 // Network input planes, float NCHW [B][nin][361], to compute-type NHWC rows of ldo channels (zero beyond nin,
 // ldo % 8 == 0), together with the board statistics of launch_mask_prep; with `gl.W` set, the same launch also

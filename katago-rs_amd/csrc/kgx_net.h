@@ -44,12 +44,13 @@ struct Op {
 
 // Planning state of one residual stream (the trunk, or the inner stream of a nested bottleneck block): its float
 // values, the two compute-type buffers that its consumer activations alternate between (so a producer never
-// writes the buffer its own input was read from), and the op that last wrote the stream, which emits the next
-// consumer's activation.
+// writes the buffer its own input was read from) with their low planes for split-operand consumers (allocated on
+// first use), and the op that last wrote the stream, which emits the next consumer's activation.
 struct StreamState {
   float* x = nullptr;
   int c = 0;
   void* act[2] = {nullptr, nullptr};
+  void* act_lo[2] = {nullptr, nullptr};
   int flip = 0;
   std::shared_ptr<ConvOut> producer;
 };
@@ -96,16 +97,22 @@ class Net {
   void scan(const std::vector<BlockDesc>& blocks, int c, int depth);
   // Whether conv c runs as an implicit GEMM (16-bit handles, 1x1 / 3x3, channel and stride alignment).
   bool igemm_eligible(const ConvDesc& c, bool nchw, int ldx, const ConvOut& o) const;
-  // conv(x) into `o`; x is a compute-type activation [rows][ldx], or the float NCHW network input.
-  std::shared_ptr<ConvOut> emit_conv(const ConvDesc& c, const void* x, int ldx, bool nchw, const ConvOut& o);
+  // conv(x) into `o`; x is a compute-type activation [rows][ldx], or the float NCHW network input. With x_lo (the
+  // low plane of a split activation) the convolution runs on split operands.
+  std::shared_ptr<ConvOut> emit_conv(const ConvDesc& c, const void* x, int ldx, bool nchw, const ConvOut& o,
+                                     const void* x_lo = nullptr);
+  // Whether a 1x1 convolution over a stream activation runs on split operands: on 16-bit handles every
+  // implicit-GEMM 1x1 does, so that only 3x3 convolutions round their operands to 16 bits.
+  bool split_1x1(const ConvDesc& c, int ldx, const ConvOut& o) const;
   void emit_stack(const std::vector<BlockDesc>& blocks, int depth);
   void emit_attention(const BlockDesc& b, int depth);
   void emit_ffn(const BlockDesc& b, int depth);
   std::shared_ptr<ConvOut> emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, const ConvOut& o,
                                            const char* cls, bool glu = false, const QkvEpi& qkv = QkvEpi(),
                                            int yt_act = ACT_ID);
-  // The activation act(bn(x)) * mask of stream `depth`, emitted by the stream's last producer.
-  void* consume(int depth, const BNDesc& bn, int act);
+  // The activation act(bn(x)) * mask of stream `depth`, emitted by the stream's last producer; with `lo`, also its
+  // low plane (split operands), returned there.
+  void* consume(int depth, const BNDesc& bn, int act, const void** lo = nullptr);
   Emit bn_emit(const BNDesc& bn, int act, void* out, int ld);
   Prologue bn_pro(const BNDesc& bn, int act, const float* prebias = nullptr, int ld_prebias = 0);
   RowProg row_prog_base() const;  // a row program with the board statistics filled in

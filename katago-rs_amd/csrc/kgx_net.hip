@@ -115,14 +115,24 @@ Emit Net::bn_emit(const BNDesc& bn, int act, void* out, int ld) {
   return e;
 }
 
-void* Net::consume(int depth, const BNDesc& bn, int act) {
+void* Net::consume(int depth, const BNDesc& bn, int act, const void** lo) {
   StreamState& st = ss_[depth];
   if (!st.producer || st.producer->emit.scale) throw std::runtime_error("internal: stream activation has no producer");
   void* buf = st.act[st.flip];
-  st.flip ^= 1;
   st.producer->emit = bn_emit(bn, act, buf, st.c);
+  if (lo) {
+    // Sized like the stream's high-plane buffers: for the widest block of the stream, not this one.
+    if (!st.act_lo[st.flip]) st.act_lo[st.flip] = alloc_bytes((size_t)max_batch_ * HW * stream_c_[depth] * tsize());
+    st.producer->emit.out_lo = st.act_lo[st.flip];
+    *lo = st.act_lo[st.flip];
+  }
+  st.flip ^= 1;
   st.producer.reset();
   return buf;
+}
+
+bool Net::split_1x1(const ConvDesc& c, int ldx, const ConvOut& o) const {
+  return prec_ != PREC_F32 && c.ky == 1 && c.kx == 1 && c.dy == 1 && c.dx == 1 && igemm_eligible(c, false, ldx, o);
 }
 
 // Workspace needs of a block stack with `c` channels at nesting depth `depth`.
@@ -168,10 +178,14 @@ bool Net::igemm_eligible(const ConvDesc& c, bool nchw, int ldx, const ConvOut& o
          (nchw || (c.ic % 8 == 0 && ldx % 8 == 0));
 }
 
-std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ldx, bool nchw, const ConvOut& o) {
+std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ldx, bool nchw, const ConvOut& o,
+                                        const void* x_lo) {
   const int prec = prec_;
   const double ts = (double)tsize();
   auto out = std::make_shared<ConvOut>(o);
+  const bool split = x_lo != nullptr;
+  if (split && !(!nchw && c.ky == 1 && c.kx == 1 && igemm_eligible(c, nchw, ldx, o)))
+    throw std::runtime_error("internal: split operands for implicit-GEMM 1x1 convolutions only");
   const double in_bytes = (double)HW * c.ic * (nchw ? 4.0 : ts);
   const double out_bytes = (double)HW * c.oc * ((o.y ? 4.0 : 0.0) * (o.accumulate ? 2 : 1) + (o.yt ? ts : 0.0));
   const int ic = c.ic, oc = c.oc;
@@ -197,20 +211,22 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
       ops_.push_back(pk);
       xin = packed;
     }
-    const int icp = conv_igemm_icp(ks, icin, oc), taps = ks * ks;
-    // Filters over the (zero-padded) input channels icin, then packed per output tile.
+    const int icp = conv_igemm_icp(ks, icin, oc, split), taps = ks * ks;
+    // Filters over the (zero-padded) input channels icin, then packed per output tile (split: high and low planes).
     std::vector<float> wi((size_t)oc * icin * taps, 0.f), w;
     for (int oo = 0; oo < oc; oo++)
       for (int i = 0; i < ic; i++)
         for (int t = 0; t < taps; t++) wi[((size_t)oo * icin + i) * taps + t] = c.w[((size_t)oo * ic + i) * taps + t];
-    conv_igemm_pack_weights(ks, wi.data(), oc, icin, w);
+    conv_igemm_pack_weights(ks, wi.data(), oc, icin, w, split, prec);
     const void* dW = upload_t(w);
     Op op;
-    op.launch = [=](hipStream_t s, int B) { launch_conv_igemm(prec, ks, xin, ldin, icin, dW, icp, oc, *out, B, s); };
+    op.launch = [=](hipStream_t s, int B) {
+      launch_conv_igemm(prec, ks, xin, ldin, icin, dW, icp, oc, *out, B, s, x_lo);
+    };
     op.cls = k3 ? "conv3x3" : "conv1x1";
     op.flops_row = 2.0 * HW * ic * oc * taps;
-    op.bytes_row = (double)HW * icin * ts + out_bytes;
-    op.bytes_fixed = (double)taps * ic * oc * ts;
+    op.bytes_row = (double)HW * icin * ts * (split ? 2 : 1) + out_bytes;
+    op.bytes_fixed = (double)taps * ic * oc * ts * (split ? 2 : 1);
     op.out = out;
     op.out_c = oc;
     ops_.push_back(op);
@@ -578,22 +594,26 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
       }
       case BLOCK_NBT: {
         // x += post(bnact(inner(pre(bnact(x))))) (bin2onnx.py:1263-1269)
+        // The entry and exit 1x1 convolutions run on split operands on 16-bit handles (only 3x3 convolutions
+        // round their operands to 16 bits, as in the reference's f16 mode, backend.rs:399-403).
         const int ci = b.regular.oc;
-        const void* a = consume(depth, b.pre_bn, b.pre_act);
         StreamState& in = ss_[depth + 1];
-        in.c = ci;
-        in.producer.reset();
         ConvOut o1;
         o1.y = in.x;
         o1.ldy = ci;
-        in.producer = emit_conv(b.regular, a, c, false, o1);
+        const void* a_lo = nullptr;
+        const void* a = consume(depth, b.pre_bn, b.pre_act, split_1x1(b.regular, c, o1) ? &a_lo : nullptr);
+        in.c = ci;
+        in.producer.reset();
+        in.producer = emit_conv(b.regular, a, c, false, o1, a_lo);
         emit_stack(b.inner, depth + 1);
         // The inner stream ends with this activation: its last producer computes the stream's final value only
         // for the emission, so that sum is not stored.
         const std::shared_ptr<ConvOut> last = ss_[depth + 1].producer;
-        const void* a2 = consume(depth + 1, b.mid_bn, b.mid_act);
+        const void* a2_lo = nullptr;
+        const void* a2 = consume(depth + 1, b.mid_bn, b.mid_act, split_1x1(b.final_conv, ci, res) ? &a2_lo : nullptr);
         if (last) last->y_dead = true;
-        ss_[depth].producer = emit_conv(b.final_conv, a2, ci, false, res);
+        ss_[depth].producer = emit_conv(b.final_conv, a2, ci, false, res, a2_lo);
         break;
       }
       case BLOCK_ATTN:
@@ -886,7 +906,8 @@ void Net::run_ops(int B, hipStream_t s) {
     pc.ms += ms;
     pc.flops += ops_[k].flops_row * B;
     pc.bytes += ops_[k].bytes_row * B + ops_[k].bytes_fixed;
-    if (ops_[k].out && ops_[k].out->emit.scale) pc.bytes += (double)HW * ops_[k].out_c * tsize() * B;
+    if (ops_[k].out && ops_[k].out->emit.scale)
+      pc.bytes += (double)HW * ops_[k].out_c * tsize() * B * (ops_[k].out->emit.out_lo ? 2 : 1);
   }
 }
 

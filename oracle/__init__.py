@@ -32,7 +32,8 @@ def lib():
         for fn in (L.kgo_forward_f64, L.kgo_forward_f32):
             fn.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p,
                            ctypes.c_void_p, ctypes.c_int]
-        L.kgo_forward_f64_q.argtypes = [ctypes.c_void_p, ctypes.c_int] + [ctypes.c_void_p] * 4 + [ctypes.c_int] * 3
+        for fn in (L.kgo_forward_f64_q, L.kgo_forward_f32_q):
+            fn.argtypes = [ctypes.c_void_p, ctypes.c_int] + [ctypes.c_void_p] * 4 + [ctypes.c_int] * 5
         L.kgo_round_operands.argtypes = [ctypes.c_void_p, ctypes.c_long, ctypes.c_int]
         L.kgo_conv_direct_f64.argtypes = [ctypes.c_int] * 4 + [ctypes.c_void_p] * 3
         L.kgo_wino_filter_f64.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_void_p, ctypes.c_void_p]
@@ -43,6 +44,11 @@ def lib():
                                            ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         _lib = L
     return _lib
+
+
+# Layer classes of the 16-bit rounding points (QC_* in kgo_oracle.cpp).
+QCLASS = {"stem": 1, "conv3": 2, "gconv": 4, "nbt_in": 8, "nbt_out": 16, "token": 32}
+QC_ALL = 63
 
 
 def _p(a):
@@ -70,11 +76,13 @@ class Model:
             self._h = None
 
     def forward(self, spatial, glob, meta=None, dtype=np.float64, threads=None, operands=None, acts=True,
-                weights=True):
+                weights=True, classes=None, weight_classes=None):
         """Raw output rows [n, row_len] (policy P x 362 with pass last, value 3, score S, ownership 361).
 
-        operands="f16" / "bf16" evaluates in double with the trunk's GEMM operands rounded to that 16-bit type
-        (activations when `acts`, weights when `weights`), as a 16-bit handle computes them."""
+        operands="f16" / "bf16" evaluates with the trunk's GEMM operands rounded to that 16-bit type
+        (activations when `acts`, weights when `weights`), as a 16-bit handle computes them; `classes` (names of
+        QCLASS, default all) limits the rounding to those layer classes, and `weight_classes` (default: `classes`)
+        that of the weights. Accumulation is in double, or in float with dtype=np.float32."""
         n = spatial.shape[0]
         spatial = np.ascontiguousarray(spatial, np.float32)
         glob = np.ascontiguousarray(glob, np.float32)
@@ -86,9 +94,13 @@ class Model:
         out = np.zeros((n, self.row_len), dtype)
         if operands is not None:
             q = {"f16": 1, "bf16": 2}[operands]
-            out = np.zeros((n, self.row_len), np.float64)
-            if lib().kgo_forward_f64_q(self._h, n, _p(spatial), _p(glob), _p(meta), _p(out), threads,
-                                       q if acts else 0, q if weights else 0) != 0:
+            f32 = dtype == np.float32
+            out = np.zeros((n, self.row_len), np.float32 if f32 else np.float64)
+            cls = QC_ALL if classes is None else sum(QCLASS[c] for c in set(classes))
+            wcls = cls if weight_classes is None else sum(QCLASS[c] for c in set(weight_classes))
+            fn = lib().kgo_forward_f32_q if f32 else lib().kgo_forward_f64_q
+            if fn(self._h, n, _p(spatial), _p(glob), _p(meta), _p(out), threads, q if acts else 0,
+                  q if weights else 0, cls, wcls) != 0:
                 raise RuntimeError(lib().kgo_last_error().decode())
             return out
         fn = lib().kgo_forward_f64 if dtype == np.float64 else lib().kgo_forward_f32

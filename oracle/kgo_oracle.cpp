@@ -374,6 +374,10 @@ R act(R a, int kind) {
 // normal range from 2^-14, subnormal quantum 2^-24, overflow above 65504 to infinity) or bfloat16 (8 significant
 // bits, float32's exponent range). Used to emulate a forward pass whose GEMM operands are 16-bit.
 enum { Q_NONE = 0, Q_F16 = 1, Q_BF16 = 2 };
+// Layer classes of the rounding points: the stem convolution, the 3x3 convolutions of residual and gpool
+// blocks, a gpool block's pooling convolution, a nested bottleneck's entry and exit 1x1 convolutions, and
+// the transformer token GEMMs with the attention operands.
+enum { QC_STEM = 1, QC_CONV3 = 2, QC_GCONV = 4, QC_NBT_IN = 8, QC_NBT_OUT = 16, QC_TOKEN = 32, QC_ALL = 63 };
 double round_operand(double x, int q) {
   if (q == Q_NONE || x == 0.0 || !std::isfinite(x)) return x;
   int e;
@@ -395,23 +399,29 @@ struct Fwd {
   // Operand emulation (double only): the trunk's convolution and token-GEMM operands (inputs and weights), the
   // q/k/v projections and the attention output are rounded to 16 bits; accumulation, residual streams, pooling,
   // normalization statistics and the heads stay exact. qa / qw choose the rounding of activations / weights.
+  // qclass restricts the rounding to the layer classes whose QC_* bit it holds (all by default), which
+  // attributes a 16-bit forward pass's error to its rounding points.
   int qa = Q_NONE, qw = Q_NONE;
+  int qclass = QC_ALL, qclass_w = QC_ALL;  // activation and weight rounding classes
 
   Fwd(const Model& mm, int nn, int th) : m(mm), n(nn), threads(th) {}
 
   R ra(R v) const { return qa ? (R)round_operand((double)v, qa) : v; }
   R rw(R v) const { return qw ? (R)round_operand((double)v, qw) : v; }
+  bool tokq() const { return (qclass & QC_TOKEN) != 0; }
+  bool tokq_w() const { return (qclass_w & QC_TOKEN) != 0; }
 
-  // "same" convolution, zero padding, on [n][C][HW]; `half` marks a trunk convolution (16-bit operands when
-  // emulated).
-  std::vector<R> conv(const std::vector<R>& x0, const Conv& c, bool half = false) {
+  // "same" convolution, zero padding, on [n][C][HW]; `cls` is the QC_* class of a trunk convolution (16-bit
+  // operands when emulated), 0 for the float convolutions of the heads.
+  std::vector<R> conv(const std::vector<R>& x0, const Conv& c, int cls = 0) {
+    const bool half = cls != 0 && (qclass & cls) != 0;
     std::vector<R> xr;
     if (half && qa) {
       xr = x0;
       for (auto& v : xr) v = ra(v);
     }
     const std::vector<R>& x = (half && qa) ? xr : x0;
-    const bool hw = half && qw;
+    const bool hw = cls != 0 && (qclass_w & cls) != 0 && qw;
     std::vector<R> out((size_t)n * c.oc * HW, R(0));
     const int py = (c.ky / 2) * c.dy, px = (c.kx / 2) * c.dx;
 #pragma omp parallel for collapse(2) schedule(static) num_threads(threads)
@@ -540,12 +550,13 @@ struct Fwd {
     const size_t rows = (size_t)n * HW;
     std::vector<R> out(rows * mm.oc, R(0));
     std::vector<R> wr((size_t)mm.ic * mm.oc);
-    for (size_t k = 0; k < wr.size(); k++) wr[k] = rw((R)mm.w[k]);
+    const bool q = tokq(), qwt = tokq_w();
+    for (size_t k = 0; k < wr.size(); k++) wr[k] = qwt ? rw((R)mm.w[k]) : (R)mm.w[k];
 #pragma omp parallel for schedule(static) num_threads(threads)
     for (long r = 0; r < (long)rows; r++) {
       R* o = &out[r * mm.oc];
       for (int i = 0; i < mm.ic; i++) {
-        const R xv = ra(t[r * mm.ic + i]);
+        const R xv = q ? ra(t[r * mm.ic + i]) : t[r * mm.ic + i];
         const R* w = &wr[(size_t)i * mm.oc];
         for (int j = 0; j < mm.oc; j++) o[j] += xv * w[j];
       }
@@ -608,7 +619,8 @@ struct Fwd {
     std::vector<R> xn = tf_rmsnorm(t, bl, C);
     std::vector<R> q = tok_matmul(xn, bl.q), k = tok_matmul(xn, bl.k), v = tok_matmul(xn, bl.v);
     // With 16-bit storage: v is stored as projected; q and k are stored once, after rotation and scaling below.
-    if (qa)
+    const bool q16 = qa && tokq();
+    if (q16)
       for (auto& z : v) z = ra(z);
     const int H = bl.heads, KV = bl.kvh, dq = bl.dq, dv = bl.dv, g = H / KV;
     if (bl.rope) {
@@ -634,7 +646,7 @@ struct Fwd {
       rot(k, KV, false);
     }
     R scale = (R)(1.0f / std::sqrt((float)dq));
-    if (qa) {
+    if (q16) {
       // 16-bit storage feeds the matrix cores: the scaled, rotated queries and the rotated keys are operands.
       for (auto& z : q) z = ra(z * scale);
       for (auto& z : k) z = ra(z);
@@ -663,7 +675,7 @@ struct Fwd {
           // With 16-bit storage the unnormalized probabilities are operands too; the denominator stays exact.
           const R inv = R(1) / den;
           for (int j = 0; j < HW; j++) {
-            const R pj = ra(sc[j]) * inv;
+            const R pj = (q16 ? ra(sc[j]) : sc[j]) * inv;
             const R* vj = &v[((size_t)b * HW + j) * KV * dv + (size_t)kh * dv];
             for (int d = 0; d < dv; d++) oi[d] += pj * vj[d];
           }
@@ -708,27 +720,27 @@ struct Fwd {
       const Block& bl = blocks[i];
       if (bl.kind == B_RES) {
         std::vector<R> t = bn_act_mask(x, bl.pre_bn, bl.pre_act);
-        t = conv(t, bl.regular, true);
+        t = conv(t, bl.regular, QC_CONV3);
         t = bn_act_mask(t, bl.mid_bn, bl.mid_act);
-        t = conv(t, bl.final_, true);
+        t = conv(t, bl.final_, QC_CONV3);
         add(x, t);
       } else if (bl.kind == B_GPOOL) {
         std::vector<R> t = bn_act_mask(x, bl.pre_bn, bl.pre_act);
-        std::vector<R> reg = conv(t, bl.regular, true);
-        std::vector<R> gg = conv(t, bl.gconv, true);
+        std::vector<R> reg = conv(t, bl.regular, QC_CONV3);
+        std::vector<R> gg = conv(t, bl.gconv, QC_GCONV);
         gg = bn_act_mask(gg, bl.gbn, bl.gact);
         std::vector<R> pooled = gpool(gg, bl.gconv.oc);
         std::vector<R> bias = matmul(pooled, bl.gmul);
         add_nc_bias(reg, bias, bl.regular.oc);
         reg = bn_act_mask(reg, bl.mid_bn, bl.mid_act);
-        reg = conv(reg, bl.final_, true);
+        reg = conv(reg, bl.final_, QC_CONV3);
         add(x, reg);
       } else if (bl.kind == B_NBT) {
         std::vector<R> t = bn_act_mask(x, bl.pre_bn, bl.pre_act);
-        t = conv(t, bl.regular, true);
+        t = conv(t, bl.regular, QC_NBT_IN);
         block_stack(t, bl.inner, bl.regular.oc);
         t = bn_act_mask(t, bl.mid_bn, bl.mid_act);
-        t = conv(t, bl.final_, true);
+        t = conv(t, bl.final_, QC_NBT_OUT);
         add(x, t);
       }
       i++;
@@ -753,7 +765,7 @@ struct Fwd {
     for (size_t k = 0; k < x.size(); k++) x[k] = bin[k];
     // The device runs 1x1 and 3x3 stems on 16-bit operands and other stems (old nets' 5x5) on float ones.
     const bool stem16 = m.stem.ky == m.stem.kx && (m.stem.ky == 1 || m.stem.ky == 3) && m.stem.dy == 1 && m.stem.dx == 1;
-    x = conv(x, m.stem, stem16);
+    x = conv(x, m.stem, stem16 ? QC_STEM : 0);
     std::vector<R> g((size_t)n * m.nglob);
     for (size_t k = 0; k < g.size(); k++) g[k] = glob[k];
     add_nc_bias(x, matmul(g, m.stem_mm), C);
@@ -930,13 +942,16 @@ int kgo_forward_f64(const void* mp, int n, const float* bin, const float* glob, 
   } catch (const std::exception& e) { g_err = e.what(); return 1; }
 }
 
-// kgo_forward_f64 with 16-bit operand emulation: act_q / weight_q = 0 (exact), 1 (float16), 2 (bfloat16).
+// kgo_forward_f64 with 16-bit operand emulation: act_q / weight_q = 0 (exact), 1 (float16), 2 (bfloat16);
+// classes / wclasses: the QC_* bits of the layer classes whose activations / weights are rounded.
 int kgo_forward_f64_q(const void* mp, int n, const float* bin, const float* glob, const float* meta, double* out,
-                      int threads, int act_q, int weight_q) {
+                      int threads, int act_q, int weight_q, int classes, int wclasses) {
   try {
     Fwd<double> f(*(const Model*)mp, n, threads < 1 ? 1 : threads);
     f.qa = act_q;
     f.qw = weight_q;
+    f.qclass = classes;
+    f.qclass_w = wclasses;
     f.run(bin, glob, meta, out);
     return 0;
   } catch (const std::exception& e) { g_err = e.what(); return 1; }
@@ -944,11 +959,13 @@ int kgo_forward_f64_q(const void* mp, int n, const float* bin, const float* glob
 
 // kgo_forward_f32 with 16-bit operand emulation (float accumulation, as the device accumulates).
 int kgo_forward_f32_q(const void* mp, int n, const float* bin, const float* glob, const float* meta, float* out,
-                      int threads, int act_q, int weight_q) {
+                      int threads, int act_q, int weight_q, int classes, int wclasses) {
   try {
     Fwd<float> f(*(const Model*)mp, n, threads < 1 ? 1 : threads);
     f.qa = act_q;
     f.qw = weight_q;
+    f.qclass = classes;
+    f.qclass_w = wclasses;
     f.run(bin, glob, meta, out);
     return 0;
   } catch (const std::exception& e) { g_err = e.what(); return 1; }

@@ -5,6 +5,8 @@
   are 19x19 boards, row 20 a 9x9 board, row 24 a 13x13 board). These are weight-free data: realistic inputs
   whose board masks are not full. Reading them needs the reference checkout (REFERENCE env var, default
   /root/reference); the rest of this script does not.
+- m0_all.npz: all 26 positions of those fixtures (spatial and global inputs; rows 0-19 are 19x19 boards,
+  20-23 9x9 and 24-25 13x13), for the benchmark nets. fixtures/m0/b10c128.*_input.f32 hold the same bytes.
 - oracle_tiny.npz: for each small test net (katago-rs_amd.synth.tiny_nets, seed 1), the oracle's float64 raw
   outputs on seeded inputs (3 rows: 19x19, 9x9, 13x13 boards) and on the m0 positions.
 
@@ -37,6 +39,7 @@ def main():
         meta = np.fromfile(os.path.join(d, "b18c384nbt-humanv0.meta_input.f32"), "<f4").reshape(-1, 192)
         np.savez_compressed(m0_path, spatial=binp[M0_ROWS], glob=glob[M0_ROWS], meta=meta[M0_ROWS],
                             rows=np.array(M0_ROWS))
+        np.savez_compressed(os.path.join(HERE, "m0_all.npz"), spatial=binp, glob=glob)
     m0 = np.load(m0_path)
 
     out = {}

@@ -1,18 +1,17 @@
 """Parity of the HIP forward pass (through the C ABI) with the float64 CPU oracle, on the device.
 
-Tolerances, per output group (policy, value, score, ownership) of each row block:
+Tolerances, per output group (policy, value, score, ownership) of each row block, with no allowance:
 - f32: max |gpu - oracle| <= 1e-4 * max |oracle| over the group (the f32 tier's 1e-4 relative error);
-- f16: max |gpu - oracle| <= 2e-2 absolute, or, where the float16 format itself is farther than that from the
-  float64 network, within 1.5x of the format's own error: the distance of the "float16 network" (the oracle
-  evaluated with the kernels' operands rounded to float16 at the kernels' rounding points) from the float64 one;
-- bf16: the same with 1e-1 absolute (8-bit mantissa operands; no reference tier exists).
-16-bit handles are also held to that 16-bit network: max |gpu - emulation| <= 2 x the format's error
-+ 1e-4 * max(1, max |oracle|). The deep synthetic nets amplify rounding: evaluating the float16 network with
-float32 instead of float64 accumulation alone moves b18c384nbt's outputs by about as much as the format error
-(1.8e-2 against 1.9e-2), so the emulation cannot pin the device closer than that; on the shallow nets it matches
-to 1e-6.
+- f16: max |gpu - oracle| <= 2e-2 absolute;
+- bf16: max |gpu - oracle| <= 1.6e-1 absolute: the f16 bound scaled by 8, the ratio of the two types' unit
+  roundoffs (2^-8 against 2^-11; no reference tier exists for bf16).
+16-bit handles round the operands of their 3x3 convolutions (stem included) and of the transformer token GEMMs
+and attention; the 1x1 convolutions of the trunk run on split (high + low) 16-bit operands, float-accurate, as
+the reference's f16 mode keeps them in float (crates/katago-nn-burn/src/backend.rs:399-403). They are also held
+to the "16-bit network", the oracle evaluated with the same operands rounded at the same points:
+max |gpu - emulation| <= 2 x the format's own error (emulation against float64) + 1e-4 * max(1, max |oracle|).
 Index work (symmetry, padding rows, batch buckets, tile scatter) is checked bit-exactly where the arithmetic
-is identical: a row's outputs must not depend on the batch it runs in.
+is identical: a row's outputs must not depend on the batch it runs in, nor on its position in it.
 """
 
 import os
@@ -23,7 +22,9 @@ import pytest
 pytestmark = pytest.mark.gpu
 
 GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
-TOL = {"f32": ("rel", 1e-4), "f16": ("abs", 2e-2), "bf16": ("abs", 1e-1)}
+TOL = {"f32": ("rel", 1e-4), "f16": ("abs", 2e-2), "bf16": ("abs", 1.6e-1)}
+# The layer classes whose operands 16-bit handles round (oracle.QCLASS): all but the nested-bottleneck 1x1s.
+ROUNDED = ("stem", "conv3", "gconv", "token")
 
 
 def groups(P, S):
@@ -55,7 +56,7 @@ def check(out, ref, P, S, prec, what, ref_q=None):
             bound = 2.0 * fmt[k] + 1e-4 * max(1.0, s)
             assert e <= bound, f"{what} [{prec}] {k}: max |gpu - {prec} network| {e:.3e} > {bound:.3e}"
     for k, (e, s) in errs.items():
-        bound = tol * max(s, 1e-30) if kind == "rel" else max(tol, 1.5 * fmt[k])
+        bound = tol * max(s, 1e-30) if kind == "rel" else tol
         assert e <= bound, f"{what} [{prec}] {k}: max err {e:.3e} > {bound:.3e} (|ref| max {s:.3e})"
 
 
@@ -63,7 +64,7 @@ def emulated(oracle, model_bytes, prec, spatial, glob, meta=None):
     """The oracle with the 16-bit handle's operand rounding (None for f32)."""
     if prec == "f32":
         return None
-    return oracle.Model(model_bytes).forward(spatial, glob, meta, operands=prec)
+    return oracle.Model(model_bytes).forward(spatial, glob, meta, operands=prec, classes=ROUNDED)
 
 
 @pytest.fixture(scope="module")
@@ -124,28 +125,48 @@ def test_winograd_f2_benchmark_config(kgx, synth, oracle, monkeypatch):
     h.close()
 
 
-CONFIG_ROWS = {"b10c128": 8, "b18c384nbt": 2, "b10c384h6": 2, "b10c512h8": 1, "tf3-b11c768": 1}
-
-
+# Rows compared with the oracle in every benchmark batch: boards 19, 19, 13 and 9 (make_inputs cycles the sizes),
+# so masked pooling, masked attention keys and partial-board row programs are checked at the configs' shapes.
+CONFIG_ROWS = [0, 1, 2, 3]
+CONFIGS = ["b10c128", "b18c384nbt", "b10c384h6", "b10c512h8", "tf3-b11c768"]
 # bf16 handles run the f16 kernels' bf16 instantiations; the headline net covers those of its shapes.
-CONFIG_CASES = [(n, p) for n in CONFIG_ROWS for p in ("f32", "f16")] + [("b18c384nbt", "bf16")]
+CONFIG_CASES = [(n, p) for n in CONFIGS for p in ("f32", "f16")] + [("b18c384nbt", "bf16")]
 
 
 @pytest.mark.parametrize("name,prec", CONFIG_CASES)
 def test_benchmark_configs_match_oracle(kgx, synth, oracle, name, prec):
     arch_fn, batch = synth.CONFIGS[name]
     mb = synth.write_model(arch_fn(), synth.CONFIG_SEEDS[name])
-    n = CONFIG_ROWS[name]
+    rows = CONFIG_ROWS
     sp, gl, _ = synth.make_inputs(batch, 17, board_sizes=[19, 19, 13, 9])
     net = kgx.Net(mb)
     h = kgx.Handle(net, batch, prec)
     out = h.forward(sp, gl)
-    ref = oracle.Model(mb).forward(sp[:n], gl[:n])
-    check(out[:n], ref, net.P, net.S, prec, name, emulated(oracle, mb, prec, sp[:n], gl[:n]))
-    # The full batch stays finite, and a row's outputs do not depend on the rest of its batch.
+    ref = oracle.Model(mb).forward(sp[rows], gl[rows])
+    check(out[rows], ref, net.P, net.S, prec, name, emulated(oracle, mb, prec, sp[rows], gl[rows]))
     assert np.all(np.isfinite(out))
-    again = h.forward(sp[:n], gl[:n])
-    assert np.array_equal(again, out[:n])
+    # Row independence over the whole batch (crates/katago-nn-burn/tests/batch_buckets.rs:98-120): the rows
+    # [k:] run alone, at other offsets of every pixel tile, equal the full batch's rows bit for bit.
+    for k in (1, 3, batch // 2 + 1, batch - 1):
+        again = h.forward(sp[k:], gl[k:])
+        assert np.array_equal(again, out[k:]), f"{name} [{prec}]: rows {k}: differ when run alone"
+    h.close()
+
+
+@pytest.mark.parametrize("name,prec", [(n, p) for n in ("b10c128", "b18c384nbt") for p in ("f32", "f16")])
+def test_benchmark_nets_on_reference_positions(kgx, synth, oracle, name, prec):
+    """The 26 featurized positions of the reference's raw-output fixtures (fixtures/m0/*.bin_input.f32 and
+    *.global_input.f32: 20 positions on 19x19 boards, four on 9x9, two on 13x13), through the benchmark nets,
+    against the oracle."""
+    m0 = np.load(os.path.join(GOLDEN, "m0_all.npz"))
+    arch_fn, _ = synth.CONFIGS[name]
+    mb = synth.write_model(arch_fn(), synth.CONFIG_SEEDS[name])
+    sp, gl = m0["spatial"], m0["glob"]
+    net = kgx.Net(mb)
+    h = kgx.Handle(net, len(sp), prec)
+    out = h.forward(sp, gl)
+    check(out, oracle.Model(mb).forward(sp, gl), net.P, net.S, prec, name + " m0",
+          emulated(oracle, mb, prec, sp, gl))
     h.close()
 
 

@@ -187,3 +187,97 @@ def test_synthetic_inputs_follow_the_benchmark_distribution(synth):
     frac = sp[0::2, 1:].mean()
     assert 0.27 < frac < 0.33
     assert np.all(np.abs(gl[:, 5]) <= 1) and set(np.unique(np.delete(gl, 5, axis=1))) <= {0.0, 1.0}
+
+
+def test_handle_entry_points_reject_a_null_handle(kgx):
+    """Every entry point that takes a handle returns an error for a NULL one (no device work is started)."""
+    L = kgx.lib()
+    p = kgx.ctypes.c_void_p()
+    calls = {
+        "kg_sync": lambda: L.kg_sync(None),
+        "kg_profile_enable": lambda: L.kg_profile_enable(None, 1),
+        "kg_profile_reset": lambda: L.kg_profile_reset(None),
+        "kg_run": lambda: L.kg_run(None, 1, None),
+        "kg_forward": lambda: L.kg_forward(None, 1, None, None, None, None),
+        "kg_handle_set_batch_buckets": lambda: L.kg_handle_set_batch_buckets(None, None, 0),
+        "kg_handle_device_buffers": lambda: L.kg_handle_device_buffers(None, kgx.ctypes.byref(p), None, None, None),
+        "kg_get_output": lambda: L.kg_get_output(None, 1, None, None),
+    }
+    for name, call in calls.items():
+        assert call() != 0, name
+        err = L.kg_last_error().decode()
+        assert "null handle" in err, (name, err)
+    assert L.kg_profile_read(None, None, None, None, None, None, 0) == -1
+    assert L.kg_handle_stream(None) is None
+    assert L.kg_handle_is_using_fp16(None) == 0
+
+
+def test_copy_outputs_sentinels_follow_every_reference_branch(kgx):
+    """kg_copy_outputs on rows of distinct sentinel values: every field comes from the slot copy_outputs reads
+    (backend.rs:622-731), for every model-version branch and policy channel count, at optimism 0 (channel 0
+    exactly), 1 (channel 1 exactly) and 0.25, with the pass logits at c * 362 + 361 and the inverse symmetry."""
+    import outputs_spec as spec
+    for v, P in spec.CASES:
+        S = spec.score_channels(v)
+        raw = spec.sentinel_row(P, S)
+        for opt in spec.OPTIMISMS:
+            pol, fields, own = spec.expected(raw, P, S, v, opt)
+            if opt in (0.0, 1.0) and (P == 2 or (P == 4 and v >= 16)):
+                c = int(opt)  # exact: the row's own channel c, pass logit included
+                assert np.array_equal(pol, raw[c * 362:(c + 1) * 362]), (v, P, opt)
+            for sym in (0, 3, 5):
+                res = kgx.copy_outputs(raw[None], P, S, v, sym, opt)[0]
+                want_pol = np.append(kgx.copy_with_symmetry(pol[:361].reshape(1, 19, 19), sym, reverse=True).ravel(),
+                                     pol[361])
+                assert np.array_equal(res["policy"], want_pol), (v, P, opt, sym)
+                got = np.array([res[k] for k in spec.FIELDS], np.float32)
+                assert np.array_equal(got, fields), (v, P, opt, sym, got, fields)
+                want_own = kgx.copy_with_symmetry(own.reshape(1, 19, 19), sym, reverse=True).ravel()
+                assert np.array_equal(res["ownership"], want_own), (v, P, opt, sym)
+    with pytest.raises(kgx.KgError, match="score value channels"):
+        kgx.copy_outputs(spec.sentinel_row(1, 4)[None], 1, 4, 9, 0, 0.0)
+    with pytest.raises(kgx.KgError, match="symmetry"):
+        kgx.copy_outputs(spec.sentinel_row(1, 6)[None], 1, 6, 9, 8, 0.0)
+
+
+def test_model_version_table_matches_reference_fixture(kgx):
+    """NNModelVersion's per-version input layout against KataGo's own outputs
+    (fixtures/upstream-v1.18.2/unit/oracle/modelversion_desc.txt, extracted by tests/golden/gen_modelversion.py):
+    values for versions 3..17, the reference's error text for -2..2 and 18..20, and the meta encoder channels."""
+    import json
+    fx = json.load(open(os.path.join(ROOT, "tests", "golden", "modelversion_desc.json")))
+    idx = {"getInputsVersion": 0, "getNumSpatialFeatures": 1, "getNumGlobalFeatures": 2}
+    n = 0
+    for e in fx["V"]:
+        fn, arg = e["fn"], e["arg"]
+        call = (lambda a=arg: kgx.model_version_features(a)[idx[fn]]) if fn in idx else \
+            (lambda a=arg: kgx.meta_encoder_channels(a))
+        if "err" in e:
+            with pytest.raises(kgx.KgError) as ei:
+                call()
+            assert str(ei.value) == e["err"], (fn, arg)
+        else:
+            assert call() == e["value"], (fn, arg)
+        n += 1
+    assert n == 74
+
+
+def test_model_post_process_defaults_match_reference_fixture(kgx, synth):
+    """A model before version 13 stores no post-process parameters: the desc carries ModelPostProcessParams'
+    defaults, which the reference's fixture pins (P lines of modelversion_desc.txt)."""
+    import json
+    fx = json.load(open(os.path.join(ROOT, "tests", "golden", "modelversion_desc.json")))["P"]
+    net = kgx.Net(synth.write_model(synth.tiny_nets()["t_v8"], 1))
+    names = ["tdScoreMultiplier", "scoreMeanMultiplier", "scoreStdevMultiplier", "leadMultiplier",
+             "varianceTimeMultiplier", "shorttermValueErrorMultiplier", "shorttermScoreErrorMultiplier"]
+    assert list(net.desc.post_process_params) == [fx[k] for k in names]
+
+
+def test_handle_rejects_input_counts_of_another_model_version(kgx, synth):
+    """BurnInputBuffers::new asserts the model's input channels against its version (backend.rs:184-188); the
+    handle refuses such a model before touching a device."""
+    arch = synth.tiny_nets()["t_res"]
+    arch.num_global_channels = 18
+    net = kgx.Net(synth.write_model(arch, 1))
+    with pytest.raises(kgx.KgError, match="model version 14 takes 22 spatial and 19 global input features"):
+        kgx.Handle(net, 2, "f16")

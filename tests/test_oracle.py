@@ -198,3 +198,22 @@ def test_operand_emulation_without_rounding_is_the_float64_forward(oracle, synth
     assert np.array_equal(m.forward(sp, gl, operands="f16", acts=False, weights=False), ref)
     q = m.forward(sp, gl, operands="f16")
     assert 0 < np.abs(q - ref).max() < 2e-2
+
+
+def test_oracle_copy_outputs_sentinels_follow_every_reference_branch(oracle):
+    """The oracle's copy_outputs restatement on sentinel rows, against the branch-by-branch reading of
+    backend.rs:622-731 (tests/outputs_spec.py) and the brute-force-pinned symmetry copy."""
+    import outputs_spec as spec
+    for v, P in spec.CASES:
+        S = spec.score_channels(v)
+        raw = spec.sentinel_row(P, S)
+        for opt in spec.OPTIMISMS:
+            pol, fields, own = spec.expected(raw, P, S, v, opt)
+            for sym in (0, 6):
+                gp, gf, go = oracle.copy_outputs_row(raw, P, S, v, sym, opt)
+                wp = np.append(oracle.copy_with_symmetry(pol[:361].reshape(1, 1, 19, 19), sym, reverse=True).ravel(),
+                               pol[361])
+                assert np.array_equal(gp, wp), (v, P, opt, sym)
+                assert np.array_equal(gf, fields), (v, P, opt, sym, gf, fields)
+                assert np.array_equal(go, oracle.copy_with_symmetry(own.reshape(1, 1, 19, 19), sym,
+                                                                    reverse=True).ravel()), (v, P, opt, sym)
