@@ -122,6 +122,17 @@ int kg_handle_device_buffers(kg_handle* handle, float** bin, float** global, flo
 int kg_run(kg_handle* handle, int n, float* out);
 int kg_sync(kg_handle* handle);
 
+/* kg_run (out = NULL) without any allocation. No counterpart in the reference: it is for callers that cannot
+ * allocate device memory, such as code under HIP graph capture, tight serving loops and harnesses that forbid
+ * allocation. The forward pass runs on the inputs in the handle's device buffers and leaves its rows in the
+ * handle's device output buffer (kg_handle_device_buffers), enqueued on the handle's stream without waiting
+ * (kg_sync waits), as eager kernel launches only: no graph capture of its own, no event, no allocation. Its whole
+ * workspace (activations and per-row partial results) is one static device array of 64 MiB per GPU, shared by
+ * every call on that GPU and keeping the last call's contents: calls that overlap on one GPU, from any handle,
+ * race and must be ordered by the caller. A batch whose workspace does not fit is rejected with an error that
+ * names the capacity (the handle plans, at creation, the largest batch up to max_batch that fits). */
+int kg_run_static(kg_handle* handle, int n);
+
 /* The handle's stream (a hipStream_t), for callers that order their own device work after kg_run. */
 void* kg_handle_stream(kg_handle* handle);
 

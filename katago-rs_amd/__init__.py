@@ -35,7 +35,7 @@ EXPORTS = [
     "kg_copy_with_symmetry",
     "kg_handle_is_using_fp16", "kg_forward", "kg_handle_device_buffers", "kg_run", "kg_sync", "kg_handle_stream",
     "kg_get_output", "kg_profile_enable", "kg_profile_reset", "kg_profile_read",
-    "kg_model_version_features", "kg_meta_encoder_channels", "kg_copy_outputs",
+    "kg_model_version_features", "kg_meta_encoder_channels", "kg_copy_outputs", "kg_run_static",
 ]
 
 _lib = None
@@ -121,6 +121,7 @@ def lib():
                                                ctypes.POINTER(vp)]
         L.kg_run.argtypes = [vp, ci, vp]
         L.kg_sync.argtypes = [vp]
+        L.kg_run_static.argtypes = [vp, ci]
         L.kg_handle_stream.argtypes = [vp]
         L.kg_handle_stream.restype = vp
         L.kg_get_output.argtypes = [vp, ci, ctypes.POINTER(RowInput), ctypes.POINTER(NNOutput)]
@@ -301,6 +302,11 @@ class Handle:
                                 out.size < n * self.net.row_len):
             raise ValueError(f"out must be contiguous float32 with room for {n} rows of {self.net.row_len}")
         _check(lib().kg_run(self._h, n, _ptr(out)))
+
+    def run_static(self, n: int):
+        """The allocation-free forward pass (kg_run_static): inputs in the device buffers, outputs left in the
+        device output buffer, enqueued without waiting."""
+        _check(lib().kg_run_static(self._h, n))
 
     def sync(self):
         _check(lib().kg_sync(self._h))

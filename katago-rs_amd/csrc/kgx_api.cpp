@@ -25,6 +25,10 @@ struct kg_handle {
   int precision = 0;
   hipStream_t stream = nullptr;
   std::unique_ptr<kgx::Net> net;
+  // The allocation-free plan of kg_run_static (workspace in the static scratch) and its largest batch; null when
+  // one row's workspace does not fit.
+  std::unique_ptr<kgx::Net> net_static;
+  int static_batch = 0;
   std::vector<int> buckets;
   int model_version = 0, P = 1, S = 1, nin = 0, nglob = 0, nmeta = 0;
   // Pinned host staging: the InputBuffers of the reference (backend.rs:150-212) and the readback.
@@ -158,6 +162,34 @@ int padded_batch_size(const std::vector<int>& buckets, int n, int max_batch) {
   return best < 0 ? n : best;
 }
 
+// Plans kg_run_static's forward pass in the device's static scratch, for the largest batch up to max_batch whose
+// workspace fits (the workspace grows linearly with the batch, up to tile rounding). Planning allocates no device
+// memory; it only reuses the handle's weights and assigns workspace addresses.
+void plan_static(kg_handle* h, const kgx::ModelDesc& m) {
+  char* base = (char*)kgx::static_scratch(h->device);
+  const size_t cap = kgx::kStaticScratchBytes;
+  auto plan = std::make_unique<kgx::Net>(m, *h->net, h->max_batch, base, cap);
+  int b = h->max_batch;
+  if (!plan->fits()) {
+    const size_t wmax = plan->workspace_bytes();
+    auto one = std::make_unique<kgx::Net>(m, *h->net, 1, base, cap);
+    plan.reset();
+    b = 0;
+    if (one->fits()) {
+      const double per_row = (double)(wmax - one->workspace_bytes()) / (h->max_batch - 1);
+      b = std::min(h->max_batch - 1, 1 + (int)((double)(cap - one->workspace_bytes()) / per_row));
+      for (; b > 1; b--) {
+        plan = std::make_unique<kgx::Net>(m, *h->net, b, base, cap);
+        if (plan->fits()) break;
+        plan.reset();
+      }
+      if (b == 1) plan = std::move(one);
+    }
+  }
+  h->static_batch = plan ? b : 0;
+  h->net_static = std::move(plan);
+}
+
 // Runs the first `n_run` rows already staged in the device input buffers; reads `n` rows back into h_out.
 void run_and_read(kg_handle* h, int n_run, int n, float* out) {
   h->net->forward(n_run, h->stream);
@@ -267,6 +299,7 @@ int kg_handle_create(const kg_net* net, int device, int max_batch, int precision
     KGX_HIP(hipSetDevice(device));
     KGX_HIP(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
     h->net = std::make_unique<kgx::Net>(m, device, max_batch, precision);
+    plan_static(h.get(), m);
     KGX_HIP(hipHostMalloc((void**)&h->h_bin, (size_t)max_batch * h->nin * HW * 4, hipHostMallocDefault));
     KGX_HIP(hipHostMalloc((void**)&h->h_glob, (size_t)max_batch * h->nglob * 4, hipHostMallocDefault));
     if (h->nmeta) KGX_HIP(hipHostMalloc((void**)&h->h_meta, (size_t)max_batch * h->nmeta * 4, hipHostMallocDefault));
@@ -358,6 +391,23 @@ int kg_run(kg_handle* h, int n, float* out) {
     const int n_run = padded_batch_size(h->buckets, n, h->max_batch);
     if (out) run_and_read(h, n_run, n, out);
     else h->net->forward(n_run, h->stream);
+  });
+}
+
+int kg_run_static(kg_handle* h, int n) {
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    std::lock_guard<std::mutex> lock(h->mu);
+    const int mib = (int)(kgx::kStaticScratchBytes >> 20);
+    if (!h->net_static)
+      throw std::runtime_error("kgx backend: one row of this network needs more workspace than the static scratch (" +
+                               std::to_string(mib) + " MiB)");
+    if (n < 1 || n > h->static_batch)
+      throw std::runtime_error("kgx backend: batch size " + std::to_string(n) + " out of range for the static scratch (" +
+                               std::to_string(mib) + " MiB holds the workspace of at most " +
+                               std::to_string(h->static_batch) + " rows of this network)");
+    KGX_HIP(hipSetDevice(h->device));
+    h->net_static->forward_eager(padded_batch_size(h->buckets, n, h->static_batch), h->stream);
   });
 }
 

@@ -512,6 +512,23 @@ static void bias_act8_launch(const float* x, int ldx, int C, const float* prebia
   }
 }
 
+__global__ __launch_bounds__(256) void fill_zero_kernel(u32x4* __restrict__ p, size_t n16, unsigned* __restrict__ tail,
+                                                       int ntail) {
+  const size_t stride = (size_t)gridDim.x * 256;
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) p[i] = u32x4{0, 0, 0, 0};
+  if (blockIdx.x == 0 && (int)threadIdx.x < ntail) tail[threadIdx.x] = 0u;
+}
+
+void launch_fill_zero(void* p, size_t bytes, hipStream_t s) {
+  if ((uintptr_t)p % 16 || bytes % 4) throw std::runtime_error("fill_zero: 16-byte aligned, whole words only");
+  if (!bytes) return;
+  const size_t n16 = bytes / 16;
+  const int ntail = (int)((bytes % 16) / 4);
+  const int blocks = (int)std::min<size_t>(1024, std::max<size_t>(1, (n16 + 255) / 256));
+  fill_zero_kernel<<<blocks, 256, 0, s>>>((u32x4*)p, n16, (unsigned*)((char*)p + n16 * 16), ntail);
+  KGX_CHECK_LAUNCH();
+}
+
 void launch_bias_act(int prec, const float* x, int ldx, int C, const float* prebias, int ld_prebias, const float* scale,
                      const float* bias, int act, const float* mask, void* out, int ldo, int rows, hipStream_t s) {
   // 16-byte path for 16-bit outputs when every row and channel group is 16-byte aligned.

@@ -145,6 +145,10 @@ void launch_conv_direct(int prec, const void* x, int ldx, bool nchw_f32, int IC,
 void launch_bias_act(int prec, const float* x, int ldx, int C, const float* prebias, int ld_prebias, const float* scale,
                      const float* bias, int act, const float* mask, void* out, int ldo, int rows, hipStream_t s);
 
+// Zero `bytes` (a multiple of 4) at p, 16-byte aligned: a kernel rather than hipMemsetAsync, so that a caller may
+// capture it in a graph.
+void launch_fill_zero(void* p, size_t bytes, hipStream_t s);
+
 // mask[b][pos] = bin[b][0][pos]; area = sum; s1 = (sqrt(area)-14)*0.1; s2 = (sqrt(area)-14)^2*0.01-0.1.
 void launch_mask_prep(const float* bin, int nin, float* mask, float* area, float* s1, float* s2, int B,
                       hipStream_t s);

@@ -19,6 +19,11 @@ namespace kgx {
     if (e_ != hipSuccess) throw std::runtime_error(std::string(#call) + ": " + hipGetErrorString(e_));    \
   } while (0)
 
+// The static device workspace of the allocation-free forward pass: its size, and its address on `device` (looked
+// up once per device; `device` must be current).
+constexpr size_t kStaticScratchBytes = 64ull << 20;
+void* static_scratch(int device);
+
 struct DeviceBuffer {
   void* ptr = nullptr;
   size_t bytes = 0;
@@ -64,10 +69,20 @@ struct ProfileClass {
 class Net {
  public:
   Net(const ModelDesc& model, int device, int max_batch, int prec);
+  // A second plan of `primary`'s network that allocates nothing: its weights are the primary's (uploaded in the
+  // same order), its inputs and outputs are the primary's device buffers, and its workspace is bump-allocated
+  // from [ws_base, ws_base + ws_cap) (the planning only records addresses; fits() tells whether they stayed
+  // within the capacity).
+  Net(const ModelDesc& model, const Net& primary, int max_batch, char* ws_base, size_t ws_cap);
   ~Net();
 
   // Enqueues the forward pass over the first B rows of the device input buffers on `stream`.
   void forward(int B, hipStream_t stream);
+  // The forward pass of a workspace plan (second constructor): eager launches only (no graph capture, no event,
+  // no allocation), after clearing the workspace regions the planning zeroes once in a primary plan.
+  void forward_eager(int B, hipStream_t stream);
+  bool fits() const { return ws_used_ <= ws_cap_; }
+  size_t workspace_bytes() const { return ws_used_; }
 
   int prec() const { return prec_; }
   int max_batch() const { return max_batch_; }
@@ -86,10 +101,12 @@ class Net {
   void set_use_graphs(bool on) { use_graphs_ = on; }
 
  private:
-  // Allocation and upload.
+  // Allocation and upload. A workspace plan (primary_ set) bump-allocates workspace and takes the primary's
+  // uploads in order.
   float* alloc_f(size_t n);
   void* alloc_bytes(size_t bytes);
   const float* upload_f(const std::vector<float>& v);
+  const void* take_upload(size_t bytes);
   const void* upload_t(const std::vector<float>& v);  // converted to the compute type
   size_t tsize() const { return prec_ == PREC_F32 ? 4 : 2; }
 
@@ -124,6 +141,12 @@ class Net {
 
   enum ConvMode { CONV_IGEMM, CONV_WINO2, CONV_WINO4 };
   int device_, max_batch_, prec_;
+  const Net* primary_ = nullptr;
+  std::vector<std::pair<const void*, size_t>> uploads_;  // device copies of the weights, in upload order
+  size_t upload_next_ = 0;                               // workspace plan: the next primary upload to take
+  char* ws_base_ = nullptr;
+  size_t ws_cap_ = 0, ws_used_ = 0;
+  std::vector<std::pair<void*, size_t>> zero_;           // workspace regions cleared before every eager forward
   ConvMode conv_mode_ = CONV_WINO4;
   int wino_tm_ = 4;
   int nin_ = 0, nglob_ = 0, nmeta_ = 0, row_len_ = 0;

@@ -9,9 +9,34 @@
 #include <cmath>
 #include <cstdlib>
 #include <cstring>
+#include <map>
+#include <mutex>
 #include <stdexcept>
 
 namespace kgx {
+
+// The workspace of the allocation-free forward pass (kg_run_static): one static device array per GPU, loaded with
+// the library's code object. Host code never uses the array's name as an address: static_scratch() looks up each
+// device's copy once, with that device current, and every launch takes that pointer.
+static __device__ __align__(256) char scratch[kStaticScratchBytes];
+
+void* static_scratch(int device) {
+  static std::mutex mu;
+  static std::map<int, void*> ptrs;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = ptrs.find(device);
+  if (it != ptrs.end()) return it->second;
+  int cur = -1;
+  KGX_HIP(hipGetDevice(&cur));
+  if (cur != device) throw std::runtime_error("internal: static scratch looked up on another device");
+  void* p = nullptr;
+  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    throw std::runtime_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+  ptrs.emplace(device, p);
+  return p;
+}
+
 namespace {
 
 uint16_t f32_to_f16_bits(float f) {
@@ -49,6 +74,16 @@ Net::Net(const ModelDesc& m, int device, int max_batch, int prec) : device_(devi
   build(m);
 }
 
+Net::Net(const ModelDesc& m, const Net& primary, int max_batch, char* ws_base, size_t ws_cap)
+    : device_(primary.device_), max_batch_(max_batch), prec_(primary.prec_), primary_(&primary), ws_base_(ws_base),
+      ws_cap_(ws_cap) {
+  if (max_batch < 1 || max_batch > primary.max_batch_) throw std::runtime_error("internal: workspace plan batch");
+  conv_mode_ = primary.conv_mode_;
+  wino_tm_ = primary.wino_tm_;
+  build(m);
+  if (upload_next_ != primary.uploads_.size()) throw std::runtime_error("internal: workspace plan weights differ");
+}
+
 int Net::t_pad(int B) const { return round_up(B * wino_tiles(wino_tm_), 128); }
 
 Net::~Net() {
@@ -60,8 +95,14 @@ Net::~Net() {
 float* Net::alloc_f(size_t n) { return (float*)alloc_bytes(n * sizeof(float)); }
 
 void* Net::alloc_bytes(size_t bytes) {
-  auto b = std::make_unique<DeviceBuffer>();
   bytes = std::max<size_t>(bytes, 256);
+  if (primary_) {
+    // Workspace plan: addresses only, 256-byte aligned; the caller checks fits() before running it.
+    const size_t off = (ws_used_ + 255) / 256 * 256;
+    ws_used_ = off + bytes;
+    return ws_base_ + off;
+  }
+  auto b = std::make_unique<DeviceBuffer>();
   KGX_HIP(hipMalloc(&b->ptr, bytes));
   b->bytes = bytes;
   void* p = b->ptr;
@@ -69,18 +110,28 @@ void* Net::alloc_bytes(size_t bytes) {
   return p;
 }
 
+const void* Net::take_upload(size_t bytes) {
+  if (upload_next_ >= primary_->uploads_.size() || primary_->uploads_[upload_next_].second != bytes)
+    throw std::runtime_error("internal: workspace plan weights differ");
+  return primary_->uploads_[upload_next_++].first;
+}
+
 const float* Net::upload_f(const std::vector<float>& v) {
+  if (primary_) return (const float*)take_upload(v.size() * sizeof(float));
   float* d = alloc_f(v.size());
   KGX_HIP(hipMemcpy(d, v.data(), v.size() * sizeof(float), hipMemcpyHostToDevice));
+  uploads_.emplace_back(d, v.size() * sizeof(float));
   return d;
 }
 
 const void* Net::upload_t(const std::vector<float>& v) {
   if (prec_ == PREC_F32) return upload_f(v);
+  if (primary_) return take_upload(v.size() * 2);
   std::vector<uint16_t> h(v.size());
   for (size_t k = 0; k < v.size(); k++) h[k] = prec_ == PREC_F16 ? f32_to_f16_bits(v[k]) : f32_to_bf16_bits(v[k]);
   void* d = alloc_bytes(h.size() * 2);
   KGX_HIP(hipMemcpy(d, h.data(), h.size() * 2, hipMemcpyHostToDevice));
+  uploads_.emplace_back(d, h.size() * 2);
   return d;
 }
 
@@ -634,13 +685,21 @@ void Net::build(const ModelDesc& m) {
   nmeta_ = m.num_meta;
   row_len_ = m.row_len();
 
-  d_bin_ = alloc_f((size_t)max_batch_ * nin_ * HW);
-  d_glob_ = alloc_f((size_t)max_batch_ * nglob_);
-  d_meta_ = nmeta_ ? alloc_f((size_t)max_batch_ * nmeta_) : nullptr;
-  d_out_ = alloc_f((size_t)max_batch_ * row_len_);
-  KGX_HIP(hipMemset(d_bin_, 0, (size_t)max_batch_ * nin_ * HW * 4));
-  KGX_HIP(hipMemset(d_glob_, 0, (size_t)max_batch_ * nglob_ * 4));
-  if (d_meta_) KGX_HIP(hipMemset(d_meta_, 0, (size_t)max_batch_ * nmeta_ * 4));
+  if (primary_) {
+    // A workspace plan reads and writes the primary's input and output buffers.
+    d_bin_ = primary_->d_bin_;
+    d_glob_ = primary_->d_glob_;
+    d_meta_ = primary_->d_meta_;
+    d_out_ = primary_->d_out_;
+  } else {
+    d_bin_ = alloc_f((size_t)max_batch_ * nin_ * HW);
+    d_glob_ = alloc_f((size_t)max_batch_ * nglob_);
+    d_meta_ = nmeta_ ? alloc_f((size_t)max_batch_ * nmeta_) : nullptr;
+    d_out_ = alloc_f((size_t)max_batch_ * row_len_);
+    KGX_HIP(hipMemset(d_bin_, 0, (size_t)max_batch_ * nin_ * HW * 4));
+    KGX_HIP(hipMemset(d_glob_, 0, (size_t)max_batch_ * nglob_ * 4));
+    if (d_meta_) KGX_HIP(hipMemset(d_meta_, 0, (size_t)max_batch_ * nmeta_ * 4));
+  }
   mask_ = alloc_f(Mx);
   area_ = alloc_f(max_batch_);
   s1_ = alloc_f(max_batch_);
@@ -857,15 +916,18 @@ void Net::build(const ModelDesc& m) {
 
   // Winograd workspace, sized by the largest convolution.
   // Zeroed once: padding tile rows are read by the GEMMs but never written.
+  // A workspace plan clears them before every forward instead (its memory is shared and keeps older contents).
   if (wino_v_elems_) {
     wino_v_ = alloc_bytes(wino_v_elems_ * tsize());
-    KGX_HIP(hipMemset(wino_v_, 0, wino_v_elems_ * tsize()));
+    if (primary_) zero_.emplace_back(wino_v_, wino_v_elems_ * tsize());
+    else KGX_HIP(hipMemset(wino_v_, 0, wino_v_elems_ * tsize()));
   }
   if (wino_m_elems_) {
     wino_m_ = alloc_f(wino_m_elems_);
-    KGX_HIP(hipMemset(wino_m_, 0, wino_m_elems_ * 4));
+    if (primary_) zero_.emplace_back(wino_m_, wino_m_elems_ * 4);
+    else KGX_HIP(hipMemset(wino_m_, 0, wino_m_elems_ * 4));
   }
-  KGX_HIP(hipDeviceSynchronize());
+  if (!primary_) KGX_HIP(hipDeviceSynchronize());
 }
 
 void Net::run_ops(int B, hipStream_t s) {
@@ -909,6 +971,13 @@ void Net::run_ops(int B, hipStream_t s) {
     if (ops_[k].out && ops_[k].out->emit.scale)
       pc.bytes += (double)HW * ops_[k].out_c * tsize() * B * (ops_[k].out->emit.out_lo ? 2 : 1);
   }
+}
+
+void Net::forward_eager(int B, hipStream_t s) {
+  if (!primary_ || !fits()) throw std::runtime_error("internal: not a runnable workspace plan");
+  if (B < 1 || B > max_batch_) throw std::runtime_error("batch size out of range");
+  for (const auto& z : zero_) launch_fill_zero(z.first, z.second, s);
+  for (const Op& op : ops_) op.launch(s, B);
 }
 
 void Net::forward(int B, hipStream_t s) {
