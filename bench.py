@@ -10,10 +10,16 @@ Prints one JSON line. Besides the throughput it carries
 - "roofline": the dominant kernel class's algorithmic work per launch over its average launch time, measured
   with HIP events around every kernel launch on the library's stream during a second timed region of the same
   K steps (events need eager launches; the throughput region replays a HIP graph);
-- "cpu_baseline": the float32 CPU oracle on a bounded sample of the same workload, on this host's cores.
+- "cpu_baseline": the float32 CPU oracle on bounded samples of the same workload and of b10c128 at batch 8, on one
+  thread and on all the host cores this run may use (at most 16), with the host's CPU model and core count, beside
+  the reference's published single-thread flex figures (README.md:89, 98 of the reference);
 - "roofline.traffic": HBM bytes per launch of the dominant kernel class, from the rocprofv3 FETCH_SIZE and
   WRITE_SIZE passes recorded in profiles/traffic.json (each scaled by the same counter's reading for a device copy
-  of known size, `--copy-probe-mb`); null when no measurement for that class and workload is recorded.
+  of known size, `--copy-probe-mb`); null when no measurement for that class and workload is recorded;
+- "roofline.rocprof": the same kernel's average duration in the committed rocprofv3 kernel trace of this command
+  (profiles/kernel_trace.json) and the fraction it gives, beside the event-timed one;
+- "other_workloads": b10c128 float32 at batch 8 (the reference's CPU-runnable config) on the GPU, beside the
+  reference's published RX 6800 XT figure.
 """
 
 import argparse
@@ -34,6 +40,11 @@ PEAK_HBM_GBS = 8000.0
 # The headline metric's name for the default workload; other workloads are named the same way.
 HEADLINE = "evals/s b18c384nbt fp16 batch 32 on 1 MI355X; MFMA util % + HBM GB/s %"
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
+TRACE_FILE = os.path.join(ROOT, "profiles", "kernel_trace.json")
+# The reference's published single-thread flex (burn CPU) throughput, i7-8700K (README.md:89, 98), evals/s.
+PUBLISHED_FLEX = {"b10c128 batch 8": 33.0, "b18c384nbt batch 8": 2.5}
+# The reference's published ROCm f32 throughput of b10c128 at batch 8 on an RX 6800 XT (README.md:85-86), evals/s.
+PUBLISHED_B10C128_F32_B8 = 2617.0
 
 
 def copy_probe(mb):
@@ -55,15 +66,73 @@ def copy_probe(mb):
     print(json.dumps({"copy_probe_bytes": n}))
 
 
-def recorded_traffic(kernel, workload):
-    """HBM bytes per launch of `kernel` on `workload` from the committed counter passes, or None."""
+def _recorded(path, kernel, workload):
     try:
-        with open(TRAFFIC_FILE) as f:
+        with open(path) as f:
             rec = json.load(f)
     except (OSError, ValueError):
         return None
-    e = rec.get(workload, {}).get(kernel)
+    return rec.get(workload, {}).get(kernel)
+
+
+def recorded_traffic(kernel, workload):
+    """HBM bytes per launch of `kernel` on `workload` from the committed counter passes, or None."""
+    e = _recorded(TRAFFIC_FILE, kernel, workload)
     return None if e is None else e.get("bytes_per_launch")
+
+
+def recorded_trace_us(kernel, workload):
+    """The average duration (us) of `kernel` on `workload` in the committed rocprofv3 kernel trace, or None."""
+    e = _recorded(TRACE_FILE, kernel, workload)
+    return None if e is None else e.get("avg_us")
+
+
+def cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def time_oracle(oracle, synth, config, rows, threads):
+    """evals/s of the float32 CPU oracle on `rows` rows of `config`'s benchmark inputs (one warm-up row first)."""
+    arch_fn, _ = synth.CONFIGS[config]
+    arch = arch_fn()
+    om = oracle.Model(synth.write_model(arch, synth.CONFIG_SEEDS[config]))
+    sp, gl, me = synth.make_inputs(rows, 1234, meta=arch.meta_encoder)
+    om.forward(sp[:1], gl[:1], None if me is None else me[:1], dtype=np.float32, threads=threads)
+    t = time.perf_counter()
+    om.forward(sp, gl, me, dtype=np.float32, threads=threads)
+    dt = time.perf_counter() - t
+    return {"value": rows / dt, "rows": rows, "threads": threads, "seconds": round(dt, 2)}
+
+
+def time_gpu_workload(kgx, synth, hip, config, precision, batch, steps, warmup):
+    """evals/s of `config` at `batch` on the GPU: inputs resident, each step one forward and its readback."""
+    arch_fn, _ = synth.CONFIGS[config]
+    arch = arch_fn()
+    net = kgx.Net(synth.write_model(arch, synth.CONFIG_SEEDS[config]))
+    h = kgx.Handle(net, batch, precision, device=0)
+    sp, gl, me = synth.make_inputs(batch, 1234, meta=arch.meta_encoder)
+    d_bin, d_glob, d_meta, _ = h.device_buffers()
+    assert hip.hipMemcpy(d_bin, sp.ctypes.data, sp.nbytes, 1) == 0
+    assert hip.hipMemcpy(d_glob, gl.ctypes.data, gl.nbytes, 1) == 0
+    if me is not None:
+        assert hip.hipMemcpy(d_meta, me.ctypes.data, me.nbytes, 1) == 0
+    out = np.empty((batch, net.row_len), np.float32)
+    for _ in range(warmup):
+        h.run(batch, out)
+    h.sync()
+    t = time.perf_counter()
+    for _ in range(steps):
+        h.run(batch, out)
+        out.sum(dtype=np.float64)
+    dt = time.perf_counter() - t
+    h.close()
+    return {"value": batch * steps / dt, "unit": "evals/s", "ms_per_step": dt / steps * 1e3, "steps": steps}
 
 
 def main():
@@ -75,8 +144,10 @@ def main():
     ap.add_argument("--precision", default="f16", choices=["f16", "bf16", "f32"])
     ap.add_argument("--batch", type=int, default=0, help="override the config's batch size")
     ap.add_argument("--cpu-rows", type=int, default=-1,
-                    help="rows in the CPU-baseline sample (-1: the whole batch, 0: skip)")
+                    help="rows in the all-core CPU-baseline sample (-1: the whole batch, 0: skip the CPU baseline)")
+    ap.add_argument("--cpu-rows-1t", type=int, default=2, help="rows in the single-thread CPU-baseline sample")
     ap.add_argument("--cpu-threads", type=int, default=0, help="CPU-baseline threads (0: min(16, cores))")
+    ap.add_argument("--other-workloads", type=int, default=1, help="also time b10c128 f32 batch 8 (0: skip)")
     ap.add_argument("--handles", type=int, default=2,
                     help="also time this many handles in flight, one thread each (reported as 'pipelined'; 1: skip)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
@@ -132,6 +203,16 @@ def main():
     evals_per_s = batch * args.steps / dt
     if not np.isfinite(checksum):
         raise RuntimeError("non-finite outputs")
+    # The reference bench's own method beside the exact K steps: at least 8 iterations and at least 2 s
+    # (crates/katago-nn-burn/examples/bench.rs:49-53).
+    ns, t0 = 0, time.perf_counter()
+    while ns < 8 or time.perf_counter() - t0 < 2.0:
+        step()
+        ns += 1
+    h.sync()
+    sdt = time.perf_counter() - t0
+    sustained = {"value": batch * ns / sdt, "steps": ns, "seconds": round(sdt, 3),
+                 "method": "at least 8 iterations and at least 2 s, as the reference's examples/bench.rs"}
 
     # Second timed region: the same K steps launched eagerly with HIP events around every kernel.
     h.profile(True)
@@ -205,21 +286,39 @@ def main():
     workload = f"{args.config} {args.precision} batch {batch}"
     roof["traffic"] = recorded_traffic(dname, workload)
 
+    rp_us = recorded_trace_us(dname, workload)
+    if rp_us:
+        roof["rocprof"] = {"avg_launch_us": rp_us, "achieved": roof["work_per_launch"] / (rp_us * 1e-6) /
+                           (1e12 if roof["unit"] == "TFLOP/s" else 1e9)}
+        roof["rocprof"]["frac"] = roof["rocprof"]["achieved"] / roof["peak"]
+        roof["rocprof"]["source"] = "profiles/kernel_trace.json (rocprofv3 --kernel-trace --stats of this command)"
+
+    other = None
+    if args.other_workloads and (args.config, args.precision, batch) == ("b18c384nbt", "f16", 32):
+        r = time_gpu_workload(kgx, synth, hip, "b10c128", "f32", 8, max(args.steps, 100), args.warmup)
+        r["published_rx6800xt_rocm_f32"] = PUBLISHED_B10C128_F32_B8
+        other = {"b10c128 f32 batch 8": r}
+
     cpu = None
     if args.cpu_rows < 0:
         args.cpu_rows = batch
     if args.cpu_rows > 0:
         import oracle
         threads = args.cpu_threads or min(16, os.cpu_count() or 1)
-        om = oracle.Model(model)
         n = min(args.cpu_rows, batch)
-        om.forward(sp[:1], gl[:1], None if me is None else me[:1], dtype=np.float32, threads=threads)
-        t2 = time.perf_counter()
-        om.forward(sp[:n], gl[:n], None if me is None else me[:n], dtype=np.float32, threads=threads)
-        cdt = time.perf_counter() - t2
-        cpu = {"value": n / cdt, "unit": "evals/s", "cores": threads, "kind": "port",
-               "sample": f"{n} rows of the same workload through the float32 CPU oracle (direct convolution), "
-                         f"{cdt:.1f} s"}
+        allc = time_oracle(oracle, synth, args.config, n, threads)
+        one = time_oracle(oracle, synth, args.config, max(1, args.cpu_rows_1t), 1)
+        cpu = {"value": allc["value"], "unit": "evals/s", "cores": threads, "kind": "port",
+               "sample": f"{n} rows of the same workload through the float32 CPU oracle (direct convolution, "
+                         f"plain loops) on {threads} threads, {allc['seconds']} s",
+               "single_thread": one, "nproc": os.cpu_count(), "cpu_model": cpu_model(),
+               "published_flex_1_thread_i7_8700k": PUBLISHED_FLEX}
+        if args.config == "b18c384nbt":
+            cpu["b10c128 batch 8"] = {"all_cores": time_oracle(oracle, synth, "b10c128", 8, threads),
+                                      "single_thread": time_oracle(oracle, synth, "b10c128", 8, 1)}
+            cpu["note"] = ("The oracle is a plain-loop restatement: per core it runs "
+                           f"{PUBLISHED_FLEX['b18c384nbt batch 8'] / max(one['value'], 1e-9):.1f}x slower than "
+                           "the reference's published flex figure for b18c384nbt (different CPU, batch 8).")
 
     res = {
         "metric": HEADLINE if (args.config, args.precision, batch) == ("b18c384nbt", "f16", 32) else
@@ -245,6 +344,8 @@ def main():
         "profiled_ms_per_step": prof_ms_per_step,
         "checksum": checksum,
         "pipelined": pipelined,
+        "other_workloads": other,
+        "sustained": sustained,
     }
     print(json.dumps(res))
 

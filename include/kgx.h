@@ -129,8 +129,10 @@ int kg_sync(kg_handle* handle);
  * (kg_sync waits), as eager kernel launches only: no graph capture of its own, no event, no allocation. Its whole
  * workspace (activations and per-row partial results) is one static device array of 64 MiB per GPU, shared by
  * every call on that GPU and keeping the last call's contents: calls that overlap on one GPU, from any handle,
- * race and must be ordered by the caller. A batch whose workspace does not fit is rejected with an error that
- * names the capacity (the handle plans, at creation, the largest batch up to max_batch that fits). */
+ * race and must be ordered by the caller. The first call on a handle looks the array up on the handle's device
+ * and plans the forward pass for the largest batch up to max_batch whose workspace fits (host work only, no
+ * device allocation); make that first call outside any stream capture. A batch whose workspace does not fit is
+ * rejected with an error that names the capacity. */
 int kg_run_static(kg_handle* handle, int n);
 
 /* The handle's stream (a hipStream_t), for callers that order their own device work after kg_run. */

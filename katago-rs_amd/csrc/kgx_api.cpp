@@ -16,7 +16,7 @@
 #include "kgx_net.h"
 
 struct kg_net {
-  kgx::ModelDesc model;
+  std::shared_ptr<const kgx::ModelDesc> model;  // shared with the handles, which may outlive the net object
 };
 
 struct kg_handle {
@@ -25,10 +25,12 @@ struct kg_handle {
   int precision = 0;
   hipStream_t stream = nullptr;
   std::unique_ptr<kgx::Net> net;
-  // The allocation-free plan of kg_run_static (workspace in the static scratch) and its largest batch; null when
-  // one row's workspace does not fit.
+  // The model (kept for the allocation-free plan), and the plan of kg_run_static with its workspace in the static
+  // scratch, made by its first call on the handle: static_batch is -1 before, then the plan's largest batch (0 when
+  // one row's workspace does not fit).
+  std::shared_ptr<const kgx::ModelDesc> model;
   std::unique_ptr<kgx::Net> net_static;
-  int static_batch = 0;
+  int static_batch = -1;
   std::vector<int> buckets;
   int model_version = 0, P = 1, S = 1, nin = 0, nglob = 0, nmeta = 0;
   // Pinned host staging: the InputBuffers of the reference (backend.rs:150-212) and the readback.
@@ -164,7 +166,8 @@ int padded_batch_size(const std::vector<int>& buckets, int n, int max_batch) {
 
 // Plans kg_run_static's forward pass in the device's static scratch, for the largest batch up to max_batch whose
 // workspace fits (the workspace grows linearly with the batch, up to tile rounding). Planning allocates no device
-// memory; it only reuses the handle's weights and assigns workspace addresses.
+// memory; it looks up the scratch's address on the handle's device (once per device), reuses the handle's weights
+// and assigns workspace addresses.
 void plan_static(kg_handle* h, const kgx::ModelDesc& m) {
   char* base = (char*)kgx::static_scratch(h->device);
   const size_t cap = kgx::kStaticScratchBytes;
@@ -236,7 +239,7 @@ int kg_net_load(const void* model_bytes, size_t len, const char* expected_sha256
       throw std::runtime_error("Error loading or parsing model file: expectedSha256 is not supported by the kgx backend");
     if (!model_bytes || len == 0) throw std::runtime_error("Error loading or parsing model file: empty model");
     auto net = std::make_unique<kg_net>();
-    net->model = kgx::parse_model((const uint8_t*)model_bytes, len);
+    net->model = std::make_shared<const kgx::ModelDesc>(kgx::parse_model((const uint8_t*)model_bytes, len));
     *out = net.release();
   });
 }
@@ -246,7 +249,7 @@ void kg_net_free(kg_net* net) { delete net; }
 int kg_net_desc(const kg_net* net, kg_model_desc* d) {
   return guarded([&] {
     if (!net || !d) throw std::runtime_error("null argument");
-    const kgx::ModelDesc& m = net->model;
+    const kgx::ModelDesc& m = *net->model;
     std::memset(d, 0, sizeof(*d));
     std::strncpy(d->name, m.name.c_str(), sizeof(d->name) - 1);
     d->model_version = m.version;
@@ -279,7 +282,7 @@ int kg_handle_create(const kg_net* net, int device, int max_batch, int precision
     h->device = device;
     h->max_batch = max_batch;
     h->precision = precision;
-    const kgx::ModelDesc& m = net->model;
+    const kgx::ModelDesc& m = *net->model;
     // The input buffers' layout must be the model version's (BurnInputBuffers::new, backend.rs:184-188).
     int iv = 0, nsp = 0, ngl = 0;
     model_version_features(m.version, iv, nsp, ngl);
@@ -299,7 +302,7 @@ int kg_handle_create(const kg_net* net, int device, int max_batch, int precision
     KGX_HIP(hipSetDevice(device));
     KGX_HIP(hipStreamCreateWithFlags(&h->stream, hipStreamNonBlocking));
     h->net = std::make_unique<kgx::Net>(m, device, max_batch, precision);
-    plan_static(h.get(), m);
+    h->model = net->model;
     KGX_HIP(hipHostMalloc((void**)&h->h_bin, (size_t)max_batch * h->nin * HW * 4, hipHostMallocDefault));
     KGX_HIP(hipHostMalloc((void**)&h->h_glob, (size_t)max_batch * h->nglob * 4, hipHostMallocDefault));
     if (h->nmeta) KGX_HIP(hipHostMalloc((void**)&h->h_meta, (size_t)max_batch * h->nmeta * 4, hipHostMallocDefault));
@@ -399,6 +402,8 @@ int kg_run_static(kg_handle* h, int n) {
     if (!h) throw std::runtime_error("null handle");
     std::lock_guard<std::mutex> lock(h->mu);
     const int mib = (int)(kgx::kStaticScratchBytes >> 20);
+    KGX_HIP(hipSetDevice(h->device));
+    if (h->static_batch < 0) plan_static(h, *h->model);
     if (!h->net_static)
       throw std::runtime_error("kgx backend: one row of this network needs more workspace than the static scratch (" +
                                std::to_string(mib) + " MiB)");
@@ -406,7 +411,6 @@ int kg_run_static(kg_handle* h, int n) {
       throw std::runtime_error("kgx backend: batch size " + std::to_string(n) + " out of range for the static scratch (" +
                                std::to_string(mib) + " MiB holds the workspace of at most " +
                                std::to_string(h->static_batch) + " rows of this network)");
-    KGX_HIP(hipSetDevice(h->device));
     h->net_static->forward_eager(padded_batch_size(h->buckets, n, h->static_batch), h->stream);
   });
 }

@@ -321,7 +321,7 @@ typedef IgCfg<1, 192, 48, 128, 4, 1, 2, 1, 2> Ig1k128;
 // Split-operand 1x1 (float-accurate): the same tiles with both operand planes staged, one workgroup per CU
 // (138.5 KB of LDS at 128 channels per stage; 154 KB for two 64-channel stage buffers).
 typedef IgCfg<1, 192, 48, 128, 4, 1, 2, 1, 2, false, true> Ig1k128s;
-typedef IgCfg<1, 192, 48, 64, 4, 1, 2, 2, 2, false, true> Ig1s;
+typedef IgCfg<1, 192, 96, 64, 4, 2, 1, 1, 2, false, true> Ig1s;
 
 enum { IG3_48, IG3_64, IG3_96, IG1_48, IG1_128, IG1_48S, IG1_128S };
 static int igemm_kind(int ks, int ic, int oc, bool split) {
@@ -373,6 +373,18 @@ static void igemm_dispatch(int kind, const void* x, const void* xlo, int ldx, in
 }
 
 thread_local LaunchTiming g_launch_timing;
+
+const char* conv_igemm_class(int ks, int ic, int oc, bool split) {
+  switch (igemm_kind(ks, ic, oc, split)) {
+    case IG3_48: return "conv3x3";
+    case IG3_64: return "conv3x3_n64";
+    case IG3_96: return "conv3x3_n96";
+    case IG1_128: return "conv1x1_k128";
+    case IG1_128S: return "conv1x1_split_k128";
+    case IG1_48S: return "conv1x1_split_n96";
+    default: return "conv1x1";
+  }
+}
 
 int conv_igemm_icp(int ks, int ic, int oc, bool split) {
   int bn, bk;

@@ -119,6 +119,9 @@ struct LaunchTiming {
 extern thread_local LaunchTiming g_launch_timing;
 
 int conv_igemm_icp(int ks, int ic, int oc, bool split = false);
+// The profiling class of the configuration a convolution of these channel counts runs with (one per kernel
+// instantiation: "conv3x3" is the 48-column 3x3 tile, "conv1x1_split_k128" the split 1x1 on 128-channel stages, ...).
+const char* conv_igemm_class(int ks, int ic, int oc, bool split = false);
 // w [oc][ic][ks][ks] -> [oc tile][tap][BN][icp] float; with `split` -> [oc tile][hi, lo][tap][BN][icp], the low
 // plane holding w - round(w) for the compute type `prec`.
 void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector<float>& out, bool split = false,

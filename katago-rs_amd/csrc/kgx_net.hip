@@ -274,7 +274,7 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
     op.launch = [=](hipStream_t s, int B) {
       launch_conv_igemm(prec, ks, xin, ldin, icin, dW, icp, oc, *out, B, s, x_lo);
     };
-    op.cls = k3 ? "conv3x3" : "conv1x1";
+    op.cls = conv_igemm_class(ks, icin, oc, split);
     op.flops_row = 2.0 * HW * ic * oc * taps;
     op.bytes_row = (double)HW * icin * ts * (split ? 2 : 1) + out_bytes;
     op.bytes_fixed = (double)taps * ic * oc * ts * (split ? 2 : 1);
