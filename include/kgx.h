@@ -161,6 +161,19 @@ typedef struct {
  * version). n must be in [1, max_batch]. */
 int kg_get_output(kg_handle* handle, int n, const kg_row_input* rows, kg_nn_output* outputs);
 
+/* get_output with the readback on a helper thread (backend.rs:598-605 and read_on_helper_thread,
+ * backend.rs:743-753): copy_inputs runs on the calling thread (the rows are read before the call returns), the
+ * uploads, the forward pass and one readback are enqueued, and the call returns; a helper OS thread then waits for
+ * the device, runs copy_outputs into `outputs` and calls done(user, status) when done is not NULL (status 0 on
+ * success). `outputs` (and their owner maps) must stay valid until then. `done` runs on the helper thread and must
+ * not call functions on this handle (they would wait for that same thread). The next call on the handle, kg_wait
+ * included, first waits for that thread; kg_wait also returns the helper's status, with its message in
+ * kg_last_error() on failure. When the call itself fails, nothing was enqueued and `done` is not called. */
+typedef void (*kg_done_fn)(void* user, int status);
+int kg_get_output_async(kg_handle* handle, int n, const kg_row_input* rows, kg_nn_output* outputs, kg_done_fn done,
+                        void* user);
+int kg_wait(kg_handle* handle);
+
 /* copy_outputs alone (backend.rs:622-731), on the host: n raw rows of P*362 + 3 + S + 361 floats (kg_forward /
  * kg_run output) to NNOutput fields, with each row's symmetry (0..7) and policy optimism. For callers that run
  * the forward pass with kg_run on device-filled inputs. S must be the model version's score channel count. */

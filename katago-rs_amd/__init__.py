@@ -36,7 +36,10 @@ EXPORTS = [
     "kg_handle_is_using_fp16", "kg_forward", "kg_handle_device_buffers", "kg_run", "kg_sync", "kg_handle_stream",
     "kg_get_output", "kg_profile_enable", "kg_profile_reset", "kg_profile_read",
     "kg_model_version_features", "kg_meta_encoder_channels", "kg_copy_outputs", "kg_run_static",
+    "kg_get_output_async", "kg_wait",
 ]
+# Completion callback of kg_get_output_async: (user, status).
+DONE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int)
 
 _lib = None
 
@@ -122,6 +125,8 @@ def lib():
         L.kg_run.argtypes = [vp, ci, vp]
         L.kg_sync.argtypes = [vp]
         L.kg_run_static.argtypes = [vp, ci]
+        L.kg_get_output_async.argtypes = [vp, ci, ctypes.POINTER(RowInput), ctypes.POINTER(NNOutput), DONE_FN, vp]
+        L.kg_wait.argtypes = [vp]
         L.kg_handle_stream.argtypes = [vp]
         L.kg_handle_stream.restype = vp
         L.kg_get_output.argtypes = [vp, ci, ctypes.POINTER(RowInput), ctypes.POINTER(NNOutput)]
@@ -315,9 +320,8 @@ class Handle:
     def stream(self) -> int:
         return lib().kg_handle_stream(self._h)
 
-    def get_output(self, rows, want_ownership=True):
-        """NeuralNet::get_output. rows: list of dicts with spatial [C,19,19], glob [G], meta [192] or None,
-        symmetry, policy_optimism. Returns a list of dicts of NNOutput fields."""
+    def _rows(self, rows, want_ownership):
+        """Row inputs and output structures of get_output; `keep` holds the arrays they point into."""
         n = len(rows)
         keep = []
         arr = (RowInput * n)()
@@ -343,8 +347,36 @@ class Handle:
             own = np.zeros(HW, np.float32) if want_ownership else None
             owners.append(own)
             outs[i].white_owner_map = None if own is None else _ptr(own).value
-        _check(lib().kg_get_output(self._h, n, arr, outs))
-        return [_output_dict(outs[i], owners[i]) for i in range(n)]
+        return arr, outs, owners, keep
+
+    def get_output(self, rows, want_ownership=True):
+        """NeuralNet::get_output. rows: list of dicts with spatial [C,19,19], glob [G], meta [192] or None,
+        symmetry, policy_optimism. Returns a list of dicts of NNOutput fields."""
+        arr, outs, owners, _keep = self._rows(rows, want_ownership)
+        _check(lib().kg_get_output(self._h, len(rows), arr, outs))
+        return [_output_dict(outs[i], owners[i]) for i in range(len(rows))]
+
+    def get_output_async(self, rows, want_ownership=True, done=None):
+        """get_output with the readback on the library's helper thread: returns once the batch is enqueued.
+        `done(status)`, if given, is called from that thread. Returns a pending result whose wait() joins it
+        (kg_wait) and gives the list of dicts of NNOutput fields."""
+        arr, outs, owners, keep = self._rows(rows, want_ownership)
+        cb = DONE_FN((lambda user, status: done(status)) if done else (lambda user, status: None))
+        _check(lib().kg_get_output_async(self._h, len(rows), arr, outs, cb, None))
+        handle = self
+
+        class Pending:
+            def wait(self_inner):
+                _check(lib().kg_wait(handle._h))
+                self_inner._keep = (arr, keep, cb)
+                return [_output_dict(outs[i], owners[i]) for i in range(len(owners))]
+
+        p = Pending()
+        p._keep = (arr, outs, owners, keep, cb)  # alive until the helper thread has written the outputs
+        return p
+
+    def wait(self):
+        _check(lib().kg_wait(self._h))
 
     # --- kernel timing ---
     def profile(self, enable: bool):

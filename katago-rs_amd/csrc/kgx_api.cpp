@@ -10,6 +10,7 @@
 #include <mutex>
 #include <stdexcept>
 #include <string>
+#include <thread>
 #include <vector>
 
 #include "kgx_model.h"
@@ -38,6 +39,10 @@ struct kg_handle {
   float* h_glob = nullptr;
   float* h_meta = nullptr;
   float* h_out = nullptr;
+  // The readback of kg_get_output_async runs on this helper thread; the next call on the handle joins it first.
+  std::thread helper;
+  int helper_status = 0;
+  std::string helper_error;
   std::mutex mu;
 };
 
@@ -202,6 +207,30 @@ void run_and_read(kg_handle* h, int n_run, int n, float* out) {
   if (out) std::memcpy(out, h->h_out, bytes);
 }
 
+// Joins the helper thread of a previous kg_get_output_async (its outputs must be complete before the handle's
+// buffers are reused). Caller holds h->mu.
+int settle(kg_handle* h) {
+  if (h->helper.joinable()) h->helper.join();
+  return h->helper_status;
+}
+
+// copy_inputs (backend.rs:497-546): rows to the pinned staging buffers, with each row's symmetry.
+void copy_inputs(kg_handle* h, int n, const kg_row_input* rows) {
+  for (int r = 0; r < n; r++) {
+    const kg_row_input& in = rows[r];
+    if (in.symmetry < 0 || in.symmetry > 7) throw std::runtime_error("kgx backend: symmetry must be in [0, 8)");
+    if (!in.row_spatial || (h->nglob && !in.row_global)) throw std::runtime_error("kgx backend: null input row");
+    std::memcpy(h->h_glob + (size_t)r * h->nglob, in.row_global, (size_t)h->nglob * 4);
+    if (h->nmeta) {
+      if (!in.row_meta) throw std::runtime_error("kgx backend: the network needs a meta row");
+      std::memcpy(h->h_meta + (size_t)r * h->nmeta, in.row_meta, (size_t)h->nmeta * 4);
+    } else if (in.row_meta) {
+      throw std::runtime_error("kgx backend: the network takes no meta row");
+    }
+    copy_with_symmetry(in.row_spatial, h->h_bin + (size_t)r * h->nin * HW, h->nin, POS, POS, in.symmetry, false);
+  }
+}
+
 void upload_rows(kg_handle* h, int n) {
   KGX_HIP(hipMemcpyAsync(h->net->d_bin(), h->h_bin, (size_t)n * h->nin * HW * 4, hipMemcpyHostToDevice, h->stream));
   KGX_HIP(hipMemcpyAsync(h->net->d_global(), h->h_glob, (size_t)n * h->nglob * 4, hipMemcpyHostToDevice, h->stream));
@@ -316,6 +345,10 @@ int kg_handle_create(const kg_net* net, int device, int max_batch, int precision
 
 void kg_handle_free(kg_handle* h) {
   if (!h) return;
+  {
+    std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
+  }
   (void)hipSetDevice(h->device);
   if (h->stream) (void)hipStreamSynchronize(h->stream);
   h->net.reset();
@@ -332,6 +365,7 @@ int kg_handle_set_batch_buckets(kg_handle* h, const int* buckets, int count) {
     if (!h) throw std::runtime_error("null handle");
     if (count > 0 && !buckets) throw std::runtime_error("null buckets");
     std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
     h->buckets.clear();
     for (int k = 0; k < count; k++)
       if (buckets[k] > 0) h->buckets.push_back(buckets[k]);
@@ -361,6 +395,7 @@ int kg_forward(kg_handle* h, int n, const float* bin, const float* global, const
     if (!h) throw std::runtime_error("null handle");
     if (!bin || (h->nglob && !global) || !out) throw std::runtime_error("kgx backend: null input or output buffer");
     std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
     if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
     if (h->nmeta && !meta) throw std::runtime_error("kgx backend: the network needs a meta_input");
     if (!h->nmeta && meta) throw std::runtime_error("kgx backend: the network takes no meta_input");
@@ -378,6 +413,7 @@ int kg_handle_device_buffers(kg_handle* h, float** bin, float** global, float** 
   return guarded([&] {
     if (!h) throw std::runtime_error("null handle");
     std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
     if (bin) *bin = h->net->d_bin();
     if (global) *global = h->net->d_global();
     if (meta) *meta = h->net->d_meta();
@@ -389,6 +425,7 @@ int kg_run(kg_handle* h, int n, float* out) {
   return guarded([&] {
     if (!h) throw std::runtime_error("null handle");
     std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
     if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
     KGX_HIP(hipSetDevice(h->device));
     const int n_run = padded_batch_size(h->buckets, n, h->max_batch);
@@ -401,6 +438,7 @@ int kg_run_static(kg_handle* h, int n) {
   return guarded([&] {
     if (!h) throw std::runtime_error("null handle");
     std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
     const int mib = (int)(kgx::kStaticScratchBytes >> 20);
     KGX_HIP(hipSetDevice(h->device));
     if (h->static_batch < 0) plan_static(h, *h->model);
@@ -418,6 +456,10 @@ int kg_run_static(kg_handle* h, int n) {
 int kg_sync(kg_handle* h) {
   return guarded([&] {
     if (!h) throw std::runtime_error("null handle");
+    {
+      std::lock_guard<std::mutex> lock(h->mu);
+      settle(h);
+    }
     KGX_HIP(hipStreamSynchronize(h->stream));
   });
 }
@@ -429,20 +471,9 @@ int kg_get_output(kg_handle* h, int n, const kg_row_input* rows, kg_nn_output* o
     if (!h) throw std::runtime_error("null handle");
     if (!rows || !outputs) throw std::runtime_error("null rows or outputs");
     std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
     if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
-    // copy_inputs (backend.rs:497-546).
-    for (int r = 0; r < n; r++) {
-      const kg_row_input& in = rows[r];
-      if (in.symmetry < 0 || in.symmetry > 7) throw std::runtime_error("kgx backend: symmetry must be in [0, 8)");
-      std::memcpy(h->h_glob + (size_t)r * h->nglob, in.row_global, (size_t)h->nglob * 4);
-      if (h->nmeta) {
-        if (!in.row_meta) throw std::runtime_error("kgx backend: the network needs a meta row");
-        std::memcpy(h->h_meta + (size_t)r * h->nmeta, in.row_meta, (size_t)h->nmeta * 4);
-      } else if (in.row_meta) {
-        throw std::runtime_error("kgx backend: the network takes no meta row");
-      }
-      copy_with_symmetry(in.row_spatial, h->h_bin + (size_t)r * h->nin * HW, h->nin, POS, POS, in.symmetry, false);
-    }
+    copy_inputs(h, n, rows);
     // run_network (backend.rs:549-619).
     KGX_HIP(hipSetDevice(h->device));
     const int n_run = padded_batch_size(h->buckets, n, h->max_batch);
@@ -453,6 +484,62 @@ int kg_get_output(kg_handle* h, int n, const kg_row_input* rows, kg_nn_output* o
     for (int r = 0; r < n; r++)
       copy_outputs_row(h->h_out + (size_t)r * rl, h->P, h->S, h->model_version, rows[r].symmetry,
                        rows[r].policy_optimism, outputs[r]);
+  });
+}
+
+int kg_get_output_async(kg_handle* h, int n, const kg_row_input* rows, kg_nn_output* outputs, kg_done_fn done,
+                        void* user) {
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    if (!rows || !outputs) throw std::runtime_error("null rows or outputs");
+    std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
+    if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
+    // copy_inputs on the calling thread (the inputs are read before the call returns), then the whole batch is
+    // enqueued: uploads, the forward pass, one readback into the pinned output rows.
+    copy_inputs(h, n, rows);
+    std::vector<int> sym(n);
+    std::vector<float> opt(n);
+    for (int r = 0; r < n; r++) {
+      sym[r] = rows[r].symmetry;
+      opt[r] = rows[r].policy_optimism;
+    }
+    KGX_HIP(hipSetDevice(h->device));
+    const int n_run = padded_batch_size(h->buckets, n, h->max_batch);
+    upload_rows(h, n);
+    h->net->forward(n_run, h->stream);
+    KGX_HIP(hipMemcpyAsync(h->h_out, h->net->d_out(), (size_t)n * h->net->row_len() * sizeof(float),
+                           hipMemcpyDeviceToHost, h->stream));
+    // read_on_helper_thread (backend.rs:743-753): a fresh OS thread waits for the device and runs copy_outputs.
+    h->helper_status = 0;
+    h->helper_error.clear();
+    h->helper = std::thread([h, n, outputs, done, user, sym = std::move(sym), opt = std::move(opt)] {
+      int st = 0;
+      try {
+        KGX_HIP(hipSetDevice(h->device));
+        KGX_HIP(hipStreamSynchronize(h->stream));
+        const int rl = h->net->row_len();
+        for (int r = 0; r < n; r++)
+          copy_outputs_row(h->h_out + (size_t)r * rl, h->P, h->S, h->model_version, sym[r], opt[r], outputs[r]);
+      } catch (const std::exception& e) {
+        st = 1;
+        h->helper_error = std::string("kgx backend: readback failed: ") + e.what();
+      }
+      h->helper_status = st;
+      if (done) done(user, st);
+    });
+  });
+}
+
+int kg_wait(kg_handle* h) {
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    std::lock_guard<std::mutex> lock(h->mu);
+    if (settle(h) != 0) {
+      const std::string msg = h->helper_error;
+      h->helper_status = 0;
+      throw std::runtime_error(msg);
+    }
   });
 }
 
@@ -495,6 +582,7 @@ int kg_profile_enable(kg_handle* h, int enable) {
   return guarded([&] {
     if (!h) throw std::runtime_error("null handle");
     std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
     h->net->set_profiling(enable != 0);
   });
 }
@@ -503,6 +591,7 @@ int kg_profile_reset(kg_handle* h) {
   return guarded([&] {
     if (!h) throw std::runtime_error("null handle");
     std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
     h->net->reset_profile();
   });
 }

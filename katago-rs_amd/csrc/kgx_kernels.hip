@@ -578,79 +578,114 @@ __global__ __launch_bounds__(256) void rmsnorm_tok_kernel(const float* __restric
   for (int c = lane; c < C; c += 64) o[c] = to_t<T>(xr[c] * rs * w[c] * mk);
 }
 
-// Vector form: each lane holds eight consecutive channels per 512-channel chunk of RPW rows, so a row is read
-// once with 16-byte loads (a wave reads 2 KB contiguous per chunk), the loads of all RPW rows are in flight before
-// the first reduction, and the outputs go out as 16-byte (8 x 16-bit) or 2 x 16-byte (float) stores.
-constexpr int RMS_RPW = 2;
-
-template <typename T, int CH>
-__global__ __launch_bounds__(256) void rmsnorm_tok8_kernel(const float* __restrict__ x, int ldx, int C,
-                                                           const float* __restrict__ w, float eps,
-                                                           const float* __restrict__ mask, T* __restrict__ out,
-                                                           int ldo, int rows) {
-  const int lane = threadIdx.x & 63, row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * RMS_RPW;
-  floatx4 v[RMS_RPW][CH][2];
+// Vector form: a row is spread over LPR lanes (a power of two with C = 8 NV LPR, so no lane idles: C = 384 takes
+// 16 lanes of 24 channels, 512 takes 64 lanes of 8), each lane holding NV vectors of eight consecutive channels
+// (vector j of lane l covers channels 8 (j LPR + l), so a row's lanes read 32 LPR contiguous bytes per vector). A
+// wave covers 64 / LPR rows per pass and PASSES passes; every load of x and of the gains is issued before the first
+// reduction, which runs over the LPR lanes of the row (log2 LPR shuffles).
+template <typename T, int NV, int LPR>
+__global__ __launch_bounds__(256) void rmsnorm_lanes_kernel(const float* __restrict__ x, int ldx, int C,
+                                                            const float* __restrict__ w, float eps,
+                                                            const float* __restrict__ mask, T* __restrict__ out,
+                                                            int ldo, int rows) {
+  // Two passes (row groups per lane group) when a pass covers at most two rows of a wave, else one: two to four rows
+  // per wave (C = 512 at 64 lanes per row is slower at four rows per wave than at two).
+  constexpr int lpr = LPR, rg = 64 / LPR, PASSES = rg <= 2 ? 2 : 1;
+  const int lane = threadIdx.x & 63, g = lane / lpr, l = lane - g * lpr;
+  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * rg * PASSES + g;
+  floatx4 v[PASSES][NV][2], wv[NV][2];
 #pragma unroll
-  for (int r = 0; r < RMS_RPW; r++) {
-    const int row = min(row0 + r, rows - 1);
+  for (int p = 0; p < PASSES; p++) {
+    const float* xr = x + (size_t)min(row0 + p * rg, rows - 1) * ldx;
 #pragma unroll
-    for (int ch = 0; ch < CH; ch++) {
-      const int c = ch * 512 + lane * 8;
-      v[r][ch][0] = v[r][ch][1] = floatx4{0.f, 0.f, 0.f, 0.f};
-      if (c < C) {
-        const float* xp = x + (size_t)row * ldx + c;
-        v[r][ch][0] = *(const floatx4*)xp;
-        v[r][ch][1] = *(const floatx4*)(xp + 4);
-      }
+    for (int j = 0; j < NV; j++) {
+      const int c = (j * lpr + l) * 8;
+      v[p][j][0] = *(const floatx4*)(xr + c);
+      v[p][j][1] = *(const floatx4*)(xr + c + 4);
     }
   }
 #pragma unroll
-  for (int r = 0; r < RMS_RPW; r++) {
-    const int row = row0 + r;
+  for (int j = 0; j < NV; j++) {
+    const int c = (j * lpr + l) * 8;
+    wv[j][0] = *(const floatx4*)(w + c);
+    wv[j][1] = *(const floatx4*)(w + c + 4);
+  }
+#pragma unroll
+  for (int p = 0; p < PASSES; p++) {
+    const int row = row0 + p * rg;
     float ss = 0.f;
 #pragma unroll
-    for (int ch = 0; ch < CH; ch++)
+    for (int j = 0; j < NV; j++)
 #pragma unroll
       for (int h = 0; h < 2; h++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) ss += v[r][ch][h][e] * v[r][ch][h][e];
+        for (int e = 0; e < 4; e++) ss += v[p][j][h][e] * v[p][j][h][e];
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+    for (int off = lpr >> 1; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
     if (row >= rows) continue;
     const float rs = 1.f / sqrtf(ss / (float)C + eps), mk = mask[row];
+    T* op = out + (size_t)row * ldo;
 #pragma unroll
-    for (int ch = 0; ch < CH; ch++) {
-      const int c = ch * 512 + lane * 8;
-      if (c < C) {
-        const floatx4 w0 = *(const floatx4*)(w + c), w1 = *(const floatx4*)(w + c + 4);
-        const floatx4 a = v[r][ch][0] * rs * w0 * mk, b = v[r][ch][1] * rs * w1 * mk;
-        T* op = out + (size_t)row * ldo + c;
-        store4<T>(op, a[0], a[1], a[2], a[3]);
-        store4<T>(op + 4, b[0], b[1], b[2], b[3]);
-      }
+    for (int j = 0; j < NV; j++) {
+      const int c = (j * lpr + l) * 8;
+      const floatx4 a = v[p][j][0] * rs * wv[j][0] * mk, b = v[p][j][1] * rs * wv[j][1] * mk;
+      store4<T>(op + c, a[0], a[1], a[2], a[3]);
+      store4<T>(op + c + 4, b[0], b[1], b[2], b[3]);
     }
   }
 }
 
+template <typename T, int NV, int LPR>
+static void rmsnorm_lanes(const float* x, int ldx, int C, const float* w, float eps, const float* mask, T* out, int ldo,
+                          int rows, hipStream_t s) {
+  constexpr int rg = 64 / LPR, per_wg = 4 * rg * (rg <= 2 ? 2 : 1);
+  rmsnorm_lanes_kernel<T, NV, LPR><<<(rows + per_wg - 1) / per_wg, 256, 0, s>>>(x, ldx, C, w, eps, mask, out, ldo, rows);
+}
+
+template <typename T, int LPR>
+static bool rmsnorm_nv(int nv, const float* x, int ldx, int C, const float* w, float eps, const float* mask, T* out,
+                       int ldo, int rows, hipStream_t s) {
+  switch (nv) {
+    case 1: rmsnorm_lanes<T, 1, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s); return true;
+    case 2: rmsnorm_lanes<T, 2, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s); return true;
+    case 3: rmsnorm_lanes<T, 3, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s); return true;
+    case 4: rmsnorm_lanes<T, 4, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s); return true;
+    default: return false;
+  }
+}
+
+// The lane layout of a row of C channels: LPR = the largest power of two up to 64 dividing C / 8, NV = C / (8 LPR);
+// layouts with more than four vectors per lane take the scalar kernel.
 template <typename T>
-static void rmsnorm_tok8(const float* x, int ldx, int C, const float* w, float eps, const float* mask, T* out, int ldo,
-                         int rows, hipStream_t s) {
-  dim3 grid((rows + 4 * RMS_RPW - 1) / (4 * RMS_RPW));
-  if (C <= 512) rmsnorm_tok8_kernel<T, 1><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, out, ldo, rows);
-  else if (C <= 1024) rmsnorm_tok8_kernel<T, 2><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, out, ldo, rows);
-  else rmsnorm_tok8_kernel<T, 4><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, out, ldo, rows);
+static bool rmsnorm_vec(const float* x, int ldx, int C, const float* w, float eps, const float* mask, T* out, int ldo,
+                        int rows, hipStream_t s) {
+  const int v8 = C / 8;
+  int lpr = 64;
+  while (lpr > 4 && v8 % lpr) lpr >>= 1;
+  if (v8 % lpr) return false;
+  const int nv = v8 / lpr;
+  switch (lpr) {
+    case 64: return rmsnorm_nv<T, 64>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s);
+    case 32: return rmsnorm_nv<T, 32>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s);
+    case 16: return rmsnorm_nv<T, 16>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s);
+    case 8: return rmsnorm_nv<T, 8>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s);
+    default: return rmsnorm_nv<T, 4>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s);
+  }
 }
 
 void launch_rmsnorm_tok(int prec, const float* x, int ldx, int C, const float* w, float eps, const float* mask,
                         void* out, int ldo, int rows, hipStream_t s) {
   const int tsz = prec == PREC_F32 ? 4 : 2;
-  if (rows > 0 && C % 8 == 0 && C <= 2048 && ldx % 4 == 0 && ldo % (16 / tsz) == 0 &&
+  if (rows > 0 && C % 8 == 0 && ldx % 4 == 0 && ldo % (16 / tsz) == 0 &&
       ((uintptr_t)x | (uintptr_t)w) % 16 == 0 && (uintptr_t)out % 16 == 0) {
-    if (prec == PREC_F16) rmsnorm_tok8<f16>(x, ldx, C, w, eps, mask, (f16*)out, ldo, rows, s);
-    else if (prec == PREC_BF16) rmsnorm_tok8<bf16>(x, ldx, C, w, eps, mask, (bf16*)out, ldo, rows, s);
-    else rmsnorm_tok8<float>(x, ldx, C, w, eps, mask, (float*)out, ldo, rows, s);
-    KGX_CHECK_LAUNCH();
-    return;
+    bool done;
+    if (prec == PREC_F16) done = rmsnorm_vec<f16>(x, ldx, C, w, eps, mask, (f16*)out, ldo, rows, s);
+    else if (prec == PREC_BF16) done = rmsnorm_vec<bf16>(x, ldx, C, w, eps, mask, (bf16*)out, ldo, rows, s);
+    else done = rmsnorm_vec<float>(x, ldx, C, w, eps, mask, (float*)out, ldo, rows, s);
+    if (done) {
+      KGX_CHECK_LAUNCH();
+      return;
+    }
   }
   dim3 grid((rows + 3) / 4);
   if (prec == PREC_F16) rmsnorm_tok_kernel<f16><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, (f16*)out, ldo, rows);

@@ -212,7 +212,7 @@ def test_graph_replays_are_deterministic(kgx, synth):
     h.close()
 
 
-def test_handles_in_flight_match_sequential(kgx, synth):
+def test_handles_in_flight_match_sequential(kgx, synth, oracle):
     """Several handles of one net, each driven by its own thread (the reference's serve tasks in flight,
     backend.rs:598-605): every handle's outputs equal the same handle's outputs run alone."""
     import threading
@@ -237,8 +237,48 @@ def test_handles_in_flight_match_sequential(kgx, synth):
         assert len(got[i]) == 20
         for out in got[i]:
             assert np.array_equal(out, alone[i]), i
+    # and what each handle returns is the network's output (the oracle, at the f16 tier).
+    mb = synth.write_model(arch, 4)
+    for i, (sp, gl, _) in enumerate(inputs):
+        check(alone[i], oracle.Model(mb).forward(sp, gl), net.P, net.S, "f16", f"in flight {i}",
+              emulated(oracle, mb, "f16", sp, gl))
     for h in hs:
         h.close()
+
+
+def test_get_output_async_reads_back_on_a_helper_thread(kgx, synth, oracle):
+    """kg_get_output_async (read_on_helper_thread, backend.rs:743-753): the call returns with the batch enqueued,
+    a helper thread runs copy_outputs and calls back; the result equals kg_get_output's and the oracle's
+    copy_outputs of the raw rows; a second call on the handle waits for the first."""
+    import threading
+    arch = synth.tiny_nets()["t_rms"]  # P = 4, model version 17
+    net = kgx.Net(synth.write_model(arch, 8))
+    h = kgx.Handle(net, 8, "f32")
+    sp, gl, _ = synth.make_inputs(8, 5, board_sizes=[19, 13, 9])
+    rows = [{"spatial": sp[i], "glob": gl[i], "symmetry": (3 * i) % 8, "policy_optimism": 0.5 * (i % 3)}
+            for i in range(8)]
+    calls = []
+    p1 = h.get_output_async(rows, done=lambda st: calls.append((st, threading.get_ident())))
+    p2 = h.get_output_async(rows[:3])  # joins the first call's helper before reusing the buffers
+    res2 = p2.wait()
+    res1 = p1.wait()
+    assert len(calls) == 1 and calls[0][0] == 0 and calls[0][1] != threading.get_ident()
+    sync = h.get_output(rows)
+    raw = h.forward(np.stack([oracle.copy_with_symmetry(sp[i:i + 1], rows[i]["symmetry"])[0] for i in range(8)]), gl)
+    for i in range(8):
+        pol, fields, own = oracle.copy_outputs_row(raw[i], net.P, net.S, net.version, rows[i]["symmetry"],
+                                                   rows[i]["policy_optimism"])
+        for res in (res1, sync) + ((res2,) if i < 3 else ()):
+            assert np.array_equal(res[i]["policy"], pol), i
+            assert np.array_equal(res[i]["ownership"], own), i
+            got = np.array([res[i][k] for k in ("white_win_prob", "white_loss_prob", "white_no_result_prob",
+                                                "white_score_mean", "white_score_mean_sq", "white_lead",
+                                                "var_time_left", "shortterm_winloss_error",
+                                                "shortterm_score_error")], np.float32)
+            assert np.array_equal(got, fields), i
+    with pytest.raises(kgx.KgError, match="symmetry"):
+        h.get_output_async([dict(rows[0], symmetry=9)])
+    h.close()
 
 
 def test_get_output_applies_symmetry_and_optimism(kgx, synth, oracle):

@@ -202,6 +202,9 @@ def test_handle_entry_points_reject_a_null_handle(kgx):
         "kg_handle_set_batch_buckets": lambda: L.kg_handle_set_batch_buckets(None, None, 0),
         "kg_handle_device_buffers": lambda: L.kg_handle_device_buffers(None, kgx.ctypes.byref(p), None, None, None),
         "kg_get_output": lambda: L.kg_get_output(None, 1, None, None),
+        "kg_get_output_async": lambda: L.kg_get_output_async(None, 1, None, None, kgx.DONE_FN(0), None),
+        "kg_wait": lambda: L.kg_wait(None),
+        "kg_run_static": lambda: L.kg_run_static(None, 1),
     }
     for name, call in calls.items():
         assert call() != 0, name
