@@ -138,8 +138,8 @@ __global__ __launch_bounds__(256) void wino_in_kernel(const void* __restrict__ x
 template <typename T, int TM>
 static void wino_in_t(const void* x, int ldx, bool nchw_f32, T* V, int B, int C, int c_pad, hipStream_t s) {
   dim3 block(64, 4), grid((c_pad + 63) / 64, B * Band<TM>::NB);
-  if (nchw_f32) wino_in_kernel<T, TM, true><<<grid, block, 0, s>>>(x, ldx, V, B, C, c_pad);
-  else wino_in_kernel<T, TM, false><<<grid, block, 0, s>>>(x, ldx, V, B, C, c_pad);
+  if (nchw_f32) launch_k(wino_in_kernel<T, TM, true>, grid, block, 0, s, x, ldx, V, B, C, c_pad);
+  else launch_k(wino_in_kernel<T, TM, false>, grid, block, 0, s, x, ldx, V, B, C, c_pad);
 }
 
 void launch_wino_in(int prec, int tm, const void* x, int ldx, bool nchw_f32, void* V, int B, int C, int c_pad,
@@ -199,8 +199,8 @@ __global__ __launch_bounds__(256) void wino_out_kernel(const float* __restrict__
 void launch_wino_out(int prec, int tm, const float* M, int oc_pad, int OC, const ConvOut& o, int B, hipStream_t s) {
   dim3 block(64, 4), grid((OC + 63) / 64, (B * wino_tiles(tm) + 3) / 4);
 #define KGX_WO(T) \
-  if (tm == 4) wino_out_kernel<T, 4><<<grid, block, 0, s>>>(M, oc_pad, OC, o, B); \
-  else wino_out_kernel<T, 2><<<grid, block, 0, s>>>(M, oc_pad, OC, o, B);
+  if (tm == 4) launch_k(wino_out_kernel<T, 4>, grid, block, 0, s, M, oc_pad, OC, o, B); \
+  else launch_k(wino_out_kernel<T, 2>, grid, block, 0, s, M, oc_pad, OC, o, B);
   if (prec == PREC_F16) { KGX_WO(f16) }
   else if (prec == PREC_BF16) { KGX_WO(bf16) }
   else { KGX_WO(float) }
@@ -383,7 +383,7 @@ static void wino2_fused_t(const void* V, const void* U, int t_pad, int icp, int 
                           hipStream_t s) {
   constexpr int TB = 32;
   dim3 grid(ocp / 64, t_pad / TB);
-  wino2_fused_kernel<T, TB, BKH><<<grid, 256, 0, s>>>((const T*)V, (const T*)U, t_pad, icp, ocp, OC, o, B);
+  launch_k(wino2_fused_kernel<T, TB, BKH>, grid, 256, 0, s, (const T*)V, (const T*)U, t_pad, icp, ocp, OC, o, B);
 }
 
 template <typename T>
@@ -440,8 +440,8 @@ void launch_conv_direct(int prec, const void* x, int ldx, bool nchw_f32, int IC,
                         int dy, int dx, const ConvOut& o, int B, hipStream_t s) {
   dim3 grid((OC + 63) / 64, HW, B);
 #define KGX_CD(T)                                                                                   \
-  if (nchw_f32) conv_direct_kernel<T, true><<<grid, 64, 0, s>>>(x, ldx, IC, w, OC, ky, kx, dy, dx, o); \
-  else conv_direct_kernel<T, false><<<grid, 64, 0, s>>>(x, ldx, IC, w, OC, ky, kx, dy, dx, o);
+  if (nchw_f32) launch_k(conv_direct_kernel<T, true>, grid, 64, 0, s, x, ldx, IC, w, OC, ky, kx, dy, dx, o); \
+  else launch_k(conv_direct_kernel<T, false>, grid, 64, 0, s, x, ldx, IC, w, OC, ky, kx, dy, dx, o);
   if (prec == PREC_F16) { KGX_CD(f16) }
   else if (prec == PREC_BF16) { KGX_CD(bf16) }
   else { KGX_CD(float) }
@@ -505,10 +505,10 @@ static void bias_act8_launch(const float* x, int ldx, int C, const float* prebia
   const long n = (long)rows * (C / 8);
   const dim3 grid((unsigned)((n + 255) / 256));
   switch (act) {
-    case ACT_RELU: bias_act8_kernel<T, ACT_RELU><<<grid, 256, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
-    case ACT_MISH: bias_act8_kernel<T, ACT_MISH><<<grid, 256, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
-    case ACT_SILU: bias_act8_kernel<T, ACT_SILU><<<grid, 256, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
-    default: bias_act8_kernel<T, ACT_ID><<<grid, 256, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
+    case ACT_RELU: launch_k(bias_act8_kernel<T, ACT_RELU>, grid, 256, 0, s, x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
+    case ACT_MISH: launch_k(bias_act8_kernel<T, ACT_MISH>, grid, 256, 0, s, x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
+    case ACT_SILU: launch_k(bias_act8_kernel<T, ACT_SILU>, grid, 256, 0, s, x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
+    default: launch_k(bias_act8_kernel<T, ACT_ID>, grid, 256, 0, s, x, ldx, C, prebias, ld_prebias, scale, bias, mask, out, ldo, rows); break;
   }
 }
 
@@ -525,7 +525,7 @@ void launch_fill_zero(void* p, size_t bytes, hipStream_t s) {
   const size_t n16 = bytes / 16;
   const int ntail = (int)((bytes % 16) / 4);
   const int blocks = (int)std::min<size_t>(1024, std::max<size_t>(1, (n16 + 255) / 256));
-  fill_zero_kernel<<<blocks, 256, 0, s>>>((u32x4*)p, n16, (unsigned*)((char*)p + n16 * 16), ntail);
+  launch_k(fill_zero_kernel, blocks, 256, 0, s, (u32x4*)p, n16, (unsigned*)((char*)p + n16 * 16), ntail);
   KGX_CHECK_LAUNCH();
 }
 
@@ -545,11 +545,11 @@ void launch_bias_act(int prec, const float* x, int ldx, int C, const float* preb
   }
   dim3 block(64, 4), grid((C + 63) / 64, (rows + 3) / 4);
   if (prec == PREC_F16)
-    bias_act_kernel<f16><<<grid, block, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, act, mask, (f16*)out, ldo, rows);
+    launch_k(bias_act_kernel<f16>, grid, block, 0, s, x, ldx, C, prebias, ld_prebias, scale, bias, act, mask, (f16*)out, ldo, rows);
   else if (prec == PREC_BF16)
-    bias_act_kernel<bf16><<<grid, block, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, act, mask, (bf16*)out, ldo, rows);
+    launch_k(bias_act_kernel<bf16>, grid, block, 0, s, x, ldx, C, prebias, ld_prebias, scale, bias, act, mask, (bf16*)out, ldo, rows);
   else
-    bias_act_kernel<float><<<grid, block, 0, s>>>(x, ldx, C, prebias, ld_prebias, scale, bias, act, mask, (float*)out, ldo, rows);
+    launch_k(bias_act_kernel<float>, grid, block, 0, s, x, ldx, C, prebias, ld_prebias, scale, bias, act, mask, (float*)out, ldo, rows);
   KGX_CHECK_LAUNCH();
 }
 

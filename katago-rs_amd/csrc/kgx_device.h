@@ -1,6 +1,7 @@
 // Device-side helpers shared by the kernel translation units.
 #pragma once
 #include <hip/hip_runtime.h>
+#include <hip/hip_ext.h>
 
 #include <cfloat>
 #include <stdexcept>
@@ -23,6 +24,22 @@ typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));  // 16-byte stag
     hipError_t e_ = hipGetLastError();                                                                        \
     if (e_ != hipSuccess) throw std::runtime_error(std::string("kernel launch: ") + hipGetErrorString(e_)); \
   } while (0)
+
+// Launches kernel k like k<<<grid, block, lds, s>>>(args...). While a profiled forward times its ops
+// (g_launch_timing set), the launch goes through hipExtLaunchKernel, whose dispatch records the events around the
+// kernel itself: the first kernel of an op records `start`, every kernel records `stop`, so an op's time spans its
+// kernels and excludes the host-side launch latency in front of them.
+template <typename... KArgs, typename... Args>
+inline void launch_k(void (*k)(KArgs...), dim3 grid, dim3 block, size_t lds, hipStream_t s, Args... args) {
+  LaunchTiming& t = g_launch_timing;
+  if (t.start) {
+    hipExtLaunchKernelGGL(k, grid, block, (std::uint32_t)lds, s, t.used ? nullptr : t.start, t.stop, 0u,
+                          static_cast<KArgs>(args)...);
+    t.used = true;
+  } else {
+    k<<<grid, block, lds, s>>>(static_cast<KArgs>(args)...);
+  }
+}
 
 template <int ACT>
 __device__ __forceinline__ float act_f(float a) {

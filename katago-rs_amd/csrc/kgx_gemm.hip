@@ -491,13 +491,13 @@ static void gemm_launch(const GemmArgs& g, hipStream_t s) {
     throw std::runtime_error("gemm: the q|k|v epilogue needs the column tile to hold whole heads");
   dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM, g.Z);
   switch (epi) {
-    case EPI_SCALAR: gemm_kernel<T, C, AF, PRO, ACT, EPI_SCALAR><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
-    case EPI_YT: gemm_kernel<T, C, AF, PRO, ACT, EPI_YT><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
-    case EPI_ACC: gemm_kernel<T, C, AF, PRO, ACT, EPI_ACC><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
-    case EPI_GLU: gemm_kernel<T, C, AF, PRO, ACT, EPI_GLU><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
-    case EPI_QKV: gemm_kernel<T, C, AF, PRO, ACT, EPI_QKV><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
-    case EPI_YTMISH: gemm_kernel<T, C, AF, PRO, ACT, EPI_YTMISH><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
-    default: gemm_kernel<T, C, AF, PRO, ACT, EPI_GEN><<<grid, C::WM * C::WN * 64, 0, s>>>(g); break;
+    case EPI_SCALAR: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_SCALAR>, grid, C::WM * C::WN * 64, 0, s, g); break;
+    case EPI_YT: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_YT>, grid, C::WM * C::WN * 64, 0, s, g); break;
+    case EPI_ACC: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_ACC>, grid, C::WM * C::WN * 64, 0, s, g); break;
+    case EPI_GLU: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_GLU>, grid, C::WM * C::WN * 64, 0, s, g); break;
+    case EPI_QKV: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_QKV>, grid, C::WM * C::WN * 64, 0, s, g); break;
+    case EPI_YTMISH: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_YTMISH>, grid, C::WM * C::WN * 64, 0, s, g); break;
+    default: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_GEN>, grid, C::WM * C::WN * 64, 0, s, g); break;
   }
 }
 

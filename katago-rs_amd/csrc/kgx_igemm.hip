@@ -16,7 +16,6 @@
 // consecutive channels of one pixel with 16-byte loads and stores (conv_store4).
 #include "kgx_device.h"
 
-#include <hip/hip_ext.h>
 #include <cstring>
 #include <vector>
 
@@ -212,7 +211,7 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   // after the loop); the wider 3x3 tiles and the 1x1 kernel read those after (read early they spill: the 1x1 is
   // held to 128 registers for two workgroups per CU).
   constexpr int G4 = BN / 4, RPE = NT / G4, EV = (BM + RPE - 1) / RPE;
-  constexpr bool YEARLY = C::KS == 3;
+  constexpr bool YEARLY = C::KS == 3 || (C::SPLIT && C::BK == 64);
   constexpr bool SEARLY = YEARLY && C::BN <= 48;  // wider column tiles would spill with these registers live
   const int ec4 = tid % G4, er0 = tid / G4, en = n0 + 4 * ec4;
   const bool eon = er0 < RPE && en < OC;
@@ -349,13 +348,7 @@ static void igemm_launch(const void* x, const void* xlo, int ldx, int IC, const 
   if (icp % C::BK != 0) throw std::runtime_error("conv_igemm: padded input channels must be a multiple of the stage");
   const int mtiles = (M + C::BM - 1) / C::BM, ntiles = (OC + C::BN - 1) / C::BN;
   dim3 grid(round_up(mtiles, 8) * ntiles);
-  if (g_launch_timing.start) {
-    hipExtLaunchKernelGGL(igemm_kernel<T, C>, grid, dim3(C::NT), 0, s, g_launch_timing.start, g_launch_timing.stop,
-                          0, (const T*)x, (const T*)xlo, ldx, IC, (const T*)w, icp, OC, M, o);
-    g_launch_timing.used = true;
-  } else {
-    igemm_kernel<T, C><<<grid, C::NT, 0, s>>>((const T*)x, (const T*)xlo, ldx, IC, (const T*)w, icp, OC, M, o);
-  }
+  launch_k(igemm_kernel<T, C>, grid, C::NT, 0, s, (const T*)x, (const T*)xlo, ldx, IC, (const T*)w, icp, OC, M, o);
 }
 
 template <typename T>
@@ -499,9 +492,9 @@ void launch_input_prep(int prec, const float* bin, int nin, void* out, int ldo, 
     throw std::runtime_error("input_prep: bad global-input bias arguments");
   const dim3 grid(B, gl.W ? 2 : 1);
   if (prec == PREC_F16)
-    input_prep_kernel<f16><<<grid, 384, 0, s>>>(bin, nin, (f16*)out, ldo, mask, area, s1, s2, gl);
+    launch_k(input_prep_kernel<f16>, grid, 384, 0, s, bin, nin, (f16*)out, ldo, mask, area, s1, s2, gl);
   else if (prec == PREC_BF16)
-    input_prep_kernel<bf16><<<grid, 384, 0, s>>>(bin, nin, (bf16*)out, ldo, mask, area, s1, s2, gl);
+    launch_k(input_prep_kernel<bf16>, grid, 384, 0, s, bin, nin, (bf16*)out, ldo, mask, area, s1, s2, gl);
   else throw std::runtime_error("input_prep: 16-bit only");
   KGX_CHECK_LAUNCH();
 }

@@ -109,9 +109,9 @@ void launch_gemm(int prec, const GemmArgs& g, hipStream_t s);
 // OC % 4 == 0. Split (1x1 only): x_lo holds the low parts of the activation (Emit::out_lo, same layout) and w
 // packs each output tile's high weight rows followed by their low parts; every product is then taken as
 // hi*hi + lo*hi + hi*lo, which carries about 22 significant bits of each operand (a float-accurate convolution).
-// Kernel-timing events for the next launch (set by a profiled forward): a launch site that supports them
-// launches through hipExtLaunchKernel, whose dispatch records `start` and `stop` around the kernel itself, and sets
-// `used`. Others leave them alone and are timed by events around their launch.
+// Kernel-timing events for the next op (set by a profiled forward): every kernel launch (launch_k) then goes
+// through hipExtLaunchKernel, whose dispatch records `start` before the op's first kernel and `stop` after each
+// kernel, and sets `used`. An op that launches no kernel (a plain copy) is timed by events around it instead.
 struct LaunchTiming {
   hipEvent_t start = nullptr, stop = nullptr;
   bool used = false;

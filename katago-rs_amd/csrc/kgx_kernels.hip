@@ -39,7 +39,7 @@ __global__ __launch_bounds__(256) void mask_prep_kernel(const float* __restrict_
 }
 
 void launch_mask_prep(const float* bin, int nin, float* mask, float* area, float* s1, float* s2, int B, hipStream_t s) {
-  mask_prep_kernel<<<B, 256, 0, s>>>(bin, nin, mask, area, s1, s2);
+  launch_k(mask_prep_kernel, B, 256, 0, s, bin, nin, mask, area, s1, s2);
   KGX_CHECK_LAUNCH();
 }
 
@@ -88,7 +88,7 @@ void launch_pool(const float* x, int ldx, int coff, int C, const Prologue& pro, 
                  const float* s2, bool value, float* out, int B, hipStream_t s) {
   dim3 grid((C + 63) / 64, B), block(64, 16);
   const bool p = pro.scale != nullptr;
-#define KGX_POOL(V, P, A) pool_kernel<V, P, A><<<grid, block, 0, s>>>(x, ldx, coff, C, pro, area, s1, s2, out)
+#define KGX_POOL(V, P, A) launch_k(pool_kernel<V, P, A>, grid, block, 0, s, x, ldx, coff, C, pro, area, s1, s2, out)
 #define KGX_POOL_ACT(V)                                   \
   if (!p) KGX_POOL(V, false, ACT_ID);                     \
   else switch (pro.act) {                                 \
@@ -156,10 +156,10 @@ void launch_small_matmul(const float* in, int ldin, int IC, const float* W, int 
   const size_t lds = ((size_t)8 * IC + 4 * 8 * 64) * sizeof(float);
   const int a = accumulate ? 1 : 0;
   switch (act) {
-    case ACT_RELU: small_mm_kernel<ACT_RELU><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
-    case ACT_MISH: small_mm_kernel<ACT_MISH><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
-    case ACT_SILU: small_mm_kernel<ACT_SILU><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
-    default: small_mm_kernel<ACT_ID><<<grid, 256, lds, s>>>(in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
+    case ACT_RELU: launch_k(small_mm_kernel<ACT_RELU>, grid, 256, lds, s, in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
+    case ACT_MISH: launch_k(small_mm_kernel<ACT_MISH>, grid, 256, lds, s, in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
+    case ACT_SILU: launch_k(small_mm_kernel<ACT_SILU>, grid, 256, lds, s, in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
+    default: launch_k(small_mm_kernel<ACT_ID>, grid, 256, lds, s, in, ldin, IC, W, OC, bias, out, ldout, ostride, a, B); break;
   }
   KGX_CHECK_LAUNCH();
 }
@@ -453,7 +453,7 @@ void launch_row_progs(const RowProgs& ps, int B, hipStream_t s) {
   if (ps.n > 1)
     for (int k = 0; k < ps.n; k++)
       if (ps.p[k].splits != 1) throw std::runtime_error("row programs: output splits need a single program");
-  row_prog_kernel<<<dim3(B, ps.n > 1 ? ps.n : ps.p[0].splits), RP_NT, lds, s>>>(ps);
+  launch_k(row_prog_kernel, dim3(B, ps.n > 1 ? ps.n : ps.p[0].splits), RP_NT, lds, s, ps);
   KGX_CHECK_LAUNCH();
 }
 
@@ -538,10 +538,10 @@ template <int HK>
 static void head_spatial_launch(const HeadSpatialArgs& a, int B, hipStream_t s) {
   dim3 grid((HW + HS_PTS - 1) / HS_PTS, B);
   switch (a.p1_act) {
-    case ACT_RELU: head_spatial_kernel<ACT_RELU, HK><<<grid, 256, 0, s>>>(a); break;
-    case ACT_MISH: head_spatial_kernel<ACT_MISH, HK><<<grid, 256, 0, s>>>(a); break;
-    case ACT_SILU: head_spatial_kernel<ACT_SILU, HK><<<grid, 256, 0, s>>>(a); break;
-    default: head_spatial_kernel<ACT_ID, HK><<<grid, 256, 0, s>>>(a); break;
+    case ACT_RELU: launch_k(head_spatial_kernel<ACT_RELU, HK>, grid, 256, 0, s, a); break;
+    case ACT_MISH: launch_k(head_spatial_kernel<ACT_MISH, HK>, grid, 256, 0, s, a); break;
+    case ACT_SILU: launch_k(head_spatial_kernel<ACT_SILU, HK>, grid, 256, 0, s, a); break;
+    default: launch_k(head_spatial_kernel<ACT_ID, HK>, grid, 256, 0, s, a); break;
   }
 }
 
@@ -639,7 +639,7 @@ template <typename T, int NV, int LPR>
 static void rmsnorm_lanes(const float* x, int ldx, int C, const float* w, float eps, const float* mask, T* out, int ldo,
                           int rows, hipStream_t s) {
   constexpr int rg = 64 / LPR, per_wg = 4 * rg * (rg <= 2 ? 2 : 1);
-  rmsnorm_lanes_kernel<T, NV, LPR><<<(rows + per_wg - 1) / per_wg, 256, 0, s>>>(x, ldx, C, w, eps, mask, out, ldo, rows);
+  launch_k(rmsnorm_lanes_kernel<T, NV, LPR>, (rows + per_wg - 1) / per_wg, 256, 0, s, x, ldx, C, w, eps, mask, out, ldo, rows);
 }
 
 template <typename T, int LPR>
@@ -688,9 +688,9 @@ void launch_rmsnorm_tok(int prec, const float* x, int ldx, int C, const float* w
     }
   }
   dim3 grid((rows + 3) / 4);
-  if (prec == PREC_F16) rmsnorm_tok_kernel<f16><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, (f16*)out, ldo, rows);
-  else if (prec == PREC_BF16) rmsnorm_tok_kernel<bf16><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, (bf16*)out, ldo, rows);
-  else rmsnorm_tok_kernel<float><<<grid, 256, 0, s>>>(x, ldx, C, w, eps, mask, (float*)out, ldo, rows);
+  if (prec == PREC_F16) launch_k(rmsnorm_tok_kernel<f16>, grid, 256, 0, s, x, ldx, C, w, eps, mask, (f16*)out, ldo, rows);
+  else if (prec == PREC_BF16) launch_k(rmsnorm_tok_kernel<bf16>, grid, 256, 0, s, x, ldx, C, w, eps, mask, (bf16*)out, ldo, rows);
+  else launch_k(rmsnorm_tok_kernel<float>, grid, 256, 0, s, x, ldx, C, w, eps, mask, (float*)out, ldo, rows);
   KGX_CHECK_LAUNCH();
 }
 
@@ -740,15 +740,15 @@ __global__ __launch_bounds__(256) void tip_rms_apply_kernel(const float* __restr
 
 void launch_tip_rms(const float* x, int C, const float* gamma, const float* beta, float eps, bool spatial, int act,
                     const float* mask, const float* area, float* rs_tmp, float* out, int B, hipStream_t s) {
-  if (spatial) tip_rms_stats_kernel<<<B, 256, 0, s>>>(x, C, mask, area, eps, rs_tmp);
+  if (spatial) launch_k(tip_rms_stats_kernel, B, 256, 0, s, x, C, mask, area, eps, rs_tmp);
   const int rows = B * HW;
   dim3 grid((rows + 3) / 4);
   const int sp = spatial ? 1 : 0;
   switch (act) {
-    case ACT_RELU: tip_rms_apply_kernel<ACT_RELU><<<grid, 256, 0, s>>>(x, C, gamma, beta, eps, sp, mask, rs_tmp, out, rows); break;
-    case ACT_MISH: tip_rms_apply_kernel<ACT_MISH><<<grid, 256, 0, s>>>(x, C, gamma, beta, eps, sp, mask, rs_tmp, out, rows); break;
-    case ACT_SILU: tip_rms_apply_kernel<ACT_SILU><<<grid, 256, 0, s>>>(x, C, gamma, beta, eps, sp, mask, rs_tmp, out, rows); break;
-    default: tip_rms_apply_kernel<ACT_ID><<<grid, 256, 0, s>>>(x, C, gamma, beta, eps, sp, mask, rs_tmp, out, rows); break;
+    case ACT_RELU: launch_k(tip_rms_apply_kernel<ACT_RELU>, grid, 256, 0, s, x, C, gamma, beta, eps, sp, mask, rs_tmp, out, rows); break;
+    case ACT_MISH: launch_k(tip_rms_apply_kernel<ACT_MISH>, grid, 256, 0, s, x, C, gamma, beta, eps, sp, mask, rs_tmp, out, rows); break;
+    case ACT_SILU: launch_k(tip_rms_apply_kernel<ACT_SILU>, grid, 256, 0, s, x, C, gamma, beta, eps, sp, mask, rs_tmp, out, rows); break;
+    default: launch_k(tip_rms_apply_kernel<ACT_ID>, grid, 256, 0, s, x, C, gamma, beta, eps, sp, mask, rs_tmp, out, rows); break;
   }
   KGX_CHECK_LAUNCH();
 }
@@ -1126,15 +1126,15 @@ template <typename T, int D>
 static void attn_mfma_d(const AttnArgs& a, int B, hipStream_t s) {
   const int nh = B * a.H;
   dim3 grid((nh + 7) / 8 * 8 * ATT_NQB);
-  if (a.q_tables > 0) attn_mfma_kernel<T, D, true><<<grid, ATT_NW * 64, 0, s>>>(a, nh);
-  else attn_mfma_kernel<T, D, false><<<grid, ATT_NW * 64, 0, s>>>(a, nh);
+  if (a.q_tables > 0) launch_k(attn_mfma_kernel<T, D, true>, grid, ATT_NW * 64, 0, s, a, nh);
+  else launch_k(attn_mfma_kernel<T, D, false>, grid, ATT_NW * 64, 0, s, a, nh);
 }
 
 template <typename T, int D>
 static void attn_d(const AttnArgs& a, int B, hipStream_t s) {
   dim3 grid((HW + 63) / 64, a.H, B);
-  if (a.q_tables > 0) attn_kernel<T, D, true><<<grid, 64, 0, s>>>(a);
-  else attn_kernel<T, D, false><<<grid, 64, 0, s>>>(a);
+  if (a.q_tables > 0) launch_k(attn_kernel<T, D, true>, grid, 64, 0, s, a);
+  else launch_k(attn_kernel<T, D, false>, grid, 64, 0, s, a);
 }
 
 template <typename T>
@@ -1190,8 +1190,8 @@ void launch_ffn_act(int prec, const float* u, int ldu, int F, bool gated, void* 
   const size_t total = (size_t)rows * F;
   dim3 grid((unsigned)((total + 255) / 256));
 #define KGX_FFN(T) \
-  if (gated) ffn_act_kernel<T, true><<<grid, 256, 0, s>>>(u, ldu, F, (T*)h, ldh, rows); \
-  else ffn_act_kernel<T, false><<<grid, 256, 0, s>>>(u, ldu, F, (T*)h, ldh, rows);
+  if (gated) launch_k(ffn_act_kernel<T, true>, grid, 256, 0, s, u, ldu, F, (T*)h, ldh, rows); \
+  else launch_k(ffn_act_kernel<T, false>, grid, 256, 0, s, u, ldu, F, (T*)h, ldh, rows);
   if (prec == PREC_F16) { KGX_FFN(f16) }
   else if (prec == PREC_BF16) { KGX_FFN(bf16) }
   else { KGX_FFN(float) }

@@ -935,8 +935,8 @@ void Net::run_ops(int B, hipStream_t s) {
     for (const Op& op : ops_) op.launch(s, B);
     return;
   }
-  // Events around every launch, plus a pair for launch sites that time their kernel itself (LaunchTiming: the
-  // implicit-GEMM convolutions), whose time then excludes the dispatch latency of an eager launch.
+  // Events around every op, plus a pair that the op's kernels record themselves (LaunchTiming, launch_k), whose
+  // span then excludes the dispatch latency of an eager launch.
   const size_t need = 4 * ops_.size();
   while (events_.size() < need) {
     hipEvent_t e;
