@@ -135,7 +135,9 @@ __device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floa
   if (o.yt) store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, v[0], v[1], v[2], v[3]);
   if (o.y) {
     if (o.accumulate) v += yacc;
-    if (!o.y_dead) *(floatx4*)(o.y + (size_t)m * o.ldy + n) = v;
+    // Non-temporal: the float stream's next reader is a later op (the next residual add, two or more launches
+    // on), so its lines go out to MALL instead of taking L2 from the activations and weights of the ops between.
+    if (!o.y_dead) __builtin_nontemporal_store(v, (floatx4*)(o.y + (size_t)m * o.ldy + n));
   }
   if (o.emit.scale) {
     float t[4];
