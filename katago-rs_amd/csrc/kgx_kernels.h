@@ -239,13 +239,13 @@ void launch_rmsnorm_tok(int prec, const float* x, int ldx, int C, const float* w
 void launch_tip_rms(const float* x, int C, const float* gamma, const float* beta, float eps, bool spatial, int act,
                     const float* mask, const float* area, float* rs_tmp, float* out, int B, hipStream_t s);
 
-// Softmax attention over the board on the fused projection buffer qkv [B*HW][ldq] (q | k | v columns),
-// RoPE applied on load (cos/sin [ntab][HW][dq/2], pair p <-> p + dq/2), key bias mask*3e4 - 3e4.
+// Softmax attention over the board on the fused projection buffer qkv [B*HW][ldq] (q | k | v columns), whose
+// queries and keys carry RoPE already (the projection's epilogue, QkvEpi), queries times `scale`; key bias
+// mask*3e4 - 3e4.
 struct AttnArgs {
   const void* qkv = nullptr; int ldq = 0;
   int q_off = 0, k_off = 0, v_off = 0;
   int H = 0, KV = 0, dq = 0, dv = 0;
-  const float* cos_t = nullptr; const float* sin_t = nullptr; int q_tables = 0, k_tables = 0;  // 0 = no RoPE
   float scale = 1.f;
   const float* mask = nullptr;
   void* out = nullptr; int ldo = 0;

@@ -757,37 +757,23 @@ void launch_tip_rms(const float* x, int C, const float* gamma, const float* beta
 // Attention: one thread per query, keys and values staged 32 at a time in LDS, online softmax
 // ---------------------------------------------------------------------------------------------------------
 
-template <typename T, int D, bool ROPE>
+template <typename T, int D>
 __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
   const int qi = blockIdx.x * 64 + threadIdx.x, h = blockIdx.y, n = blockIdx.z, tid = threadIdx.x;
   const int kvh = h / (a.H / a.KV);
-  constexpr int HALF = D / 2;
   const bool in_range = qi < HW;
   const int qrow = in_range ? qi : 0;
   const T* qkv = (const T*)a.qkv;
   float q[D], acc[D];
   {
     const T* qp = qkv + ((size_t)n * HW + qrow) * a.ldq + a.q_off + h * D;
-    if constexpr (ROPE) {
-      const int tab = a.q_tables == 1 ? 0 : kvh;  // query head h uses its kv head's table
-      const float* ct = a.cos_t + ((size_t)tab * HW + qrow) * HALF;
-      const float* st = a.sin_t + ((size_t)tab * HW + qrow) * HALF;
 #pragma unroll
-      for (int p = 0; p < HALF; p++) {
-        const float x0 = (float)qp[p], x1 = (float)qp[p + HALF];
-        q[p] = (x0 * ct[p] - x1 * st[p]) * a.scale;
-        q[p + HALF] = (x0 * st[p] + x1 * ct[p]) * a.scale;
-      }
-    } else {
-#pragma unroll
-      for (int d = 0; d < D; d++) q[d] = (float)qp[d] * a.scale;
-    }
+    for (int d = 0; d < D; d++) q[d] = (float)qp[d] * a.scale;
   }
 #pragma unroll
   for (int d = 0; d < D; d++) acc[d] = 0.f;
   float m_run = -FLT_MAX, l_run = 0.f;
   __shared__ float ks[32 * D], vs[32 * D], kb[32];
-  const int ktab = a.k_tables == 1 ? 0 : kvh;
   for (int j0 = 0; j0 < HW; j0 += 32) {
     const int cnt = min(32, HW - j0);
     for (int e = tid; e < 32 * D; e += 64) {
@@ -795,16 +781,7 @@ __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
       float kv = 0.f, vv = 0.f;
       if (j < cnt) {
         const T* row = qkv + ((size_t)n * HW + j0 + j) * a.ldq;
-        const T* kp = row + a.k_off + kvh * D;
-        if constexpr (ROPE) {
-          const int p = d < HALF ? d : d - HALF;
-          const float x0 = (float)kp[p], x1 = (float)kp[p + HALF];
-          const float c = a.cos_t[((size_t)ktab * HW + j0 + j) * HALF + p];
-          const float sn = a.sin_t[((size_t)ktab * HW + j0 + j) * HALF + p];
-          kv = d < HALF ? x0 * c - x1 * sn : x0 * sn + x1 * c;
-        } else {
-          kv = (float)kp[d];
-        }
+        kv = (float)row[a.k_off + kvh * D + d];
         vv = (float)row[a.v_off + kvh * D + d];
       }
       ks[e] = kv;
@@ -870,7 +847,7 @@ __device__ __forceinline__ int att_kpos(int kk) {
 
 // Three workgroups per CU for D <= 32; two for D = 64, whose registers spill at the three-workgroup bound (the
 // spill-free kernel is 4 % faster at b10c384h6).
-template <typename T, int D, bool ROPE>
+template <typename T, int D>
 __global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel(AttnArgs a, int nheads_total) {
   static_assert(D == 16 || D == 32 || D == 64, "head dim");
   typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
@@ -882,7 +859,8 @@ __global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel
   constexpr int KS_SZ = ATT_KT * KLD, VS_SZ = D * VLD;
   constexpr int BUF = (KS_SZ + VS_SZ) * (int)sizeof(T) + ATT_KT * 4;  // bytes per buffer: K, V^T, key bias
   constexpr int OLD = D + 8, OUT = ATT_NW * ATT_QW * OLD * (int)sizeof(T);
-  constexpr int LDS = 2 * BUF > OUT ? 2 * BUF : OUT;
+  constexpr int NBUF = 2;
+  constexpr int LDS = NBUF * BUF > OUT ? NBUF * BUF : OUT;
   constexpr int KU = ATT_KT * NCH, VU = (ATT_KT / 2) * (D / 8);  // staging units: (key, chunk pair), (key pair, chunk)
   static_assert(KU <= NT && VU <= NT && BUF % 16 == 0, "staging layout");
   constexpr float L2E = 1.4426950408889634f;
@@ -893,7 +871,6 @@ __global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel
   const int h = nh % a.H, n = nh / a.H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g = lane >> 4;
   const int kvh = h / (a.H / a.KV);
-  const int qtab = a.q_tables == 1 ? 0 : kvh, ktab = a.k_tables == 1 ? 0 : kvh;
   const T* qkv = (const T*)a.qkv;
   const T* kbase = qkv + (size_t)n * HW * a.ldq + a.k_off + kvh * D;
   const T* vbase = qkv + (size_t)n * HW * a.ldq + a.v_off + kvh * D;
@@ -901,7 +878,7 @@ __global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel
 
   // Zero K's padding columns (head dim 16) in both buffers; staging never writes them.
   if constexpr (DP > D) {
-    for (int i = tid; i < 2 * ATT_KT; i += NT) {
+    for (int i = tid; i < NBUF * ATT_KT; i += NT) {
       T* Ks = (T*)(smem + (i / ATT_KT) * BUF) + (i % ATT_KT) * KLD + D;
       *(u32x4*)Ks = u32x4{0, 0, 0, 0};
       *(u32x4*)(Ks + 8) = u32x4{0, 0, 0, 0};
@@ -922,25 +899,9 @@ __global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel
       for (int e = 0; e < 8; e++) r[e] = to_t<T>(0.f);
       if (qi < HW && d0 < D) {
         const T* qp = qkv + ((size_t)n * HW + qi) * a.ldq + a.q_off + h * D;
-        if constexpr (ROPE) {
-          const bool lo = d0 < HALF;
-          const int p0 = lo ? d0 : d0 - HALF;
-          const frag_t x0 = *(const frag_t*)(qp + p0), x1 = *(const frag_t*)(qp + p0 + HALF);
-          const float* ct = a.cos_t + ((size_t)qtab * HW + qi) * HALF + p0;
-          const float* st = a.sin_t + ((size_t)qtab * HW + qi) * HALF + p0;
-          const floatx4 c0 = *(const floatx4*)ct, c1 = *(const floatx4*)(ct + 4);
-          const floatx4 s0 = *(const floatx4*)st, s1 = *(const floatx4*)(st + 4);
+        const frag_t x = *(const frag_t*)(qp + d0);
 #pragma unroll
-          for (int e = 0; e < 8; e++) {
-            const float c = e < 4 ? c0[e & 3] : c1[e & 3], sn = e < 4 ? s0[e & 3] : s1[e & 3];
-            const float v0 = (float)x0[e], v1 = (float)x1[e];
-            r[e] = to_t<T>((lo ? v0 * c - v1 * sn : v0 * sn + v1 * c) * a.scale);
-          }
-        } else {
-          const frag_t x = *(const frag_t*)(qp + d0);
-#pragma unroll
-          for (int e = 0; e < 8; e++) r[e] = to_t<T>((float)x[e] * a.scale);
-        }
+        for (int e = 0; e < 8; e++) r[e] = to_t<T>((float)x[e] * a.scale);
       }
       qf[qt][kc] = r;
     }
@@ -949,57 +910,40 @@ __global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel
   // Staging of one key tile: registers (fetch) then LDS (stash).
   const int ku_key = tid / NCH, ku_c = (tid % NCH) * 8;            // K unit: key, first dim of the low chunk
   const int vu_pair = tid / (D / 8), vu_c = (tid % (D / 8)) * 8;  // V unit: key pair, first dim of the chunk
-  frag_t kx0, kx1, vx0, vx1;
-  floatx4 c0, c1, s0, s1;
-  float mk = 0.f;
+  struct Stage {
+    frag_t kx0, kx1, vx0, vx1;
+    float mk = 0.f;
+  };
   // Keys past the board read the last key's rows (finite values): their bias of -1e30 gives them probability 0.
-  auto fetch = [&](int t) {
+  auto fetch = [&](int t, Stage& st) {
     const int k0 = t * ATT_KT;
     if (tid < KU) {
       const int key = min(k0 + ku_key, HW - 1);
       const T* kp = kbase + (size_t)key * a.ldq + ku_c;
-      kx0 = *(const frag_t*)kp;
-      kx1 = *(const frag_t*)(kp + HALF);
-      if constexpr (ROPE) {
-        const float* ct = a.cos_t + ((size_t)ktab * HW + key) * HALF + ku_c;
-        const float* st = a.sin_t + ((size_t)ktab * HW + key) * HALF + ku_c;
-        c0 = *(const floatx4*)ct;
-        c1 = *(const floatx4*)(ct + 4);
-        s0 = *(const floatx4*)st;
-        s1 = *(const floatx4*)(st + 4);
-      }
+      st.kx0 = *(const frag_t*)kp;
+      st.kx1 = *(const frag_t*)(kp + HALF);
     }
     if (tid < VU) {
       const int key = min(k0 + 2 * vu_pair, HW - 1), key1 = min(k0 + 2 * vu_pair + 1, HW - 1);
-      vx0 = *(const frag_t*)(vbase + (size_t)key * a.ldq + vu_c);
-      vx1 = *(const frag_t*)(vbase + (size_t)key1 * a.ldq + vu_c);
+      st.vx0 = *(const frag_t*)(vbase + (size_t)key * a.ldq + vu_c);
+      st.vx1 = *(const frag_t*)(vbase + (size_t)key1 * a.ldq + vu_c);
     }
     if (tid < ATT_KT) {
       const int key = k0 + tid;
-      mk = key < HW ? mrow[key] * 3e4f - 3e4f : -1e30f;
+      st.mk = key < HW ? mrow[key] * 3e4f - 3e4f : -1e30f;
     }
   };
-  auto stash = [&](int b) {
+  auto stash = [&](int b, const Stage& st) {
     T* Ks = (T*)(smem + b * BUF);
     T* Vs = Ks + KS_SZ;
     float* kbias = (float*)(Vs + VS_SZ);
     if (tid < KU) {
-      frag_t lo = kx0, hi = kx1;
-      if constexpr (ROPE) {
-#pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const float c = e < 4 ? c0[e & 3] : c1[e & 3], sn = e < 4 ? s0[e & 3] : s1[e & 3];
-          const float v0 = (float)kx0[e], v1 = (float)kx1[e];
-          lo[e] = to_t<T>(v0 * c - v1 * sn);
-          hi[e] = to_t<T>(v0 * sn + v1 * c);
-        }
-      }
-      *(frag_t*)(Ks + ku_key * KLD + ku_c) = lo;
-      *(frag_t*)(Ks + ku_key * KLD + ku_c + HALF) = hi;
+      *(frag_t*)(Ks + ku_key * KLD + ku_c) = st.kx0;
+      *(frag_t*)(Ks + ku_key * KLD + ku_c + HALF) = st.kx1;
     }
     if (tid < VU) {
       const int kk = 2 * vu_pair, pos = (kk & ~31) + att_kpos(kk & 31);
-      const u32x4 w0 = __builtin_bit_cast(u32x4, vx0), w1 = __builtin_bit_cast(u32x4, vx1);
+      const u32x4 w0 = __builtin_bit_cast(u32x4, st.vx0), w1 = __builtin_bit_cast(u32x4, st.vx1);
 #pragma unroll
       for (int e = 0; e < 8; e++) {
         // Element e of both keys: the 16-bit halves of word e / 2.
@@ -1008,7 +952,7 @@ __global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel
             (e & 1) ? (a0 >> 16) | (a1 & 0xffff0000u) : (a0 & 0xffffu) | (a1 << 16);
       }
     }
-    if (tid < ATT_KT) kbias[tid] = mk;
+    if (tid < ATT_KT) kbias[tid] = st.mk;
   };
 
   floatx4 o[DT][QT];
@@ -1021,17 +965,23 @@ __global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel
     for (int dt = 0; dt < DT; dt++) o[dt][qt] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
-  fetch(0);
-  stash(0);
-  __syncthreads();
-  for (int t = 0; t < ATT_NKT; t++) {
-    if (t + 1 < ATT_NKT) fetch(t + 1);
-    const T* Ks = (const T*)(smem + (t & 1) * BUF);
-    const T* Vs = Ks + KS_SZ;
-    const float* kbias = (const float*)(Vs + VS_SZ);
-    // S^T tiles [key tile][query tile] of the whole 64-key tile with the key bias as initial accumulator; one
-    // maximum and one rescale per tile; numerators as B fragments of the two 32-key blocks; O^T += V^T P^T.
-    floatx4 sc[2 * KB][QT];
+  // Max over the four lane groups that hold one query's keys: lanes j and j ^ 16, then j and j ^ 32, through the
+  // gfx950 lane-swap instructions (no LDS round trip). v_permlane16_swap exchanges the odd rows of 16 lanes of its
+  // first operand with the even rows of its second, so with both holding v each lane ends with {v[j], v[j ^ 16]};
+  // v_permlane32_swap does the same for halves ({v[j], v[j ^ 32]}). Written as inline assembly: the compiler's
+  // builtins for these instructions fold the two results into one when both operands hold the same value. The
+  // s_nop covers the VALU-write to permlane-read hazard on the operands.
+  auto xmax = [](float v) {
+    float a = v, b = v;
+    asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+    float c = fmaxf(a, b), d = c;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(c), "+v"(d));
+    return fmaxf(c, d);
+  };
+  // S^T tiles [key tile][query tile] of one 64-key tile, the key bias as initial accumulator.
+  auto scores = [&](int b, floatx4 (&sc)[2 * KB][QT]) {
+    const T* Ks = (const T*)(smem + b * BUF);
+    const float* kbias = (const float*)(Ks + KS_SZ + VS_SZ);
 #pragma unroll
     for (int kt = 0; kt < 2 * KB; kt++) {
       frag_t kf[KC];
@@ -1051,22 +1001,40 @@ __global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel
         sc[kt][qt] = c;
       }
     }
-    frag_t pf[KB][QT];
+  };
+  // Numerators as B fragments of the two 32-key blocks, relative to a reference maximum per query that moves
+  // lazily: only when some query of the wave would see a numerator above 2^8 (its tile maximum more than eight
+  // binary orders above the reference) are the reference maxima raised to the running maxima, and the
+  // accumulators and sums rescaled, in one wave-uniform branch. Otherwise every numerator stays below 2^8 (in
+  // range and at full relative precision as a 16-bit operand), and O, the sums and the numerators all stay
+  // relative to the same unchanged reference.
+  auto softmax = [&](const floatx4 (&sc)[2 * KB][QT], frag_t (&pf)[KB][QT]) {
+    float mx[QT];
+    bool grow = false;
 #pragma unroll
     for (int qt = 0; qt < QT; qt++) {
-      float mx = sc[0][qt][0];
+      float m = sc[0][qt][0];
 #pragma unroll
       for (int kt = 0; kt < 2 * KB; kt++)
 #pragma unroll
-        for (int r = 0; r < 4; r++) mx = fmaxf(mx, sc[kt][qt][r]);
-      mx = fmaxf(mx, __shfl_xor(mx, 16));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = fmaxf(mref[qt], mx);
-      const float alpha = __builtin_amdgcn_exp2f((mref[qt] - mnew) * L2E);
+        for (int r = 0; r < 4; r++) m = fmaxf(m, sc[kt][qt][r]);
+      mx[qt] = xmax(m);
+      grow |= (mx[qt] - mref[qt]) * L2E > 8.f;
+    }
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
 #pragma unroll
-      for (int dt = 0; dt < DT; dt++) o[dt][qt] *= alpha;
-      mref[qt] = mnew;
-      const float ml = mnew * L2E;
+      for (int qt = 0; qt < QT; qt++) {
+        const float mnew = fmaxf(mref[qt], mx[qt]);
+        const float alpha = __builtin_amdgcn_exp2f((mref[qt] - mnew) * L2E);
+#pragma unroll
+        for (int dt = 0; dt < DT; dt++) o[dt][qt] *= alpha;
+        lsum[qt] *= alpha;
+        mref[qt] = mnew;
+      }
+    }
+#pragma unroll
+    for (int qt = 0; qt < QT; qt++) {
+      const float ml = mref[qt] * L2E;
       float ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < KB; kb++) {
@@ -1081,8 +1049,12 @@ __global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel
           }
         pf[kb][qt] = pr;
       }
-      lsum[qt] = lsum[qt] * alpha + ps;
+      lsum[qt] += ps;
     }
+  };
+  // O^T += V^T P^T.
+  auto pv = [&](int b, const frag_t (&pf)[KB][QT]) {
+    const T* Vs = (const T*)(smem + b * BUF) + KS_SZ;
 #pragma unroll
     for (int dt = 0; dt < DT; dt++) {
 #pragma unroll
@@ -1097,7 +1069,22 @@ __global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel
         }
       }
     }
-    if (t + 1 < ATT_NKT) stash((t + 1) & 1);
+  };
+
+  // Per tile t: the loads of tile t + 1 in flight during tile t's scores, softmax and O update; then tile t + 1
+  // into the other buffer and one barrier.
+  Stage st;
+  fetch(0, st);
+  stash(0, st);
+  __syncthreads();
+  for (int t = 0; t < ATT_NKT; t++) {
+    if (t + 1 < ATT_NKT) fetch(t + 1, st);
+    floatx4 sc[2 * KB][QT];
+    scores(t & 1, sc);
+    frag_t pf[KB][QT];
+    softmax(sc, pf);
+    pv(t & 1, pf);
+    if (t + 1 < ATT_NKT) stash((t + 1) & 1, st);
     __syncthreads();
   }
 
@@ -1126,15 +1113,13 @@ template <typename T, int D>
 static void attn_mfma_d(const AttnArgs& a, int B, hipStream_t s) {
   const int nh = B * a.H;
   dim3 grid((nh + 7) / 8 * 8 * ATT_NQB);
-  if (a.q_tables > 0) launch_k(attn_mfma_kernel<T, D, true>, grid, ATT_NW * 64, 0, s, a, nh);
-  else launch_k(attn_mfma_kernel<T, D, false>, grid, ATT_NW * 64, 0, s, a, nh);
+  launch_k(attn_mfma_kernel<T, D>, grid, ATT_NW * 64, 0, s, a, nh);
 }
 
 template <typename T, int D>
 static void attn_d(const AttnArgs& a, int B, hipStream_t s) {
   dim3 grid((HW + 63) / 64, a.H, B);
-  if (a.q_tables > 0) launch_k(attn_kernel<T, D, true>, grid, 64, 0, s, a);
-  else launch_k(attn_kernel<T, D, false>, grid, 64, 0, s, a);
+  launch_k(attn_kernel<T, D>, grid, 64, 0, s, a);
 }
 
 template <typename T>

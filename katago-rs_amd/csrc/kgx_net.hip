@@ -484,7 +484,6 @@ void Net::emit_attention(const BlockDesc& b, int depth) {
     AttnArgs a;
     a.qkv = qkv; a.ldq = nqkv; a.q_off = 0; a.k_off = nq; a.v_off = nq + nk;
     a.H = H; a.KV = KV; a.dq = dq; a.dv = dv;
-    a.q_tables = 0; a.k_tables = 0;
     a.scale = 1.f; a.mask = mask; a.out = ao; a.ldo = H * dv;
     launch_attention(prec, a, B, s);
   };

@@ -58,6 +58,7 @@ class Arch:
     meta_c: int = 64                   # meta encoder hidden width
     policy_channels: int = 0           # v17 only (2 or 4); derived otherwise
     rope_theta: float = 100.0
+    qk_gain: float = 1.0               # scale of the attention q and k projections (scores scale by its square)
 
 
 # Block specs:
@@ -301,8 +302,8 @@ def _write_block(w: _Writer, arch: Arch, spec, c: int, gain: float) -> dict:
               int(rope != "none"), int(rope == "learnable"))
         t.update(heads=h, kv_heads=kvh, dq=dq, dv=dv, rope=rope)
         t["ln"] = w.tf_rmsnorm("ln", c)
-        t["q"] = w.matmul("q", c, h * dq)
-        t["k"] = w.matmul("k", c, kvh * dq)
+        t["q"] = w.matmul("q", c, h * dq, gain=arch.qk_gain)
+        t["k"] = w.matmul("k", c, kvh * dq, gain=arch.qk_gain)
         t["v"] = w.matmul("v", c, kvh * dv)
         t["o"] = w.matmul("o", h * dv, c, gain=gain)
         if rope == "learnable":

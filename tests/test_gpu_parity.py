@@ -171,6 +171,33 @@ def test_benchmark_nets_on_reference_positions(kgx, synth, oracle, name, prec):
 
 
 @pytest.mark.parametrize("prec", ["f16", "bf16"])
+@pytest.mark.parametrize("qk_gain", [3.0, 6.0])
+def test_sharp_attention_matches_the_16bit_network(kgx, synth, oracle, prec, qk_gain):
+    """Attention with large score ranges: the q and k projections scaled by qk_gain (scores by its square), so
+    that a query's running maximum jumps by many binary orders between key tiles and the 16-bit attention kernel's
+    lazy rescale (the reference maximum moves only when a numerator would exceed 2^8) takes both branches, on full
+    and partial boards. Held to the 16-bit network (the oracle with the same operand rounding) with the emulation
+    bound; the absolute f16 bound does not apply, since the rounding of such sharp scores moves the network
+    itself far from float64."""
+    import dataclasses
+    arch = dataclasses.replace(synth.tiny_nets()["t_tf64"], qk_gain=qk_gain)
+    mb = synth.write_model(arch, 7)
+    sp, gl, _ = synth.make_inputs(6, 13, board_sizes=[19, 13, 9, 19, 7, 19])
+    net = kgx.Net(mb)
+    h = kgx.Handle(net, 6, prec)
+    out = h.forward(sp, gl)
+    h.close()
+    ref = oracle.Model(mb).forward(sp, gl)
+    ref_q = emulated(oracle, mb, prec, sp, gl)
+    assert np.all(np.isfinite(out))
+    fmt = errors(ref_q, ref, net.P, net.S)
+    for k, (e, s) in errors(out, ref_q, net.P, net.S).items():
+        bound = 2.0 * fmt[k][0] + 1e-4 * max(1.0, s)
+        print(f"qk_gain {qk_gain} [{prec}] {k}: |gpu - {prec} network| {e:.2e}, format {fmt[k][0]:.2e}")
+        assert e <= bound, f"qk_gain {qk_gain} [{prec}] {k}: {e:.3e} > {bound:.3e}"
+
+
+@pytest.mark.parametrize("prec", ["f16", "bf16"])
 def test_gpool_widths_the_row_emission_does_not_fit(kgx, synth, oracle, prec):
     """A global-pooling block whose regular width has no share of a multiple of 8 channels (20): 16-bit handles
     then emit the biased mid activation with a separate bias_act launch instead of in the row program."""
