@@ -826,18 +826,17 @@ __global__ __launch_bounds__(64) void attn_kernel(AttnArgs a) {
   }
 }
 
-// Attention on the matrix cores (16-bit handles). A workgroup of four waves takes 128 queries of one (batch row,
-// head); the three query blocks of a head are launched 8 workgroup ids apart, which puts them on one XCD, so its
-// K/V rows come from that XCD's L2 after the first read. Keys go in tiles of 64, double-buffered in LDS: K with
-// RoPE applied ([key][d]) and V transposed ([d][key], keys permuted as below), each tile loaded into registers one
-// tile ahead of its use. Each wave computes S^T = K Q^T for its 32 queries (keys as rows: a lane holds four
+// Attention on the matrix cores (16-bit handles). A workgroup of twelve waves takes all the queries of one
+// (batch row, head), 32 per wave, so each key tile is staged once per head. Keys go in tiles of 64,
+// double-buffered in LDS: K ([key][d], RoPE already applied by the projection) and V transposed ([d][key], keys
+// permuted as below), each tile loaded into registers one tile ahead of its use. Each wave computes S^T = K Q^T for its 32 queries (keys as rows: a lane holds four
 // consecutive keys of one query, so the reductions over keys stay in the lane but for two cross-lane steps), with
 // the key mask bias as the accumulator's initial value, then O^T += V^T P^T. P needs no data movement: for a
 // 32-key block the B operand of a lane is its own eight probabilities (keys 4g..4g+3 of the block's first 16 and
 // of its second 16, g = lane / 16), so V^T holds its keys in that order. The softmax runs online over the 64-key
 // tiles (running maximum per query, accumulators rescaled once per tile). Q carries RoPE and the 1/sqrt(d) scale
 // and is held in registers as B fragments. The output goes through LDS for 16-byte stores.
-constexpr int ATT_QW = 32, ATT_NW = 4, ATT_QB = ATT_QW * ATT_NW, ATT_NQB = (HW + ATT_QB - 1) / ATT_QB;
+constexpr int ATT_QW = 32, ATT_NW = 12, ATT_QB = ATT_QW * ATT_NW, ATT_NQB = (HW + ATT_QB - 1) / ATT_QB;
 constexpr int ATT_KT = 64, ATT_NKT = (HW + ATT_KT - 1) / ATT_KT;
 
 // Position of key kk (0..31) of a 32-key block in the permuted V^T rows.
@@ -848,7 +847,7 @@ __device__ __forceinline__ int att_kpos(int kk) {
 // Three workgroups per CU for D <= 32; two for D = 64, whose registers spill at the three-workgroup bound (the
 // spill-free kernel is 4 % faster at b10c384h6).
 template <typename T, int D>
-__global__ __launch_bounds__(ATT_NW * 64, D == 64 ? 2 : 3) void attn_mfma_kernel(AttnArgs a, int nheads_total) {
+__global__ __launch_bounds__(ATT_NW * 64, 1) void attn_mfma_kernel(AttnArgs a, int nheads_total) {
   static_assert(D == 16 || D == 32 || D == 64, "head dim");
   typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
   constexpr int NT = ATT_NW * 64;
