@@ -174,6 +174,33 @@ int kg_get_output_async(kg_handle* handle, int n, const kg_row_input* rows, kg_n
                         void* user);
 int kg_wait(kg_handle* handle);
 
+/* NNEvaluator's per-row inputs of the output post-processing (crates/katago-core/src/neuralnet/nneval.rs:1197-1500)
+ * that come from the board, the rules and MiscNNInputParams. The legality of each move needs the rules engine and
+ * stays with the caller: legal[i] is history.is_legal for NN position i (pass last), with any dagger-hack ban
+ * (nneval.rs:1213-1222) already cleared. */
+typedef struct {
+  const unsigned char* legal;   /* [362], nonzero where the move is legal; at least one */
+  int white_to_move;            /* nextPlayer == P_WHITE: the net's outputs are the mover's, flipped to white's */
+  int board_x_size, board_y_size; /* board.x_size / y_size, 1..19 */
+  float nn_policy_temperature;  /* MiscNNInputParams::nnPolicyTemperature (> 0) */
+  int enable_passing_hacks;     /* MiscNNInputParams::enablePassingHacks: pass prior capped at 19x the rest */
+  int no_result_allowed;        /* 0 when koRule != KO_SIMPLE and scoringRule != SCORING_TERRITORY */
+} kg_post_input;
+
+/* get_output (backend.rs:410-464) followed by NNEvaluator's post-processing of the fields (nneval.rs:1197-1500),
+ * with copy_outputs and the post-processing on the device: the policy softmax over the legal moves at the
+ * row's temperature (illegal moves -1), the value softmax, the score and error transforms by model version
+ * (the version 3 arctan path included), and tanh ownership from white's perspective with 0 off the board. One
+ * readback of the finished fields per batch. A nonfinite policy sum or value fails with the reference's
+ * messages ("Got nonfinite for policy sum", "Got nonfinite for nneval value"). post has n entries. */
+int kg_get_output_eval(kg_handle* handle, int n, const kg_row_input* rows, const kg_post_input* post,
+                       kg_nn_output* outputs);
+
+/* The same post-processing on n raw rows given on the host (kg_forward / kg_run layout), with each row's
+ * symmetry and policy optimism: copy_outputs plus NNEvaluator's arithmetic, on the handle's device. */
+int kg_post_outputs(kg_handle* handle, int n, const float* raw, const int* symmetry, const float* policy_optimism,
+                    const kg_post_input* post, kg_nn_output* outputs);
+
 /* copy_outputs alone (backend.rs:622-731), on the host: n raw rows of P*362 + 3 + S + 361 floats (kg_forward /
  * kg_run output) to NNOutput fields, with each row's symmetry (0..7) and policy optimism. For callers that run
  * the forward pass with kg_run on device-filled inputs. S must be the model version's score channel count. */

@@ -36,7 +36,7 @@ EXPORTS = [
     "kg_handle_is_using_fp16", "kg_forward", "kg_handle_device_buffers", "kg_run", "kg_sync", "kg_handle_stream",
     "kg_get_output", "kg_profile_enable", "kg_profile_reset", "kg_profile_read",
     "kg_model_version_features", "kg_meta_encoder_channels", "kg_copy_outputs", "kg_run_static",
-    "kg_get_output_async", "kg_wait",
+    "kg_get_output_async", "kg_wait", "kg_get_output_eval", "kg_post_outputs",
 ]
 # Completion callback of kg_get_output_async: (user, status).
 DONE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int)
@@ -79,6 +79,19 @@ class RowInput(ctypes.Structure):
         ("row_meta", ctypes.c_void_p),
         ("symmetry", ctypes.c_int),
         ("policy_optimism", ctypes.c_float),
+    ]
+
+
+class PostInput(ctypes.Structure):
+    """kg_post_input: NNEvaluator's per-row inputs of the output post-processing (nneval.rs:1197-1500)."""
+    _fields_ = [
+        ("legal", ctypes.c_void_p),
+        ("white_to_move", ctypes.c_int),
+        ("board_x_size", ctypes.c_int),
+        ("board_y_size", ctypes.c_int),
+        ("nn_policy_temperature", ctypes.c_float),
+        ("enable_passing_hacks", ctypes.c_int),
+        ("no_result_allowed", ctypes.c_int),
     ]
 
 
@@ -138,6 +151,9 @@ def lib():
         L.kg_model_version_features.argtypes = [ci, ctypes.POINTER(ci), ctypes.POINTER(ci), ctypes.POINTER(ci)]
         L.kg_meta_encoder_channels.argtypes = [ci, ctypes.POINTER(ci)]
         L.kg_copy_outputs.argtypes = [vp, ci, ci, ci, ci, vp, vp, ctypes.POINTER(NNOutput)]
+        L.kg_get_output_eval.argtypes = [vp, ci, ctypes.POINTER(RowInput), ctypes.POINTER(PostInput),
+                                         ctypes.POINTER(NNOutput)]
+        L.kg_post_outputs.argtypes = [vp, ci, vp, vp, vp, ctypes.POINTER(PostInput), ctypes.POINTER(NNOutput)]
         _ = cf
         _lib = L
     return _lib
@@ -355,6 +371,52 @@ class Handle:
         arr, outs, owners, _keep = self._rows(rows, want_ownership)
         _check(lib().kg_get_output(self._h, len(rows), arr, outs))
         return [_output_dict(outs[i], owners[i]) for i in range(len(rows))]
+
+    @staticmethod
+    def _post(post, n):
+        """post: one dict per row with legal [362] (bool), white_to_move, board_x_size, board_y_size, and optional
+        nn_policy_temperature (1.0), enable_passing_hacks (False), no_result_allowed (True)."""
+        if len(post) != n:
+            raise ValueError(f"need {n} post-processing rows, got {len(post)}")
+        arr = (PostInput * n)()
+        keep = []
+        for i, q in enumerate(post):
+            legal = np.ascontiguousarray(q["legal"], np.uint8)
+            if legal.shape != (MAX_POLICY,):
+                raise ValueError(f"legal must be [{MAX_POLICY}], got {legal.shape}")
+            keep.append(legal)
+            arr[i].legal = _ptr(legal).value
+            arr[i].white_to_move = int(bool(q["white_to_move"]))
+            arr[i].board_x_size = int(q.get("board_x_size", 19))
+            arr[i].board_y_size = int(q.get("board_y_size", 19))
+            arr[i].nn_policy_temperature = float(q.get("nn_policy_temperature", 1.0))
+            arr[i].enable_passing_hacks = int(bool(q.get("enable_passing_hacks", False)))
+            arr[i].no_result_allowed = int(bool(q.get("no_result_allowed", True)))
+        return arr, keep
+
+    def get_output_eval(self, rows, post, want_ownership=True):
+        """get_output followed by NNEvaluator's post-processing, on the device (kg_get_output_eval)."""
+        arr, outs, owners, _keep = self._rows(rows, want_ownership)
+        parr, _pkeep = self._post(post, len(rows))
+        _check(lib().kg_get_output_eval(self._h, len(rows), arr, parr, outs))
+        return [_output_dict(outs[i], owners[i]) for i in range(len(rows))]
+
+    def post_outputs(self, raw, symmetry, policy_optimism, post, want_ownership=True):
+        """copy_outputs and NNEvaluator's post-processing of raw rows given on the host, on the device
+        (kg_post_outputs)."""
+        raw = np.ascontiguousarray(raw, np.float32)
+        n = raw.shape[0]
+        if raw.shape != (n, self.net.row_len):
+            raise ValueError(f"raw rows must be [n, {self.net.row_len}], got {raw.shape}")
+        sym = np.ascontiguousarray(np.broadcast_to(symmetry, (n,)), np.int32)
+        opt = np.ascontiguousarray(np.broadcast_to(policy_optimism, (n,)), np.float32)
+        parr, _pkeep = self._post(post, n)
+        outs = (NNOutput * n)()
+        owners = [np.zeros(HW, np.float32) if want_ownership else None for _ in range(n)]
+        for i in range(n):
+            outs[i].white_owner_map = None if owners[i] is None else _ptr(owners[i]).value
+        _check(lib().kg_post_outputs(self._h, n, _ptr(raw), _ptr(sym), _ptr(opt), parr, outs))
+        return [_output_dict(outs[i], owners[i]) for i in range(n)]
 
     def get_output_async(self, rows, want_ownership=True, done=None):
         """get_output with the readback on the library's helper thread: returns once the batch is enqueued.

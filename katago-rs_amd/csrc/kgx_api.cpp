@@ -5,6 +5,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <cstring>
 #include <memory>
 #include <mutex>
@@ -39,6 +40,19 @@ struct kg_handle {
   float* h_glob = nullptr;
   float* h_meta = nullptr;
   float* h_out = nullptr;
+  // Buffers of the device post-processing (kg_get_output_eval, kg_post_outputs), allocated by their first call:
+  // device raw rows (kg_post_outputs' input), per-row parameters, legality, outputs and status, with pinned host
+  // staging for all but the raw rows (staged through h_out).
+  float* d_post_raw = nullptr;
+  kgx::PostRow* d_post_rows = nullptr;
+  unsigned char* d_legal = nullptr;
+  float* d_post_out = nullptr;
+  int* d_post_status = nullptr;
+  kgx::PostRow* h_post_rows = nullptr;
+  unsigned char* h_legal = nullptr;
+  float* h_post_out = nullptr;
+  int* h_post_status = nullptr;
+  kgx::PostModel post_model;
   // The readback of kg_get_output_async runs on this helper thread; the next call on the handle joins it first.
   std::thread helper;
   int helper_status = 0;
@@ -231,6 +245,81 @@ void copy_inputs(kg_handle* h, int n, const kg_row_input* rows) {
   }
 }
 
+// The device post-processing's buffers (first use on the handle). Caller holds h->mu, the handle's device current.
+void ensure_post(kg_handle* h) {
+  if (h->d_post_out) return;
+  const size_t B = (size_t)h->max_batch, rl = (size_t)h->net->row_len();
+  KGX_HIP(hipMalloc((void**)&h->d_post_raw, B * rl * 4));
+  KGX_HIP(hipMalloc((void**)&h->d_post_rows, B * sizeof(kgx::PostRow)));
+  KGX_HIP(hipMalloc((void**)&h->d_legal, B * (HW + 1)));
+  KGX_HIP(hipMalloc((void**)&h->d_post_status, B * sizeof(int)));
+  KGX_HIP(hipHostMalloc((void**)&h->h_post_rows, B * sizeof(kgx::PostRow), hipHostMallocDefault));
+  KGX_HIP(hipHostMalloc((void**)&h->h_legal, B * (HW + 1), hipHostMallocDefault));
+  KGX_HIP(hipHostMalloc((void**)&h->h_post_out, B * kgx::POST_LEN * 4, hipHostMallocDefault));
+  KGX_HIP(hipHostMalloc((void**)&h->h_post_status, B * sizeof(int), hipHostMallocDefault));
+  KGX_HIP(hipMalloc((void**)&h->d_post_out, B * kgx::POST_LEN * 4));
+}
+
+// NNEvaluator's inputs of the post-processing per row (nneval.rs:1197-1500), checked, into the pinned staging and
+// enqueued to the device.
+void stage_post(kg_handle* h, int n, const int* sym, const float* opt, const kg_post_input* post) {
+  for (int r = 0; r < n; r++) {
+    const kg_post_input& q = post[r];
+    if (sym[r] < 0 || sym[r] > 7) throw std::runtime_error("kgx backend: symmetry must be in [0, 8)");
+    if (!q.legal) throw std::runtime_error("kgx backend: null legality row");
+    if (q.board_x_size < 1 || q.board_x_size > POS || q.board_y_size < 1 || q.board_y_size > POS)
+      throw std::runtime_error("kgx backend: board size must be within the 19x19 input");
+    if (!(q.nn_policy_temperature > 0.f) || !std::isfinite(q.nn_policy_temperature))
+      throw std::runtime_error("kgx backend: nnPolicyTemperature must be positive");
+    int legal = 0;
+    for (int i = 0; i <= HW; i++) {
+      const unsigned char b = q.legal[i] != 0;
+      h->h_legal[(size_t)r * (HW + 1) + i] = b;
+      legal += b;
+    }
+    if (legal == 0) throw std::runtime_error("kgx backend: no legal move");  // the reference asserts legal_count > 0
+    kgx::PostRow& pr = h->h_post_rows[r];
+    pr.symmetry = sym[r];
+    pr.optimism = opt[r];
+    pr.white_to_move = q.white_to_move != 0;
+    pr.board_x = q.board_x_size;
+    pr.board_y = q.board_y_size;
+    pr.policy_scale = 1.0f / q.nn_policy_temperature;  // outputScaleMultiplier (1) / nnPolicyTemperature, in float
+    pr.passing_hacks = q.enable_passing_hacks != 0;
+    pr.no_result = q.no_result_allowed != 0;
+  }
+  KGX_HIP(hipMemcpyAsync(h->d_post_rows, h->h_post_rows, (size_t)n * sizeof(kgx::PostRow), hipMemcpyHostToDevice,
+                         h->stream));
+  KGX_HIP(hipMemcpyAsync(h->d_legal, h->h_legal, (size_t)n * (HW + 1), hipMemcpyHostToDevice, h->stream));
+}
+
+// The post-processing kernel on n raw rows on the device, one readback of its rows and statuses, and the fields
+// into the caller's outputs; a nonfinite row fails with the reference's message.
+void post_and_read(kg_handle* h, int n, const float* d_raw, kg_nn_output* outputs) {
+  kgx::launch_post(d_raw, h->net->row_len(), h->d_post_rows, h->d_legal, h->post_model, h->d_post_out,
+                   h->d_post_status, n, h->stream);
+  KGX_HIP(hipMemcpyAsync(h->h_post_out, h->d_post_out, (size_t)n * kgx::POST_LEN * 4, hipMemcpyDeviceToHost,
+                         h->stream));
+  KGX_HIP(hipMemcpyAsync(h->h_post_status, h->d_post_status, (size_t)n * sizeof(int), hipMemcpyDeviceToHost,
+                         h->stream));
+  KGX_HIP(hipStreamSynchronize(h->stream));
+  for (int r = 0; r < n; r++) {
+    const int st = h->h_post_status[r];
+    if (st & 1) throw std::runtime_error("Got nonfinite for policy sum");
+    if (st & 2) throw std::runtime_error("Got nonfinite for nneval value");
+  }
+  for (int r = 0; r < n; r++) {
+    const float* p = h->h_post_out + (size_t)r * kgx::POST_LEN;
+    kg_nn_output& o = outputs[r];
+    std::memcpy(o.policy_probs, p, (HW + 1) * sizeof(float));
+    const float* v = p + HW + 1;
+    o.white_win_prob = v[0]; o.white_loss_prob = v[1]; o.white_no_result_prob = v[2];
+    o.white_score_mean = v[3]; o.white_score_mean_sq = v[4]; o.white_lead = v[5]; o.var_time_left = v[6];
+    o.shortterm_winloss_error = v[7]; o.shortterm_score_error = v[8];
+    if (o.white_owner_map) std::memcpy(o.white_owner_map, v + 9, HW * sizeof(float));
+  }
+}
+
 void upload_rows(kg_handle* h, int n) {
   KGX_HIP(hipMemcpyAsync(h->net->d_bin(), h->h_bin, (size_t)n * h->nin * HW * 4, hipMemcpyHostToDevice, h->stream));
   KGX_HIP(hipMemcpyAsync(h->net->d_global(), h->h_glob, (size_t)n * h->nglob * 4, hipMemcpyHostToDevice, h->stream));
@@ -336,6 +425,11 @@ int kg_handle_create(const kg_net* net, int device, int max_batch, int precision
     KGX_HIP(hipHostMalloc((void**)&h->h_glob, (size_t)max_batch * h->nglob * 4, hipHostMallocDefault));
     if (h->nmeta) KGX_HIP(hipHostMalloc((void**)&h->h_meta, (size_t)max_batch * h->nmeta * 4, hipHostMallocDefault));
     KGX_HIP(hipHostMalloc((void**)&h->h_out, (size_t)max_batch * m.row_len() * 4, hipHostMallocDefault));
+    h->post_model.P = h->P;
+    h->post_model.S = h->S;
+    h->post_model.version = h->model_version;
+    // ModelPostProcessParams: the model file's floats widened to double (bin2onnx.py:1025-1031).
+    for (int k = 0; k < 7; k++) h->post_model.pp[k] = (double)m.post_process[k];
     std::memset(h->h_bin, 0, (size_t)max_batch * h->nin * HW * 4);
     std::memset(h->h_glob, 0, (size_t)max_batch * h->nglob * 4);
     if (h->nmeta) std::memset(h->h_meta, 0, (size_t)max_batch * h->nmeta * 4);
@@ -356,6 +450,15 @@ void kg_handle_free(kg_handle* h) {
   if (h->h_glob) (void)hipHostFree(h->h_glob);
   if (h->h_meta) (void)hipHostFree(h->h_meta);
   if (h->h_out) (void)hipHostFree(h->h_out);
+  if (h->d_post_raw) (void)hipFree(h->d_post_raw);
+  if (h->d_post_rows) (void)hipFree(h->d_post_rows);
+  if (h->d_legal) (void)hipFree(h->d_legal);
+  if (h->d_post_out) (void)hipFree(h->d_post_out);
+  if (h->d_post_status) (void)hipFree(h->d_post_status);
+  if (h->h_post_rows) (void)hipHostFree(h->h_post_rows);
+  if (h->h_legal) (void)hipHostFree(h->h_legal);
+  if (h->h_post_out) (void)hipHostFree(h->h_post_out);
+  if (h->h_post_status) (void)hipHostFree(h->h_post_status);
   if (h->stream) (void)hipStreamDestroy(h->stream);
   delete h;
 }
@@ -484,6 +587,49 @@ int kg_get_output(kg_handle* h, int n, const kg_row_input* rows, kg_nn_output* o
     for (int r = 0; r < n; r++)
       copy_outputs_row(h->h_out + (size_t)r * rl, h->P, h->S, h->model_version, rows[r].symmetry,
                        rows[r].policy_optimism, outputs[r]);
+  });
+}
+
+int kg_get_output_eval(kg_handle* h, int n, const kg_row_input* rows, const kg_post_input* post,
+                       kg_nn_output* outputs) {
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    if (!rows || !post || !outputs) throw std::runtime_error("null rows, post-processing inputs or outputs");
+    std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
+    if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
+    copy_inputs(h, n, rows);
+    std::vector<int> sym(n);
+    std::vector<float> opt(n);
+    for (int r = 0; r < n; r++) {
+      sym[r] = rows[r].symmetry;
+      opt[r] = rows[r].policy_optimism;
+    }
+    KGX_HIP(hipSetDevice(h->device));
+    ensure_post(h);
+    stage_post(h, n, sym.data(), opt.data(), post);
+    const int n_run = padded_batch_size(h->buckets, n, h->max_batch);
+    upload_rows(h, n);
+    h->net->forward(n_run, h->stream);
+    post_and_read(h, n, h->net->d_out(), outputs);
+  });
+}
+
+int kg_post_outputs(kg_handle* h, int n, const float* raw, const int* symmetry, const float* policy_optimism,
+                    const kg_post_input* post, kg_nn_output* outputs) {
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    if (!raw || !symmetry || !policy_optimism || !post || !outputs) throw std::runtime_error("null argument");
+    std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
+    if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
+    KGX_HIP(hipSetDevice(h->device));
+    ensure_post(h);
+    stage_post(h, n, symmetry, policy_optimism, post);
+    const size_t bytes = (size_t)n * h->net->row_len() * 4;
+    std::memcpy(h->h_out, raw, bytes);
+    KGX_HIP(hipMemcpyAsync(h->d_post_raw, h->h_out, bytes, hipMemcpyHostToDevice, h->stream));
+    post_and_read(h, n, h->d_post_raw, outputs);
   });
 }
 

@@ -252,6 +252,30 @@ struct AttnArgs {
 };
 void launch_attention(int prec, const AttnArgs& a, int B, hipStream_t s);
 
+// The per-row output post-processing on the device (kgx_post.hip): copy_outputs (optimism mix, inverse symmetry,
+// fields by model version) then NNEvaluator's policy softmax over the legal moves, value softmax, score transforms
+// and tanh ownership. Output per row: POST_LEN floats, the policy probabilities [362] (-1 for illegal moves),
+// then white win, loss, no-result probabilities, score mean, score mean square, lead, variance time left,
+// short-term winloss and score errors [9], then the ownership [361] (white's perspective, 0 off the board).
+// status[r]: 0, or bit 0 a nonfinite policy sum, bit 1 a nonfinite value or score field.
+constexpr int POST_LEN = HW + 1 + 9 + HW;
+struct PostRow {
+  int symmetry = 0;          // 0..7 (bit 0 flips y, bit 1 flips x, bit 2 transposes)
+  float optimism = 0.f;      // policy optimism
+  int white_to_move = 0;     // the net's outputs are the player to move's: 1 when that is white
+  int board_x = POS, board_y = POS;
+  float policy_scale = 1.f;  // outputScaleMultiplier / nnPolicyTemperature
+  int passing_hacks = 0;     // cap the pass prior at 19 times the other moves
+  int no_result = 1;         // no-result outcomes count (simple ko or territory scoring)
+};
+struct PostModel {
+  int P = 1, S = 6, version = 8;
+  double pp[7] = {20, 20, 20, 20, 40, 0.25, 30};  // td score, score mean, score stdev, lead, variance time, st value
+                                                   // error, st score error multipliers
+};
+void launch_post(const float* raw, int row_len, const PostRow* rows, const unsigned char* legal, const PostModel& m,
+                 float* out, int* status, int n, hipStream_t s);
+
 // FFN activation: h = silu(u[:, :F]) * u[:, F:2F] (gated) or mish(u[:, :F]), u float [rows][ldu] -> compute type.
 void launch_ffn_act(int prec, const float* u, int ldu, int F, bool gated, void* h, int ldh, int rows, hipStream_t s);
 

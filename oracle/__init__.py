@@ -42,6 +42,11 @@ def lib():
         L.kgo_padded_batch_size.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int]
         L.kgo_copy_outputs_row.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                            ctypes.c_float, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        L.kgo_postprocess_row.restype = ctypes.c_int
+        L.kgo_postprocess_row.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_float, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                          ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                          ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -157,6 +162,27 @@ def copy_outputs_row(row, P, S, version, sym, optimism, want_owner=True):
     own = np.zeros(361, np.float32) if want_owner else None
     lib().kgo_copy_outputs_row(_p(row), P, S, version, sym, ctypes.c_float(optimism), _p(pol), _p(fields), _p(own))
     return pol, fields, own
+
+
+# The model's post-process multipliers (ModelPostProcessParams: td score, score mean, score stdev, lead, variance
+# time, short-term value error, short-term score error), the defaults of the model files without them.
+DEFAULT_POST_PARAMS = (20.0, 20.0, 20.0, 20.0, 40.0, 0.25, 30.0)
+
+
+def postprocess_row(row, P, S, version, sym, optimism, legal, white, bx, by, temperature=1.0, passing_hacks=False,
+                    no_result_allowed=True, pp=DEFAULT_POST_PARAMS):
+    """NNEvaluator's post-processing of one raw row (copy_outputs, then nneval.rs:1197-1500): (status, policy
+    [362], fields [9], ownership [361]); status 1 / 2 are the reference's nonfinite policy / value errors."""
+    row = np.ascontiguousarray(row, np.float32)
+    legal = np.ascontiguousarray(legal, np.uint8)
+    ppa = np.ascontiguousarray(pp, np.float64)
+    pol = np.zeros(362, np.float32)
+    fields = np.zeros(9, np.float32)
+    own = np.zeros(361, np.float32)
+    st = lib().kgo_postprocess_row(_p(row), P, S, version, sym, ctypes.c_float(optimism), _p(legal), int(white), bx,
+                                   by, ctypes.c_float(temperature), int(passing_hacks), int(no_result_allowed),
+                                   _p(ppa), _p(pol), _p(fields), _p(own))
+    return st, pol, fields, own
 
 
 def round_operands(x, operands):

@@ -1139,4 +1139,108 @@ void kgo_copy_outputs_row(const float* row, int P, int S, int version, int sym, 
   }
 }
 
+// NNEvaluator's post-processing of one row's fields (crates/katago-core/src/neuralnet/nneval.rs:1197-1500), after
+// kgo_copy_outputs_row: the policy softmax over the legal moves (sequential float sums in position order, as the
+// reference), the passing cap (nneval.rs:1247-1258), the uniform fallback, the value softmax and score transforms
+// in double by model version (nneval.rs:1298-1477, soft_plus as nneval.rs:1582-1589), and tanh ownership from
+// white's perspective with 0 off the board (nneval.rs:1481-1497). The move legality is an input. Returns 0, or
+// 1 for a nonfinite policy sum, 2 for a nonfinite value field (the reference's two error returns).
+static double kgo_soft_plus(double x) { return x > 40.0 ? x : std::log(1.0 + std::exp(x)); }
+
+int kgo_postprocess_row(const float* row, int P, int S, int version, int sym, float optimism,
+                        const unsigned char* legal /*362*/, int white, int bx, int by, float temperature,
+                        int passing_hacks, int no_result_allowed, const double* pp /*7*/,
+                        float* policy /*362*/, float* fields /*9*/, float* owner /*361*/) {
+  float own[HW];
+  kgo_copy_outputs_row(row, P, S, version, sym, optimism, policy, fields, own);
+  const int n = HW + 1;
+  const float scaling = 1.0f / temperature;  // outputScaleMultiplier (1) / nnPolicyTemperature
+  float max_policy = -1e25f;
+  int legal_count = 0;
+  for (int i = 0; i < n; i++) {
+    float v;
+    if (legal[i]) { legal_count++; v = policy[i] * scaling; }
+    else v = -1e30f;
+    policy[i] = v;
+    if (v > max_policy) max_policy = v;
+  }
+  if (legal_count == 0) return 4;
+  float sum = 0.0f;
+  if (passing_hacks) {
+    for (int i = 0; i < n - 1; i++) { policy[i] = expf(policy[i] - max_policy); sum += policy[i]; }
+    policy[n - 1] = std::max(1e-20f, std::min(expf(policy[n - 1] - max_policy), sum * 19.0f));
+    sum += policy[n - 1];
+  } else {
+    for (int i = 0; i < n; i++) { policy[i] = expf(policy[i] - max_policy); sum += policy[i]; }
+  }
+  if (!std::isfinite(sum)) return 1;
+  if ((double)sum <= 0.0) {
+    const float uniform = 1.0f / legal_count;
+    for (int i = 0; i < n; i++) policy[i] = legal[i] ? uniform : -1.0f;
+  } else {
+    for (int i = 0; i < n; i++) policy[i] = legal[i] ? policy[i] / sum : -1.0f;
+  }
+  const float f_mean = fields[3], f_mean_sq = fields[4], f_lead = fields[5], f_var = fields[6];
+  const float f_stw = fields[7], f_sts = fields[8];
+  const double win_l = (double)fields[0], loss_l = (double)fields[1];
+  double nores_l = (double)fields[2];
+  if (version == 3) {
+    const double score_value = (double)atanf(f_mean) * 0.63661977236758134308;
+    const double mx = std::max(std::max(win_l, loss_l), nores_l);
+    double wp = std::exp(win_l - mx), lp = std::exp(loss_l - mx), np = std::exp(nores_l - mx);
+    const double ps = wp + lp + np;
+    wp /= ps; lp /= ps; np /= ps;
+    if (!std::isfinite(ps) || !std::isfinite(score_value)) return 2;
+    const double half_pi = 1.57079632679489661923, x = score_value * half_pi;
+    const double unscaled = x >= half_pi - 1e-6 ? 1e6 : x <= -half_pi + 1e-6 ? -1e6 : std::tan(x);
+    const float sm = (float)(unscaled * (2.0 * std::sqrt((double)bx * (double)by)));
+    const float wm = white ? sm : -sm;
+    fields[0] = (float)(white ? wp : lp); fields[1] = (float)(white ? lp : wp); fields[2] = (float)np;
+    fields[3] = wm; fields[4] = wm * wm; fields[5] = wm; fields[6] = -1.f; fields[7] = -1.f; fields[8] = -1.f;
+  } else if (version >= 4) {
+    if (!no_result_allowed) nores_l -= 100000.0;
+    const double mx = std::max(std::max(win_l, loss_l), nores_l);
+    double wp = std::exp(win_l - mx), lp = std::exp(loss_l - mx), np = std::exp(nores_l - mx);
+    if (!no_result_allowed) np = 0.0;
+    const double ps = wp + lp + np;
+    wp /= ps; lp /= ps; np /= ps;
+    double mean = (double)f_mean * pp[1];
+    const double stdev = kgo_soft_plus((double)f_mean_sq) * pp[2];
+    double mean_sq = mean * mean + stdev * stdev;
+    double lead = (double)f_lead * pp[3];
+    const double var = kgo_soft_plus((double)f_var) * pp[4];
+    mean *= 1.0 - np;
+    mean_sq *= 1.0 - np;
+    lead *= 1.0 - np;
+    double stw, sts;
+    if (version >= 14) {
+      const double a = kgo_soft_plus((double)f_stw * 0.5), b = kgo_soft_plus((double)f_sts * 0.5);
+      stw = std::sqrt(a * a * pp[5]);
+      sts = std::sqrt(b * b * pp[6]);
+    } else if (version >= 10) {
+      stw = std::sqrt(kgo_soft_plus((double)f_stw) * pp[5]);
+      sts = std::sqrt(kgo_soft_plus((double)f_sts) * pp[6]);
+    } else {
+      stw = kgo_soft_plus((double)f_stw);
+      sts = kgo_soft_plus((double)f_sts) * 10.0;
+    }
+    if (!std::isfinite(ps) || !std::isfinite(mean) || !std::isfinite(mean_sq) || !std::isfinite(lead) ||
+        !std::isfinite(var) || !std::isfinite(stw) || !std::isfinite(sts))
+      return 2;
+    fields[0] = (float)(white ? wp : lp); fields[1] = (float)(white ? lp : wp); fields[2] = (float)np;
+    fields[3] = white ? (float)mean : -(float)mean;
+    fields[4] = (float)mean_sq;
+    fields[5] = white ? (float)lead : -(float)lead;
+    if (version >= 9) { fields[6] = (float)var; fields[7] = (float)stw; fields[8] = (float)sts; }
+    else { fields[6] = -1.f; fields[7] = -1.f; fields[8] = -1.f; }
+  } else {
+    return 3;
+  }
+  for (int pos = 0; pos < HW; pos++) {
+    const int y = pos / POS, x = pos % POS;
+    owner[pos] = (y >= by || x >= bx) ? 0.0f : (white ? tanhf(own[pos]) : -tanhf(own[pos]));
+  }
+  return 0;
+}
+
 }  // extern "C"

@@ -1,0 +1,163 @@
+"""The device output post-processing (kg_post_outputs, kg_get_output_eval): copy_outputs
+(crates/katago-nn-burn/src/backend.rs:622-731) and NNEvaluator's arithmetic on the fields
+(crates/katago-core/src/neuralnet/nneval.rs:1197-1500), against the oracle's restatement
+(oracle.postprocess_row), on the device through the C ABI.
+
+Tolerances: the device computes the policy softmax in float with its own exp and a tree-ordered sum, the
+reference and the oracle sum in position order with glibc's expf, so probabilities agree to 2e-6 absolute plus
+2e-5 relative; the value and score fields are computed in double on both sides and agree to 2e-6 relative (the
+version 3 path through atanf and tan to 1e-5); tanh ownership to 2e-7 absolute. Illegal moves are -1 and
+off-board ownership 0 exactly.
+"""
+
+import dataclasses
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+VERSIONS = {  # model version -> (spatial, global) input channels of that version
+    3: (22, 14), 5: (22, 14), 8: (22, 19), 9: (22, 19), 10: (22, 19), 14: (22, 19), 16: (22, 19), 17: (22, 19),
+}
+
+
+def _arch(synth, v):
+    base = synth.tiny_nets()["t_v8"]
+    sp, gl = VERSIONS[v]
+    extra = {"policy_channels": 2} if v >= 17 else {}
+    return dataclasses.replace(base, model_version=v, num_input_channels=sp, num_global_channels=gl,
+                               name=f"t-post-v{v}", **extra)
+
+
+def _cases(rng, n, row_len):
+    raw = np.empty((n, row_len), np.float32)
+    raw[:] = rng.normal(0.0, 1.0, size=raw.shape)
+    raw[:, :362 * 4] *= 2.0
+    post, sym, opt = [], rng.integers(0, 8, n), rng.uniform(0.0, 1.0, n).astype(np.float32)
+    for i in range(n):
+        bx, by = [(19, 19), (13, 13), (9, 9), (19, 13), (7, 11)][i % 5]
+        legal = (rng.uniform(size=362) < 0.7).astype(np.uint8)
+        off = np.array([(p // 19 >= by or p % 19 >= bx) for p in range(361)] + [False])
+        legal[off] = 0
+        legal[361] = 1
+        post.append({"legal": legal, "white_to_move": bool(i % 2), "board_x_size": bx, "board_y_size": by,
+                     "nn_policy_temperature": [1.0, 0.5, 1.3][i % 3], "enable_passing_hacks": bool(i % 4 == 1),
+                     "no_result_allowed": bool(i % 3 != 2)})
+    return raw, sym, opt, post
+
+
+def _compare(res, ref, v, what):
+    st, pol, fields, own = ref
+    assert st == 0, f"{what}: oracle status {st}"
+    p = res["policy"]
+    illegal = pol == -1.0
+    assert np.array_equal(p[illegal], pol[illegal]), what
+    d = np.abs(p[~illegal] - pol[~illegal])
+    assert np.all(d <= 2e-6 + 2e-5 * np.abs(pol[~illegal])), f"{what}: policy max diff {d.max():.3e}"
+    names = ["white_win_prob", "white_loss_prob", "white_no_result_prob", "white_score_mean", "white_score_mean_sq",
+             "white_lead", "var_time_left", "shortterm_winloss_error", "shortterm_score_error"]
+    rel = 1e-5 if v == 3 else 2e-6
+    for k, name in enumerate(names):
+        a, b = res[name], fields[k]
+        assert abs(a - b) <= rel * max(1.0, abs(b)), f"{what}: {name} {a} vs {b}"
+    do = np.abs(res["ownership"] - own)
+    assert np.all(do <= 2e-7), f"{what}: ownership max diff {do.max():.3e}"
+    assert np.all(res["ownership"][own == 0.0] == 0.0), what
+
+
+@pytest.mark.parametrize("v", sorted(VERSIONS))
+def test_post_outputs_match_oracle(kgx, synth, oracle, v):
+    arch = _arch(synth, v)
+    net = kgx.Net(synth.write_model(arch, 3))
+    h = kgx.Handle(net, 8, "f32")
+    rng = np.random.default_rng(v)
+    raw, sym, opt, post = _cases(rng, 8, net.row_len)
+    res = h.post_outputs(raw, sym, opt, post)
+    pp = tuple(float(x) for x in net.desc.post_process_params)
+    for i in range(8):
+        q = post[i]
+        ref = oracle.postprocess_row(raw[i], net.P, net.S, v, int(sym[i]), float(opt[i]), q["legal"],
+                                     q["white_to_move"], q["board_x_size"], q["board_y_size"],
+                                     q["nn_policy_temperature"], q["enable_passing_hacks"], q["no_result_allowed"], pp)
+        _compare(res[i], ref, v, f"v{v} row {i}")
+    h.close()
+
+
+def test_post_outputs_edge_cases(kgx, synth, oracle):
+    net = kgx.Net(synth.write_model(_arch(synth, 14), 3))
+    h = kgx.Handle(net, 4, "f32")
+    rng = np.random.default_rng(5)
+    raw, sym, opt, post = _cases(rng, 4, net.row_len)
+    pp = tuple(float(x) for x in net.desc.post_process_params)
+    # The pass prior capped at 19 times the other moves: a dominant pass logit gets exactly 19 / 20.
+    raw[0, 361] = 20.0  # dominant, yet the others' sum (times 19) stays above the 1e-20 floor
+    raw[0, 362 + 361] = 20.0
+    post[0]["enable_passing_hacks"] = True
+    # A single legal move gets probability 1.
+    post[1]["legal"] = np.zeros(362, np.uint8)
+    post[1]["legal"][40] = 1
+    res = h.post_outputs(raw, sym, opt, post)
+    assert abs(res[0]["policy"][361] - 0.95) < 1e-6
+    assert res[1]["policy"][40] == 1.0 and np.all(np.delete(res[1]["policy"], 40) == -1.0)
+    for i in range(4):
+        q = post[i]
+        ref = oracle.postprocess_row(raw[i], net.P, net.S, 14, int(sym[i]), float(opt[i]), q["legal"],
+                                     q["white_to_move"], q["board_x_size"], q["board_y_size"],
+                                     q["nn_policy_temperature"], q["enable_passing_hacks"], q["no_result_allowed"], pp)
+        _compare(res[i], ref, 14, f"edge row {i}")
+    # The reference's two nonfinite errors, and the checks on the inputs.
+    bad = raw.copy()
+    bad[2, :362] = np.inf
+    post2 = [dict(q) for q in post]
+    post2[2]["legal"] = np.ones(362, np.uint8)
+    with pytest.raises(kgx.KgError, match="Got nonfinite for policy sum"):
+        h.post_outputs(bad, sym, opt, post2)
+    bad = raw.copy()
+    bad[3, net.P * 362] = np.inf
+    with pytest.raises(kgx.KgError, match="Got nonfinite for nneval value"):
+        h.post_outputs(bad, sym, opt, post)
+    post3 = [dict(q) for q in post]
+    post3[0]["legal"] = np.zeros(362, np.uint8)
+    with pytest.raises(kgx.KgError, match="no legal move"):
+        h.post_outputs(raw, sym, opt, post3)
+    post3 = [dict(q) for q in post]
+    post3[1]["board_x_size"] = 20
+    with pytest.raises(kgx.KgError, match="board size"):
+        h.post_outputs(raw, sym, opt, post3)
+    post3 = [dict(q) for q in post]
+    post3[2]["nn_policy_temperature"] = 0.0
+    with pytest.raises(kgx.KgError, match="nnPolicyTemperature"):
+        h.post_outputs(raw, sym, opt, post3)
+    # The handle still works after the errors.
+    res = h.post_outputs(raw, sym, opt, post)
+    assert abs(res[0]["policy"][361] - 0.95) < 1e-6
+    h.close()
+
+
+@pytest.mark.parametrize("prec", ["f32", "f16"])
+def test_get_output_eval_matches_forward_and_oracle(kgx, synth, oracle, prec):
+    """get_output with the post-processing on the device against the same handle's raw forward rows (inputs through
+    the row symmetry) post-processed by the oracle."""
+    arch = synth.tiny_nets()["t_rmspos"]  # v17, P = 2
+    net = kgx.Net(synth.write_model(arch, 4))
+    h = kgx.Handle(net, 6, prec)
+    sp, gl, _ = synth.make_inputs(6, 9, board_sizes=[19, 13, 9, 19, 13, 9])
+    rng = np.random.default_rng(11)
+    _, sym, opt, post = _cases(rng, 6, net.row_len)
+    for i, bs in enumerate([19, 13, 9, 19, 13, 9]):
+        post[i]["board_x_size"] = post[i]["board_y_size"] = bs
+        off = np.array([(p // 19 >= bs or p % 19 >= bs) for p in range(361)] + [False])
+        post[i]["legal"][off] = 0
+    rows = [{"spatial": sp[i], "glob": gl[i], "symmetry": int(sym[i]), "policy_optimism": float(opt[i])}
+            for i in range(6)]
+    res = h.get_output_eval(rows, post)
+    raw = h.forward(np.stack([oracle.copy_with_symmetry(sp[i:i + 1], int(sym[i]))[0] for i in range(6)]), gl)
+    pp = tuple(float(x) for x in net.desc.post_process_params)
+    for i in range(6):
+        q = post[i]
+        ref = oracle.postprocess_row(raw[i], net.P, net.S, arch.model_version, int(sym[i]), float(opt[i]),
+                                     q["legal"], q["white_to_move"], q["board_x_size"], q["board_y_size"],
+                                     q["nn_policy_temperature"], q["enable_passing_hacks"], q["no_result_allowed"], pp)
+        _compare(res[i], ref, arch.model_version, f"eval {prec} row {i}")
+    h.close()

@@ -217,3 +217,74 @@ def test_oracle_copy_outputs_sentinels_follow_every_reference_branch(oracle):
                 assert np.array_equal(gf, fields), (v, P, opt, sym, gf, fields)
                 assert np.array_equal(go, oracle.copy_with_symmetry(own.reshape(1, 1, 19, 19), sym,
                                                                     reverse=True).ravel()), (v, P, opt, sym)
+
+
+def _post_row(P, S, rng):
+    row = rng.normal(0.0, 1.0, size=P * 362 + 3 + S + 361).astype(np.float32)
+    return row
+
+
+def test_oracle_postprocess_policy_closed_forms(oracle):
+    """NNEvaluator's policy softmax (nneval.rs:1223-1292) against closed forms: two legal moves give the logistic
+    of their scaled difference; illegal moves are -1; the passing cap gives a dominant pass exactly 19 / 20; the
+    legal probabilities sum to 1."""
+    rng = np.random.default_rng(1)
+    row = _post_row(1, 6, rng)
+    legal = np.zeros(362, np.uint8)
+    legal[[10, 200]] = 1
+    for temp in (1.0, 0.5, 2.0):
+        st, pol, _, _ = oracle.postprocess_row(row, 1, 6, 14, 0, 0.0, legal, True, 19, 19, temp)
+        a, b = float(row[10]) / np.float32(temp), float(row[200]) / np.float32(temp)
+        assert st == 0
+        assert abs(pol[10] - 1.0 / (1.0 + np.exp(b - a))) < 1e-6
+        assert abs(pol[10] + pol[200] - 1.0) < 1e-6
+        assert np.all(np.delete(pol, [10, 200]) == -1.0)
+    legal = np.ones(362, np.uint8)
+    row2 = row.copy()
+    row2[361] = 20.0  # dominant, yet the others sum (times 19) stays above the 1e-20 floor
+    st, pol, _, _ = oracle.postprocess_row(row2, 1, 6, 14, 0, 0.0, legal, True, 19, 19, 1.0, True)
+    assert st == 0 and abs(pol[361] - 0.95) < 1e-6 and abs(pol.sum() - 1.0) < 1e-5
+    st, pol, _, _ = oracle.postprocess_row(row2, 1, 6, 14, 0, 0.0, legal, True, 19, 19, 1.0, False)
+    assert pol[361] > 0.9999  # without the cap the pass takes nearly everything
+
+
+def test_oracle_postprocess_value_closed_forms(oracle):
+    """The value and score transforms (nneval.rs:1298-1477) against closed forms: the value softmax sums to 1 and
+    swaps win and loss for black to move; no-result is 0 when the rules exclude it; version 9 score mean is
+    raw * 20 * (1 - noresult) and the stdev a softplus; version 3's score is 2 sqrt(area) times the raw value
+    (tan of its own arctan); ownership is +-tanh of the symmetry-mapped raw value and 0 off the board."""
+    rng = np.random.default_rng(2)
+    row = _post_row(1, 6, rng)
+    legal = np.ones(362, np.uint8)
+    st, _, fw, own_w = oracle.postprocess_row(row, 1, 6, 9, 0, 0.0, legal, True, 13, 13)
+    st2, _, fb, own_b = oracle.postprocess_row(row, 1, 6, 9, 0, 0.0, legal, False, 13, 13)
+    assert st == 0 and st2 == 0
+    v = row[362:365].astype(np.float64)
+    e = np.exp(v - v.max())
+    e /= e.sum()
+    assert np.allclose(fw[:3], e, rtol=1e-6) and np.allclose(fb[:3], [e[1], e[0], e[2]], rtol=1e-6)
+    s = row[365:371].astype(np.float64)
+    mean = s[0] * 20.0 * (1.0 - e[2])
+    stdev = np.log1p(np.exp(s[1])) * 20.0
+    assert abs(fw[3] - mean) <= 1e-5 * max(1.0, abs(mean)) and abs(fb[3] + mean) <= 1e-5 * max(1.0, abs(mean))
+    assert abs(fw[4] - (s[0] * 20.0) ** 2 * (1.0 - e[2]) - stdev ** 2 * (1.0 - e[2])) <= 1e-4 * max(1.0, fw[4])
+    own_raw = row[371:].reshape(19, 19)
+    expect = np.tanh(own_raw.astype(np.float64))
+    expect[13:, :] = 0.0
+    expect[:, 13:] = 0.0
+    assert np.allclose(own_w.reshape(19, 19), expect, atol=1e-6) and np.allclose(own_b, -own_w)
+    st, _, fr, _ = oracle.postprocess_row(row, 1, 6, 9, 0, 0.0, legal, True, 19, 19, no_result_allowed=False)
+    assert st == 0 and fr[2] == 0.0 and abs(fr[0] + fr[1] - 1.0) < 1e-6
+    # Version 3: one score channel; tan(atan(x)) = x, times 2 sqrt(board area).
+    row3 = _post_row(1, 1, rng)
+    row3[365] = 0.3
+    st, _, f3, _ = oracle.postprocess_row(row3, 1, 1, 3, 0, 0.0, legal, True, 9, 9)
+    assert st == 0 and abs(f3[3] - 0.3 * 2.0 * 9.0) < 1e-5 and f3[4] == np.float32(f3[3]) * np.float32(f3[3])
+    assert f3[6] == -1.0 and f3[7] == -1.0 and f3[8] == -1.0
+    # Nonfinite inputs: the reference's two errors.
+    bad = row.copy()
+    bad[:362] = np.inf
+    assert oracle.postprocess_row(bad, 1, 6, 9, 0, 0.0, legal, True, 19, 19)[0] == 1
+    bad = row.copy()
+    bad[362] = np.inf
+    assert oracle.postprocess_row(bad, 1, 6, 9, 0, 0.0, legal, True, 19, 19)[0] == 2
