@@ -465,6 +465,11 @@ __global__ __launch_bounds__(C::WM * C::WN * 64, C::MINW) void gemm_kernel(GemmA
 // linears), 64x64 for the rest.
 typedef Cfg<32, 192, 64, 1, 4, true> CfgNarrow;
 typedef Cfg<128, 128, 64, 2, 2, true> CfgWide;
+// 96x96 (three workgroups per CU) for a 16-bit GEMM whose 128x128 grid would not fill two workgroups per CU: there
+// the tile's serial chain sets the time, and a tile of 56 % of the work shortens it (b10c384h6's N = 384 GEMMs at
+// batch 32: 25.4 against 27.3 us per token GEMM on average, +5.4 % end to end). On grids that fill the chip the
+// 128x128 tile's reuse wins (N = 512 and 768 at batch 64: 71.6 against 76.2 us).
+typedef Cfg<96, 96, 64, 2, 2, true, 3> CfgMid;
 typedef Cfg<64, 64, 32, 2, 2> CfgSmall;
 typedef Cfg<64, 96, 64, 2, 2, true> CfgHead;  // the heads' first convolutions: N = p1 + g1 + v1 channels <= 96
 // Float operands on the head tile take 64 channels per stage (six stages at 384 channels): 20.8 against 21.8 us
@@ -511,6 +516,13 @@ static void gemm_cfg(const GemmArgs& g, hipStream_t s) {
   else if (g.N > 192 && g.N <= 384 && g.K % bk == 0 && AF) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
   else if constexpr (!AF) {
     // (Float-A prologue kernels are not built on the wide tile: their staging registers spill there.)
+    if constexpr (sizeof(T) == 2) {
+      const long wide_tiles = (long)((g.M + 127) / 128) * ((g.N + 127) / 128);
+      if (g.N > 128 && g.K % bk == 0 && !g.qkv.dq && g.Z == 1 && wide_tiles < 512) {
+        gemm_launch<T, CfgMid, AF, PRO, ACT>(g, s);
+        return;
+      }
+    }
     if (g.N > 128 && g.K % bk == 0 && (long)((g.M + 127) / 128) * ((g.N + 127) / 128) * g.Z >= 256)
       gemm_launch<T, CfgWide, AF, PRO, ACT>(g, s);
     else gemm_launch<T, CfgSmall, AF, PRO, ACT>(g, s);
