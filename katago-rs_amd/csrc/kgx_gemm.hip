@@ -465,10 +465,12 @@ __global__ __launch_bounds__(C::WM * C::WN * 64, C::MINW) void gemm_kernel(GemmA
 // linears), 64x64 for the rest.
 typedef Cfg<32, 192, 64, 1, 4, true> CfgNarrow;
 typedef Cfg<128, 128, 64, 2, 2, true> CfgWide;
-// 96x96 (three workgroups per CU) for a 16-bit GEMM whose 128x128 grid would not fill two workgroups per CU: there
-// the tile's serial chain sets the time, and a tile of 56 % of the work shortens it (b10c384h6's N = 384 GEMMs at
-// batch 32: 25.4 against 27.3 us per token GEMM on average, +5.4 % end to end). On grids that fill the chip the
-// 128x128 tile's reuse wins (N = 512 and 768 at batch 64: 71.6 against 76.2 us).
+// 96x96 (three workgroups per CU) for a 16-bit GEMM whose 128x128 grid would not fill two workgroups per CU, or
+// whose last round of them would be nearly empty at short K: there the tile's serial chain sets the time, and a
+// tile of 56 % of the work shortens it (b10c384h6 at batch 32: N = 384 GEMMs 25.4 against 27.3 us per token
+// GEMM on average, +5.4 % end to end; the N = 1536 FFN's third round, +3.4 % more). On grids that fill the chip
+// the 128x128 tile's reuse wins (N = 512 and 768 at batch 64: 71.6 against 76.2 us; tf3's K = 768 and 3072
+// GEMMs with a nearly empty last round: -1.6 %).
 typedef Cfg<96, 96, 64, 2, 2, true, 3> CfgMid;
 typedef Cfg<64, 64, 32, 2, 2> CfgSmall;
 typedef Cfg<64, 96, 64, 2, 2, true> CfgHead;  // the heads' first convolutions: N = p1 + g1 + v1 channels <= 96
@@ -517,8 +519,10 @@ static void gemm_cfg(const GemmArgs& g, hipStream_t s) {
   else if constexpr (!AF) {
     // (Float-A prologue kernels are not built on the wide tile: their staging registers spill there.)
     if constexpr (sizeof(T) == 2) {
+      // Also when a short-K GEMM's last round of 128x128 tiles would be under a quarter full.
       const long wide_tiles = (long)((g.M + 127) / 128) * ((g.N + 127) / 128);
-      if (g.N > 128 && g.K % bk == 0 && !g.qkv.dq && g.Z == 1 && wide_tiles < 512) {
+      const bool tail = (wide_tiles % 512) * 4 < 512 && g.K <= 512;
+      if (g.N > 128 && g.K % bk == 0 && !g.qkv.dq && g.Z == 1 && (wide_tiles < 512 || tail)) {
         gemm_launch<T, CfgMid, AF, PRO, ACT>(g, s);
         return;
       }
