@@ -183,6 +183,8 @@ struct RowMM {
   int dst = -1;                               // LDS float offset of the output, or -1
   float* out = nullptr; long ldout = 0; int ostride = 1; bool accumulate = false;
   int wlds = -1;                              // LDS float offset of a staged copy of W, or -1 (read from memory)
+  int wcols = 0;                              // with wlds and output splits: the copy holds only this workgroup's
+                                              // share of the columns, [IC][wcols]
 };
 // Optional last stage: the workgroup's share [o0, o1) of the last matmul's outputs (kept in LDS at its dst) is a
 // per-row channel bias, and out[m][c] = T(act((x[m][c] + bias_row[c]) * scale[c] + bias[c]) * mask[m]) for the

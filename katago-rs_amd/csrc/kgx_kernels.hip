@@ -273,13 +273,15 @@ __device__ void row_mm(const RowMM& m, int b, float* lds, float* red, int o_begi
     const float prev = op && m.accumulate ? *op : 0.f;
     float acc = 0.f;
     if (ks < nks && o < o_end) {
-      const float* wcol = (m.wlds >= 0 ? lds + m.wlds : m.W) + o;
+      const bool slice = m.wlds >= 0 && m.wcols > 0;
+      const float* wcol = slice ? lds + m.wlds + (o - o_begin) : (m.wlds >= 0 ? lds + m.wlds : m.W) + o;
+      const int wst = slice ? m.wcols : m.OC;
       for (int i0 = ks; i0 < m.IC; i0 += KB * nks) {
         float wv[KB], xv[KB];
 #pragma unroll
         for (int j = 0; j < KB; j++) {
           const int i = i0 + j * nks;
-          wv[j] = i < m.IC ? wcol[(size_t)i * m.OC] : 0.f;
+          wv[j] = i < m.IC ? wcol[(size_t)i * wst] : 0.f;
           xv[j] = i < m.IC ? (gin ? gin[i] : lin[i]) : 0.f;
         }
 #pragma unroll
@@ -329,11 +331,13 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
     for (int i = threadIdx.x; i < 2 * per; i += RP_NT) esb[i] = i < per ? E.scale[e_o0 + i] : E.bias[e_o0 + i - per];
   }
   {
-    // Staged weights: the whole set as one list of 16-byte vectors, RP_WB loads per thread in flight.
+    // Staged weights: the whole set as one list of 16-byte vectors, RP_WB loads per thread in flight. A matmul
+    // staged as a column share (wcols) contributes the IC rows of its wcols columns from this split's first one.
     constexpr int RP_WB = 8;
+    auto staged4 = [&](const RowMM& m) { return m.IC * (m.wcols > 0 ? m.wcols : m.OC) / 4; };
     int total = 0;
     for (int k = 0; k < P.nmm; k++)
-      if (P.mm[k].wlds >= 0) total += P.mm[k].IC * P.mm[k].OC / 4;
+      if (P.mm[k].wlds >= 0) total += staged4(P.mm[k]);
     for (int v0 = 0; v0 < total; v0 += RP_NT * RP_WB) {
       floatx4 buf[RP_WB];
       float* dst[RP_WB];
@@ -344,12 +348,18 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
         if (v < total) {
           for (; k < P.nmm; k++) {
             if (P.mm[k].wlds < 0) continue;
-            const int n4 = P.mm[k].IC * P.mm[k].OC / 4;
+            const int n4 = staged4(P.mm[k]);
             if (v < n4) break;
             v -= n4;
           }
-          buf[j] = *(const floatx4*)(P.mm[k].W + 4 * v);
-          dst[j] = lds + P.mm[k].wlds + 4 * v;
+          const RowMM& m = P.mm[k];
+          if (m.wcols > 0) {
+            const int q4 = m.wcols / 4, i = v / q4, c = (v - i * q4) * 4;
+            buf[j] = *(const floatx4*)(m.W + (size_t)i * m.OC + split * m.wcols + c);
+          } else {
+            buf[j] = *(const floatx4*)(m.W + 4 * v);
+          }
+          dst[j] = lds + m.wlds + 4 * v;
         }
       }
 #pragma unroll
@@ -429,10 +439,15 @@ static size_t row_prog_check(const RowProg& p) {
         ((uintptr_t)e.x | (uintptr_t)e.out) % 16)
       throw std::runtime_error("row program: unsupported emission layout");
   }
-  for (int k = 0; k < p.nmm; k++)
-    if (p.mm[k].wlds >= 0 && ((p.mm[k].IC * p.mm[k].OC) % 4 || p.mm[k].wlds % 4 ||
-                              p.mm[k].wlds + p.mm[k].IC * p.mm[k].OC > p.lds_floats))
+  for (int k = 0; k < p.nmm; k++) {
+    const RowMM& m = p.mm[k];
+    const int cols = m.wcols > 0 ? m.wcols : m.OC;
+    if (m.wlds >= 0 && ((m.IC * cols) % 4 || m.wlds % 4 || m.wlds + m.IC * cols > p.lds_floats))
       throw std::runtime_error("row program: bad staged weight layout");
+    // A column share is this workgroup's split of the (only) matmul's outputs, in 16-byte columns.
+    if (m.wcols > 0 && (m.wlds < 0 || m.wcols % 4 || m.OC % p.splits || m.wcols != m.OC / p.splits))
+      throw std::runtime_error("row program: bad staged weight share");
+  }
   if (lds > 64 * 1024) throw std::runtime_error("row program: too much LDS");
   if (p.splits < 1 || (p.splits > 1 && p.nmm != 1))
     throw std::runtime_error("row program: output splits need exactly one matmul");

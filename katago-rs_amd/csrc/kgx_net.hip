@@ -623,10 +623,20 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
           rp.emit.x = tmp; rp.emit.ldx = ct;
           rp.emit.scale = me.scale; rp.emit.bias = me.bias; rp.emit.act = me.act;
           rp.emit.out = me.out; rp.emit.ldo = me.ld; rp.emit.prec = prec;
+          // Each workgroup's share of the matmul's weights staged in LDS with the program's first loads, so the
+          // matmul after the pooling waits for no memory (17.7 -> 12.x us per row program at b18c384nbt).
+          const int share = cr / fsplits;
+          const int woff = (rp.lds_floats + 3) / 4 * 4;
+          const size_t lds = ((size_t)woff + 3 * cg * share + 2 * 1024 + HW + 2 * cr) * sizeof(float);
+          if (cr % fsplits == 0 && share % 4 == 0 && lds <= 64 * 1024) {
+            rp.mm[0].wlds = woff;
+            rp.mm[0].wcols = share;
+            rp.lds_floats = woff + 3 * cg * share;
+          }
         }
         Op pool;
         pool.launch = [=](hipStream_t s, int B) { launch_row_prog(rp, B, s); };
-        pool.cls = "row_prog";
+        pool.cls = "row_prog_gpool";
         pool.bytes_row = (double)HW * cg * 4 + (fuse ? (double)HW * cr * (4 + tsize()) : 0.0);
         pool.flops_row = 2.0 * 3 * cg * cr;
         ops_.push_back(pool);
@@ -767,7 +777,7 @@ void Net::build(const ModelDesc& m) {
     }
     Op op;
     op.launch = [=](hipStream_t s, int B) { launch_row_prog(rp, B, s); };
-    op.cls = "row_prog";
+    op.cls = "row_prog_input";
     op.flops_row = flops;
     ops_.push_back(op);
   }
@@ -886,7 +896,7 @@ void Net::build(const ModelDesc& m) {
     for (int k = 0; k < ps.n; k++) row_prog_stage_weights(ps.p[k], 60 * 1024);
     Op op;
     op.launch = [=](hipStream_t s, int B) { launch_row_progs(ps, B, s); };
-    op.cls = "row_prog";
+    op.cls = "row_prog_heads";
     op.bytes_row = (double)HW * (2 * cg + cv) * 4;
     ops_.push_back(op);
   }
