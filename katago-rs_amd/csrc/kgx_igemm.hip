@@ -40,7 +40,7 @@ struct IgCfg {
   static constexpr bool PAIRS = BM_ == 96;
 };
 
-template <typename T, typename C>
+template <typename T, typename C, bool POOL>
 __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restrict__ X, const T* __restrict__ Xlo,
                                                                int ldx, int IC, const T* __restrict__ W, int icp,
                                                                int OC, int M, ConvOut o) {
@@ -59,7 +59,9 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   constexpr int WTM = BM / WM, WTN = BN / WN, MB = WTM / 16, NB = WTN / 16;
   static_assert(WTM % 16 == 0 && WTN % 16 == 0 && BK % 32 == 0 && NT % KV == 0, "bad tile");
   constexpr int STAGE = (PL * AR + 1 + PL * TB) * LDK * 2;  // bytes (A rows, a zero row, B rows)
-  constexpr int EPI = C::G * BM * (BN + 4) * 4;       // bytes: one float tile per wave group
+  constexpr int EPI0 = C::G * BM * (BN + 4) * 4;      // bytes: one float tile per wave group
+  // (then, with pooling partials, per wave, pooled channel and segment a sum and a maximum)
+  constexpr int EPI = EPI0 + (POOL ? NT / 64 * 64 * 2 * 12 : 0);
   constexpr int NBUF = C::NBUF;
   constexpr int SE = STAGE / (int)sizeof(T);          // stage buffer size in elements
   __shared__ __align__(16) char smem[NBUF * STAGE > EPI ? NBUF * STAGE : EPI];
@@ -210,12 +212,13 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     }
   };
   // Epilogue mapping: thread tid finishes the four channels 4 * (tid % G4) of rows tid / G4 + e * RPE, so its
-  // emit scale and bias are loaded once. The 3x3 kernel reads the residual values before the main loop so that
-  // the reads overlap it, and on 48-column tiles also the masks and emit parameters (0.4-1 us less per conv than
-  // after the loop); the wider 3x3 tiles and the 1x1 kernel read those after (read early they spill: the 1x1 is
-  // held to 128 registers for two workgroups per CU).
+  // emit scale and bias are loaded once. The 3x3 kernel reads the residual values before the main loop so that the
+  // reads overlap it (the variant with pooling partials after), and on 48-column tiles also the masks and emit
+  // parameters (0.4-1 us less per conv than after the loop); the split 192-pixel 1x1 reads the residual early too;
+  // the wider 3x3 tiles and the other 1x1 kernels read the rest after (read early they spill: the 1x1 is held to
+  // 128 registers for two workgroups per CU).
   constexpr int G4 = BN / 4, RPE = NT / G4, EV = (BM + RPE - 1) / RPE;
-  constexpr bool YEARLY = C::KS == 3 || (C::SPLIT && C::BK == 64 && !C::PAIRS);
+  constexpr bool YEARLY = (C::KS == 3 && !POOL) || (C::SPLIT && C::BK == 64 && !C::PAIRS);
   constexpr bool SEARLY = YEARLY && C::BN <= 48;  // wider column tiles would spill with these registers live
   const int ec4 = tid % G4, er0 = tid / G4, en = n0 + 4 * ec4;
   const bool eon = er0 < RPE && en < OC;
@@ -249,11 +252,33 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   };
   if constexpr (YEARLY) load_y();
   if constexpr (SEARLY) load_side();
+  // Board pooling partials (PoolPart): the tile's last CT = BN - pp.rpt columns are pooled channels, summed and
+  // maxed per segment of the tile (the batch row of its first pixel, and the next one) and not stored; the regular
+  // columns before them go to y column ycol. The pooling pass has a mapping of its own: thread tid takes pooled
+  // channel pch = tid % CT of rows prow0 + j * pstep (CT a power of two from 4 to 64, so that the lanes holding
+  // one channel are CT apart in every wave). Its scale and bias, and the tile's board mask (into LDS), are read
+  // here, before the main loop, so that the pass waits for no memory.
+  const PoolPart& pp = o.pool;
+  const int ycol = POOL ? nt * pp.rpt + 4 * ec4 : en;
+  const bool pcol = POOL && 4 * ec4 >= pp.rpt;  // this thread's store columns are pooled
+  const int lct = POOL ? __builtin_ctz(BN - pp.rpt) : 0, CT = 1 << lct;
+  const int pch = tid & (CT - 1), prow0 = tid >> lct, pstep = NT >> lct;
+  __shared__ float pms[POOL ? BM : 1];
+  float psc, pbi, pmv;
+  if constexpr (POOL) {
+    static_assert(NT >= BM, "pooling partials: a thread per pixel row stages the mask");
+    psc = pp.scale[nt * CT + pch];
+    pbi = pp.bias[nt * CT + pch];
+    pmv = pp.mask[min(m0 + min(tid, BM - 1), M - 1)];
+  }
 
   // The zero row of every stage buffer (never written by the stage stores).
   for (int e = tid; e < NBUF * KV; e += NT) *(vec_t*)(As + (e / KV) * SE + ZR * LDK + (e % KV) * 8) = vec_t{0, 0, 0, 0};
   const int nk = icp / BK;
   load(0);
+  if constexpr (POOL) {
+    if (tid < BM) pms[tid] = pmv;  // ordered before the pass by the main loop's barriers
+  }
   if constexpr (NBUF == 1) {
     // One stage buffer: store, barrier, next loads in flight during the MFMAs, barrier.
     for (int kt = 0; kt < nk; kt++) {
@@ -294,11 +319,107 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
 #pragma unroll
   for (int e = 0; e < EV; e++) {
     const int row = er0 + e * RPE, m = m0 + row;
-    if (eon && row < BM && m < M) {
+    if (eon && !pcol && row < BM && m < M) {
       floatx4 sum = *(const floatx4*)(Cs + row * LDC + 4 * ec4);
 #pragma unroll
       for (int q = 1; q < G; q++) sum += *(const floatx4*)(Cs + q * BM * LDC + row * LDC + 4 * ec4);
-      conv_store4<T>(o, m, en, sum, yres[e], rmv[e], es, eb, mkv[e]);
+      conv_store4<T>(o, m, ycol, sum, yres[e], rmv[e], es, eb, mkv[e]);
+    }
+  }
+
+  if constexpr (POOL) {
+    // The pooling pass, after the stores (they drain meanwhile: its barrier waits for LDS only). Fixed-point sums as two 32-bit
+    // parts: round(x * 2^24) = hi * 2^24 + lo with hi = floor(x) and lo = round((x - hi) * 2^24) in [0, 2^24],
+    // exact per value, and summed exactly over a tile's 192 pixels for |x| < 2^23 (clamped there): hi as int,
+    // lo as unsigned (at most 192 * 2^24 < 2^32). Rows from r1 on belong to the next batch row (segment 1).
+    const int b0 = m0 / HW, r1 = (b0 + 1) * HW - m0, rows = min(BM, M - m0), pcl = pp.rpt + pch;
+    int h0 = 0, h1 = 0;
+    unsigned l0 = 0, l1 = 0;
+    float x0 = -FLT_MAX, x1 = -FLT_MAX;
+    // A rolled loop per activation: the pass runs once per workgroup, from a cold instruction cache.
+    auto pool_rows = [&](auto act_c) {
+      constexpr int A = decltype(act_c)::value;
+#pragma unroll 1
+      for (int row = prow0; row < rows; row += pstep) {
+        float a = Cs[row * LDC + pcl];
+#pragma unroll
+        for (int q = 1; q < G; q++) a += Cs[q * BM * LDC + row * LDC + pcl];
+        const float mk = pms[row], x = act_f<A>(a * psc + pbi) * mk, pen = mk * 1e4f - 1e4f;
+        const float xc = fminf(fmaxf(x, -8388607.f), 8388607.f), h = floorf(xc);
+        const int qh = (int)h;
+        const unsigned ql = (unsigned)rintf((xc - h) * kPoolFix);
+        if (row >= r1) {
+          h1 += qh; l1 += ql; x1 = fmaxf(x1, x + pen);
+        } else {
+          h0 += qh; l0 += ql; x0 = fmaxf(x0, x + pen);
+        }
+      }
+    };
+    switch (pp.act) {
+      case ACT_RELU: pool_rows(std::integral_constant<int, ACT_RELU>{}); break;
+      case ACT_MISH: pool_rows(std::integral_constant<int, ACT_MISH>{}); break;
+      case ACT_SILU: pool_rows(std::integral_constant<int, ACT_SILU>{}); break;
+      default: pool_rows(std::integral_constant<int, ACT_ID>{}); break;
+    }
+    // Lanes pch, pch + CT, ... of a wave hold the same channel: summed by row rotations within 16-lane rows (DPP,
+    // for CT 4 and 8) and lane swaps across rows (v_permlane16_swap / v_permlane32_swap in inline assembly: the
+    // builtins fold both results into one when both operands hold the same value), so that lane pch holds the
+    // wave's total. The waves' totals then meet in LDS after the accumulator tiles and are reduced in wave order;
+    // segment 1 is written only when the tile reaches into the next batch row.
+    auto red = [&](auto v, auto op) {
+      typedef decltype(v) V;
+      auto rot = [&](V u, auto ctl) -> V {
+        return __builtin_bit_cast(V, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, u), decltype(ctl)::value,
+                                                                 0xf, 0xf, false));
+      };
+      if (CT <= 4) v = op(v, rot(v, std::integral_constant<int, 0x124>{}));  // row_ror:4
+      if (CT <= 8) v = op(v, rot(v, std::integral_constant<int, 0x128>{}));  // row_ror:8
+      if (CT <= 16) {
+        V a = v, b = v;
+        asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+        v = op(a, b);
+      }
+      if (CT <= 32) {
+        V a = v, b = v;
+        asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+        v = op(a, b);
+      }
+      return v;
+    };
+    auto add_i = [](int a, int b) { return a + b; };
+    auto add_u = [](unsigned a, unsigned b) { return a + b; };
+    auto max_f = [](float a, float b) { return fmaxf(a, b); };
+    h0 = red(h0, add_i); h1 = red(h1, add_i);
+    l0 = red(l0, add_u); l1 = red(l1, add_u);
+    x0 = red(x0, max_f); x1 = red(x1, max_f);
+    constexpr int NW = NT / 64;
+    long long* RS = (long long*)(smem + EPI0);  // [wave][channel][segment]
+    float* RX = (float*)(RS + NW * 64 * 2);
+    if (lane < CT) {
+      const int at = ((tid >> 6) * 64 + lane) * 2;
+      RS[at] = (long long)h0 * (1 << 24) + (long long)l0;
+      RS[at + 1] = (long long)h1 * (1 << 24) + (long long)l1;
+      RX[at] = x0;
+      RX[at + 1] = x1;
+    }
+    __syncthreads();
+    const bool has1 = r1 < rows;
+    if (tid < 4 * CT) {
+      const int ch = tid & (CT - 1), seg = (tid >> lct) & 1, isMax = tid >> (lct + 1);
+      if (seg == 0 || has1) {
+        const size_t at = (size_t)(mt * 2 + seg) * pp.C + nt * CT + ch;
+        if (isMax) {
+          float v = -FLT_MAX;
+#pragma unroll
+          for (int w = 0; w < NW; w++) v = fmaxf(v, RX[(w * 64 + ch) * 2 + seg]);
+          pp.pmax[at] = v;
+        } else {
+          long long v = 0;
+#pragma unroll
+          for (int w = 0; w < NW; w++) v += RS[(w * 64 + ch) * 2 + seg];
+          pp.psum[at] = v;
+        }
+      }
     }
   }
 }
@@ -358,7 +479,16 @@ static void igemm_launch(const void* x, const void* xlo, int ldx, int IC, const 
   const int mtiles = (M + C::BM - 1) / C::BM, ntiles = (OC + C::BN - 1) / C::BN;
   // Pairs: ceil(pairs / 8) pairs per XCD, two tiles each.
   dim3 grid(C::PAIRS ? 8 * ((mtiles + 15) / 16) * 2 * ntiles : round_up(mtiles, 8) * ntiles);
-  launch_k(igemm_kernel<T, C>, grid, C::NT, 0, s, (const T*)x, (const T*)xlo, ldx, IC, (const T*)w, icp, OC, M, o);
+  if constexpr (C::KS == 3 && 64 % (C::BN / 4) == 0) {
+    if (o.pool.psum) {
+      launch_k(igemm_kernel<T, C, true>, grid, C::NT, 0, s, (const T*)x, (const T*)xlo, ldx, IC, (const T*)w, icp, OC,
+               M, o);
+      return;
+    }
+  }
+  if (o.pool.psum) throw std::runtime_error("conv_igemm: no pooling partials for this convolution's tile");
+  launch_k(igemm_kernel<T, C, false>, grid, C::NT, 0, s, (const T*)x, (const T*)xlo, ldx, IC, (const T*)w, icp, OC, M,
+           o);
 }
 
 template <typename T>
@@ -386,6 +516,23 @@ const char* conv_igemm_class(int ks, int ic, int oc, bool split) {
     case IG1_128S: return "conv1x1_split_k128";
     case IG1_48S: return "conv1x1_split_n96";
     default: return "conv1x1";
+  }
+}
+
+int conv_igemm_pool_cols(int ks, int ic, int oc) {
+  // The 3x3 tiles of 64 columns (16 channel groups: the lane swaps of the partials' reduction), 192 pixels each.
+  return igemm_kind(ks, ic, oc, false) == IG3_64 ? Ig3n64::BN : 0;
+}
+
+int conv_igemm_tile_rows(int ks, int ic, int oc, bool split) {
+  switch (igemm_kind(ks, ic, oc, split)) {
+    case IG3_48: return Ig3::BM;
+    case IG3_64: return Ig3n64::BM;
+    case IG3_96: return Ig3n96::BM;
+    case IG1_128: return Ig1k128::BM;
+    case IG1_128S: return Ig1k128s::BM;
+    case IG1_48S: return Ig1sh::BM;
+    default: return Ig1::BM;
   }
 }
 
@@ -440,6 +587,15 @@ void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const v
     throw std::runtime_error("conv_igemm: channel counts must be multiples of 8 (inputs) and 4 (outputs)");
   if ((o.y && o.ldy % 4) || (o.yt && o.ldyt % 4) || (o.colbias && o.ld_colbias % 4) || (o.emit.scale && o.emit.ld % 4))
     throw std::runtime_error("conv_igemm: output strides must be multiples of 4");
+  if (o.pool.psum) {
+    const int pbn = conv_igemm_pool_cols(ks, IC, OC);
+    const PoolPart& p = o.pool;
+    const int ct = pbn - p.rpt;  // pooled channels per tile: a power of two from 4 to 64
+    if (!pbn || OC % pbn || p.rpt < 0 || ct < 4 || ct > 64 || (ct & (ct - 1)) ||
+        p.C != OC / pbn * (pbn - p.rpt) || !p.pmax ||
+        !p.scale || !p.bias || !p.mask || o.colbias || o.rowmask || o.accumulate || o.yt || o.emit.scale || x_lo)
+      throw std::runtime_error("conv_igemm: unsupported pooling partials");
+  }
   const int M = B * HW, kind = igemm_kind(ks, IC, OC, split);
   if (prec == PREC_F16) igemm_dispatch<f16>(kind, x, x_lo, ldx, IC, w, icp, OC, o, M, s);
   else igemm_dispatch<bf16>(kind, x, x_lo, ldx, IC, w, icp, OC, o, M, s);

@@ -40,6 +40,27 @@ struct Emit {
   int ld = 0;
 };
 
+// Board pooling partials of an implicit-GEMM convolution's pooled branch (a global-pooling block's gpool
+// channels), computed in the epilogue. The convolution's weights interleave the branches per column tile of BN
+// outputs (conv_igemm_pool_cols): tile t's first `rpt` columns are regular channels t * rpt + j, stored to y as
+// usual (y holds the regular channels only, in their own order); its other BN - rpt columns are pooled channels
+// c = t * (BN - rpt) + j, which are not stored. Every workgroup thus carries an equal share of the pooling. Per
+// tile of BM pixels mt (conv_igemm_tile_rows) and segment s (0: the batch row of the tile's first pixel, 1: the
+// next row, when the tile reaches into it),
+//   psum[(mt * 2 + s) * C + c] = sum of round(x * 2^24) over the segment's pixels (64-bit integers: exact, so a
+//                                row's sum does not depend on how its tiles cut it, i.e. on its batch position),
+//   pmax[(mt * 2 + s) * C + c] = max of x + (mask[m] * 1e4 - 1e4),
+// with x = act(v * scale[c] + bias[c]) * mask[m]. Requires rpt a multiple of 4, (BN - rpt) / 4 a power of two up
+// to 16, C = (OC / BN) (BN - rpt), and no colbias, rowmask, residual, compute-type copy or emission.
+constexpr float kPoolFix = 16777216.f;  // 2^24: the fixed-point scale of the partial sums
+struct PoolPart {
+  long long* psum = nullptr;
+  float* pmax = nullptr;
+  const float* scale = nullptr; const float* bias = nullptr; int act = ACT_ID;
+  const float* mask = nullptr;
+  int rpt = 0, C = 0;
+};
+
 // Output of a convolution or GEMM, element (m, n) with accumulated value v:
 // v += colbias[m / HW][n]; v *= rowmask[m]; yt = T(v); y = (accumulate ? y : 0) + v; then the emission from y.
 struct ConvOut {
@@ -51,6 +72,7 @@ struct ConvOut {
   const float* rowmask = nullptr;
   void* yt = nullptr; int ldyt = 0;
   Emit emit;
+  PoolPart pool;  // implicit-GEMM convolutions only
 };
 
 // Winograd F(tm x tm, 3x3), tm = 4 (36 tile points, 25 tiles per board) or 2 (16 points, 100 tiles).
@@ -122,6 +144,10 @@ int conv_igemm_icp(int ks, int ic, int oc, bool split = false);
 // The profiling class of the configuration a convolution of these channel counts runs with (one per kernel
 // instantiation: "conv3x3" is the 48-column 3x3 tile, "conv1x1_split_k128" the split 1x1 on 128-channel stages, ...).
 const char* conv_igemm_class(int ks, int ic, int oc, bool split = false);
+// Pixels per tile of the convolution of these channel counts (the tile of PoolPart's partials), and the columns
+// per tile (BN) when its kernel computes pooling partials (3x3 with 64-channel column tiles, 192 pixels), else 0.
+int conv_igemm_tile_rows(int ks, int ic, int oc, bool split = false);
+int conv_igemm_pool_cols(int ks, int ic, int oc);
 // w [oc][ic][ks][ks] -> [oc tile][tap][BN][icp] float; with `split` -> [oc tile][hi, lo][tap][BN][icp], the low
 // plane holding w - round(w) for the compute type `prec`.
 void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector<float>& out, bool split = false,
@@ -170,6 +196,8 @@ void launch_small_matmul(const float* in, int ldin, int IC, const float* W, int 
 // a stride, optionally accumulated). Replaces a pooling launch plus a launch per matmul.
 struct RowPool {
   const float* x = nullptr; int ldx = 0, coff = 0, C = 0;
+  // Or the producer's partials (PoolPart, tiles of ppt pixels): the row's sums and maxima are combined from them.
+  const long long* psum = nullptr; const float* pmax = nullptr; int ppt = 0;
   const float* scale = nullptr; const float* bias = nullptr; int act = ACT_ID;  // prologue (scale null: none)
   bool value = false;
   int dst = 0;  // LDS float offset of the 3C features

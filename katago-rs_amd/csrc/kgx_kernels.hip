@@ -308,6 +308,23 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
   float* mk = red + 2 * RP_NT;
   if (P.npool > 0)
     for (int p = threadIdx.x; p < HW; p += RP_NT) mk[p] = P.mask[(size_t)b * HW + p];
+  // Pooling from the producer's partials (RowPool::part, first pooling only): this thread's channel's sums and
+  // maxima of the row's tiles (at most three), loaded with the program's first loads.
+  const RowPool* pq = P.npool > 0 && P.pool[0].psum ? &P.pool[0] : nullptr;
+  long long pps[3] = {0, 0, 0};
+  float ppm[3] = {-FLT_MAX, -FLT_MAX, -FLT_MAX};
+  if (pq && (int)threadIdx.x < pq->C) {
+    const int t0 = b * HW / pq->ppt, t1 = (b * HW + HW - 1) / pq->ppt;
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+      const int t = t0 + j;
+      if (t <= t1) {
+        const size_t at = (size_t)(t * 2 + (t * pq->ppt / HW == b ? 0 : 1)) * pq->C + threadIdx.x;
+        pps[j] = pq->psum[at];
+        ppm[j] = pq->pmax[at];
+      }
+    }
+  }
   // The emission's inputs come first: this thread's x vectors into registers, the share's batch-norm scale and
   // bias into LDS after the mask (the barrier after the weight staging publishes them).
   const RowEmit& E = P.emit;
@@ -368,7 +385,22 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
     }
     __syncthreads();
   }
-  for (int k = 0; k < P.npool; k++) row_pool(P, P.pool[k], b, lds + P.pool[k].dst, red, mk);
+  for (int k = 0; k < P.npool; k++) {
+    if (k == 0 && pq) {
+      if ((int)threadIdx.x < pq->C) {
+        const float s = (float)((double)(pps[0] + pps[1] + pps[2]) / (double)kPoolFix);
+        const float m = fmaxf(fmaxf(ppm[0], ppm[1]), ppm[2]);
+        const float mean = s / P.area[b];
+        float* feat = lds + pq->dst;
+        feat[threadIdx.x] = mean;
+        feat[pq->C + threadIdx.x] = mean * P.s1[b];
+        feat[2 * pq->C + threadIdx.x] = pq->value ? mean * P.s2[b] : m;
+      }
+      __syncthreads();
+    } else {
+      row_pool(P, P.pool[k], b, lds + P.pool[k].dst, red, mk);
+    }
+  }
   for (int k = 0; k < P.nmm; k++) {
     const RowMM& m = P.mm[k];
     int o0 = 0, o1 = m.OC;
@@ -452,8 +484,14 @@ static size_t row_prog_check(const RowProg& p) {
   if (p.splits < 1 || (p.splits > 1 && p.nmm != 1))
     throw std::runtime_error("row program: output splits need exactly one matmul");
   for (int k = 0; k < p.npool; k++) {
-    // Pooled in chunks of 64 channels: every chunk's C/4 threads per point must divide 64 (16-byte loads).
     const RowPool& q = p.pool[k];
+    // From partials: the first pooling only, a thread per channel, at most three tiles per row.
+    if (q.psum) {
+      if (k != 0 || !q.pmax || q.C > RP_NT || q.ppt * 2 < HW - 1)
+        throw std::runtime_error("row program: unsupported pooling partials");
+      continue;
+    }
+    // Pooled in chunks of 64 channels: every chunk's C/4 threads per point must divide 64 (16-byte loads).
     const int last = q.C % 64 ? q.C % 64 : 64;
     if (q.C < 4 || last % 4 || 64 % (last / 4) || q.ldx % 4 || q.coff % 4)
       throw std::runtime_error("row program: unsupported pooled channel count or layout");

@@ -238,7 +238,9 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
   if (split && !(!nchw && c.ky == 1 && c.kx == 1 && igemm_eligible(c, nchw, ldx, o)))
     throw std::runtime_error("internal: split operands for implicit-GEMM 1x1 convolutions only");
   const double in_bytes = (double)HW * c.ic * (nchw ? 4.0 : ts);
-  const double out_bytes = (double)HW * c.oc * ((o.y ? 4.0 : 0.0) * (o.accumulate ? 2 : 1) + (o.yt ? ts : 0.0));
+  // (A convolution with pooling partials stores only its regular channels.)
+  const double out_bytes = (double)HW * (c.oc - (o.pool.psum ? o.pool.C : 0)) *
+                           ((o.y ? 4.0 : 0.0) * (o.accumulate ? 2 : 1) + (o.yt ? ts : 0.0));
   const int ic = c.ic, oc = c.oc;
   const bool k3 = c.ky == 3 && c.kx == 3 && c.dy == 1 && c.dx == 1;
   if (igemm_eligible(c, nchw, ldx, o)) {
@@ -591,6 +593,43 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
         ConvOut o1;
         o1.y = tmp_;
         o1.ldy = ct;
+        // The pooled branch's batch norm and activation, and on the implicit-GEMM path its board pooling as
+        // partials of the conv's tiles (PoolPart), so that the row program reads at most three partials per board
+        // instead of its 361 rows, and the branch's float output is not stored. The branches' filters are then
+        // interleaved per column tile (cr / tiles regular, then cg / tiles pooled channels), which spreads the
+        // pooling over all workgroups of the conv's single wave (b18c384nbt: 48 + 16 of 64 columns per tile).
+        const float* gsc = upload_f(b.gbn.scale);
+        const float* gbi = upload_f(b.gbn.bias);
+        long long* psum = nullptr;
+        float* pmax = nullptr;
+        const int pbn = conv_igemm_pool_cols(both.ky, c, ct), ptiles = pbn ? ct / pbn : 0;
+        const int pgroups = ptiles ? cg / ptiles / 4 : 0;  // pooled channel groups per tile: a power of two <= 16
+        if (igemm_eligible(both, false, c, o1) && pbn && ct % pbn == 0 && cr % (4 * ptiles) == 0 &&
+            cg % (4 * ptiles) == 0 && pgroups > 0 && pgroups <= 16 && (pgroups & (pgroups - 1)) == 0 &&
+            conv_igemm_tile_rows(both.ky, c, ct) == 192) {
+          const int rpt = cr / ptiles, gpt = cg / ptiles;
+          const size_t fl = both.w.size() / ct;  // floats per output channel
+          std::vector<float> w;
+          w.reserve(both.w.size());
+          for (int t = 0; t < ptiles; t++) {
+            const auto reg = both.w.begin() + (size_t)t * rpt * fl;
+            const auto gp = both.w.begin() + ((size_t)cr + (size_t)t * gpt) * fl;
+            w.insert(w.end(), reg, reg + (size_t)rpt * fl);
+            w.insert(w.end(), gp, gp + (size_t)gpt * fl);
+          }
+          both.w.swap(w);
+          const size_t n = ((size_t)max_batch_ * HW + 191) / 192 * 2 * cg;
+          psum = (long long*)alloc_bytes(n * sizeof(long long));
+          pmax = alloc_f(n);
+          o1.pool.psum = psum;
+          o1.pool.pmax = pmax;
+          o1.pool.scale = gsc;
+          o1.pool.bias = gbi;
+          o1.pool.act = b.gact;
+          o1.pool.mask = mask_;
+          o1.pool.rpt = rpt;
+          o1.pool.C = cg;
+        }
         emit_conv(both, a, c, false, o1);
         // Pooling of the gpool branch (after its batch norm and activation) and the matmul to the bias of the
         // regular branch, one workgroup per row.
@@ -599,8 +638,13 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
         RowProg rp = row_prog_base();
         rp.npool = 1;
         rp.pool[0].x = tmp; rp.pool[0].ldx = ct; rp.pool[0].coff = cr; rp.pool[0].C = cg;
-        rp.pool[0].scale = upload_f(b.gbn.scale); rp.pool[0].bias = upload_f(b.gbn.bias); rp.pool[0].act = b.gact;
+        rp.pool[0].scale = gsc; rp.pool[0].bias = gbi; rp.pool[0].act = b.gact;
         rp.pool[0].dst = 0;
+        if (psum) {
+          rp.pool[0].psum = psum;
+          rp.pool[0].pmax = pmax;
+          rp.pool[0].ppt = 192;
+        }
         rp.nmm = 1;
         rp.mm[0].src = 0; rp.mm[0].IC = 3 * cg; rp.mm[0].OC = cr; rp.mm[0].W = upload_f(b.gmul.w);
         rp.mm[0].out = gb; rp.mm[0].ldout = cr;

@@ -212,6 +212,27 @@ def test_gpool_widths_the_row_emission_does_not_fit(kgx, synth, oracle, prec):
     h.close()
 
 
+@pytest.mark.parametrize("prec", ["f16", "bf16"])
+@pytest.mark.parametrize("cr,cg", [(224, 32), (128, 128), (160, 64)])
+def test_gpool_conv_pooling_partials(kgx, synth, oracle, prec, cr, cg):
+    """A global-pooling block whose joint 3x3 (cr + cg outputs) runs on 64-column tiles: with 256 outputs its
+    pooled branch is reduced to per-tile partials in the convolution's epilogue (the filters interleaved per tile:
+    56 regular + 8 pooled, or 32 + 32 columns each), with 224 the row program pools the stored branch. Oracle
+    parity on ragged boards, and rows that equal the full batch's bit for bit at other offsets of the 192-pixel
+    tiles."""
+    arch = synth.Arch(f"t-gp{cr}-{cg}", 14, 64, [("res", 64), ("gpool", cr, cg), ("res", 64)], gpool_c=cg,
+                      p1_c=16, g1_c=16, v1_c=16, v2_c=24)
+    mb = synth.write_model(arch, 5)
+    sp, gl, _ = synth.make_inputs(7, 12, board_sizes=[19, 13, 9, 19, 7, 19, 11])
+    net = kgx.Net(mb)
+    h = kgx.Handle(net, 7, prec)
+    out = h.forward(sp, gl)
+    check(out, oracle.Model(mb).forward(sp, gl), net.P, net.S, prec, arch.name, emulated(oracle, mb, prec, sp, gl))
+    for k in (1, 2, 4):
+        assert np.array_equal(h.forward(sp[k:], gl[k:]), out[k:]), f"{arch.name} [{prec}]: rows {k}:"
+    h.close()
+
+
 def test_rows_do_not_depend_on_batch_or_bucket(kgx, synth):
     arch = synth.tiny_nets()["t_nbt"]
     net = kgx.Net(synth.write_model(arch, 3))
