@@ -127,7 +127,8 @@ __device__ __forceinline__ void store4(T* p, float a, float b, float c, float d)
   }
 }
 
-template <typename T>
+// ACT >= 0: the emission's activation, known to the caller (o.emit.act); -1: chosen here at run time.
+template <typename T, int ACT = -1>
 __device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floatx4 v, floatx4 yacc, float rm,
                                             floatx4 es, floatx4 eb, float mk) {
   if (o.colbias) v += *(const floatx4*)(o.colbias + (size_t)(m / HW) * o.ld_colbias + n);
@@ -142,7 +143,11 @@ __device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floa
   if (o.emit.scale) {
     float t[4];
 #pragma unroll
-    for (int e = 0; e < 4; e++) t[e] = act_rt(v[e] * es[e] + eb[e], o.emit.act) * mk;
+    for (int e = 0; e < 4; e++) {
+      const float a = v[e] * es[e] + eb[e];
+      if constexpr (ACT >= 0) t[e] = act_f<ACT>(a) * mk;
+      else t[e] = act_rt(a, o.emit.act) * mk;
+    }
     store4<T>((T*)o.emit.out + (size_t)m * o.emit.ld + n, t[0], t[1], t[2], t[3]);
     if (o.emit.out_lo) {
       // Split operands: the low part is what the 16-bit high part leaves of the float activation (exact in float).

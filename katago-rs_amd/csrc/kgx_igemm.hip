@@ -316,15 +316,25 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   if constexpr (!YEARLY) load_y();
   if constexpr (!SEARLY) load_side();
 
+  // The stores, in one copy per emission activation: the epilogue runs once per workgroup from a cold
+  // instruction cache, where one contiguous path is faster than a branch per value.
+  auto store_rows = [&](auto act_c) {
 #pragma unroll
-  for (int e = 0; e < EV; e++) {
-    const int row = er0 + e * RPE, m = m0 + row;
-    if (eon && !pcol && row < BM && m < M) {
-      floatx4 sum = *(const floatx4*)(Cs + row * LDC + 4 * ec4);
+    for (int e = 0; e < EV; e++) {
+      const int row = er0 + e * RPE, m = m0 + row;
+      if (eon && !pcol && row < BM && m < M) {
+        floatx4 sum = *(const floatx4*)(Cs + row * LDC + 4 * ec4);
 #pragma unroll
-      for (int q = 1; q < G; q++) sum += *(const floatx4*)(Cs + q * BM * LDC + row * LDC + 4 * ec4);
-      conv_store4<T>(o, m, ycol, sum, yres[e], rmv[e], es, eb, mkv[e]);
+        for (int q = 1; q < G; q++) sum += *(const floatx4*)(Cs + q * BM * LDC + row * LDC + 4 * ec4);
+        conv_store4<T, decltype(act_c)::value>(o, m, ycol, sum, yres[e], rmv[e], es, eb, mkv[e]);
+      }
     }
+  };
+  switch (o.emit.act) {
+    case ACT_RELU: store_rows(std::integral_constant<int, ACT_RELU>{}); break;
+    case ACT_MISH: store_rows(std::integral_constant<int, ACT_MISH>{}); break;
+    case ACT_SILU: store_rows(std::integral_constant<int, ACT_SILU>{}); break;
+    default: store_rows(std::integral_constant<int, ACT_ID>{}); break;
   }
 
   if constexpr (POOL) {
