@@ -127,20 +127,33 @@ __device__ __forceinline__ void store4(T* p, float a, float b, float c, float d)
   }
 }
 
-// ACT >= 0: the emission's activation, known to the caller (o.emit.act); -1: chosen here at run time.
-template <typename T, int ACT = -1>
+// The outputs a ConvOut asks for, as a bit set (store_flags): known to a caller that specializes conv_store4 on
+// them, so that the store path has no branch.
+enum StoreFlags {
+  SF_COLBIAS = 1, SF_ROWMASK = 2, SF_YT = 4, SF_Y = 8, SF_ACC = 16, SF_YDEAD = 32, SF_EMIT = 64, SF_LO = 128
+};
+__device__ __forceinline__ int store_flags(const ConvOut& o) {
+  return (o.colbias ? SF_COLBIAS : 0) | (o.rowmask ? SF_ROWMASK : 0) | (o.yt ? SF_YT : 0) | (o.y ? SF_Y : 0) |
+         (o.y && o.accumulate ? SF_ACC : 0) | (o.y && o.y_dead ? SF_YDEAD : 0) | (o.emit.scale ? SF_EMIT : 0) |
+         (o.emit.scale && o.emit.out_lo ? SF_LO : 0);
+}
+
+// ACT >= 0: the emission's activation, known to the caller (o.emit.act); -1: chosen here at run time. FL >= 0:
+// store_flags(o), known to the caller; -1: read from o here.
+template <typename T, int ACT = -1, int FL = -1>
 __device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floatx4 v, floatx4 yacc, float rm,
                                             floatx4 es, floatx4 eb, float mk) {
-  if (o.colbias) v += *(const floatx4*)(o.colbias + (size_t)(m / HW) * o.ld_colbias + n);
-  if (o.rowmask) v *= rm;
-  if (o.yt) store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, v[0], v[1], v[2], v[3]);
-  if (o.y) {
-    if (o.accumulate) v += yacc;
+  const int fl = FL >= 0 ? FL : store_flags(o);
+  if (fl & SF_COLBIAS) v += *(const floatx4*)(o.colbias + (size_t)(m / HW) * o.ld_colbias + n);
+  if (fl & SF_ROWMASK) v *= rm;
+  if (fl & SF_YT) store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, v[0], v[1], v[2], v[3]);
+  if (fl & SF_Y) {
+    if (fl & SF_ACC) v += yacc;
     // Non-temporal: the float stream's next reader is a later op (the next residual add, two or more launches
     // on), so its lines go out to MALL instead of taking L2 from the activations and weights of the ops between.
-    if (!o.y_dead) __builtin_nontemporal_store(v, (floatx4*)(o.y + (size_t)m * o.ldy + n));
+    if (!(fl & SF_YDEAD)) __builtin_nontemporal_store(v, (floatx4*)(o.y + (size_t)m * o.ldy + n));
   }
-  if (o.emit.scale) {
+  if (fl & SF_EMIT) {
     float t[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) {
@@ -149,7 +162,7 @@ __device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floa
       else t[e] = act_rt(a, o.emit.act) * mk;
     }
     store4<T>((T*)o.emit.out + (size_t)m * o.emit.ld + n, t[0], t[1], t[2], t[3]);
-    if (o.emit.out_lo) {
+    if (fl & SF_LO) {
       // Split operands: the low part is what the 16-bit high part leaves of the float activation (exact in float).
       float l[4];
 #pragma unroll

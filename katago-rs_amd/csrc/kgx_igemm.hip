@@ -316,9 +316,10 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   if constexpr (!YEARLY) load_y();
   if constexpr (!SEARLY) load_side();
 
-  // The stores, in one copy per emission activation: the epilogue runs once per workgroup from a cold
-  // instruction cache, where one contiguous path is faster than a branch per value.
-  auto store_rows = [&](auto act_c) {
+  // The stores, in one copy per emission activation, and for mish per set of outputs that the networks' convs
+  // ask for (store_flags): the epilogue runs once per workgroup from a cold instruction cache, where one
+  // contiguous path is faster than a branch per value.
+  auto store_rows = [&](auto act_c, auto fl_c) {
 #pragma unroll
     for (int e = 0; e < EV; e++) {
       const int row = er0 + e * RPE, m = m0 + row;
@@ -326,15 +327,39 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
         floatx4 sum = *(const floatx4*)(Cs + row * LDC + 4 * ec4);
 #pragma unroll
         for (int q = 1; q < G; q++) sum += *(const floatx4*)(Cs + q * BM * LDC + row * LDC + 4 * ec4);
-        conv_store4<T, decltype(act_c)::value>(o, m, ycol, sum, yres[e], rmv[e], es, eb, mkv[e]);
+        conv_store4<T, decltype(act_c)::value, decltype(fl_c)::value>(o, m, ycol, sum, yres[e], rmv[e], es, eb,
+                                                                       mkv[e]);
       }
     }
   };
-  switch (o.emit.act) {
-    case ACT_RELU: store_rows(std::integral_constant<int, ACT_RELU>{}); break;
-    case ACT_MISH: store_rows(std::integral_constant<int, ACT_MISH>{}); break;
-    case ACT_SILU: store_rows(std::integral_constant<int, ACT_SILU>{}); break;
-    default: store_rows(std::integral_constant<int, ACT_ID>{}); break;
+  typedef std::integral_constant<int, ACT_MISH> Mish;
+  typedef std::integral_constant<int, -1> AnyFlags;
+  // (Not for the 64-column 3x3 without partials: at 256 registers with its early residual loads, it spills.)
+  constexpr bool SPEC = !(C::KS == 3 && C::BN == 64 && !POOL);
+  const int sfl = store_flags(o);
+  switch (!SPEC ? -1 : !(sfl & SF_EMIT) ? sfl : o.emit.act == ACT_MISH ? sfl : -1) {
+    // a global-pooling block's first conv (pooling partials); a block's first conv; a nested block's entry 1x1;
+    // a block's last conv, its stream's last, into a split 1x1
+    case SF_Y: store_rows(std::integral_constant<int, ACT_ID>{}, std::integral_constant<int, SF_Y>{}); break;
+    case SF_EMIT: store_rows(Mish{}, std::integral_constant<int, SF_EMIT>{}); break;
+    case SF_Y | SF_EMIT: store_rows(Mish{}, std::integral_constant<int, SF_Y | SF_EMIT>{}); break;
+    case SF_Y | SF_ACC | SF_EMIT: store_rows(Mish{}, std::integral_constant<int, SF_Y | SF_ACC | SF_EMIT>{}); break;
+    case SF_Y | SF_ACC | SF_YDEAD | SF_EMIT:
+      store_rows(Mish{}, std::integral_constant<int, SF_Y | SF_ACC | SF_YDEAD | SF_EMIT>{});
+      break;
+    case SF_Y | SF_ACC | SF_EMIT | SF_LO:
+      store_rows(Mish{}, std::integral_constant<int, SF_Y | SF_ACC | SF_EMIT | SF_LO>{});
+      break;
+    case SF_COLBIAS | SF_Y | SF_EMIT | SF_LO:  // the stem into a nested block's entry 1x1
+      store_rows(Mish{}, std::integral_constant<int, SF_COLBIAS | SF_Y | SF_EMIT | SF_LO>{});
+      break;
+    default:
+      switch (o.emit.act) {
+        case ACT_RELU: store_rows(std::integral_constant<int, ACT_RELU>{}, AnyFlags{}); break;
+        case ACT_MISH: store_rows(Mish{}, AnyFlags{}); break;
+        case ACT_SILU: store_rows(std::integral_constant<int, ACT_SILU>{}, AnyFlags{}); break;
+        default: store_rows(std::integral_constant<int, ACT_ID>{}, AnyFlags{}); break;
+      }
   }
 
   if constexpr (POOL) {
