@@ -421,26 +421,41 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
       if (v < HW * e_n8) {
         const int p = v / e_n8, cl = (v - p * e_n8) * 8, c = e_o0 + cl;
         const float m = mk[p];
+        // One activation branch per vector (not per value: the program runs once per workgroup, from a cold
+        // instruction cache).
         float t[8];
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-          const float a = ex[k][e >> 2][e & 3] + rb[c + e];
-          t[e] = act_rt(a * esb[cl + e] + esb[per + cl + e], E.act) * m;
+        for (int e = 0; e < 8; e++) t[e] = (ex[k][e >> 2][e & 3] + rb[c + e]) * esb[cl + e] + esb[per + cl + e];
+        switch (E.act) {
+          case ACT_RELU:
+#pragma unroll
+            for (int e = 0; e < 8; e++) t[e] = act_f<ACT_RELU>(t[e]) * m;
+            break;
+          case ACT_MISH:
+#pragma unroll
+            for (int e = 0; e < 8; e++) t[e] = act_f<ACT_MISH>(t[e]) * m;
+            break;
+          case ACT_SILU:
+#pragma unroll
+            for (int e = 0; e < 8; e++) t[e] = act_f<ACT_SILU>(t[e]) * m;
+            break;
+          default:
+#pragma unroll
+            for (int e = 0; e < 8; e++) t[e] *= m;
         }
         u32x4 w;
+        if (E.prec == PREC_F16) {
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          unsigned short lo, hi;
-          if (E.prec == PREC_F16) {
+          for (int e = 0; e < 4; e++) {
             const f16 l = to_t<f16>(t[2 * e]), h = to_t<f16>(t[2 * e + 1]);
-            lo = __builtin_bit_cast(unsigned short, l);
-            hi = __builtin_bit_cast(unsigned short, h);
-          } else {
-            const bf16 l = to_t<bf16>(t[2 * e]), h = to_t<bf16>(t[2 * e + 1]);
-            lo = __builtin_bit_cast(unsigned short, l);
-            hi = __builtin_bit_cast(unsigned short, h);
+            w[e] = __builtin_bit_cast(unsigned short, l) | ((unsigned)__builtin_bit_cast(unsigned short, h) << 16);
           }
-          w[e] = lo | ((unsigned)hi << 16);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            const bf16 l = to_t<bf16>(t[2 * e]), h = to_t<bf16>(t[2 * e + 1]);
+            w[e] = __builtin_bit_cast(unsigned short, l) | ((unsigned)__builtin_bit_cast(unsigned short, h) << 16);
+          }
         }
         *(u32x4*)((unsigned short*)E.out + ((size_t)b * HW + p) * E.ldo + c) = w;
       }
