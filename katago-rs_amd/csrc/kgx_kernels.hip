@@ -1022,14 +1022,15 @@ __global__ __launch_bounds__(ATT_NW * 64, 1) void attn_mfma_kernel(AttnArgs a, i
     if (tid < ATT_KT) kbias[tid] = st.mk;
   };
 
-  floatx4 o[DT][QT];
-  float mref[QT], lsum[QT];
+  // O^T tiles, and in tile DT every query's sum of its 16-bit numerators (an all-ones A operand: the MFMA pipe,
+  // which this kernel leaves idle most of the time, adds them instead of the VALU).
+  floatx4 o[DT + 1][QT];
+  float mref[QT];
 #pragma unroll
   for (int qt = 0; qt < QT; qt++) {
     mref[qt] = -FLT_MAX;
-    lsum[qt] = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < DT; dt++) o[dt][qt] = floatx4{0.f, 0.f, 0.f, 0.f};
+    for (int dt = 0; dt <= DT; dt++) o[dt][qt] = floatx4{0.f, 0.f, 0.f, 0.f};
   }
 
   // Max over the four lane groups that hold one query's keys: lanes j and j ^ 16, then j and j ^ 32, through the
@@ -1072,7 +1073,7 @@ __global__ __launch_bounds__(ATT_NW * 64, 1) void attn_mfma_kernel(AttnArgs a, i
   // Numerators as B fragments of the two 32-key blocks, relative to a reference maximum per query that moves
   // lazily: only when some query of the wave would see a numerator above 2^8 (its tile maximum more than eight
   // binary orders above the reference) are the reference maxima raised to the running maxima, and the
-  // accumulators and sums rescaled, in one wave-uniform branch. Otherwise every numerator stays below 2^8 (in
+  // accumulators (the sums' tile with them) rescaled, in one wave-uniform branch. Otherwise every numerator stays below 2^8 (in
   // range and at full relative precision as a 16-bit operand), and O, the sums and the numerators all stay
   // relative to the same unchanged reference.
   auto softmax = [&](const floatx4 (&sc)[2 * KB][QT], frag_t (&pf)[KB][QT]) {
@@ -1094,29 +1095,22 @@ __global__ __launch_bounds__(ATT_NW * 64, 1) void attn_mfma_kernel(AttnArgs a, i
         const float mnew = fmaxf(mref[qt], mx[qt]);
         const float alpha = __builtin_amdgcn_exp2f((mref[qt] - mnew) * L2E);
 #pragma unroll
-        for (int dt = 0; dt < DT; dt++) o[dt][qt] *= alpha;
-        lsum[qt] *= alpha;
+        for (int dt = 0; dt <= DT; dt++) o[dt][qt] *= alpha;
         mref[qt] = mnew;
       }
     }
 #pragma unroll
     for (int qt = 0; qt < QT; qt++) {
       const float ml = mref[qt] * L2E;
-      float ps = 0.f;
 #pragma unroll
       for (int kb = 0; kb < KB; kb++) {
         frag_t pr;
 #pragma unroll
         for (int j = 0; j < 2; j++)
 #pragma unroll
-          for (int r = 0; r < 4; r++) {
-            const float pv = __builtin_amdgcn_exp2f(fmaf(sc[2 * kb + j][qt][r], L2E, -ml));
-            ps += pv;
-            pr[4 * j + r] = to_t<T>(pv);
-          }
+          for (int r = 0; r < 4; r++) pr[4 * j + r] = to_t<T>(__builtin_amdgcn_exp2f(fmaf(sc[2 * kb + j][qt][r], L2E, -ml)));
         pf[kb][qt] = pr;
       }
-      lsum[qt] += ps;
     }
   };
   // O^T += V^T P^T.
@@ -1136,6 +1130,18 @@ __global__ __launch_bounds__(ATT_NW * 64, 1) void attn_mfma_kernel(AttnArgs a, i
         }
       }
     }
+    frag_t ones;
+#pragma unroll
+    for (int e = 0; e < 8; e++) ones[e] = to_t<T>(1.f);
+#pragma unroll
+    for (int kb = 0; kb < KB; kb++)
+#pragma unroll
+      for (int qt = 0; qt < QT; qt++) {
+        if constexpr (std::is_same<T, f16>::value)
+          o[DT][qt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf[kb][qt], o[DT][qt], 0, 0, 0);
+        else
+          o[DT][qt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ones, pf[kb][qt], o[DT][qt], 0, 0, 0);
+      }
   };
 
   // Per tile t: the loads of tile t + 1 in flight during tile t's scores, softmax and O update; then tile t + 1
@@ -1155,14 +1161,12 @@ __global__ __launch_bounds__(ATT_NW * 64, 1) void attn_mfma_kernel(AttnArgs a, i
     __syncthreads();
   }
 
-  // Normalize (each lane's sum covers its own keys: add the four lane groups), transpose through LDS
+  // Normalize by the sums' tile (every element of a query's column holds its sum), transpose through LDS
   // ([wave][query][d]) and store 16-byte vectors of the queries on the board.
   T* Os = (T*)smem + wave * ATT_QW * OLD;
 #pragma unroll
   for (int qt = 0; qt < QT; qt++) {
-    float l = lsum[qt];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
+    const float l = o[DT][qt][0];
     const float inv = l > 0.f ? 1.f / l : 0.f;
 #pragma unroll
     for (int dt = 0; dt < DT; dt++)
