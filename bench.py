@@ -17,7 +17,8 @@ Prints one JSON line. Besides the throughput it carries
   WRITE_SIZE passes recorded in profiles/traffic.json (each scaled by the same counter's reading for a device copy
   of known size, `--copy-probe-mb`); null when no measurement for that class and workload is recorded;
 - "roofline.rocprof": the same kernel's average duration in the committed rocprofv3 kernel trace of this command
-  (profiles/kernel_trace.json) and the fraction it gives, beside the event-timed one;
+  (profiles/kernel_trace.json, which names the build it was taken on) and the fraction it gives, beside the
+  event-timed one;
 - "other_workloads": b10c128 float32 at batch 8 (the reference's CPU-runnable config) on the GPU, beside the
   reference's published RX 6800 XT figure.
 """
@@ -291,7 +292,8 @@ def main():
         roof["rocprof"] = {"avg_launch_us": rp_us, "achieved": roof["work_per_launch"] / (rp_us * 1e-6) /
                            (1e12 if roof["unit"] == "TFLOP/s" else 1e9)}
         roof["rocprof"]["frac"] = roof["rocprof"]["achieved"] / roof["peak"]
-        roof["rocprof"]["source"] = "profiles/kernel_trace.json (rocprofv3 --kernel-trace --stats of this command)"
+        roof["rocprof"]["source"] = ("profiles/kernel_trace.json: rocprofv3 --kernel-trace --stats of this command "
+                                     "on the build recorded there (not the build that ran here)")
 
     other = None
     if args.other_workloads and (args.config, args.precision, batch) == ("b18c384nbt", "f16", 32):
