@@ -161,3 +161,33 @@ def test_get_output_eval_matches_forward_and_oracle(kgx, synth, oracle, prec):
                                      q["nn_policy_temperature"], q["enable_passing_hacks"], q["no_result_allowed"], pp)
         _compare(res[i], ref, arch.model_version, f"eval {prec} row {i}")
     h.close()
+
+
+def test_post_outputs_match_reference_skipnn_fixture(kgx, synth):
+    """kg_post_outputs on the reference's own skip-NN evaluations (fixtures/upstream-v1.18.2/unit/oracle/
+    nneval_skipnn.txt, regenerated by tests/golden/gen_nneval_skipnn.py; the oracle reproduces them bit for bit):
+    every policy probability, value field and ownership value against the fixture, to the tolerances above."""
+    import os
+    z = np.load(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden", "nneval_skipnn.npz"))
+    net = kgx.Net(synth.write_model(synth.tiny_nets()["t_rmspos"], 4))  # model version 17, P = 2, S = 6
+    assert (net.P, net.S, net.desc.model_version, net.row_len) == (2, 6, 17, 1094)
+    assert tuple(float(x) for x in net.desc.post_process_params) == (20.0, 20.0, 20.0, 20.0, 40.0, 0.25, 30.0)
+    n = len(z["line"])
+    raw = np.zeros((n, net.row_len), np.float32)
+    raw[:, :362] = z["raw_policy"]
+    raw[:, 362:724] = z["raw_policy"]
+    raw[:, 724:727] = z["raw_value"]
+    raw[:, 727:733] = z["raw_score"]
+    raw[:, 733:] = z["raw_owner"]
+    post = [{"legal": z["legal"][i], "white_to_move": bool(z["white"][i]), "board_x_size": int(z["board"][i][0]),
+             "board_y_size": int(z["board"][i][1]), "nn_policy_temperature": float(z["temperature"][i]),
+             "enable_passing_hacks": bool(z["passing"][i]), "no_result_allowed": bool(z["no_result"][i])}
+            for i in range(n)]
+    h = kgx.Handle(net, n, "f32")
+    res = h.post_outputs(raw, np.zeros(n, np.int64), z["optimism"].astype(np.float32), post)
+    h.close()
+    for i in range(n):
+        exp_own = z["exp_owner"][i].view(np.float32) if z["owner"][i] else None
+        ref = (0, z["exp_policy"][i].view(np.float32), z["exp_fields"][i].view(np.float32),
+               exp_own if exp_own is not None else res[i]["ownership"])
+        _compare(res[i], ref, 17, f"fixture line {int(z['line'][i])}")

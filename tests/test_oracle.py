@@ -288,3 +288,46 @@ def test_oracle_postprocess_value_closed_forms(oracle):
     bad = row.copy()
     bad[362] = np.inf
     assert oracle.postprocess_row(bad, 1, 6, 9, 0, 0.0, legal, True, 19, 19)[0] == 2
+
+
+def _skipnn_rows():
+    """The evaluations of tests/golden/nneval_skipnn.npz as raw rows (P = 2 equal policy channels, so the optimism
+    mix leaves them unchanged; S = 6; symmetry 0) with their post-processing inputs."""
+    z = np.load(os.path.join(GOLDEN, "nneval_skipnn.npz"))
+    rows = np.zeros((len(z["line"]), 2 * 362 + 3 + 6 + 361), np.float32)
+    rows[:, :362] = z["raw_policy"]
+    rows[:, 362:724] = z["raw_policy"]
+    rows[:, 724:727] = z["raw_value"]
+    rows[:, 727:733] = z["raw_score"]
+    rows[:, 733:] = z["raw_owner"]
+    return z, rows
+
+
+def test_skipnn_generator_known_answers():
+    """The Rand restatement behind tests/golden/nneval_skipnn.npz: the known-answer sequences of the reference's
+    own generator self-tests (core/rand.rs XorShift1024Mult::test, PCG32::test)."""
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("gen_nneval_skipnn", os.path.join(GOLDEN, "gen_nneval_skipnn.py"))
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    gen.check_generators()
+
+
+def test_oracle_postprocess_matches_reference_skipnn_fixture(oracle):
+    """NNEvaluator's post-processing (nneval.rs:1197-1500, model version 17, default post-process parameters) of
+    the reference's own skip-NN evaluations (fixtures/upstream-v1.18.2/unit/oracle/nneval_skipnn.txt, regenerated
+    by tests/golden/gen_nneval_skipnn.py): 19 evaluations on boards from 6x6 to 19x19, with and without the
+    passing hack and owner map, both players to move, rules with and without no-result. Every policy probability,
+    value field and ownership value equals the fixture's float bits."""
+    z, rows = _skipnn_rows()
+    for i in range(len(rows)):
+        bx, by = (int(v) for v in z["board"][i])
+        st, pol, fields, own = oracle.postprocess_row(
+            rows[i], 2, 6, 17, 0, float(np.float32(z["optimism"][i])), z["legal"][i], bool(z["white"][i]), bx, by,
+            float(z["temperature"][i]), bool(z["passing"][i]), bool(z["no_result"][i]))
+        what = f"fixture line {int(z['line'][i])}"
+        assert st == 0, what
+        assert np.array_equal(pol.view(np.uint32), z["exp_policy"][i]), what
+        assert np.array_equal(fields.view(np.uint32), z["exp_fields"][i]), what
+        if z["owner"][i]:
+            assert np.array_equal(own.view(np.uint32), z["exp_owner"][i]), what
