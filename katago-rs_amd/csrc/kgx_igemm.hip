@@ -90,23 +90,6 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   const int r0 = tid / KV, kv8 = (tid % KV) * 8;
   const T* wb = W + ((size_t)nt * PL * TB + r0) * icp + kv8;
 
-  // Tap validity of this lane's A rows: bit t of vmask[i] is set when row m's neighbour at tap t is on the board.
-  unsigned vmask[MB];
-#pragma unroll
-  for (int i = 0; i < MB; i++) {
-    const int m = m0 + wm * WTM + i * 16 + r16;
-    unsigned bits = 0;
-    if (m < M) {
-      const int p = m % HW, y = p / POS, x = p - y * POS;
-#pragma unroll
-      for (int t = 0; t < TAPS; t++) {
-        const int dy = C::KS == 3 ? t / 3 - 1 : 0, dx = C::KS == 3 ? t % 3 - 1 : 0;
-        if ((unsigned)(y + dy) < (unsigned)POS && (unsigned)(x + dx) < (unsigned)POS) bits |= 1u << t;
-      }
-    }
-    vmask[i] = bits;
-  }
-
   vec_t ra[AV], rb[BV];
   auto load = [&](int k0) {
 #pragma unroll
@@ -133,6 +116,30 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     for (int v = 0; v < BV; v++)
       if ((PL * TB) % RP == 0 || r0 + v * RP < PL * TB) *(vec_t*)(bb + v * RP * LDK) = rb[v];
   };
+
+  // The first stage's loads go out before the rest of the set-up (the tap masks, the epilogue's early loads), which
+  // runs while they are in flight. Not in the 64-column 3x3: without partials, at 256 registers with its early
+  // residual loads, it would spill; with partials it measured slower (its mask, staged in LDS before the main
+  // loop, then waits behind the whole first stage).
+  constexpr bool LOAD_FIRST = !(C::KS == 3 && C::BN == 64);
+  if constexpr (LOAD_FIRST) load(0);
+
+  // Tap validity of this lane's A rows: bit t of vmask[i] is set when row m's neighbour at tap t is on the board.
+  unsigned vmask[MB];
+#pragma unroll
+  for (int i = 0; i < MB; i++) {
+    const int m = m0 + wm * WTM + i * 16 + r16;
+    unsigned bits = 0;
+    if (m < M) {
+      const int p = m % HW, y = p / POS, x = p - y * POS;
+#pragma unroll
+      for (int t = 0; t < TAPS; t++) {
+        const int dy = C::KS == 3 ? t / 3 - 1 : 0, dx = C::KS == 3 ? t % 3 - 1 : 0;
+        if ((unsigned)(y + dy) < (unsigned)POS && (unsigned)(x + dx) < (unsigned)POS) bits |= 1u << t;
+      }
+    }
+    vmask[i] = bits;
+  }
 
   floatx4 acc[MB][NB];
 #pragma unroll
@@ -275,7 +282,7 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   // The zero row of every stage buffer (never written by the stage stores).
   for (int e = tid; e < NBUF * KV; e += NT) *(vec_t*)(As + (e / KV) * SE + ZR * LDK + (e % KV) * 8) = vec_t{0, 0, 0, 0};
   const int nk = icp / BK;
-  load(0);
+  if constexpr (!LOAD_FIRST) load(0);
   if constexpr (POOL) {
     if (tid < BM) pms[tid] = pmv;  // ordered before the pass by the main loop's barriers
   }
