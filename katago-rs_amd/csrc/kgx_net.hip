@@ -478,7 +478,7 @@ void Net::emit_attention(const BlockDesc& b, int depth) {
   QkvEpi qe;
   qe.cos = dcos; qe.sin = dsin; qe.dq = dq; qe.nq = nq; qe.nk = nk; qe.H = H; qe.KV = KV; qe.tables = ntab;
   qe.qscale = 1.0f / std::sqrt((float)dq);
-  emit_token_gemm(nrm_, c, dWqkv, nqkv, c, oq, "token_gemm", false, qe);
+  emit_token_gemm(nrm_, c, dWqkv, nqkv, c, oq, "token_gemm_qkv", false, qe);
   void* qkv = qkv_;
   void* ao = ao_;
   Op at;
@@ -495,7 +495,7 @@ void Net::emit_attention(const BlockDesc& b, int depth) {
   ops_.push_back(at);
   ConvOut oo;
   oo.y = x; oo.ldy = c; oo.accumulate = true; oo.rowmask = mask;
-  ss_[depth].producer = emit_token_gemm(ao_, H * dv, dWo, c, H * dv, oo, "token_gemm");
+  ss_[depth].producer = emit_token_gemm(ao_, H * dv, dWo, c, H * dv, oo, "token_gemm_out");
 }
 
 // TransformerFFNBlock (bin2onnx.py:1423-1438): RMSNorm, linear1 (| gate), SiLU(l1) * gate (the plain FFN, which
@@ -538,15 +538,15 @@ void Net::emit_ffn(const BlockDesc& b, int depth) {
   if (fused && b.swiglu) {
     o1.yt = h_;
     o1.ldyt = F;
-    emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm", true);
+    emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm_ffn1", true);
   } else if (fused) {
     o1.yt = h_;
     o1.ldyt = F;
-    emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm", false, QkvEpi(), ACT_MISH);
+    emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm_ffn1", false, QkvEpi(), ACT_MISH);
   } else {
     o1.y = u_;
     o1.ldy = Fu;
-    emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm");
+    emit_token_gemm(nrm_, c, dW1, Fu, c, o1, "token_gemm_ffn1");
     float* u = u_;
     void* h = h_;
     const bool gated = b.swiglu;
@@ -558,7 +558,7 @@ void Net::emit_ffn(const BlockDesc& b, int depth) {
   }
   ConvOut o2;
   o2.y = x; o2.ldy = c; o2.accumulate = true; o2.rowmask = mask;
-  ss_[depth].producer = emit_token_gemm(h_, F, dW2, c, F, o2, "token_gemm");
+  ss_[depth].producer = emit_token_gemm(h_, F, dW2, c, F, o2, "token_gemm_ffn2");
 }
 
 void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
