@@ -357,6 +357,9 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     case SF_Y | SF_ACC | SF_EMIT | SF_LO:
       store_rows(Mish{}, std::integral_constant<int, SF_Y | SF_ACC | SF_EMIT | SF_LO>{});
       break;
+    case SF_Y | SF_ACC | SF_YDEAD | SF_EMIT | SF_LO:  // the trunk's last conv into the split head 1x1
+      store_rows(Mish{}, std::integral_constant<int, SF_Y | SF_ACC | SF_YDEAD | SF_EMIT | SF_LO>{});
+      break;
     case SF_COLBIAS | SF_Y | SF_EMIT | SF_LO:  // the stem into a nested block's entry 1x1
       store_rows(Mish{}, std::integral_constant<int, SF_COLBIAS | SF_Y | SF_EMIT | SF_LO>{});
       break;

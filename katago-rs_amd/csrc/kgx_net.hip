@@ -832,9 +832,37 @@ void Net::build(const ModelDesc& m) {
   emit_stack(m.blocks, 0);
 
   // --- Trunk tip and heads (bin2onnx.py:1489-1531). ---
+  for (const ConvDesc* hc : {&m.p1, &m.g1, &m.v1, &m.p2, &m.own})
+    if (hc->ky != 1 || hc->kx != 1) throw std::runtime_error(hc->name + ": head convolutions must be 1x1");
+  const int cp = m.p1.oc, cg = m.g1.oc, cv = m.v1.oc, nh = cp + cg + cv;
+  if (C % 8 != 0) throw std::runtime_error("trunk channels must be a multiple of 8");
+  // The head convolutions p1 | g1 | v1 as one 1x1 convolution into H.
+  ConvDesc hconv;
+  hconv.name = "p1|g1|v1";
+  hconv.ky = hconv.kx = 1;
+  hconv.ic = C;
+  hconv.oc = nh;
+  hconv.w.resize((size_t)nh * C);
+  std::memcpy(hconv.w.data(), m.p1.w.data(), (size_t)cp * C * 4);
+  std::memcpy(hconv.w.data() + (size_t)cp * C, m.g1.w.data(), (size_t)cg * C * 4);
+  std::memcpy(hconv.w.data() + (size_t)(cp + cg) * C, m.v1.w.data(), (size_t)cv * C * 4);
+  float* H = alloc_f(Mx * nh);
+  ConvOut hout;
+  hout.y = H;
+  hout.ldy = nh;
   const float* head_in = trunk_;
   Prologue tip_pro;
-  if (m.trunk_norm_kind == 0) {
+  if (m.trunk_norm_kind == 0 && split_1x1(hconv, C, hout)) {
+    // 16-bit handles: the trunk's last producer emits the tip activation as split operands (high and low 16-bit
+    // planes) instead of storing the float trunk, and the head convolution runs on them like the nested blocks'
+    // 1x1 convolutions (about 22 significant bits per operand, where the float GEMM below has 24).
+    const std::shared_ptr<ConvOut> last = ss_[0].producer;
+    const void* tip_lo = nullptr;
+    const void* tip = consume(0, m.tip_bn, m.tip_act, &tip_lo);
+    last->y_dead = true;
+    emit_conv(hconv, tip, C, false, hout, tip_lo);
+    ops_.back().cls = "head_1x1";
+  } else if (m.trunk_norm_kind == 0) {
     tip_pro = bn_pro(m.tip_bn, m.tip_act);
   } else {
     float* tip = alloc_f(Mx * C);
@@ -851,19 +879,9 @@ void Net::build(const ModelDesc& m) {
     ops_.push_back(op);
     head_in = tip;
   }
-  for (const ConvDesc* hc : {&m.p1, &m.g1, &m.v1, &m.p2, &m.own})
-    if (hc->ky != 1 || hc->kx != 1) throw std::runtime_error(hc->name + ": head convolutions must be 1x1");
-  const int cp = m.p1.oc, cg = m.g1.oc, cv = m.v1.oc, nh = cp + cg + cv;
-  if (C % 8 != 0) throw std::runtime_error("trunk channels must be a multiple of 8");
-  std::vector<float> wh((size_t)nh * C);
-  std::memcpy(wh.data(), m.p1.w.data(), (size_t)cp * C * 4);
-  std::memcpy(wh.data() + (size_t)cp * C, m.g1.w.data(), (size_t)cg * C * 4);
-  std::memcpy(wh.data() + (size_t)(cp + cg) * C, m.v1.w.data(), (size_t)cv * C * 4);
-  // The head GEMM runs on float operands in every precision: it is under 1% of the work, and its outputs feed
-  // the policy and ownership logits directly.
-  const float* dWh = upload_f(wh);
-  float* H = alloc_f(Mx * nh);
-  {
+  if (!(m.trunk_norm_kind == 0 && split_1x1(hconv, C, hout))) {
+    // Float operands: float handles, and the trunk-tip RMSNorm's output.
+    const float* dWh = upload_f(hconv.w);
     const int prec = PREC_F32;
     Op op;
     op.launch = [=](hipStream_t s, int B) {
