@@ -213,6 +213,9 @@ struct RowMM {
   int wlds = -1;                              // LDS float offset of a staged copy of W, or -1 (read from memory)
   int wcols = 0;                              // with wlds and output splits: the copy holds only this workgroup's
                                               // share of the columns, [IC][wcols]
+  bool bias_lds = false;                      // with wlds (whole columns): the copy holds the bias after W, at
+                                              // wlds + IC * OC (the bias follows W in memory too)
+  int w4 = 0;                                 // 16-byte vectors in the staged copy (0 without wlds)
 };
 // Optional last stage: the workgroup's share [o0, o1) of the last matmul's outputs (kept in LDS at its dst) is a
 // per-row channel bias, and out[m][c] = T(act((x[m][c] + bias_row[c]) * scale[c] + bias[c]) * mask[m]) for the

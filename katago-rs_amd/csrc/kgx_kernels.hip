@@ -268,7 +268,7 @@ __device__ void row_mm(const RowMM& m, int b, float* lds, float* red, int o_begi
     const int o = o_begin + ch * 64 + lane;
     const bool fin = w < nc && o < o_end;  // this thread finishes output o
     // Every global load of the stage is issued before its first barrier (a load after one costs a round trip).
-    const float bo = fin && m.bias ? m.bias[o] : 0.f;
+    const float bo = fin && m.bias ? (m.bias_lds ? lds[m.wlds + m.IC * m.OC + o] : m.bias[o]) : 0.f;
     float* op = fin && m.out ? m.out + (size_t)b * m.ldout + (size_t)o * m.ostride : nullptr;
     const float prev = op && m.accumulate ? *op : 0.f;
     float acc = 0.f;
@@ -351,10 +351,8 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
     // Staged weights: the whole set as one list of 16-byte vectors, RP_WB loads per thread in flight. A matmul
     // staged as a column share (wcols) contributes the IC rows of its wcols columns from this split's first one.
     constexpr int RP_WB = 8;
-    auto staged4 = [&](const RowMM& m) { return m.IC * (m.wcols > 0 ? m.wcols : m.OC) / 4; };
     int total = 0;
-    for (int k = 0; k < P.nmm; k++)
-      if (P.mm[k].wlds >= 0) total += staged4(P.mm[k]);
+    for (int k = 0; k < P.nmm; k++) total += P.mm[k].w4;
     for (int v0 = 0; v0 < total; v0 += RP_NT * RP_WB) {
       floatx4 buf[RP_WB];
       float* dst[RP_WB];
@@ -364,8 +362,7 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
         dst[j] = nullptr;
         if (v < total) {
           for (; k < P.nmm; k++) {
-            if (P.mm[k].wlds < 0) continue;
-            const int n4 = staged4(P.mm[k]);
+            const int n4 = P.mm[k].w4;
             if (v < n4) break;
             v -= n4;
           }
@@ -374,7 +371,7 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
             const int q4 = m.wcols / 4, i = v / q4, c = (v - i * q4) * 4;
             buf[j] = *(const floatx4*)(m.W + (size_t)i * m.OC + split * m.wcols + c);
           } else {
-            buf[j] = *(const floatx4*)(m.W + 4 * v);
+            buf[j] = *(const floatx4*)(m.W + 4 * v);  // (with bias_lds, the bias follows W in memory)
           }
           dst[j] = lds + m.wlds + 4 * v;
         }
@@ -488,9 +485,13 @@ static size_t row_prog_check(const RowProg& p) {
   }
   for (int k = 0; k < p.nmm; k++) {
     const RowMM& m = p.mm[k];
+    // (A staged bias's copy is padded to 16 bytes, as in memory.)
     const int cols = m.wcols > 0 ? m.wcols : m.OC;
-    if (m.wlds >= 0 && ((m.IC * cols) % 4 || m.wlds % 4 || m.wlds + m.IC * cols > p.lds_floats))
+    const int n = m.bias_lds ? ((m.IC + 1) * cols + 3) / 4 * 4 : m.IC * cols;
+    if (m.wlds >= 0 ? n % 4 || m.wlds % 4 || m.wlds + n > p.lds_floats || m.w4 != n / 4 : m.w4 != 0 || m.bias_lds)
       throw std::runtime_error("row program: bad staged weight layout");
+    if (m.bias_lds && (m.wcols > 0 || m.bias != m.W + (size_t)m.IC * m.OC))
+      throw std::runtime_error("row program: a staged bias must follow its whole W");
     // A column share is this workgroup's split of the (only) matmul's outputs, in 16-byte columns.
     if (m.wcols > 0 && (m.wlds < 0 || m.wcols % 4 || m.OC % p.splits || m.wcols != m.OC / p.splits))
       throw std::runtime_error("row program: bad staged weight share");
@@ -528,9 +529,15 @@ void launch_row_progs(const RowProgs& ps, int B, hipStream_t s) {
 void row_prog_stage_weights(RowProg& p, size_t max_bytes) {
   int off = (p.lds_floats + 3) / 4 * 4;
   for (int k = 0; k < p.nmm; k++) {
-    const int n = p.mm[k].IC * p.mm[k].OC;
+    RowMM& m = p.mm[k];
+    // A bias stored right after W in memory (padded to 16 bytes there) is staged with it, so the matmul waits on
+    // no load.
+    const bool fold = m.bias && m.bias == m.W + (size_t)m.IC * m.OC;
+    const int n = fold ? ((m.IC + 1) * m.OC + 3) / 4 * 4 : m.IC * m.OC;
     if (n % 4 == 0 && ((size_t)off + n + 2 * RP_NT + HW) * sizeof(float) <= max_bytes) {
-      p.mm[k].wlds = off;
+      m.wlds = off;
+      m.bias_lds = fold;
+      m.w4 = n / 4;
       off += n;
     }
   }

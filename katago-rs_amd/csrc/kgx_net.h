@@ -106,6 +106,9 @@ class Net {
   float* alloc_f(size_t n);
   void* alloc_bytes(size_t bytes);
   const float* upload_f(const std::vector<float>& v);
+  // A row-program matrix and its bias as one upload (the bias right after W, padded to 16 bytes), so that the
+  // program's weight staging copies the bias with W.
+  void upload_mm(RowMM& mm, const std::vector<float>& w, const std::vector<float>& b);
   const void* take_upload(size_t bytes);
   const void* upload_t(const std::vector<float>& v);  // converted to the compute type
   size_t tsize() const { return prec_ == PREC_F32 ? 4 : 2; }

@@ -124,6 +124,16 @@ const float* Net::upload_f(const std::vector<float>& v) {
   return d;
 }
 
+void Net::upload_mm(RowMM& mm, const std::vector<float>& w, const std::vector<float>& b) {
+  if (w.size() != (size_t)mm.IC * mm.OC || b.size() != (size_t)mm.OC)
+    throw std::runtime_error("internal: row matmul and bias sizes differ");
+  std::vector<float> wb((w.size() + b.size() + 3) / 4 * 4, 0.f);
+  std::copy(w.begin(), w.end(), wb.begin());
+  std::copy(b.begin(), b.end(), wb.begin() + w.size());
+  mm.W = upload_f(wb);
+  mm.bias = mm.W + w.size();
+}
+
 const void* Net::upload_t(const std::vector<float>& v) {
   if (prec_ == PREC_F32) return upload_f(v);
   if (primary_) return take_upload(v.size() * 2);
@@ -675,6 +685,7 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
           if (cr % fsplits == 0 && share % 4 == 0 && lds <= 64 * 1024) {
             rp.mm[0].wlds = woff;
             rp.mm[0].wcols = share;
+            rp.mm[0].w4 = 3 * cg * share / 4;
             rp.lds_floats = woff + 3 * cg * share;
           }
         }
@@ -929,7 +940,7 @@ void Net::build(const ModelDesc& m) {
       if (v15) {
         const int fp = rp.lds_floats; rp.lds_floats += ph;  // pass hidden layer
         RowMM& p1 = rp.mm[rp.nmm++];
-        p1.src = 0; p1.IC = 3 * cg; p1.OC = ph; p1.W = upload_f(m.pass1.w); p1.bias = upload_f(m.pass_bias.b);
+        p1.src = 0; p1.IC = 3 * cg; p1.OC = ph; upload_mm(p1, m.pass1.w, m.pass_bias.b);
         p1.act = m.pass_act; p1.dst = fp;
         RowMM& p2 = rp.mm[rp.nmm++];
         p2.src = fp; p2.IC = ph; p2.OC = P; p2.W = upload_f(m.pass2.w);
@@ -946,14 +957,20 @@ void Net::build(const ModelDesc& m) {
       rp.npool = 1; rp.pool[0] = pv; rp.lds_floats = 3 * cv;
       const int f2 = rp.lds_floats; rp.lds_floats += c2;  // v2
       RowMM& v2 = rp.mm[rp.nmm++];
-      v2.src = 0; v2.IC = 3 * cv; v2.OC = c2; v2.W = upload_f(m.v2.w); v2.bias = upload_f(m.v2_bias.b);
+      v2.src = 0; v2.IC = 3 * cv; v2.OC = c2; upload_mm(v2, m.v2.w, m.v2_bias.b);
       v2.act = m.v2_act; v2.dst = f2;
-      RowMM& v3 = rp.mm[rp.nmm++];
-      v3.src = f2; v3.IC = c2; v3.OC = 3; v3.W = upload_f(m.v3.w); v3.bias = upload_f(m.v3_bias.b);
-      v3.out = out + P * (HW + 1); v3.ldout = rl;
-      RowMM& sv = rp.mm[rp.nmm++];
-      sv.src = f2; sv.IC = c2; sv.OC = S; sv.W = upload_f(m.sv3.w); sv.bias = upload_f(m.sv3_bias.b);
-      sv.out = out + P * (HW + 1) + 3; sv.ldout = rl;
+      // v3 (3 value logits) and sv3 (S score values) side by side: their outputs are adjacent in the row.
+      RowMM& vs = rp.mm[rp.nmm++];
+      vs.src = f2; vs.IC = c2; vs.OC = 3 + S;
+      std::vector<float> wvs((size_t)c2 * (3 + S)), bvs(3 + S);
+      for (int i = 0; i < c2; i++) {
+        for (int o = 0; o < 3; o++) wvs[(size_t)i * (3 + S) + o] = m.v3.w[(size_t)i * 3 + o];
+        for (int o = 0; o < S; o++) wvs[(size_t)i * (3 + S) + 3 + o] = m.sv3.w[(size_t)i * S + o];
+      }
+      for (int o = 0; o < 3; o++) bvs[o] = m.v3_bias.b[o];
+      for (int o = 0; o < S; o++) bvs[3 + o] = m.sv3_bias.b[o];
+      upload_mm(vs, wvs, bvs);
+      vs.out = out + P * (HW + 1); vs.ldout = rl;
     }
     for (int k = 0; k < ps.n; k++) row_prog_stage_weights(ps.p[k], 60 * 1024);
     Op op;
