@@ -231,10 +231,14 @@ def main():
         avg_ms = v["ms"] / n
         c = {"launches_per_step": v["launches"] / args.steps, "avg_us": avg_ms * 1e3,
              "share": v["ms"] / total_kernel_ms if total_kernel_ms else 0.0}
+        # Both roofline fractions of every class (algorithmic flops and bytes per launch over its event time):
+        # latency-bound kernels reach neither, and the 1x1 convolutions' bound is the higher one.
         if v["flops"] > 0:
             c["tflops"] = v["flops"] / (v["ms"] * 1e-3) / 1e12
+            c["mfma_frac"] = c["tflops"] / PEAK_TFLOPS[args.precision]
         if v["bytes"] > 0:
             c["gbs"] = v["bytes"] / (v["ms"] * 1e-3) / 1e9
+            c["hbm_frac"] = c["gbs"] / PEAK_HBM_GBS
         classes[k] = c
     dom = max(prof.items(), key=lambda kv: kv[1]["ms"])
     dname, dv = dom

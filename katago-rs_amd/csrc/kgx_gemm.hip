@@ -473,6 +473,12 @@ typedef Cfg<128, 128, 64, 2, 2, true> CfgWide;
 // GEMMs with a nearly empty last round: -1.6 %).
 typedef Cfg<96, 96, 64, 2, 2, true, 3> CfgMid;
 typedef Cfg<64, 64, 32, 2, 2> CfgSmall;
+// 64x128 (three workgroups per CU) for a q|k|v projection whose 128x128 grid is under two rounds of two per CU: the
+// tile still holds whole 64-channel heads for the rotation, and half-size tiles even out the rounds (b10c384h6 at
+// batch 32: 819 tiles of 128x128 for 512 slots, 30.2 -> 25.6 us, +3.4 % end to end). Measured and rejected: the
+// same tile at batch 64 (tf3-b11c768's q|k|v 120.8 -> 124.0 us) and for b10c384h6's other GEMMs in place of 96x96
+// (FFN2 27.5 -> 31.9 us).
+typedef Cfg<64, 128, 64, 2, 2, true, 3> CfgQkv;
 typedef Cfg<64, 96, 64, 2, 2, true> CfgHead;  // the heads' first convolutions: N = p1 + g1 + v1 channels <= 96
 // Float operands on the head tile take 64 channels per stage (six stages at 384 channels): 20.8 against 21.8 us
 // with 32 at b18c384nbt batch 32. Its 87 KB of LDS allow one workgroup per CU.
@@ -524,6 +530,10 @@ static void gemm_cfg(const GemmArgs& g, hipStream_t s) {
       const bool tail = (wide_tiles % 512) * 4 < 512 && g.K <= 512;
       if (g.N > 128 && g.K % bk == 0 && !g.qkv.dq && g.Z == 1 && (wide_tiles < 512 || tail)) {
         gemm_launch<T, CfgMid, AF, PRO, ACT>(g, s);
+        return;
+      }
+      if (g.qkv.dq && g.N > 128 && g.K % bk == 0 && g.Z == 1 && wide_tiles < 1024) {
+        gemm_launch<T, CfgQkv, AF, PRO, ACT>(g, s);
         return;
       }
     }
