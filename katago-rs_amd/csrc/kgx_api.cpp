@@ -216,7 +216,7 @@ void plan_static(kg_handle* h, const kgx::ModelDesc& m) {
 void run_and_read(kg_handle* h, int n_run, int n, float* out) {
   h->net->forward(n_run, h->stream);
   const size_t bytes = (size_t)n * h->net->row_len() * sizeof(float);
-  KGX_HIP(hipMemcpyAsync(h->h_out, h->net->d_out(), bytes, hipMemcpyDeviceToHost, h->stream));
+  kgx::launch_readback(h->net->d_out(), h->h_out, bytes / sizeof(float), h->stream);
   KGX_HIP(hipStreamSynchronize(h->stream));
   if (out) std::memcpy(out, h->h_out, bytes);
 }
@@ -424,7 +424,8 @@ int kg_handle_create(const kg_net* net, int device, int max_batch, int precision
     KGX_HIP(hipHostMalloc((void**)&h->h_bin, (size_t)max_batch * h->nin * HW * 4, hipHostMallocDefault));
     KGX_HIP(hipHostMalloc((void**)&h->h_glob, (size_t)max_batch * h->nglob * 4, hipHostMallocDefault));
     if (h->nmeta) KGX_HIP(hipHostMalloc((void**)&h->h_meta, (size_t)max_batch * h->nmeta * 4, hipHostMallocDefault));
-    KGX_HIP(hipHostMalloc((void**)&h->h_out, (size_t)max_batch * m.row_len() * 4, hipHostMallocDefault));
+    // Coherent: the readback kernel's stores go straight to host memory.
+    KGX_HIP(hipHostMalloc((void**)&h->h_out, (size_t)max_batch * m.row_len() * 4, hipHostMallocCoherent));
     h->post_model.P = h->P;
     h->post_model.S = h->S;
     h->post_model.version = h->model_version;
@@ -654,8 +655,7 @@ int kg_get_output_async(kg_handle* h, int n, const kg_row_input* rows, kg_nn_out
     const int n_run = padded_batch_size(h->buckets, n, h->max_batch);
     upload_rows(h, n);
     h->net->forward(n_run, h->stream);
-    KGX_HIP(hipMemcpyAsync(h->h_out, h->net->d_out(), (size_t)n * h->net->row_len() * sizeof(float),
-                           hipMemcpyDeviceToHost, h->stream));
+    kgx::launch_readback(h->net->d_out(), h->h_out, (size_t)n * h->net->row_len(), h->stream);
     // read_on_helper_thread (backend.rs:743-753): a fresh OS thread waits for the device and runs copy_outputs.
     h->helper_status = 0;
     h->helper_error.clear();

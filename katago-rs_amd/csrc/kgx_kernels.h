@@ -264,6 +264,11 @@ struct HeadSpatialArgs {
 };
 void launch_head_spatial(const HeadSpatialArgs& a, int B, hipStream_t s);
 
+// Copies n floats of device memory into pinned, coherent host memory with 16-byte stores over the bus, and makes
+// them visible to the host before the kernel ends (a system-scope fence): the rows' readback as one kernel on the
+// stream, without a DMA engine's start-up. Both pointers 16-byte aligned.
+void launch_readback(const float* src, float* host_dst, size_t n, hipStream_t s);
+
 // Per-token RMSNorm of transformer blocks: out = x * (1/sqrt(sum(x^2)/C + eps)) * w * mask[row] (compute type).
 void launch_rmsnorm_tok(int prec, const float* x, int ldx, int C, const float* w, float eps, const float* mask,
                         void* out, int ldo, int rows, hipStream_t s);

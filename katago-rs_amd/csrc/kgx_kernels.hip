@@ -632,6 +632,26 @@ void launch_head_spatial(const HeadSpatialArgs& a, int B, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// Readback
+// ---------------------------------------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void readback_kernel(const float* __restrict__ src, float* __restrict__ dst,
+                                                       size_t n) {
+  const size_t n4 = n / 4, step = (size_t)gridDim.x * 256;
+  for (size_t i = blockIdx.x * 256 + threadIdx.x; i < n4; i += step)
+    ((floatx4*)dst)[i] = ((const floatx4*)src)[i];
+  if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) dst[4 * n4 + threadIdx.x] = src[4 * n4 + threadIdx.x];
+  __threadfence_system();
+}
+
+void launch_readback(const float* src, float* host_dst, size_t n, hipStream_t s) {
+  if (n == 0) return;
+  if (((uintptr_t)src | (uintptr_t)host_dst) % 16) throw std::runtime_error("readback: pointers not 16-byte aligned");
+  const size_t blocks = std::min<size_t>((n / 4 + 255) / 256 + 1, 1024);
+  launch_k(readback_kernel, dim3((unsigned)blocks), 256, 0, s, src, host_dst, n);
+  KGX_CHECK_LAUNCH();
+}
+
+// ---------------------------------------------------------------------------------------------------------
 // RMSNorm
 // ---------------------------------------------------------------------------------------------------------
 
