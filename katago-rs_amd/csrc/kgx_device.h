@@ -172,6 +172,15 @@ __device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floa
   }
 }
 
+// One 16-byte-per-lane load straight into LDS (buffer_load ... lds): lane i's bytes [off, off + 16) of the
+// range [base, base + nbytes) land at lds + 16 i; offsets past the range read as zero. The buffer resource is
+// built here so that kernels never hold its type.
+__device__ __forceinline__ void lds_load16(const void* base, int nbytes, void* lds, int off) {
+  typedef __attribute__((address_space(3))) void* lds_ptr_t;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(__builtin_amdgcn_make_buffer_rsrc((void*)base, 0, nbytes, 0x00020000),
+                                           (lds_ptr_t)lds, 16, off, 0, 0, 0);
+}
+
 // Winograd F(TM x TM, 3x3) geometry on the 19x19 board.
 template <int TM>
 struct Wino {

@@ -21,15 +21,6 @@ struct Cfg {
   static constexpr bool KFULL = KFULL_;
 };
 
-// One 16-byte-per-lane load straight into LDS (buffer_load ... lds): lane i's bytes [off, off + 16) of the
-// range [base, base + nbytes) land at lds + 16 i; offsets past the range read as zero. The buffer resource is
-// built here so that kernels never hold its type.
-__device__ __forceinline__ void lds_load16(const void* base, int nbytes, void* lds, int off) {
-  typedef __attribute__((address_space(3))) void* lds_ptr_t;
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(__builtin_amdgcn_make_buffer_rsrc((void*)base, 0, nbytes, 0x00020000),
-                                           (lds_ptr_t)lds, 16, off, 0, 0, 0);
-}
-
 // Epilogue variants, chosen at launch so that a kernel carries only its own epilogue code (a kernel holding all
 // of them ran 15-25 % slower on the token GEMMs, its main loop unchanged).
 enum GemmEpi {

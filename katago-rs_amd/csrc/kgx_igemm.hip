@@ -22,8 +22,14 @@
 namespace kgx {
 
 template <int KS_, int BM_, int BN_, int BK_, int WM_, int WN_, int G_, int NBUF_, int MINW_ = 2,
-          bool INTERLEAVE_ = false, bool SPLIT_ = false>
+          bool INTERLEAVE_ = false, bool SPLIT_ = false, bool WDMA_ = false>
 struct IgCfg {
+  // Weights straight into LDS (one 16-bit plane, one stage buffer for the pixel rows): each stage's weights go
+  // from memory into one of two LDS buffers (buffer_load ... lds, 16 bytes per lane) while the previous stage's
+  // MFMAs run, so only the pixel rows pass through registers and LDS store instructions. The weight rows are
+  // BK = 64 channels (128 bytes) unpadded, their 16-byte chunks swizzled (chunk ^ (row / 2 % 8)), which keeps the
+  // 16-row fragment reads conflict-free without the pad.
+  static constexpr bool WDMA = WDMA_;
   // Split operands (1x1): the stage holds the high and the low plane of both operands, and each step takes
   // hi*hi + lo*hi + hi*lo (three MFMAs), a product of about 22 significant bits per operand.
   static constexpr bool SPLIT = SPLIT_;
@@ -64,8 +70,15 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   constexpr int EPI = EPI0 + (POOL ? NT / 64 * 64 * 2 * 12 : 0);
   constexpr int NBUF = C::NBUF;
   constexpr int SE = STAGE / (int)sizeof(T);          // stage buffer size in elements
-  __shared__ __align__(16) char smem[NBUF * STAGE > EPI ? NBUF * STAGE : EPI];
-  T* As = (T*)smem;
+  static_assert(!C::WDMA || (NBUF == 1 && PL == 1 && BK == 64 && sizeof(T) == 2 && TB % 8 == 0 && BN % 16 == 0),
+                "weights into LDS: one 16-bit plane of 128-byte rows, one pixel-row buffer");
+  // Weights into LDS: two weight buffers of TB unpadded rows first (1 KB aligned, as each direct load fills one
+  // KB), then the pixel rows and the zero row.
+  constexpr int WSE = TB * BK;                          // weight buffer size in elements
+  constexpr int LDSB = C::WDMA ? 2 * WSE * (int)sizeof(T) + (ZR + 1) * LDK * (int)sizeof(T) : NBUF * STAGE;
+  __shared__ __align__(1024) char smem[LDSB > EPI ? LDSB : EPI];
+  T* Bw = (T*)smem;
+  T* As = C::WDMA ? Bw + 2 * WSE : (T*)smem;
   T* Bs = As + (ZR + 1) * LDK;
   typedef u32x4 vec_t;
   typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
@@ -100,10 +113,12 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
       const bool ok = ((PL * AR) % RP == 0 || r < PL * AR) && gr >= 0 && gr < M && k0 + kv8 < IC;
       ra[v] = ok ? *(const vec_t*)((lo ? Xlo : X) + (size_t)gr * ldx + kv8 + k0) : vec_t{0, 0, 0, 0};
     }
+    if constexpr (!C::WDMA) {
 #pragma unroll
-    for (int v = 0; v < BV; v++) {
-      const bool ok = (PL * TB) % RP == 0 || r0 + v * RP < PL * TB;
-      rb[v] = ok ? *(const vec_t*)(wb + (size_t)v * RP * icp + k0) : vec_t{0, 0, 0, 0};
+      for (int v = 0; v < BV; v++) {
+        const bool ok = (PL * TB) % RP == 0 || r0 + v * RP < PL * TB;
+        rb[v] = ok ? *(const vec_t*)(wb + (size_t)v * RP * icp + k0) : vec_t{0, 0, 0, 0};
+      }
     }
   };
   auto store = [&](int buf) {
@@ -112,9 +127,31 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
 #pragma unroll
     for (int v = 0; v < AV; v++)
       if ((PL * AR) % RP == 0 || r0 + v * RP < PL * AR) *(vec_t*)(ab + v * RP * LDK) = ra[v];
+    if constexpr (!C::WDMA) {
 #pragma unroll
-    for (int v = 0; v < BV; v++)
-      if ((PL * TB) % RP == 0 || r0 + v * RP < PL * TB) *(vec_t*)(bb + v * RP * LDK) = rb[v];
+      for (int v = 0; v < BV; v++)
+        if ((PL * TB) % RP == 0 || r0 + v * RP < PL * TB) *(vec_t*)(bb + v * RP * LDK) = rb[v];
+    }
+  };
+  // Weights into LDS: instruction q of wave wv fills weight rows [8 (q NW + wv), + 8) of a buffer, lane i row
+  // i / 8 at stored chunk i % 8, loaded from chunk (i % 8) ^ (row / 2 % 8) of that row's stage slice.
+  constexpr int NW = NT / 64, WI = TB / 8, WQ = C::WDMA ? (WI + NW - 1) / NW : 1;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const T* wtile = W + (size_t)nt * PL * TB * icp;
+  const int wbytes = TB * icp * (int)sizeof(T);
+  int woff[WQ];
+#pragma unroll
+  for (int q = 0; q < WQ; q++) {
+    const int row = (q * NW + wv) * 8 + (lane >> 3);
+    woff[q] = row * icp * (int)sizeof(T) + (((lane & 7) ^ ((row >> 1) & 7)) * 16);
+  }
+  auto issue_w = [&](int buf, int k0) {
+    if constexpr (C::WDMA) {
+#pragma unroll
+      for (int q = 0; q < WQ; q++)
+        if (WI % NW == 0 || q * NW + wv < WI)
+          lds_load16(wtile, wbytes, Bw + buf * WSE + (q * NW + wv) * 8 * BK, woff[q] + k0 * (int)sizeof(T));
+    }
   };
 
   // The first stage's loads go out before the rest of the set-up (the tap masks, the epilogue's early loads), which
@@ -122,7 +159,10 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   // residual loads, it would spill; with partials it measured slower (its mask, staged in LDS before the main
   // loop, then waits behind the whole first stage).
   constexpr bool LOAD_FIRST = !(C::KS == 3 && C::BN == 64);
-  if constexpr (LOAD_FIRST) load(0);
+  if constexpr (LOAD_FIRST) {
+    issue_w(0, 0);
+    load(0);
+  }
 
   // Tap validity of this lane's A rows: bit t of vmask[i] is set when row m's neighbour at tap t is on the board.
   unsigned vmask[MB];
@@ -149,7 +189,10 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
 
   // The MFMA steps of one group over the staged stage: its share of the (tap, 32-channel slice) pairs, with the
   // fragments of the next step read from LDS while the current step's MFMAs run.
-  auto mma = [&](auto gc, int sb) {
+  // Fragment reads of the swizzled weight rows: fragment rows start at multiples of 16, so a row's swizzle is
+  // (r16 / 2) % 8 and the chunk of K offset kk is (kk / 8) ^ (g4 ^ (r16 / 2) % 8).
+  const int wsw = g4 ^ ((r16 >> 1) & 7);
+  auto mma = [&](auto gc, int sb, int wbuf) {
     constexpr int g = decltype(gc)::value;
     constexpr int KK = BK / 32, ST = TAPS * KK, S0 = g * ST / G, S = (g + 1) * ST / G - S0;
     frag_t a[2][MB], b[2][NB];
@@ -157,7 +200,8 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     auto fetch = [&](int s, int fb) {
       const int t = (S0 + s) / KK, kk = ((S0 + s) % KK) * 32;
       const int shift = C::KS == 3 ? (t / 3 - 1) * POS + (t % 3 - 1) : 0;
-      const T* bs = Bs + sb * SE + (t * BN + wn * WTN + r16) * LDK + g4 * 8 + kk;
+      const T* bs = C::WDMA ? Bw + wbuf * WSE + (t * BN + wn * WTN + r16) * BK + (((kk / 8) ^ wsw) * 8)
+                            : Bs + sb * SE + (t * BN + wn * WTN + r16) * LDK + g4 * 8 + kk;
 #pragma unroll
       for (int i = 0; i < MB; i++) {
         // Rows whose neighbour is off the board read the zero row, so no loaded value needs masking.
@@ -168,7 +212,7 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
       }
 #pragma unroll
       for (int j = 0; j < NB; j++) {
-        b[fb][j] = *(const frag_t*)(bs + j * 16 * LDK);
+        b[fb][j] = *(const frag_t*)(bs + j * 16 * (C::WDMA ? BK : LDK));
         if constexpr (C::SPLIT) bl[fb][j] = *(const frag_t*)(bs + (TB + j * 16) * LDK);
       }
     };
@@ -210,12 +254,12 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     }
   };
 
-  auto compute = [&](int buf) {
+  auto compute = [&](int buf, int wbuf = 0) {
     if constexpr (G == 1) {
-      mma(std::integral_constant<int, 0>{}, buf);
+      mma(std::integral_constant<int, 0>{}, buf, wbuf);
     } else {
-      if (grp == 0) mma(std::integral_constant<int, 0>{}, buf);
-      else mma(std::integral_constant<int, G - 1>{}, buf);
+      if (grp == 0) mma(std::integral_constant<int, 0>{}, buf, wbuf);
+      else mma(std::integral_constant<int, G - 1>{}, buf, wbuf);
     }
   };
   // Epilogue mapping: thread tid finishes the four channels 4 * (tid % G4) of rows tid / G4 + e * RPE, so its
@@ -282,11 +326,30 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   // The zero row of every stage buffer (never written by the stage stores).
   for (int e = tid; e < NBUF * KV; e += NT) *(vec_t*)(As + (e / KV) * SE + ZR * LDK + (e % KV) * 8) = vec_t{0, 0, 0, 0};
   const int nk = icp / BK;
-  if constexpr (!LOAD_FIRST) load(0);
+  if constexpr (!LOAD_FIRST) {
+    issue_w(0, 0);
+    load(0);
+  }
   if constexpr (POOL) {
     if (tid < BM) pms[tid] = pmv;  // ordered before the pass by the main loop's barriers
   }
-  if constexpr (NBUF == 1) {
+  if constexpr (C::WDMA) {
+    // Pixel rows: store, barrier, next loads in flight during the MFMAs, barrier. Weights: stage kt + 1 streams
+    // into the other weight buffer while stage kt's MFMAs run. The compiler does not count the direct loads, so
+    // each wave waits for its own before the barrier.
+    for (int kt = 0; kt < nk; kt++) {
+      store(0);
+      __builtin_amdgcn_sched_barrier(0);
+      asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      __syncthreads();
+      if (kt + 1 < nk) {
+        issue_w((kt + 1) & 1, (kt + 1) * BK);
+        load((kt + 1) * BK);
+      }
+      compute(0, kt & 1);
+      __syncthreads();
+    }
+  } else if constexpr (NBUF == 1) {
     // One stage buffer: store, barrier, next loads in flight during the MFMAs, barrier.
     for (int kt = 0; kt < nk; kt++) {
       store(0);
@@ -475,7 +538,7 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
 // buffers. Equal pixel tiles give every convolution the same tile -> XCD mapping, so a layer reads the
 // activations its producer wrote from the same XCD's L2. The 1x1 kernel keeps two workgroups per CU (four waves
 // per SIMD, at most 128 registers): its 384-channel outputs are 512 workgroups.
-typedef IgCfg<3, 192, 48, 64, 4, 1, 2, 1> Ig3;
+typedef IgCfg<3, 192, 48, 64, 4, 1, 2, 1, 2, false, false, true> Ig3;
 typedef IgCfg<1, 192, 48, 64, 4, 1, 2, 2, 4> Ig1;
 // Wider output tiles keep a 3x3 convolution with more than 192 output channels at four column tiles (one wave
 // of workgroups on 256 CUs at batch 32): 64 channels for up to 256 (a global-pooling block's first conv), 96 for
