@@ -4,6 +4,8 @@
 // compute-type store, float store or residual add, and emission of the next consumer's activation).
 #include "kgx_device.h"
 
+#include <climits>
+
 namespace kgx {
 
 // Cfg: BM x BN output tile per workgroup of WM x WN waves, each wave (BM/WM) x (BN/WN) built from
@@ -34,7 +36,11 @@ enum GemmEpi {
 };
 
 template <typename T, typename C, bool AF, bool PRO, int ACT, int EPI>
-__global__ __launch_bounds__(C::WM * C::WN * 64, C::MINW) void gemm_kernel(GemmArgs g) {
+// The operands' pointers, strides and sizes lead the arguments (copies of g's fields) so that they are preloaded
+// into SGPRs at wave launch; by-value structs are not, and the first stage's loads would wait for them.
+__global__ __launch_bounds__(C::WM * C::WN * 64, C::MINW) void gemm_kernel(const void* gA, const void* gBt, long sA,
+                                                                          long sB, int M, int N, int K, int lda,
+                                                                          int ldb, GemmArgs g) {
   constexpr int BM = C::BM, BN = C::BN, WM = C::WM, WN = C::WN, NT = WM * WN * 64;
   constexpr int VEC = Tile<T>::VEC;
   constexpr int BK = sizeof(T) == 2 ? C::BKH : C::BKH / 2;
@@ -63,11 +69,10 @@ __global__ __launch_bounds__(C::WM * C::WN * 64, C::MINW) void gemm_kernel(GemmA
   const int wm = wave / WN, wn = wave % WN;
   const int z = blockIdx.z;
   const int n0 = blockIdx.x * BN, m0 = blockIdx.y * BM;
-  const int M = g.M, N = g.N, K = g.K;
 
-  const T* At = (const T*)g.A + (size_t)z * g.sA;
-  const float* Af = (const float*)g.A + (size_t)z * g.sA;
-  const T* Bt = (const T*)g.Bt + (size_t)z * g.sB;
+  const T* At = (const T*)gA + (size_t)z * sA;
+  const float* Af = (const float*)gA + (size_t)z * sA;
+  const T* Bt = (const T*)gBt + (size_t)z * sB;
 
   // Thread-invariant parts of the staged vectors' addresses; per stage only the uniform K offset moves.
   int a_row[AV], a_kk[AV], a_s[AV], b_row[BV], b_kk[BV], b_s[BV];
@@ -85,10 +90,9 @@ __global__ __launch_bounds__(C::WM * C::WN * 64, C::MINW) void gemm_kernel(GemmA
     b_kk[v] = (idx % KV) * VEC;
     b_s[v] = b_row[v] * LDK + (SWZ ? ((b_kk[v] / VEC) ^ ((b_row[v] >> 1) & 7)) * VEC : b_kk[v]);
   }
-  const T* At0 = At + (size_t)m0 * g.lda;
-  const float* Af0 = Af + (size_t)m0 * g.lda;
-  const T* Bt0 = Bt + (size_t)n0 * g.ldb;
-  const int lda = (int)g.lda, ldb = (int)g.ldb;
+  const T* At0 = At + (size_t)m0 * lda;
+  const float* Af0 = Af + (size_t)m0 * lda;
+  const T* Bt0 = Bt + (size_t)n0 * ldb;
   int a_off[AV], b_off[BV];  // clamped-row offsets (KFULL)
 #pragma unroll
   for (int v = 0; v < AV; v++) a_off[v] = min(a_row[v], M - 1 - m0) * lda + a_kk[v];
@@ -494,14 +498,18 @@ static void gemm_launch(const GemmArgs& g, hipStream_t s) {
   if (g.qkv.dq && C::BN % g.qkv.dq)
     throw std::runtime_error("gemm: the q|k|v epilogue needs the column tile to hold whole heads");
   dim3 grid((g.N + C::BN - 1) / C::BN, (g.M + C::BM - 1) / C::BM, g.Z);
+  if (g.lda > INT_MAX || g.ldb > INT_MAX) throw std::runtime_error("gemm: row stride beyond the int range");
+  auto go = [&](auto kernel) {
+    launch_k(kernel, grid, C::WM * C::WN * 64, 0, s, g.A, g.Bt, g.sA, g.sB, g.M, g.N, g.K, (int)g.lda, (int)g.ldb, g);
+  };
   switch (epi) {
-    case EPI_SCALAR: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_SCALAR>, grid, C::WM * C::WN * 64, 0, s, g); break;
-    case EPI_YT: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_YT>, grid, C::WM * C::WN * 64, 0, s, g); break;
-    case EPI_ACC: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_ACC>, grid, C::WM * C::WN * 64, 0, s, g); break;
-    case EPI_GLU: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_GLU>, grid, C::WM * C::WN * 64, 0, s, g); break;
-    case EPI_QKV: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_QKV>, grid, C::WM * C::WN * 64, 0, s, g); break;
-    case EPI_YTMISH: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_YTMISH>, grid, C::WM * C::WN * 64, 0, s, g); break;
-    default: launch_k(gemm_kernel<T, C, AF, PRO, ACT, EPI_GEN>, grid, C::WM * C::WN * 64, 0, s, g); break;
+    case EPI_SCALAR: go(gemm_kernel<T, C, AF, PRO, ACT, EPI_SCALAR>); break;
+    case EPI_YT: go(gemm_kernel<T, C, AF, PRO, ACT, EPI_YT>); break;
+    case EPI_ACC: go(gemm_kernel<T, C, AF, PRO, ACT, EPI_ACC>); break;
+    case EPI_GLU: go(gemm_kernel<T, C, AF, PRO, ACT, EPI_GLU>); break;
+    case EPI_QKV: go(gemm_kernel<T, C, AF, PRO, ACT, EPI_QKV>); break;
+    case EPI_YTMISH: go(gemm_kernel<T, C, AF, PRO, ACT, EPI_YTMISH>); break;
+    default: go(gemm_kernel<T, C, AF, PRO, ACT, EPI_GEN>); break;
   }
 }
 

@@ -942,7 +942,11 @@ __device__ __forceinline__ int att_kpos(int kk) {
 // Three workgroups per CU for D <= 32; two for D = 64, whose registers spill at the three-workgroup bound (the
 // spill-free kernel is 4 % faster at b10c384h6).
 template <typename T, int D>
-__global__ __launch_bounds__(ATT_NW * 64, 1) void attn_mfma_kernel(AttnArgs a, int nheads_total) {
+// The fields that the first loads need lead the arguments (copies of a's) so that they are preloaded into SGPRs
+// at wave launch; by-value structs are not.
+__global__ __launch_bounds__(ATT_NW * 64, 1) void attn_mfma_kernel(const void* a_qkv, const float* a_mask,
+                                                                   int nheads_total, int a_H, int a_KV, int a_ldq,
+                                                                   int a_q_off, int a_k_off, int a_v_off, AttnArgs a) {
   static_assert(D == 16 || D == 32 || D == 64, "head dim");
   typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
   constexpr int NT = ATT_NW * 64;
@@ -962,13 +966,13 @@ __global__ __launch_bounds__(ATT_NW * 64, 1) void attn_mfma_kernel(AttnArgs a, i
 
   const int g0 = blockIdx.x, slot = g0 >> 3, qb = slot % ATT_NQB, nh = (slot / ATT_NQB) * 8 + (g0 & 7);
   if (nh >= nheads_total) return;
-  const int h = nh % a.H, n = nh / a.H;
+  const int h = nh % a_H, n = nh / a_H;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, l16 = lane & 15, g = lane >> 4;
-  const int kvh = h / (a.H / a.KV);
-  const T* qkv = (const T*)a.qkv;
-  const T* kbase = qkv + (size_t)n * HW * a.ldq + a.k_off + kvh * D;
-  const T* vbase = qkv + (size_t)n * HW * a.ldq + a.v_off + kvh * D;
-  const float* mrow = a.mask + (size_t)n * HW;
+  const int kvh = h / (a_H / a_KV);
+  const T* qkv = (const T*)a_qkv;
+  const T* kbase = qkv + (size_t)n * HW * a_ldq + a_k_off + kvh * D;
+  const T* vbase = qkv + (size_t)n * HW * a_ldq + a_v_off + kvh * D;
+  const float* mrow = a_mask + (size_t)n * HW;
 
   // Zero K's padding columns (head dim 16) in both buffers; staging never writes them.
   if constexpr (DP > D) {
@@ -992,7 +996,7 @@ __global__ __launch_bounds__(ATT_NW * 64, 1) void attn_mfma_kernel(AttnArgs a, i
 #pragma unroll
       for (int e = 0; e < 8; e++) r[e] = to_t<T>(0.f);
       if (qi < HW && d0 < D) {
-        const T* qp = qkv + ((size_t)n * HW + qi) * a.ldq + a.q_off + h * D;
+        const T* qp = qkv + ((size_t)n * HW + qi) * a_ldq + a_q_off + h * D;
         const frag_t x = *(const frag_t*)(qp + d0);
 #pragma unroll
         for (int e = 0; e < 8; e++) r[e] = to_t<T>((float)x[e] * a.scale);
@@ -1013,14 +1017,14 @@ __global__ __launch_bounds__(ATT_NW * 64, 1) void attn_mfma_kernel(AttnArgs a, i
     const int k0 = t * ATT_KT;
     if (tid < KU) {
       const int key = min(k0 + ku_key, HW - 1);
-      const T* kp = kbase + (size_t)key * a.ldq + ku_c;
+      const T* kp = kbase + (size_t)key * a_ldq + ku_c;
       st.kx0 = *(const frag_t*)kp;
       st.kx1 = *(const frag_t*)(kp + HALF);
     }
     if (tid < VU) {
       const int key = min(k0 + 2 * vu_pair, HW - 1), key1 = min(k0 + 2 * vu_pair + 1, HW - 1);
-      st.vx0 = *(const frag_t*)(vbase + (size_t)key * a.ldq + vu_c);
-      st.vx1 = *(const frag_t*)(vbase + (size_t)key1 * a.ldq + vu_c);
+      st.vx0 = *(const frag_t*)(vbase + (size_t)key * a_ldq + vu_c);
+      st.vx1 = *(const frag_t*)(vbase + (size_t)key1 * a_ldq + vu_c);
     }
     if (tid < ATT_KT) {
       const int key = k0 + tid;
@@ -1211,7 +1215,8 @@ template <typename T, int D>
 static void attn_mfma_d(const AttnArgs& a, int B, hipStream_t s) {
   const int nh = B * a.H;
   dim3 grid((nh + 7) / 8 * 8 * ATT_NQB);
-  launch_k(attn_mfma_kernel<T, D>, grid, ATT_NW * 64, 0, s, a, nh);
+  launch_k(attn_mfma_kernel<T, D>, grid, ATT_NW * 64, 0, s, a.qkv, a.mask, nh, a.H, a.KV, a.ldq, a.q_off, a.k_off,
+           a.v_off, a);
 }
 
 template <typename T, int D>
