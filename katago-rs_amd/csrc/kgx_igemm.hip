@@ -104,7 +104,22 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   const T* wb = W + ((size_t)nt * PL * TB + r0) * icp + kv8;
 
   vec_t ra[AV], rb[BV];
+  bool aok[AV];  // weights-into-LDS: whether pixel-row vector v is real (else zeroed after its load lands)
   auto load = [&](int k0) {
+    if constexpr (C::WDMA) {
+      // Pixel rows by loads the compiler does not track (it would wait for every load in flight, the weights'
+      // direct loads included, before the stores that consume them): rows outside the board read a clamped row
+      // and are zeroed once the wait before the stores has passed.
+#pragma unroll
+      for (int v = 0; v < AV; v++) {
+        const int r = r0 + v * RP;
+        const int gr = m0 - HALO + r;
+        aok[v] = ((PL * AR) % RP == 0 || r < PL * AR) && gr >= 0 && gr < M && k0 + kv8 < IC;
+        const T* p = X + (size_t)min(max(gr, 0), M - 1) * ldx + (k0 + kv8 < IC ? k0 + kv8 : 0);
+        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(ra[v]) : "v"(p) : "memory");
+      }
+      return;
+    }
 #pragma unroll
     for (int v = 0; v < AV; v++) {
       const int r = r0 + v * RP;
@@ -337,17 +352,37 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     // Pixel rows: store, barrier, next loads in flight during the MFMAs, barrier. Weights: stage kt + 1 streams
     // into the other weight buffer while stage kt's MFMAs run. The compiler does not count the direct loads, so
     // each wave waits for its own before the barrier.
+    static_assert(AV == 4, "the wait below ties four pixel-row vectors");
     for (int kt = 0; kt < nk; kt++) {
+      // This wave's pixel rows of stage kt have landed when at most the stage's weight loads (issued after them:
+      // WQ or WQ - 1 per wave) are in flight, as vector memory counts return in issue order. The wait names the
+      // row registers, so nothing reads them before it. Stage 0's rows were issued before the set-up's loads.
+      if (kt == 0)
+        asm volatile("s_waitcnt vmcnt(0)" : "+v"(ra[0]), "+v"(ra[1]), "+v"(ra[2]), "+v"(ra[3]) :: "memory");
+      else if (WI % NW == 0 || wv < WI % NW)
+        asm volatile("s_waitcnt vmcnt(%4)" : "+v"(ra[0]), "+v"(ra[1]), "+v"(ra[2]), "+v"(ra[3]) : "n"(WQ) : "memory");
+      else
+        asm volatile("s_waitcnt vmcnt(%4)" : "+v"(ra[0]), "+v"(ra[1]), "+v"(ra[2]), "+v"(ra[3]) : "n"(WQ - 1)
+                     : "memory");
+#pragma unroll
+      for (int v = 0; v < AV; v++)
+        if (!aok[v]) ra[v] = vec_t{0, 0, 0, 0};
       store(0);
       __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       __syncthreads();
       if (kt + 1 < nk) {
-        issue_w((kt + 1) & 1, (kt + 1) * BK);
         load((kt + 1) * BK);
+        issue_w((kt + 1) & 1, (kt + 1) * BK);
       }
       compute(0, kt & 1);
-      __syncthreads();
+      // Every wave is done reading this stage from LDS. An LDS-only barrier: __syncthreads() would also wait for
+      // the next stage's loads, which the wait before the stores above handles.
+      __builtin_amdgcn_sched_barrier(0);
+      __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_sched_barrier(0);
     }
   } else if constexpr (NBUF == 1) {
     // One stage buffer: store, barrier, next loads in flight during the MFMAs, barrier.
