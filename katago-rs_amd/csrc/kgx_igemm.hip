@@ -75,7 +75,9 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   // Weights into LDS: two weight buffers of TB unpadded rows first (1 KB aligned, as each direct load fills one
   // KB), then the pixel rows and the zero row.
   constexpr int WSE = TB * BK;                          // weight buffer size in elements
-  constexpr int LDSB = C::WDMA ? 2 * WSE * (int)sizeof(T) + (ZR + 1) * LDK * (int)sizeof(T) : NBUF * STAGE;
+  // (then, where the waves' direct loads do not divide the weight rows evenly, a spare KB for the surplus loads)
+  constexpr int WSPARE = C::WDMA ? (2 * WSE * (int)sizeof(T) + (ZR + 1) * LDK * (int)sizeof(T) + 1023) / 1024 * 1024 : 0;
+  constexpr int LDSB = C::WDMA ? WSPARE + ((TB / 8) % (NT / 64) ? 1024 : 0) : NBUF * STAGE;
   __shared__ __align__(1024) char smem[LDSB > EPI ? LDSB : EPI];
   T* Bw = (T*)smem;
   T* As = C::WDMA ? Bw + 2 * WSE : (T*)smem;
@@ -104,19 +106,18 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   const T* wb = W + ((size_t)nt * PL * TB + r0) * icp + kv8;
 
   vec_t ra[AV], rb[BV];
-  bool aok[AV];  // weights-into-LDS: whether pixel-row vector v is real (else zeroed after its load lands)
+  bool aok[AV];  // weights into LDS: whether pixel-row vector v holds real data (else it is stored as zeros)
   auto load = [&](int k0) {
     if constexpr (C::WDMA) {
-      // Pixel rows by loads the compiler does not track (it would wait for every load in flight, the weights'
-      // direct loads included, before the stores that consume them): rows outside the board read a clamped row
-      // and are zeroed once the wait before the stores has passed.
+      // Unconditional loads of clamped (in-range) rows, zeroed when stored where the row lies off the batch or
+      // the channels beyond IC: with no branch around a load, the compiler's count of the loads issued after the
+      // rows (the weights' direct loads) stays exact, so its wait before the row stores leaves those in flight.
 #pragma unroll
       for (int v = 0; v < AV; v++) {
         const int r = r0 + v * RP;
         const int gr = m0 - HALO + r;
-        aok[v] = ((PL * AR) % RP == 0 || r < PL * AR) && gr >= 0 && gr < M && k0 + kv8 < IC;
-        const T* p = X + (size_t)min(max(gr, 0), M - 1) * ldx + (k0 + kv8 < IC ? k0 + kv8 : 0);
-        asm volatile("global_load_dwordx4 %0, %1, off" : "=v"(ra[v]) : "v"(p) : "memory");
+        aok[v] = gr >= 0 && gr < M && k0 + kv8 < IC;
+        ra[v] = *(const vec_t*)(X + (size_t)min(max(gr, 0), M - 1) * ldx + (k0 + kv8 < IC ? k0 + kv8 : 0));
       }
       return;
     }
@@ -141,7 +142,8 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     T* bb = Bs + buf * SE + r0 * LDK + kv8;
 #pragma unroll
     for (int v = 0; v < AV; v++)
-      if ((PL * AR) % RP == 0 || r0 + v * RP < PL * AR) *(vec_t*)(ab + v * RP * LDK) = ra[v];
+      if ((PL * AR) % RP == 0 || r0 + v * RP < PL * AR)
+        *(vec_t*)(ab + v * RP * LDK) = !C::WDMA || aok[v] ? ra[v] : vec_t{0, 0, 0, 0};
     if constexpr (!C::WDMA) {
 #pragma unroll
       for (int v = 0; v < BV; v++)
@@ -149,23 +151,29 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     }
   };
   // Weights into LDS: instruction q of wave wv fills weight rows [8 (q NW + wv), + 8) of a buffer, lane i row
-  // i / 8 at stored chunk i % 8, loaded from chunk (i % 8) ^ (row / 2 % 8) of that row's stage slice.
+  // i / 8 at stored chunk i % 8, loaded from chunk (i % 8) ^ (row / 2 % 8) of that row's stage slice. Every wave
+  // issues WQ of them per stage: where WI is not a multiple of NW, the last instruction of waves WI % NW and up
+  // reloads the tile's last 8 rows into a spare KB of LDS that nothing reads. So no load is under a branch and
+  // the compiler counts exactly how many direct loads follow the pixel rows.
   constexpr int NW = NT / 64, WI = TB / 8, WQ = C::WDMA ? (WI + NW - 1) / NW : 1;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const T* wtile = W + (size_t)nt * PL * TB * icp;
   const int wbytes = TB * icp * (int)sizeof(T);
+  T* const Wspare = (T*)(smem + WSPARE);
   int woff[WQ];
 #pragma unroll
   for (int q = 0; q < WQ; q++) {
-    const int row = (q * NW + wv) * 8 + (lane >> 3);
+    const int row = min(q * NW + wv, WI - 1) * 8 + (lane >> 3);
     woff[q] = row * icp * (int)sizeof(T) + (((lane & 7) ^ ((row >> 1) & 7)) * 16);
   }
   auto issue_w = [&](int buf, int k0) {
     if constexpr (C::WDMA) {
 #pragma unroll
-      for (int q = 0; q < WQ; q++)
-        if (WI % NW == 0 || q * NW + wv < WI)
-          lds_load16(wtile, wbytes, Bw + buf * WSE + (q * NW + wv) * 8 * BK, woff[q] + k0 * (int)sizeof(T));
+      for (int q = 0; q < WQ; q++) {
+        T* dst = Bw + buf * WSE + (q * NW + wv) * 8 * BK;
+        if (WI % NW != 0 && q == WQ - 1 && q * NW + wv >= WI) dst = Wspare;
+        lds_load16(wtile, wbytes, dst, woff[q] + k0 * (int)sizeof(T));
+      }
     }
   };
 
@@ -174,9 +182,11 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   // residual loads, it would spill; with partials it measured slower (its mask, staged in LDS before the main
   // loop, then waits behind the whole first stage).
   constexpr bool LOAD_FIRST = !(C::KS == 3 && C::BN == 64);
+  // (Pixel rows before weights, as in every later stage: the compiler's wait before the row stores then leaves the
+  // weights in flight on every path into the main loop.)
   if constexpr (LOAD_FIRST) {
-    issue_w(0, 0);
     load(0);
+    issue_w(0, 0);
   }
 
   // Tap validity of this lane's A rows: bit t of vmask[i] is set when row m's neighbour at tap t is on the board.
@@ -342,31 +352,19 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   for (int e = tid; e < NBUF * KV; e += NT) *(vec_t*)(As + (e / KV) * SE + ZR * LDK + (e % KV) * 8) = vec_t{0, 0, 0, 0};
   const int nk = icp / BK;
   if constexpr (!LOAD_FIRST) {
-    issue_w(0, 0);
     load(0);
+    issue_w(0, 0);
   }
   if constexpr (POOL) {
     if (tid < BM) pms[tid] = pmv;  // ordered before the pass by the main loop's barriers
   }
   if constexpr (C::WDMA) {
     // Pixel rows: store, barrier, next loads in flight during the MFMAs, barrier. Weights: stage kt + 1 streams
-    // into the other weight buffer while stage kt's MFMAs run. The compiler does not count the direct loads, so
-    // each wave waits for its own before the barrier.
-    static_assert(AV == 4, "the wait below ties four pixel-row vectors");
+    // into the other weight buffer while stage kt's MFMAs run. The pixel rows are ordinary loads issued before the
+    // stage's direct weight loads, so the wait the compiler places before the row stores (it counts both kinds)
+    // leaves the weights in flight while the rows are stored. The compiler does not order LDS reads after direct
+    // loads into LDS, so each wave waits for all of its loads before the barrier that publishes the stage.
     for (int kt = 0; kt < nk; kt++) {
-      // This wave's pixel rows of stage kt have landed when at most the stage's weight loads (issued after them:
-      // WQ or WQ - 1 per wave) are in flight, as vector memory counts return in issue order. The wait names the
-      // row registers, so nothing reads them before it. Stage 0's rows were issued before the set-up's loads.
-      if (kt == 0)
-        asm volatile("s_waitcnt vmcnt(0)" : "+v"(ra[0]), "+v"(ra[1]), "+v"(ra[2]), "+v"(ra[3]) :: "memory");
-      else if (WI % NW == 0 || wv < WI % NW)
-        asm volatile("s_waitcnt vmcnt(%4)" : "+v"(ra[0]), "+v"(ra[1]), "+v"(ra[2]), "+v"(ra[3]) : "n"(WQ) : "memory");
-      else
-        asm volatile("s_waitcnt vmcnt(%4)" : "+v"(ra[0]), "+v"(ra[1]), "+v"(ra[2]), "+v"(ra[3]) : "n"(WQ - 1)
-                     : "memory");
-#pragma unroll
-      for (int v = 0; v < AV; v++)
-        if (!aok[v]) ra[v] = vec_t{0, 0, 0, 0};
       store(0);
       __builtin_amdgcn_sched_barrier(0);
       asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -376,13 +374,16 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
         issue_w((kt + 1) & 1, (kt + 1) * BK);
       }
       compute(0, kt & 1);
-      // Every wave is done reading this stage from LDS. An LDS-only barrier: __syncthreads() would also wait for
-      // the next stage's loads, which the wait before the stores above handles.
+      // Every wave is done reading this stage from LDS before the next row stores and weight loads overwrite it.
+      // The barrier waits for this wave's LDS reads only: a fence (__syncthreads(), or one scoped to LDS) would
+      // also wait for the next stage's loads in flight, the direct ones counting as LDS writes. The compiler
+      // moves no memory access across the two clobbers, nor the clobbers across the barrier.
+      asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
       __builtin_amdgcn_s_barrier();
-      asm volatile("" ::: "memory");
       __builtin_amdgcn_sched_barrier(0);
+      asm volatile("" ::: "memory");
     }
   } else if constexpr (NBUF == 1) {
     // One stage buffer: store, barrier, next loads in flight during the MFMAs, barrier.

@@ -314,6 +314,11 @@ struct PostModel {
 void launch_post(const float* raw, int row_len, const PostRow* rows, const unsigned char* legal, const PostModel& m,
                  float* out, int* status, int n, hipStream_t s);
 
+// The static device workspace of the allocation-free forward pass (kg_run_static): its size, and its address on
+// `device` (looked up once per device, with `device` current).
+constexpr size_t kStaticScratchBytes = 64ull << 20;
+void* static_scratch(int device);
+
 // FFN activation: h = silu(u[:, :F]) * u[:, F:2F] (gated) or mish(u[:, :F]), u float [rows][ldu] -> compute type.
 void launch_ffn_act(int prec, const float* u, int ldu, int F, bool gated, void* h, int ldh, int rows, hipStream_t s);
 

@@ -7,8 +7,38 @@
 #include "kgx_device.h"
 
 #include <cmath>
+#include <map>
+#include <mutex>
 
 namespace kgx {
+
+// The workspace of the allocation-free forward pass (kg_run_static): one static device array per GPU. Host code
+// never uses the array's name as an address: static_scratch() looks up each device's copy once, with that device
+// current, and every launch takes that pointer.
+// The array is initialized data (one nonzero byte), not a zero-fill section, so that this code object's size in
+// memory equals its size in the file: a zero-fill section at file offset 0x400 with 64 MiB extends the ELF's
+// section extent 64 MiB past its bytes, and a tool that copies a loaded code object by that extent reads past the
+// library's mapping. The offload bundle of this file is compressed (the Makefile), so the library stays small. The
+// forward pass writes or clears every byte it reads here, so the initial contents do not matter.
+static __device__ __align__(256) char scratch[kStaticScratchBytes] = {1};
+
+void* static_scratch(int device) {
+  static std::mutex mu;
+  static std::map<int, void*> ptrs;
+  std::lock_guard<std::mutex> lock(mu);
+  auto it = ptrs.find(device);
+  if (it != ptrs.end()) return it->second;
+  int cur = -1;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) throw std::runtime_error(std::string("hipGetDevice: ") + hipGetErrorString(e));
+  if (cur != device) throw std::runtime_error("internal: static scratch looked up on another device");
+  void* p = nullptr;
+  e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+  if (e != hipSuccess || !p)
+    throw std::runtime_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+  ptrs.emplace(device, p);
+  return p;
+}
 
 // ---------------------------------------------------------------------------------------------------------
 // Board mask and pooling

@@ -19,11 +19,6 @@ namespace kgx {
     if (e_ != hipSuccess) throw std::runtime_error(std::string(#call) + ": " + hipGetErrorString(e_));    \
   } while (0)
 
-// The static device workspace of the allocation-free forward pass: its size, and its address on `device` (looked
-// up once per device; `device` must be current).
-constexpr size_t kStaticScratchBytes = 64ull << 20;
-void* static_scratch(int device);
-
 struct DeviceBuffer {
   void* ptr = nullptr;
   size_t bytes = 0;

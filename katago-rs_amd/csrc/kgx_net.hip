@@ -15,28 +15,6 @@
 
 namespace kgx {
 
-// The workspace of the allocation-free forward pass (kg_run_static): one static device array per GPU, loaded with
-// the library's code object. Host code never uses the array's name as an address: static_scratch() looks up each
-// device's copy once, with that device current, and every launch takes that pointer.
-static __device__ __align__(256) char scratch[kStaticScratchBytes];
-
-void* static_scratch(int device) {
-  static std::mutex mu;
-  static std::map<int, void*> ptrs;
-  std::lock_guard<std::mutex> lock(mu);
-  auto it = ptrs.find(device);
-  if (it != ptrs.end()) return it->second;
-  int cur = -1;
-  KGX_HIP(hipGetDevice(&cur));
-  if (cur != device) throw std::runtime_error("internal: static scratch looked up on another device");
-  void* p = nullptr;
-  const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-  if (e != hipSuccess || !p)
-    throw std::runtime_error(std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
-  ptrs.emplace(device, p);
-  return p;
-}
-
 namespace {
 
 uint16_t f32_to_f16_bits(float f) {
