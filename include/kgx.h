@@ -216,6 +216,34 @@ int kg_profile_reset(kg_handle* handle);
 int kg_profile_read(kg_handle* handle, const char** names, long* launches, double* ms, double* flops,
                     double* bytes, int max_classes);
 
+/* Launch geometry of the 16-bit implicit-GEMM convolution, for host-side checks of its index maps. No counterpart
+ * in the reference (its convolutions are cubecl kernels with their own tiling, crates/katago-nn-burn/src/wino/
+ * kernels.rs); these call the same functions as the kernel and its launcher, and launch nothing.
+ * kg_conv_geometry: the configuration that a ks x ks convolution of ic -> oc channels (split: split operands, 1x1
+ * only) over `pixels` pixels (batch x 361) runs. */
+typedef struct {
+  int grid;                /* workgroups launched */
+  int threads;             /* threads per workgroup */
+  int tile_rows, tile_cols;/* pixels and output channels per workgroup */
+  int stage_channels;      /* input channels per K stage */
+  int pixel_tiles, col_tiles;
+  int pairs;               /* 1: 96-pixel tiles whose two halves of a 192-pixel tile share an XCD */
+  int weights_direct;      /* 1: the stage's weights go from memory straight into LDS */
+  int weight_rows;         /* weight rows per stage (taps x tile_cols) */
+  int waves;               /* waves per workgroup */
+  int direct_instructions; /* direct loads (8 rows of 128 bytes each) that fill one stage's weight rows */
+  int direct_per_wave;     /* direct loads each wave issues per stage */
+} kg_conv_geometry_t;
+int kg_conv_geometry(int ks, int ic, int oc, int split, int pixels, kg_conv_geometry_t* out);
+/* The (pixel tile, column tile) that workgroup `workgroup` computes; -1, -1 when it exits at once. */
+int kg_conv_tile_of(int ks, int ic, int oc, int split, int pixels, int workgroup, int* pixel_tile, int* col_tile);
+/* Weights straight into LDS: the weight row and 16-byte chunk that lane `lane` of wave `wave` reads with its
+ * direct load q of a stage, and the LDS weight row and chunk it fills (dst_row -1: a spare area nothing reads). */
+int kg_conv_weight_load(int ks, int ic, int oc, int split, int q, int wave, int lane, int* src_row, int* src_chunk,
+                        int* dst_row, int* dst_chunk);
+/* The stored chunk of logical 16-byte chunk `chunk` of LDS weight row `row` (what the fragment reads address). */
+int kg_conv_weight_chunk(int row, int chunk);
+
 #ifdef __cplusplus
 }
 #endif

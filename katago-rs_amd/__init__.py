@@ -37,6 +37,7 @@ EXPORTS = [
     "kg_get_output", "kg_profile_enable", "kg_profile_reset", "kg_profile_read",
     "kg_model_version_features", "kg_meta_encoder_channels", "kg_copy_outputs", "kg_run_static",
     "kg_get_output_async", "kg_wait", "kg_get_output_eval", "kg_post_outputs",
+    "kg_conv_geometry", "kg_conv_tile_of", "kg_conv_weight_load", "kg_conv_weight_chunk",
 ]
 # Completion callback of kg_get_output_async: (user, status).
 DONE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int)
@@ -93,6 +94,13 @@ class PostInput(ctypes.Structure):
         ("enable_passing_hacks", ctypes.c_int),
         ("no_result_allowed", ctypes.c_int),
     ]
+
+
+class ConvGeometry(ctypes.Structure):
+    """kg_conv_geometry_t: the launch geometry of the 16-bit implicit-GEMM convolution of given shapes."""
+    _fields_ = [(f, ctypes.c_int) for f in (
+        "grid", "threads", "tile_rows", "tile_cols", "stage_channels", "pixel_tiles", "col_tiles", "pairs",
+        "weights_direct", "weight_rows", "waves", "direct_instructions", "direct_per_wave")]
 
 
 class NNOutput(ctypes.Structure):
@@ -154,6 +162,10 @@ def lib():
         L.kg_get_output_eval.argtypes = [vp, ci, ctypes.POINTER(RowInput), ctypes.POINTER(PostInput),
                                          ctypes.POINTER(NNOutput)]
         L.kg_post_outputs.argtypes = [vp, ci, vp, vp, vp, ctypes.POINTER(PostInput), ctypes.POINTER(NNOutput)]
+        L.kg_conv_geometry.argtypes = [ci, ci, ci, ci, ci, ctypes.POINTER(ConvGeometry)]
+        L.kg_conv_tile_of.argtypes = [ci, ci, ci, ci, ci, ci, ctypes.POINTER(ci), ctypes.POINTER(ci)]
+        L.kg_conv_weight_load.argtypes = [ci, ci, ci, ci, ci, ci, ci] + [ctypes.POINTER(ci)] * 4
+        L.kg_conv_weight_chunk.argtypes = [ci, ci]
         _ = cf
         _lib = L
     return _lib
@@ -193,6 +205,31 @@ def copy_with_symmetry(src, symmetry: int, reverse: bool = False) -> np.ndarray:
     _check(lib().kg_copy_with_symmetry(_ptr(a), _ptr(out), a.shape[0], a.shape[1], a.shape[2], int(symmetry),
                                        int(bool(reverse))))
     return out
+
+
+def conv_geometry(ks: int, ic: int, oc: int, split: bool, pixels: int) -> dict:
+    """The launch geometry of the 16-bit implicit-GEMM convolution ks x ks, ic -> oc, over `pixels` pixels."""
+    g = ConvGeometry()
+    _check(lib().kg_conv_geometry(ks, ic, oc, int(split), pixels, ctypes.byref(g)))
+    return {f: getattr(g, f) for f, _ in ConvGeometry._fields_}
+
+
+def conv_tile_of(ks: int, ic: int, oc: int, split: bool, pixels: int, workgroup: int):
+    """(pixel tile, column tile) of a workgroup of that convolution's launch; (-1, -1) if it exits at once."""
+    mt, nt = ctypes.c_int(), ctypes.c_int()
+    _check(lib().kg_conv_tile_of(ks, ic, oc, int(split), pixels, workgroup, ctypes.byref(mt), ctypes.byref(nt)))
+    return mt.value, nt.value
+
+
+def conv_weight_load(ks: int, ic: int, oc: int, split: bool, q: int, wave: int, lane: int):
+    """(src row, src chunk, dst row, dst chunk) of direct weight load q of (wave, lane); dst row -1: spare."""
+    r = [ctypes.c_int() for _ in range(4)]
+    _check(lib().kg_conv_weight_load(ks, ic, oc, int(split), q, wave, lane, *[ctypes.byref(x) for x in r]))
+    return tuple(x.value for x in r)
+
+
+def conv_weight_chunk(row: int, chunk: int) -> int:
+    return lib().kg_conv_weight_chunk(row, chunk)
 
 
 def model_version_features(model_version: int):

@@ -492,6 +492,46 @@ int kg_copy_with_symmetry(const float* src, float* dst, int channels, int h, int
   });
 }
 
+int kg_conv_geometry(int ks, int ic, int oc, int split, int pixels, kg_conv_geometry_t* out) {
+  return guarded([&] {
+    if (!out) throw std::runtime_error("null output");
+    if ((ks != 1 && ks != 3) || ic < 1 || oc < 1 || pixels < 1 || (split && ks != 1))
+      throw std::runtime_error("bad convolution shape");
+    const kgx::IgemmGeometry g = kgx::conv_igemm_geometry(ks, ic, oc, split != 0, pixels);
+    *out = kg_conv_geometry_t{g.grid, g.threads, g.tile_rows, g.tile_cols, g.stage_channels, g.pixel_tiles,
+                              g.col_tiles, g.pairs, g.weights_direct, g.weight_rows, g.waves,
+                              g.direct_instructions, g.direct_per_wave};
+  });
+}
+
+int kg_conv_tile_of(int ks, int ic, int oc, int split, int pixels, int workgroup, int* pixel_tile, int* col_tile) {
+  return guarded([&] {
+    if (!pixel_tile || !col_tile) throw std::runtime_error("null output");
+    if ((ks != 1 && ks != 3) || ic < 1 || oc < 1 || pixels < 1 || (split && ks != 1))
+      throw std::runtime_error("bad convolution shape");
+    const kgx::IgemmGeometry g = kgx::conv_igemm_geometry(ks, ic, oc, split != 0, pixels);
+    if (workgroup < 0 || workgroup >= g.grid) throw std::runtime_error("workgroup out of range");
+    kgx::conv_igemm_tile_of(g, workgroup, *pixel_tile, *col_tile);
+  });
+}
+
+int kg_conv_weight_load(int ks, int ic, int oc, int split, int q, int wave, int lane, int* src_row, int* src_chunk,
+                        int* dst_row, int* dst_chunk) {
+  return guarded([&] {
+    if (!src_row || !src_chunk || !dst_row || !dst_chunk) throw std::runtime_error("null output");
+    if ((ks != 1 && ks != 3) || ic < 1 || oc < 1 || (split && ks != 1)) throw std::runtime_error("bad convolution shape");
+    const kgx::IgemmGeometry g = kgx::conv_igemm_geometry(ks, ic, oc, split != 0, 1);
+    if (!g.weights_direct) throw std::runtime_error("this convolution stages its weights through registers");
+    if (q < 0 || q >= g.direct_per_wave || wave < 0 || wave >= g.waves || lane < 0 || lane >= 64)
+      throw std::runtime_error("direct load index out of range");
+    kgx::conv_igemm_weight_load(g, q, wave, lane, *src_row, *src_chunk, *dst_row, *dst_chunk);
+  });
+}
+
+int kg_conv_weight_chunk(int row, int chunk) {
+  return row >= 0 && chunk >= 0 && chunk < 8 ? kgx::conv_igemm_weight_chunk(row, chunk) : -1;
+}
+
 int kg_handle_is_using_fp16(const kg_handle* h) { return h && h->precision != KG_PRECISION_F32 ? 1 : 0; }
 
 int kg_forward(kg_handle* h, int n, const float* bin, const float* global, const float* meta, float* out) {

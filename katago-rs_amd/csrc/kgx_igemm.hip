@@ -46,6 +46,31 @@ struct IgCfg {
   static constexpr bool PAIRS = BM_ == 96;
 };
 
+// XCD-aware tile order: workgroup g runs on XCD g % 8, so the ntl column tiles of one pixel tile are given the
+// ids g, g + 8, ... of one XCD: they share its L2 for the pixel rows they all read, and their halves of the cache
+// lines they write meet in the same L2. With 96-pixel tiles in pairs, both halves of a 192-pixel tile go to one
+// XCD, as the 192-pixel convolutions around them map that tile. Workgroup g takes pixel tile mt and column tile
+// nt; ids beyond the last pixel tile (the grid is rounded to 8) exit.
+__host__ __device__ inline void igemm_tile_of(int g, int ntl, bool pairs, int& mt, int& nt) {
+  const int slot = g >> 3, u = slot / ntl;
+  nt = slot % ntl;
+  mt = pairs ? 2 * ((u >> 1) * 8 + (g & 7)) + (u & 1) : u * 8 + (g & 7);
+}
+
+// Weights into LDS, one stage: wi instructions of 64 lanes fill the stage's wi * 8 weight rows of 128 bytes,
+// instruction q of wave wv (nw waves) filling rows [8 (q nw + wv), + 8), lane i row i / 8 at stored chunk i % 8.
+// Every wave issues the same number of instructions: one beyond the wi-th (q nw + wv >= wi) reloads the last 8
+// rows into a spare area (dst_row8 = -1) that nothing reads, so that no load of the kernel sits under a branch.
+__host__ __device__ inline void wdma_slot(int q, int wv, int lane, int nw, int wi, int& src_row, int& dst_row8) {
+  const int ins = q * nw + wv;
+  src_row = (ins < wi ? ins : wi - 1) * 8 + (lane >> 3);
+  dst_row8 = ins < wi ? ins * 8 : -1;
+}
+// The stored 16-byte chunk of logical chunk c of weight row `row` (chunk ^ (row / 2 % 8)): conflict-free 16-row
+// fragment reads of unpadded 128-byte rows. The swizzle is its own inverse, so a lane that stores chunk s loads the
+// row's logical chunk wdma_chunk(row, s).
+__host__ __device__ inline int wdma_chunk(int row, int c) { return c ^ ((row >> 1) & 7); }
+
 template <typename T, typename C, bool POOL>
 __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restrict__ X, const T* __restrict__ Xlo,
                                                                int ldx, int IC, const T* __restrict__ W, int icp,
@@ -88,12 +113,8 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int grp = wave / (WM * WN), wl = wave - grp * (WM * WN);
   const int wm = wl / WN, wn = wl % WN;
-  // XCD-aware tile order: workgroup g runs on XCD g % 8, so the NTL output tiles of one pixel tile are given the
-  // ids g, g + 8, ... of one XCD: they share its L2 for the pixel rows they all read, and their halves of the
-  // cache lines they write meet in the same L2. Ids beyond the last pixel tile (grid rounded to 8) exit.
-  const int g = blockIdx.x, ntl = (OC + BN - 1) / BN;
-  const int slot = g >> 3, nt = slot % ntl, u = slot / ntl;
-  const int mt = C::PAIRS ? 2 * ((u >> 1) * 8 + (g & 7)) + (u & 1) : u * 8 + (g & 7);
+  int mt, nt;
+  igemm_tile_of(blockIdx.x, (OC + BN - 1) / BN, C::PAIRS, mt, nt);
   if (mt * BM >= M) return;
   const int n0 = nt * BN, m0 = mt * BM;
   const int r16 = lane & 15, g4 = lane >> 4;
@@ -150,30 +171,26 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
         if ((PL * TB) % RP == 0 || r0 + v * RP < PL * TB) *(vec_t*)(bb + v * RP * LDK) = rb[v];
     }
   };
-  // Weights into LDS: instruction q of wave wv fills weight rows [8 (q NW + wv), + 8) of a buffer, lane i row
-  // i / 8 at stored chunk i % 8, loaded from chunk (i % 8) ^ (row / 2 % 8) of that row's stage slice. Every wave
-  // issues WQ of them per stage: where WI is not a multiple of NW, the last instruction of waves WI % NW and up
-  // reloads the tile's last 8 rows into a spare KB of LDS that nothing reads. So no load is under a branch and
-  // the compiler counts exactly how many direct loads follow the pixel rows.
+  // Weights into LDS (wdma_slot): WQ direct loads per wave and stage, each lane loading the logical chunk that
+  // its stored chunk holds. With no load under a branch, the compiler counts exactly how many direct loads follow
+  // the pixel rows.
   constexpr int NW = NT / 64, WI = TB / 8, WQ = C::WDMA ? (WI + NW - 1) / NW : 1;
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const T* wtile = W + (size_t)nt * PL * TB * icp;
   const int wbytes = TB * icp * (int)sizeof(T);
   T* const Wspare = (T*)(smem + WSPARE);
-  int woff[WQ];
+  int woff[WQ], wdst[WQ];
 #pragma unroll
   for (int q = 0; q < WQ; q++) {
-    const int row = min(q * NW + wv, WI - 1) * 8 + (lane >> 3);
-    woff[q] = row * icp * (int)sizeof(T) + (((lane & 7) ^ ((row >> 1) & 7)) * 16);
+    int row;
+    wdma_slot(q, wv, lane, NW, WI, row, wdst[q]);
+    woff[q] = row * icp * (int)sizeof(T) + wdma_chunk(row, lane & 7) * 16;
   }
   auto issue_w = [&](int buf, int k0) {
     if constexpr (C::WDMA) {
 #pragma unroll
-      for (int q = 0; q < WQ; q++) {
-        T* dst = Bw + buf * WSE + (q * NW + wv) * 8 * BK;
-        if (WI % NW != 0 && q == WQ - 1 && q * NW + wv >= WI) dst = Wspare;
-        lds_load16(wtile, wbytes, dst, woff[q] + k0 * (int)sizeof(T));
-      }
+      for (int q = 0; q < WQ; q++)
+        lds_load16(wtile, wbytes, wdst[q] < 0 ? Wspare : Bw + buf * WSE + wdst[q] * BK, woff[q] + k0 * (int)sizeof(T));
     }
   };
 
@@ -214,9 +231,8 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
 
   // The MFMA steps of one group over the staged stage: its share of the (tap, 32-channel slice) pairs, with the
   // fragments of the next step read from LDS while the current step's MFMAs run.
-  // Fragment reads of the swizzled weight rows: fragment rows start at multiples of 16, so a row's swizzle is
-  // (r16 / 2) % 8 and the chunk of K offset kk is (kk / 8) ^ (g4 ^ (r16 / 2) % 8).
-  const int wsw = g4 ^ ((r16 >> 1) & 7);
+  // Fragment reads of the swizzled weight rows: fragment rows start at multiples of 16, so a row's swizzle is that
+  // of row r16, and lane group g4's chunk of K offset kk is wdma_chunk(r16, kk / 8 ^ g4).
   auto mma = [&](auto gc, int sb, int wbuf) {
     constexpr int g = decltype(gc)::value;
     constexpr int KK = BK / 32, ST = TAPS * KK, S0 = g * ST / G, S = (g + 1) * ST / G - S0;
@@ -225,7 +241,7 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     auto fetch = [&](int s, int fb) {
       const int t = (S0 + s) / KK, kk = ((S0 + s) % KK) * 32;
       const int shift = C::KS == 3 ? (t / 3 - 1) * POS + (t % 3 - 1) : 0;
-      const T* bs = C::WDMA ? Bw + wbuf * WSE + (t * BN + wn * WTN + r16) * BK + (((kk / 8) ^ wsw) * 8)
+      const T* bs = C::WDMA ? Bw + wbuf * WSE + (t * BN + wn * WTN + r16) * BK + wdma_chunk(r16, (kk / 8) ^ g4) * 8
                             : Bs + sb * SE + (t * BN + wn * WTN + r16) * LDK + g4 * 8 + kk;
 #pragma unroll
       for (int i = 0; i < MB; i++) {
@@ -650,6 +666,54 @@ static void igemm_dispatch(int kind, const void* x, const void* xlo, int ldx, in
 }
 
 thread_local LaunchTiming g_launch_timing;
+
+template <typename C>
+static IgemmGeometry igemm_geometry_of(int OC, int M) {
+  IgemmGeometry gm;
+  const int mtiles = (M + C::BM - 1) / C::BM, ntiles = (OC + C::BN - 1) / C::BN;
+  gm.grid = C::PAIRS ? 8 * ((mtiles + 15) / 16) * 2 * ntiles : round_up(mtiles, 8) * ntiles;  // as igemm_launch
+  gm.threads = C::NT;
+  gm.tile_rows = C::BM;
+  gm.tile_cols = C::BN;
+  gm.stage_channels = C::BK;
+  gm.col_tiles = ntiles;
+  gm.pixel_tiles = mtiles;
+  gm.pairs = C::PAIRS;
+  gm.weights_direct = C::WDMA;
+  gm.weight_rows = C::TAPS * C::BN;
+  gm.waves = C::NT / 64;
+  gm.direct_instructions = C::WDMA ? C::TAPS * C::BN / 8 : 0;
+  gm.direct_per_wave = C::WDMA ? (gm.direct_instructions + gm.waves - 1) / gm.waves : 0;
+  return gm;
+}
+
+IgemmGeometry conv_igemm_geometry(int ks, int ic, int oc, bool split, int M) {
+  switch (igemm_kind(ks, ic, oc, split)) {
+    case IG3_48: return igemm_geometry_of<Ig3>(oc, M);
+    case IG3_64: return igemm_geometry_of<Ig3n64>(oc, M);
+    case IG3_96: return igemm_geometry_of<Ig3n96>(oc, M);
+    case IG1_128: return igemm_geometry_of<Ig1k128>(oc, M);
+    case IG1_128S: return igemm_geometry_of<Ig1k128s>(oc, M);
+    case IG1_48S: return igemm_geometry_of<Ig1sh>(oc, M);
+    default: return igemm_geometry_of<Ig1>(oc, M);
+  }
+}
+
+void conv_igemm_tile_of(const IgemmGeometry& gm, int g, int& mt, int& nt) {
+  igemm_tile_of(g, gm.col_tiles, gm.pairs, mt, nt);
+  if (mt >= gm.pixel_tiles) mt = nt = -1;
+}
+
+void conv_igemm_weight_load(const IgemmGeometry& gm, int q, int wave, int lane, int& src_row, int& src_chunk,
+                            int& dst_row, int& dst_chunk) {
+  int row8;
+  wdma_slot(q, wave, lane, gm.waves, gm.direct_instructions, src_row, row8);
+  src_chunk = wdma_chunk(src_row, lane & 7);
+  dst_row = row8 < 0 ? -1 : row8 + (lane >> 3);
+  dst_chunk = lane & 7;
+}
+
+int conv_igemm_weight_chunk(int row, int chunk) { return wdma_chunk(row, chunk); }
 
 const char* conv_igemm_class(int ks, int ic, int oc, bool split) {
   switch (igemm_kind(ks, ic, oc, split)) {

@@ -148,6 +148,19 @@ const char* conv_igemm_class(int ks, int ic, int oc, bool split = false);
 // per tile (BN) when its kernel computes pooling partials (3x3 with 64-channel column tiles, 192 pixels), else 0.
 int conv_igemm_tile_rows(int ks, int ic, int oc, bool split = false);
 int conv_igemm_pool_cols(int ks, int ic, int oc);
+// The launch geometry of the convolution of these shapes over M pixels, and the index maps its kernel uses (the
+// same functions): workgroup -> (pixel tile, column tile), -1 for a workgroup that exits at once; with the weights
+// straight into LDS, the weight row and chunk that direct load q of (wave, lane) reads and the LDS row and chunk it
+// fills (-1: the spare area), and the stored chunk of a row's logical chunk.
+struct IgemmGeometry {
+  int grid, threads, tile_rows, tile_cols, stage_channels, pixel_tiles, col_tiles, pairs;
+  int weights_direct, weight_rows, waves, direct_instructions, direct_per_wave;
+};
+IgemmGeometry conv_igemm_geometry(int ks, int ic, int oc, bool split, int M);
+void conv_igemm_tile_of(const IgemmGeometry& gm, int g, int& mt, int& nt);
+void conv_igemm_weight_load(const IgemmGeometry& gm, int q, int wave, int lane, int& src_row, int& src_chunk,
+                            int& dst_row, int& dst_chunk);
+int conv_igemm_weight_chunk(int row, int chunk);
 // w [oc][ic][ks][ks] -> [oc tile][tap][BN][icp] float; with `split` -> [oc tile][hi, lo][tap][BN][icp], the low
 // plane holding w - round(w) for the compute type `prec`.
 void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector<float>& out, bool split = false,
