@@ -216,6 +216,52 @@ int kg_profile_reset(kg_handle* handle);
 int kg_profile_read(kg_handle* handle, const char** names, long* launches, double* ms, double* flops,
                     double* bytes, int max_classes);
 
+/* A position for the device featurizer: the board, and the results of the rules engine (board history, ladder
+ * search, area) that NNInputs::fill_row_v7 reads (crates/katago-core/src/neuralnet/nninputs.rs:1336-1800). Points
+ * are indexed x + y * x_size (0 <= x < x_size, 0 <= y < y_size); colours and players are 0 empty, 1 black, 2 white.
+ * The caller applies fill_row_v7's history rules: history_turns is min(maxTurnsOfHistoryToInclude,
+ * numApproxValidTurnsThisPhase) as fill_row_v7 computes them (0 when a pass would end the game and it hides the
+ * history), and pass_would_end_phase is 0 where it suppresses that feature. */
+typedef struct {
+  int x_size, y_size;              /* board size, 1..19 (at most the layout's) */
+  int next_player;                 /* the player to move (1 or 2) */
+  int ko_loc;                      /* Board::ko_loc, or -1 */
+  int encore_phase;                /* hist.encore_phase: 0, 1 or 2 */
+  int ko_rule;                     /* Rules::KO_SIMPLE 0, KO_POSITIONAL 1, KO_SITUATIONAL 2, KO_SPIGHT 3 */
+  int scoring_rule;                /* Rules::SCORING_AREA 0, SCORING_TERRITORY 1 */
+  int tax_rule;                    /* Rules::TAX_NONE 0, TAX_SEKI 1, TAX_ALL 2 */
+  int multi_stone_suicide_legal;   /* hist.rules.multi_stone_suicide_legal */
+  int has_button;                  /* hist.has_button */
+  int pass_would_end_phase;        /* hist.pass_would_end_phase(board, next_player), or 0 where suppressed */
+  int history_turns;               /* see above */
+  int num_moves;                   /* entries of move_loc / move_player, most recent first, 0..5 */
+  int move_loc[5];                 /* the move's point, -1 a pass, -2 Board::NULL_LOC */
+  int move_player[5];
+  float self_komi;                 /* hist.current_self_komi(next_player, drawEquivalentWinsForWhite) */
+  double playout_doubling_advantage; /* MiscNNInputParams::playout_doubling_advantage */
+  unsigned char color[361];        /* board.colors */
+  unsigned char area[361];         /* the area colour: calculate_area (area scoring, no tax) or
+                                    * calculate_independent_life_area, as fill_row_v7 chooses by the rules */
+  unsigned char encore_start[361]; /* hist.second_encore_start_colors */
+  unsigned char marks[361];        /* bit 0 hist.super_ko_banned, bit 1 hist.ko_recap_blocked, bits 2..5 the ladder
+                                    * features 14..17 (iter_ladders over the board and the two previous boards) */
+} kg_position;
+
+/* The device featurizer: fill_row_v7 (nninputs.rs:1336-1800) for n positions, then copy_inputs' symmetry
+ * (backend.rs:497-546, nninputs.rs:756-874), into the handle's device input buffers (the layout kg_run reads), on
+ * the handle's stream, without waiting. The features that are functions of the board and the position's fields
+ * (on-board, stones, liberties 1/2/3 by chain, ko, history, area, encore and ladder planes, the 19 globals) are
+ * computed on the device. symmetry[i] in 0..7 (NULL: 0). The network must take the version-7 inputs (22 spatial, 19
+ * global features: model versions 8 and up). Rejects a position whose fields are out of range, as the reference's
+ * asserts would. A following kg_run (out != NULL) returns the rows. */
+int kg_featurize(kg_handle* handle, int n, const kg_position* rows, const int* symmetry);
+
+/* The same featurizer with fill_row_v7's own layout arguments, between host buffers: bin gets n rows of 22 planes of
+ * nn_x_len x nn_y_len (NCHW, or NHWC with use_nhwc), global n rows of 19, each after its symmetry (copy_inputs_with_
+ * symmetry of the row; NULL: none). Runs on `device` and waits; allocates device memory for the call. */
+int kg_featurize_rows(int device, int n, const kg_position* rows, int nn_x_len, int nn_y_len, int use_nhwc,
+                      const int* symmetry, float* bin, float* global);
+
 /* Launch geometry of the 16-bit implicit-GEMM convolution, for host-side checks of its index maps. No counterpart
  * in the reference (its convolutions are cubecl kernels with their own tiling, crates/katago-nn-burn/src/wino/
  * kernels.rs); these call the same functions as the kernel and its launcher, and launch nothing.

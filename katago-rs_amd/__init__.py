@@ -38,6 +38,7 @@ EXPORTS = [
     "kg_model_version_features", "kg_meta_encoder_channels", "kg_copy_outputs", "kg_run_static",
     "kg_get_output_async", "kg_wait", "kg_get_output_eval", "kg_post_outputs",
     "kg_conv_geometry", "kg_conv_tile_of", "kg_conv_weight_load", "kg_conv_weight_chunk",
+    "kg_featurize", "kg_featurize_rows",
 ]
 # Completion callback of kg_get_output_async: (user, status).
 DONE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int)
@@ -94,6 +95,49 @@ class PostInput(ctypes.Structure):
         ("enable_passing_hacks", ctypes.c_int),
         ("no_result_allowed", ctypes.c_int),
     ]
+
+
+class Position(ctypes.Structure):
+    """kg_position: a position for the device featurizer (fill_row_v7's inputs, nninputs.rs:1336-1800)."""
+    _fields_ = [(f, ctypes.c_int) for f in (
+        "x_size", "y_size", "next_player", "ko_loc", "encore_phase", "ko_rule", "scoring_rule", "tax_rule",
+        "multi_stone_suicide_legal", "has_button", "pass_would_end_phase", "history_turns", "num_moves")] + [
+        ("move_loc", ctypes.c_int * 5), ("move_player", ctypes.c_int * 5), ("self_komi", ctypes.c_float),
+        ("playout_doubling_advantage", ctypes.c_double), ("color", ctypes.c_ubyte * 361),
+        ("area", ctypes.c_ubyte * 361), ("encore_start", ctypes.c_ubyte * 361), ("marks", ctypes.c_ubyte * 361)]
+
+
+def make_positions(items):
+    """A ctypes array of Position from dicts with keys meta (x_size, y_size, next_player, ko_loc, encore_phase,
+    ko_rule, scoring_rule, tax_rule, multi_stone_suicide_legal, has_button, pass_would_end_phase, history_turns,
+    num_moves), color, marks, area, enc ([361] uint8, index x + y * x_size), moves ([10]: loc, player per move),
+    self_komi and pda."""
+    arr = (Position * len(items))()
+    names = [f for f, _ in Position._fields_[:13]]
+    for i, it in enumerate(items):
+        p = arr[i]
+        for f, v in zip(names, it["meta"]):
+            setattr(p, f, int(v))
+        mv = np.asarray(it["moves"], np.int32)
+        for k in range(5):
+            p.move_loc[k] = int(mv[2 * k])
+            p.move_player[k] = int(mv[2 * k + 1])
+        p.self_komi = float(it["self_komi"])
+        p.playout_doubling_advantage = float(it["pda"])
+        for f, key in (("color", "color"), ("area", "area"), ("encore_start", "enc"), ("marks", "marks")):
+            ctypes.memmove(getattr(p, f), np.ascontiguousarray(it[key], np.uint8).ctypes.data, 361)
+    return arr
+
+
+def featurize_rows(positions, nn_x: int = 19, nn_y: int = 19, nhwc: bool = False, symmetry=None, device: int = 0):
+    """The device featurizer between host buffers (kg_featurize_rows): ([n, 22 * nn_x * nn_y], [n, 19]) float32."""
+    n = len(positions)
+    bin_ = np.empty((n, 22 * nn_x * nn_y), np.float32)
+    glob = np.empty((n, 19), np.float32)
+    sym = None if symmetry is None else np.ascontiguousarray(symmetry, np.int32)
+    _check(lib().kg_featurize_rows(device, n, positions, nn_x, nn_y, int(bool(nhwc)), _ptr(sym), _ptr(bin_),
+                                   _ptr(glob)))
+    return bin_, glob
 
 
 class ConvGeometry(ctypes.Structure):
@@ -162,6 +206,8 @@ def lib():
         L.kg_get_output_eval.argtypes = [vp, ci, ctypes.POINTER(RowInput), ctypes.POINTER(PostInput),
                                          ctypes.POINTER(NNOutput)]
         L.kg_post_outputs.argtypes = [vp, ci, vp, vp, vp, ctypes.POINTER(PostInput), ctypes.POINTER(NNOutput)]
+        L.kg_featurize.argtypes = [vp, ci, ctypes.POINTER(Position), vp]
+        L.kg_featurize_rows.argtypes = [ci, ci, ctypes.POINTER(Position), ci, ci, ci, vp, vp, vp]
         L.kg_conv_geometry.argtypes = [ci, ci, ci, ci, ci, ctypes.POINTER(ConvGeometry)]
         L.kg_conv_tile_of.argtypes = [ci, ci, ci, ci, ci, ci, ctypes.POINTER(ci), ctypes.POINTER(ci)]
         L.kg_conv_weight_load.argtypes = [ci, ci, ci, ci, ci, ci, ci] + [ctypes.POINTER(ci)] * 4
@@ -360,6 +406,11 @@ class Handle:
                                 out.size < n * self.net.row_len):
             raise ValueError(f"out must be contiguous float32 with room for {n} rows of {self.net.row_len}")
         _check(lib().kg_run(self._h, n, _ptr(out)))
+
+    def featurize(self, positions, symmetry=None):
+        """The device featurizer (kg_featurize) into the handle's device input buffers, without waiting."""
+        sym = None if symmetry is None else np.ascontiguousarray(symmetry, np.int32)
+        _check(lib().kg_featurize(self._h, len(positions), positions, _ptr(sym)))
 
     def run_static(self, n: int):
         """The allocation-free forward pass (kg_run_static): inputs in the device buffers, outputs left in the

@@ -53,6 +53,14 @@ struct kg_handle {
   float* h_post_out = nullptr;
   int* h_post_status = nullptr;
   kgx::PostModel post_model;
+  // The device featurizer's buffers (kg_featurize, first use): positions and symmetries on the device, their pinned
+  // staging, and an event after their upload (the next call waits for it before overwriting the staging).
+  kg_position* d_pos = nullptr;
+  int* d_pos_sym = nullptr;
+  kg_position* h_pos = nullptr;
+  int* h_pos_sym = nullptr;
+  hipEvent_t pos_uploaded = nullptr;
+  bool pos_pending = false;
   // The readback of kg_get_output_async runs on this helper thread; the next call on the handle joins it first.
   std::thread helper;
   int helper_status = 0;
@@ -460,6 +468,11 @@ void kg_handle_free(kg_handle* h) {
   if (h->h_legal) (void)hipHostFree(h->h_legal);
   if (h->h_post_out) (void)hipHostFree(h->h_post_out);
   if (h->h_post_status) (void)hipHostFree(h->h_post_status);
+  if (h->d_pos) (void)hipFree(h->d_pos);
+  if (h->d_pos_sym) (void)hipFree(h->d_pos_sym);
+  if (h->h_pos) (void)hipHostFree(h->h_pos);
+  if (h->h_pos_sym) (void)hipHostFree(h->h_pos_sym);
+  if (h->pos_uploaded) (void)hipEventDestroy(h->pos_uploaded);
   if (h->stream) (void)hipStreamDestroy(h->stream);
   delete h;
 }
@@ -653,6 +666,72 @@ int kg_get_output_eval(kg_handle* h, int n, const kg_row_input* rows, const kg_p
     upload_rows(h, n);
     h->net->forward(n_run, h->stream);
     post_and_read(h, n, h->net->d_out(), outputs);
+  });
+}
+
+int kg_featurize(kg_handle* h, int n, const kg_position* rows, const int* symmetry) {
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    if (!rows) throw std::runtime_error("null positions");
+    std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
+    if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
+    if (h->nin != 22 || h->nglob != 19)
+      throw std::runtime_error("kgx featurizer: the network does not take the version-7 inputs (22 spatial and 19 "
+                               "global features)");
+    for (int r = 0; r < n; r++) {
+      kgx::validate_position(rows[r], POS, POS);
+      if (symmetry && (symmetry[r] < 0 || symmetry[r] > 7))
+        throw std::runtime_error("kgx backend: symmetry must be in [0, 8)");
+    }
+    KGX_HIP(hipSetDevice(h->device));
+    if (!h->d_pos) {
+      const size_t B = (size_t)h->max_batch;
+      KGX_HIP(hipMalloc((void**)&h->d_pos, B * sizeof(kg_position)));
+      KGX_HIP(hipMalloc((void**)&h->d_pos_sym, B * sizeof(int)));
+      KGX_HIP(hipHostMalloc((void**)&h->h_pos, B * sizeof(kg_position), hipHostMallocDefault));
+      KGX_HIP(hipHostMalloc((void**)&h->h_pos_sym, B * sizeof(int), hipHostMallocDefault));
+      KGX_HIP(hipEventCreateWithFlags(&h->pos_uploaded, hipEventDisableTiming));
+    }
+    if (h->pos_pending) KGX_HIP(hipEventSynchronize(h->pos_uploaded));
+    std::memcpy(h->h_pos, rows, (size_t)n * sizeof(kg_position));
+    for (int r = 0; r < n; r++) h->h_pos_sym[r] = symmetry ? symmetry[r] : 0;
+    KGX_HIP(hipMemcpyAsync(h->d_pos, h->h_pos, (size_t)n * sizeof(kg_position), hipMemcpyHostToDevice, h->stream));
+    KGX_HIP(hipMemcpyAsync(h->d_pos_sym, h->h_pos_sym, (size_t)n * sizeof(int), hipMemcpyHostToDevice, h->stream));
+    KGX_HIP(hipEventRecord(h->pos_uploaded, h->stream));
+    h->pos_pending = true;
+    kgx::launch_featurize(h->d_pos, n, POS, POS, false, h->d_pos_sym, h->net->d_bin(), h->net->d_global(), h->nglob,
+                          h->stream);
+  });
+}
+
+int kg_featurize_rows(int device, int n, const kg_position* rows, int nn_x_len, int nn_y_len, int use_nhwc,
+                      const int* symmetry, float* bin, float* global) {
+  return guarded([&] {
+    if (!rows || !bin || !global) throw std::runtime_error("null argument");
+    if (n < 1) throw std::runtime_error("kgx featurizer: no positions");
+    if (nn_x_len < 1 || nn_y_len < 1 || nn_x_len > POS || nn_y_len > POS)
+      throw std::runtime_error("kgx featurizer: nn_x_len and nn_y_len must be in [1, 19]");
+    for (int r = 0; r < n; r++) {
+      kgx::validate_position(rows[r], nn_x_len, nn_y_len);
+      if (symmetry && (symmetry[r] < 0 || symmetry[r] > 7))
+        throw std::runtime_error("kgx backend: symmetry must be in [0, 8)");
+    }
+    KGX_HIP(hipSetDevice(device));
+    const size_t row = (size_t)22 * nn_x_len * nn_y_len;
+    kgx::DeviceBuffer d_pos, d_sym, d_bin, d_glob;  // freed on every exit
+    KGX_HIP(hipMalloc(&d_pos.ptr, (size_t)n * sizeof(kg_position)));
+    KGX_HIP(hipMalloc(&d_sym.ptr, (size_t)n * sizeof(int)));
+    KGX_HIP(hipMalloc(&d_bin.ptr, (size_t)n * row * 4));
+    KGX_HIP(hipMalloc(&d_glob.ptr, (size_t)n * 19 * 4));
+    std::vector<int> sym(n, 0);
+    if (symmetry) std::copy(symmetry, symmetry + n, sym.begin());
+    KGX_HIP(hipMemcpy(d_pos.ptr, rows, (size_t)n * sizeof(kg_position), hipMemcpyHostToDevice));
+    KGX_HIP(hipMemcpy(d_sym.ptr, sym.data(), (size_t)n * sizeof(int), hipMemcpyHostToDevice));
+    kgx::launch_featurize((const kg_position*)d_pos.ptr, n, nn_x_len, nn_y_len, use_nhwc != 0, (const int*)d_sym.ptr,
+                          (float*)d_bin.ptr, (float*)d_glob.ptr, 19, nullptr);
+    KGX_HIP(hipMemcpy(bin, d_bin.ptr, (size_t)n * row * 4, hipMemcpyDeviceToHost));
+    KGX_HIP(hipMemcpy(global, d_glob.ptr, (size_t)n * 19 * 4, hipMemcpyDeviceToHost));
   });
 }
 

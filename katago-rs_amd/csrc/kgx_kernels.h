@@ -5,6 +5,8 @@
 #include <cstdint>
 #include <vector>
 
+#include "kgx.h"
+
 namespace kgx {
 
 constexpr int POS = 19;
@@ -326,6 +328,13 @@ struct PostModel {
 };
 void launch_post(const float* raw, int row_len, const PostRow* rows, const unsigned char* legal, const PostModel& m,
                  float* out, int* status, int n, hipStream_t s);
+
+// The device featurizer (kgx_featurize.hip): rejects a position outside fill_row_v7's assumptions for an nn_x x nn_y
+// layout; launches fill_row_v7 plus the input symmetry for n device-resident positions into n rows of 22 planes
+// (NCHW, or NHWC) and n rows of ld_glob floats (the 19 globals first).
+void validate_position(const kg_position& p, int nn_x, int nn_y);
+void launch_featurize(const kg_position* rows, int n, int nn_x, int nn_y, bool nhwc, const int* syms, float* bin,
+                      float* glob, int ld_glob, hipStream_t s);
 
 // The static device workspace of the allocation-free forward pass (kg_run_static): its size, and its address on
 // `device` (looked up once per device, with `device` current).

@@ -47,6 +47,10 @@ def lib():
                                           ctypes.c_float, ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int,
                                           ctypes.c_float, ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
                                           ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p]
+        L.kgo_featurize.restype = ctypes.c_int
+        L.kgo_featurize.argtypes = [ctypes.c_void_p] * 6 + [ctypes.c_float, ctypes.c_double, ctypes.c_int,
+                                                             ctypes.c_int, ctypes.c_int, ctypes.c_void_p,
+                                                             ctypes.c_void_p]
         _lib = L
     return _lib
 
@@ -190,3 +194,18 @@ def round_operands(x, operands):
     a = np.array(x, np.float64, copy=True, order="C")
     lib().kgo_round_operands(_p(a), a.size, {"f16": 1, "bf16": 2}[operands])
     return a
+
+
+def featurize(meta, color, marks, area, enc, moves, self_komi, pda, nn_x=19, nn_y=19, nhwc=False):
+    """fill_row_v7's spatial row (22 planes of nn_x * nn_y, NCHW or NHWC) and 19 global features for one position
+    (kgo_featurize: the board and the rules engine's results as inputs)."""
+    m = np.ascontiguousarray(meta, np.int32)
+    arrs = [np.ascontiguousarray(a, np.uint8) for a in (color, marks, area, enc)]
+    mv = np.ascontiguousarray(moves, np.int32)
+    row = np.empty(22 * nn_x * nn_y, np.float32)
+    glob = np.empty(19, np.float32)
+    rc = lib().kgo_featurize(_p(m), *[_p(a) for a in arrs], _p(mv), float(self_komi), float(pda), nn_x, nn_y,
+                             int(bool(nhwc)), _p(row), _p(glob))
+    if rc != 0:
+        raise ValueError(f"kgo_featurize: bad position ({rc})")
+    return row, glob
