@@ -256,6 +256,15 @@ typedef struct {
  * asserts would. A following kg_run (out != NULL) returns the rows. */
 int kg_featurize(kg_handle* handle, int n, const kg_position* rows, const int* symmetry);
 
+/* NNEvaluator's evaluation of n positions with everything between on the device: the featurizer (kg_featurize)
+ * into the handle's input buffers, the forward pass (padded to a bucket), then get_output's copy_outputs and
+ * NNEvaluator's post-processing (kg_get_output_eval), one readback of the finished fields. symmetry and
+ * policy_optimism per row (NULL: 0 for every row); post and outputs as in kg_get_output_eval. The reference runs
+ * these as three steps on the host around the backend (fill_row_bufs, nneval.rs:709-790; get_output,
+ * backend.rs:410-464; the post-processing, nneval.rs:1197-1500). The network must take no metadata inputs. */
+int kg_evaluate_positions(kg_handle* handle, int n, const kg_position* rows, const int* symmetry,
+                          const float* policy_optimism, const kg_post_input* post, kg_nn_output* outputs);
+
 /* The same featurizer with fill_row_v7's own layout arguments, between host buffers: bin gets n rows of 22 planes of
  * nn_x_len x nn_y_len (NCHW, or NHWC with use_nhwc), global n rows of 19, each after its symmetry (copy_inputs_with_
  * symmetry of the row; NULL: none). Runs on `device` and waits; allocates device memory for the call. */

@@ -38,7 +38,7 @@ EXPORTS = [
     "kg_model_version_features", "kg_meta_encoder_channels", "kg_copy_outputs", "kg_run_static",
     "kg_get_output_async", "kg_wait", "kg_get_output_eval", "kg_post_outputs",
     "kg_conv_geometry", "kg_conv_tile_of", "kg_conv_weight_load", "kg_conv_weight_chunk",
-    "kg_featurize", "kg_featurize_rows",
+    "kg_featurize", "kg_featurize_rows", "kg_evaluate_positions",
 ]
 # Completion callback of kg_get_output_async: (user, status).
 DONE_FN = ctypes.CFUNCTYPE(None, ctypes.c_void_p, ctypes.c_int)
@@ -208,6 +208,8 @@ def lib():
         L.kg_post_outputs.argtypes = [vp, ci, vp, vp, vp, ctypes.POINTER(PostInput), ctypes.POINTER(NNOutput)]
         L.kg_featurize.argtypes = [vp, ci, ctypes.POINTER(Position), vp]
         L.kg_featurize_rows.argtypes = [ci, ci, ctypes.POINTER(Position), ci, ci, ci, vp, vp, vp]
+        L.kg_evaluate_positions.argtypes = [vp, ci, ctypes.POINTER(Position), vp, vp, ctypes.POINTER(PostInput),
+                                            ctypes.POINTER(NNOutput)]
         L.kg_conv_geometry.argtypes = [ci, ci, ci, ci, ci, ctypes.POINTER(ConvGeometry)]
         L.kg_conv_tile_of.argtypes = [ci, ci, ci, ci, ci, ci, ctypes.POINTER(ci), ctypes.POINTER(ci)]
         L.kg_conv_weight_load.argtypes = [ci, ci, ci, ci, ci, ci, ci] + [ctypes.POINTER(ci)] * 4
@@ -488,6 +490,20 @@ class Handle:
         parr, _pkeep = self._post(post, len(rows))
         _check(lib().kg_get_output_eval(self._h, len(rows), arr, parr, outs))
         return [_output_dict(outs[i], owners[i]) for i in range(len(rows))]
+
+    def evaluate_positions(self, positions, symmetry, policy_optimism, post, want_ownership=True):
+        """Featurizer, forward pass and NNEvaluator's post-processing, all on the device (kg_evaluate_positions):
+        positions from make_positions, one symmetry and policy optimism per row, post as in get_output_eval."""
+        n = len(positions)
+        sym = np.ascontiguousarray(np.broadcast_to(symmetry, (n,)), np.int32)
+        opt = np.ascontiguousarray(np.broadcast_to(policy_optimism, (n,)), np.float32)
+        parr, _pkeep = self._post(post, n)
+        outs = (NNOutput * n)()
+        owners = [np.zeros(HW, np.float32) if want_ownership else None for _ in range(n)]
+        for i in range(n):
+            outs[i].white_owner_map = None if owners[i] is None else _ptr(owners[i]).value
+        _check(lib().kg_evaluate_positions(self._h, n, positions, _ptr(sym), _ptr(opt), parr, outs))
+        return [_output_dict(outs[i], owners[i]) for i in range(n)]
 
     def post_outputs(self, raw, symmetry, policy_optimism, post, want_ownership=True):
         """copy_outputs and NNEvaluator's post-processing of raw rows given on the host, on the device

@@ -335,6 +335,39 @@ void upload_rows(kg_handle* h, int n) {
     KGX_HIP(hipMemcpyAsync(h->net->d_meta(), h->h_meta, (size_t)n * h->nmeta * 4, hipMemcpyHostToDevice, h->stream));
 }
 
+// The device featurizer for n positions into the handle's input buffers, enqueued on its stream (kg_featurize).
+// Caller holds h->mu; every position and symmetry is checked before anything is enqueued.
+void enqueue_featurize(kg_handle* h, int n, const kg_position* rows, const int* symmetry) {
+  if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
+  if (h->nin != 22 || h->nglob != 19)
+    throw std::runtime_error("kgx featurizer: the network does not take the version-7 inputs (22 spatial and 19 "
+                             "global features)");
+  for (int r = 0; r < n; r++) {
+    kgx::validate_position(rows[r], POS, POS);
+    if (symmetry && (symmetry[r] < 0 || symmetry[r] > 7))
+      throw std::runtime_error("kgx backend: symmetry must be in [0, 8)");
+  }
+  KGX_HIP(hipSetDevice(h->device));
+  if (!h->d_pos) {
+    const size_t B = (size_t)h->max_batch;
+    KGX_HIP(hipMalloc((void**)&h->d_pos, B * sizeof(kg_position)));
+    KGX_HIP(hipMalloc((void**)&h->d_pos_sym, B * sizeof(int)));
+    KGX_HIP(hipHostMalloc((void**)&h->h_pos, B * sizeof(kg_position), hipHostMallocDefault));
+    KGX_HIP(hipHostMalloc((void**)&h->h_pos_sym, B * sizeof(int), hipHostMallocDefault));
+    KGX_HIP(hipEventCreateWithFlags(&h->pos_uploaded, hipEventDisableTiming));
+  }
+  // The previous call's upload must have left the staging before it is overwritten.
+  if (h->pos_pending) KGX_HIP(hipEventSynchronize(h->pos_uploaded));
+  std::memcpy(h->h_pos, rows, (size_t)n * sizeof(kg_position));
+  for (int r = 0; r < n; r++) h->h_pos_sym[r] = symmetry ? symmetry[r] : 0;
+  KGX_HIP(hipMemcpyAsync(h->d_pos, h->h_pos, (size_t)n * sizeof(kg_position), hipMemcpyHostToDevice, h->stream));
+  KGX_HIP(hipMemcpyAsync(h->d_pos_sym, h->h_pos_sym, (size_t)n * sizeof(int), hipMemcpyHostToDevice, h->stream));
+  KGX_HIP(hipEventRecord(h->pos_uploaded, h->stream));
+  h->pos_pending = true;
+  kgx::launch_featurize(h->d_pos, n, POS, POS, false, h->d_pos_sym, h->net->d_bin(), h->net->d_global(), h->nglob,
+                        h->stream);
+}
+
 }  // namespace
 
 extern "C" {
@@ -675,33 +708,29 @@ int kg_featurize(kg_handle* h, int n, const kg_position* rows, const int* symmet
     if (!rows) throw std::runtime_error("null positions");
     std::lock_guard<std::mutex> lock(h->mu);
     settle(h);
-    if (n < 1 || n > h->max_batch) throw std::runtime_error("kgx backend: batch size out of range");
-    if (h->nin != 22 || h->nglob != 19)
-      throw std::runtime_error("kgx featurizer: the network does not take the version-7 inputs (22 spatial and 19 "
-                               "global features)");
+    enqueue_featurize(h, n, rows, symmetry);
+  });
+}
+
+int kg_evaluate_positions(kg_handle* h, int n, const kg_position* rows, const int* symmetry,
+                          const float* policy_optimism, const kg_post_input* post, kg_nn_output* outputs) {
+  return guarded([&] {
+    if (!h) throw std::runtime_error("null handle");
+    if (!rows || !post || !outputs) throw std::runtime_error("null positions, post-processing inputs or outputs");
+    std::lock_guard<std::mutex> lock(h->mu);
+    settle(h);
+    if (h->nmeta) throw std::runtime_error("kgx featurizer: the network takes metadata inputs, which it does not write");
+    enqueue_featurize(h, n, rows, symmetry);
+    std::vector<int> sym(n, 0);
+    std::vector<float> opt(n, 0.f);
     for (int r = 0; r < n; r++) {
-      kgx::validate_position(rows[r], POS, POS);
-      if (symmetry && (symmetry[r] < 0 || symmetry[r] > 7))
-        throw std::runtime_error("kgx backend: symmetry must be in [0, 8)");
+      if (symmetry) sym[r] = symmetry[r];
+      if (policy_optimism) opt[r] = policy_optimism[r];
     }
-    KGX_HIP(hipSetDevice(h->device));
-    if (!h->d_pos) {
-      const size_t B = (size_t)h->max_batch;
-      KGX_HIP(hipMalloc((void**)&h->d_pos, B * sizeof(kg_position)));
-      KGX_HIP(hipMalloc((void**)&h->d_pos_sym, B * sizeof(int)));
-      KGX_HIP(hipHostMalloc((void**)&h->h_pos, B * sizeof(kg_position), hipHostMallocDefault));
-      KGX_HIP(hipHostMalloc((void**)&h->h_pos_sym, B * sizeof(int), hipHostMallocDefault));
-      KGX_HIP(hipEventCreateWithFlags(&h->pos_uploaded, hipEventDisableTiming));
-    }
-    if (h->pos_pending) KGX_HIP(hipEventSynchronize(h->pos_uploaded));
-    std::memcpy(h->h_pos, rows, (size_t)n * sizeof(kg_position));
-    for (int r = 0; r < n; r++) h->h_pos_sym[r] = symmetry ? symmetry[r] : 0;
-    KGX_HIP(hipMemcpyAsync(h->d_pos, h->h_pos, (size_t)n * sizeof(kg_position), hipMemcpyHostToDevice, h->stream));
-    KGX_HIP(hipMemcpyAsync(h->d_pos_sym, h->h_pos_sym, (size_t)n * sizeof(int), hipMemcpyHostToDevice, h->stream));
-    KGX_HIP(hipEventRecord(h->pos_uploaded, h->stream));
-    h->pos_pending = true;
-    kgx::launch_featurize(h->d_pos, n, POS, POS, false, h->d_pos_sym, h->net->d_bin(), h->net->d_global(), h->nglob,
-                          h->stream);
+    ensure_post(h);
+    stage_post(h, n, sym.data(), opt.data(), post);
+    h->net->forward(padded_batch_size(h->buckets, n, h->max_batch), h->stream);
+    post_and_read(h, n, h->net->d_out(), outputs);
   });
 }
 

@@ -7,7 +7,8 @@ nninputs.rs:1336-1800, with copy_inputs' symmetry) through the C ABI, bit for bi
   positions of every board size, all eight symmetries, both layouts, including one chain snaking over the whole
   board (the longest label propagation);
 - through a handle: kg_featurize into the device input buffers, then kg_run, equals kg_forward on the oracle's rows,
-  and the device buffers hold exactly the oracle's rows."""
+  and the device buffers hold exactly the oracle's rows; kg_evaluate_positions (featurizer, forward, post-processing
+  on the device) equals kg_get_output_eval on the oracle's rows, field for field."""
 
 import ctypes
 
@@ -142,3 +143,40 @@ def test_all_symmetries_of_the_fixture_layouts(kgx, oracle):
             for s, row in zip(range(8), rows):
                 want, _ = _oracle_row(oracle, p, nx, ny, nhwc, s)
                 assert np.array_equal(row, want), (pid, ei, nx, ny, nhwc, s)
+
+
+@pytest.mark.parametrize("prec", ["f32", "f16"])
+def test_evaluate_positions_equals_get_output_eval_on_oracle_rows(kgx, synth, oracle, prec):
+    """Positions in, NNEvaluator's fields out, everything between on the device: the same bits as get_output_eval
+    on the oracle's featurized rows (get_output applies the row symmetry to them), through a bucket larger than n."""
+    arch = synth.tiny_nets()["t_rmspos"]  # model version 17: the version-7 inputs, P = 2
+    net = kgx.Net(synth.write_model(arch, 4))
+    h = kgx.Handle(net, 8, prec)
+    h.set_batch_buckets([8])
+    rng = np.random.default_rng(31)
+    n = 5
+    positions = [fc.random_position(rng, s, s) for s in (19, 13, 9, 19, 7)]
+    sym = rng.integers(0, 8, n)
+    opt = rng.uniform(0, 1, n).astype(np.float32)
+    post = []
+    for p in positions:
+        xs, ys = int(p["meta"][0]), int(p["meta"][1])
+        legal = np.zeros(362, np.uint8)
+        for y in range(ys):
+            for x in range(xs):
+                legal[y * 19 + x] = p["color"][x + y * xs] == 0
+        legal[361] = 1
+        post.append({"legal": legal, "white_to_move": int(p["meta"][2]) == 2, "board_x_size": xs,
+                     "board_y_size": ys, "nn_policy_temperature": 1.0, "enable_passing_hacks": False,
+                     "no_result_allowed": True})
+    got = h.evaluate_positions(kgx.make_positions(positions), sym, opt, post)
+    rows = []
+    for p, s_, o in zip(positions, sym, opt):
+        row, glob = oracle.featurize(**p)
+        rows.append({"spatial": row.reshape(22, 19, 19), "glob": glob, "symmetry": int(s_), "policy_optimism": float(o)})
+    want = h.get_output_eval(rows, post)
+    for i in range(n):
+        for k in want[i]:
+            a, b = np.atleast_1d(np.asarray(got[i][k])), np.atleast_1d(np.asarray(want[i][k]))
+            assert a.dtype == b.dtype and a.shape == b.shape and a.tobytes() == b.tobytes(), (prec, i, k)
+    h.close()
