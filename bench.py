@@ -136,6 +136,71 @@ def time_gpu_workload(kgx, synth, hip, config, precision, batch, steps, warmup):
     return {"value": batch * steps / dt, "unit": "evals/s", "ms_per_step": dt / steps * 1e3, "steps": steps}
 
 
+def time_featurizer(kgx, synth, hip, net, precision, batch, steps):
+    """The device featurizer (kg_featurize) and the whole device path (kg_evaluate_positions: featurizer, forward
+    pass, post-processing, one readback of the finished fields) on `batch` seeded 19x19 positions. The featurizer is
+    timed with HIP events on the handle's stream around its upload and kernel; the whole path by the wall clock per
+    call, as a caller sees it."""
+    h = kgx.Handle(net, batch, precision, device=0)
+    pos = kgx.make_positions(synth.make_positions(batch, 77))
+    sym = np.ascontiguousarray(np.arange(batch) % 8, np.int32)
+    hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+    hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventSynchronize.argtypes = [ctypes.c_void_p]
+    hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+    hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+    stream = ctypes.c_void_p(h.stream)
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    assert hip.hipEventCreate(ctypes.byref(e0)) == 0 and hip.hipEventCreate(ctypes.byref(e1)) == 0
+    for _ in range(5):
+        h.featurize(pos, sym)
+    h.sync()
+    reps = max(steps, 20)
+    assert hip.hipEventRecord(e0, stream) == 0
+    for _ in range(reps):
+        h.featurize(pos, sym)
+    assert hip.hipEventRecord(e1, stream) == 0
+    assert hip.hipEventSynchronize(e1) == 0
+    ms = ctypes.c_float()
+    assert hip.hipEventElapsedTime(ctypes.byref(ms), e0, e1) == 0
+    us = ms.value * 1e3 / reps
+    hip.hipEventDestroy(e0)
+    hip.hipEventDestroy(e1)
+    # 1552 bytes read and 22 * 361 + 19 floats written per position
+    bytes_per_batch = batch * (ctypes.sizeof(kgx.Position) + (22 * 361 + 19) * 4)
+    # The whole device path, with its ctypes arguments built once (the caller's own marshalling is not timed).
+    lib = kgx.lib()
+    legal = [np.concatenate([np.ones(361, np.uint8), np.ones(1, np.uint8)]) for _ in range(batch)]
+    post = (kgx.PostInput * batch)()
+    for i in range(batch):
+        post[i].legal = legal[i].ctypes.data
+        post[i].white_to_move = int(pos[i].next_player == 2)
+        post[i].board_x_size = post[i].board_y_size = 19
+        post[i].nn_policy_temperature = 1.0
+        post[i].enable_passing_hacks = 0
+        post[i].no_result_allowed = 1
+    outs = (kgx.NNOutput * batch)()
+    owners = [np.zeros(361, np.float32) for _ in range(batch)]
+    for i in range(batch):
+        outs[i].white_owner_map = owners[i].ctypes.data
+    opt = np.zeros(batch, np.float32)
+    call = lambda: lib.kg_evaluate_positions(h._h, batch, pos, sym.ctypes.data, opt.ctypes.data, post, outs)
+    for _ in range(5):
+        assert call() == 0, lib.kg_last_error().decode()
+    t = time.perf_counter()
+    for _ in range(steps):
+        assert call() == 0, lib.kg_last_error().decode()
+    dt = time.perf_counter() - t
+    h.close()
+    return {"positions": batch, "featurize_us_per_batch": us,
+            "featurize_note": "kg_featurize: upload of the positions and the kernel, HIP events on the handle's stream",
+            "featurize_gbs": bytes_per_batch / (us * 1e-6) / 1e9,
+            "featurize_bytes_per_batch": bytes_per_batch,
+            "evaluate_positions": {"value": batch * steps / dt, "unit": "evals/s", "ms_per_call": dt / steps * 1e3,
+                                   "note": "kg_evaluate_positions: positions to NNEvaluator's fields, featurizer, "
+                                           "forward, post-processing and one readback on the device"}}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -299,6 +364,9 @@ def main():
         roof["rocprof"]["source"] = ("profiles/kernel_trace.json: rocprofv3 --kernel-trace --stats of this command "
                                      "on the build recorded there (not the build that ran here)")
 
+    featurizer = time_featurizer(kgx, synth, hip, net, args.precision, batch, args.steps) if (
+        net.num_input_channels == 22 and net.num_global == 19 and net.num_meta == 0) else None
+
     other = None
     if args.other_workloads and (args.config, args.precision, batch) == ("b18c384nbt", "f16", 32):
         r = time_gpu_workload(kgx, synth, hip, "b10c128", "f32", 8, max(args.steps, 100), args.warmup)
@@ -352,6 +420,7 @@ def main():
         "pipelined": pipelined,
         "other_workloads": other,
         "sustained": sustained,
+        "featurizer": featurizer,
     }
     print(json.dumps(res))
 

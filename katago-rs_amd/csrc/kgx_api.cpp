@@ -53,12 +53,11 @@ struct kg_handle {
   float* h_post_out = nullptr;
   int* h_post_status = nullptr;
   kgx::PostModel post_model;
-  // The device featurizer's buffers (kg_featurize, first use): positions and symmetries on the device, their pinned
-  // staging, and an event after their upload (the next call waits for it before overwriting the staging).
-  kg_position* d_pos = nullptr;
-  int* d_pos_sym = nullptr;
-  kg_position* h_pos = nullptr;
-  int* h_pos_sym = nullptr;
+  // The device featurizer's staging (kg_featurize, first use): one pinned block of the symmetries (max_batch ints,
+  // padded to 256 bytes) followed by the positions, which the kernel reads over the bus (no copy of its own); and an
+  // event after that kernel (the next call waits for it before overwriting the staging).
+  char* h_feat = nullptr;
+  size_t feat_sym_bytes = 0;
   hipEvent_t pos_uploaded = nullptr;
   bool pos_pending = false;
   // The readback of kg_get_output_async runs on this helper thread; the next call on the handle joins it first.
@@ -348,24 +347,21 @@ void enqueue_featurize(kg_handle* h, int n, const kg_position* rows, const int* 
       throw std::runtime_error("kgx backend: symmetry must be in [0, 8)");
   }
   KGX_HIP(hipSetDevice(h->device));
-  if (!h->d_pos) {
-    const size_t B = (size_t)h->max_batch;
-    KGX_HIP(hipMalloc((void**)&h->d_pos, B * sizeof(kg_position)));
-    KGX_HIP(hipMalloc((void**)&h->d_pos_sym, B * sizeof(int)));
-    KGX_HIP(hipHostMalloc((void**)&h->h_pos, B * sizeof(kg_position), hipHostMallocDefault));
-    KGX_HIP(hipHostMalloc((void**)&h->h_pos_sym, B * sizeof(int), hipHostMallocDefault));
+  const size_t B = (size_t)h->max_batch;
+  if (!h->h_feat) {
+    h->feat_sym_bytes = (B * sizeof(int) + 255) / 256 * 256;
+    KGX_HIP(hipHostMalloc((void**)&h->h_feat, h->feat_sym_bytes + B * sizeof(kg_position), hipHostMallocDefault));
     KGX_HIP(hipEventCreateWithFlags(&h->pos_uploaded, hipEventDisableTiming));
   }
-  // The previous call's upload must have left the staging before it is overwritten.
+  // The previous call's kernel must have read the staging before it is overwritten.
   if (h->pos_pending) KGX_HIP(hipEventSynchronize(h->pos_uploaded));
-  std::memcpy(h->h_pos, rows, (size_t)n * sizeof(kg_position));
-  for (int r = 0; r < n; r++) h->h_pos_sym[r] = symmetry ? symmetry[r] : 0;
-  KGX_HIP(hipMemcpyAsync(h->d_pos, h->h_pos, (size_t)n * sizeof(kg_position), hipMemcpyHostToDevice, h->stream));
-  KGX_HIP(hipMemcpyAsync(h->d_pos_sym, h->h_pos_sym, (size_t)n * sizeof(int), hipMemcpyHostToDevice, h->stream));
+  int* h_sym = (int*)h->h_feat;
+  for (int r = 0; r < n; r++) h_sym[r] = symmetry ? symmetry[r] : 0;
+  std::memcpy(h->h_feat + h->feat_sym_bytes, rows, (size_t)n * sizeof(kg_position));
+  kgx::launch_featurize((const kg_position*)(h->h_feat + h->feat_sym_bytes), n, POS, POS, false, (const int*)h->h_feat,
+                        h->net->d_bin(), h->net->d_global(), h->nglob, h->stream);
   KGX_HIP(hipEventRecord(h->pos_uploaded, h->stream));
   h->pos_pending = true;
-  kgx::launch_featurize(h->d_pos, n, POS, POS, false, h->d_pos_sym, h->net->d_bin(), h->net->d_global(), h->nglob,
-                        h->stream);
 }
 
 }  // namespace
@@ -501,10 +497,7 @@ void kg_handle_free(kg_handle* h) {
   if (h->h_legal) (void)hipHostFree(h->h_legal);
   if (h->h_post_out) (void)hipHostFree(h->h_post_out);
   if (h->h_post_status) (void)hipHostFree(h->h_post_status);
-  if (h->d_pos) (void)hipFree(h->d_pos);
-  if (h->d_pos_sym) (void)hipFree(h->d_pos_sym);
-  if (h->h_pos) (void)hipHostFree(h->h_pos);
-  if (h->h_pos_sym) (void)hipHostFree(h->h_pos_sym);
+  if (h->h_feat) (void)hipHostFree(h->h_feat);
   if (h->pos_uploaded) (void)hipEventDestroy(h->pos_uploaded);
   if (h->stream) (void)hipStreamDestroy(h->stream);
   delete h;

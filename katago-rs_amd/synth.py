@@ -429,3 +429,30 @@ def make_inputs(n: int, seed: int, board_sizes: Optional[List[int]] = None, num_
         glob[:, 5] = rng.uniform(-1.0, 1.0, n).astype(np.float32)
     meta_rows = rng.random((n, 192)).astype(np.float32) if meta else None
     return spatial, glob, meta_rows
+
+
+def make_positions(n: int, seed: int, size: int = 19):
+    """Seeded positions for the device featurizer (fields of kg_position, as dicts for make_positions): boards of
+    `size` x `size` with stones on about half the points (Bernoulli(0.5), each colour alike), area rules with a
+    komi of 7.5 from white's side, a few ko, superko and ladder marks, and five alternating history moves."""
+    rng = np.random.default_rng(seed)
+    out = []
+    npts = size * size
+    for _ in range(n):
+        pla = int(rng.integers(1, 3))
+        color = np.zeros(361, np.uint8)
+        color[:npts] = np.where(rng.random(npts) < 0.5, rng.integers(1, 3, npts), 0)
+        marks = np.zeros(361, np.uint8)
+        marks[:npts] = (rng.random(npts) < 0.05) * rng.integers(1, 64, npts)
+        area = np.zeros(361, np.uint8)
+        area[:npts] = color[:npts]
+        empties = np.flatnonzero(color[:npts] == 0)
+        moves = np.zeros(10, np.int32)
+        for k in range(5):
+            moves[2 * k] = int(rng.integers(0, npts))
+            moves[2 * k + 1] = 3 - pla if k % 2 == 0 else pla
+        meta = np.array([size, size, pla, int(empties[0]) if len(empties) else -1, 0, 0, 0, 0, 0, 0, 0, 5, 5],
+                        np.int32)
+        out.append(dict(meta=meta, color=color, marks=marks, area=area, enc=np.zeros(361, np.uint8), moves=moves,
+                        self_komi=7.5 if pla == 2 else -7.5, pda=0.0))
+    return out
