@@ -298,6 +298,11 @@ int kg_conv_weight_load(int ks, int ic, int oc, int split, int q, int wave, int 
                         int* dst_row, int* dst_chunk);
 /* The stored chunk of logical 16-byte chunk `chunk` of LDS weight row `row` (what the fragment reads address). */
 int kg_conv_weight_chunk(int row, int chunk);
+/* The nested-bottleneck junction launch (one block's exit 1x1 convolution, 192 -> 384, and the next block's entry
+ * 1x1, 384 -> 192, in one kernel) over `pixels` pixels: its workgroup count, and the 48-pixel tile that workgroup
+ * `workgroup` computes (-1 when it exits at once). No counterpart in the reference: the index map its kernel uses,
+ * for host-side checks. */
+int kg_junction_tile_of(int pixels, int workgroup, int* grid, int* tile);
 
 #ifdef __cplusplus
 }

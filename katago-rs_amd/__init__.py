@@ -37,7 +37,7 @@ EXPORTS = [
     "kg_get_output", "kg_profile_enable", "kg_profile_reset", "kg_profile_read",
     "kg_model_version_features", "kg_meta_encoder_channels", "kg_copy_outputs", "kg_run_static",
     "kg_get_output_async", "kg_wait", "kg_get_output_eval", "kg_post_outputs",
-    "kg_conv_geometry", "kg_conv_tile_of", "kg_conv_weight_load", "kg_conv_weight_chunk",
+    "kg_conv_geometry", "kg_conv_tile_of", "kg_conv_weight_load", "kg_conv_weight_chunk", "kg_junction_tile_of",
     "kg_featurize", "kg_featurize_rows", "kg_evaluate_positions",
 ]
 # Completion callback of kg_get_output_async: (user, status).
@@ -214,6 +214,7 @@ def lib():
         L.kg_conv_tile_of.argtypes = [ci, ci, ci, ci, ci, ci, ctypes.POINTER(ci), ctypes.POINTER(ci)]
         L.kg_conv_weight_load.argtypes = [ci, ci, ci, ci, ci, ci, ci] + [ctypes.POINTER(ci)] * 4
         L.kg_conv_weight_chunk.argtypes = [ci, ci]
+        L.kg_junction_tile_of.argtypes = [ci, ci, ctypes.POINTER(ci), ctypes.POINTER(ci)]
         _ = cf
         _lib = L
     return _lib
@@ -260,6 +261,13 @@ def conv_geometry(ks: int, ic: int, oc: int, split: bool, pixels: int) -> dict:
     g = ConvGeometry()
     _check(lib().kg_conv_geometry(ks, ic, oc, int(split), pixels, ctypes.byref(g)))
     return {f: getattr(g, f) for f, _ in ConvGeometry._fields_}
+
+
+def junction_tile_of(pixels: int, workgroup: int):
+    """(workgroups of the junction launch over `pixels` pixels, the 48-pixel tile of `workgroup` or -1)."""
+    grid, tile = ctypes.c_int(), ctypes.c_int()
+    _check(lib().kg_junction_tile_of(pixels, workgroup, ctypes.byref(grid), ctypes.byref(tile)))
+    return grid.value, tile.value
 
 
 def conv_tile_of(ks: int, ic: int, oc: int, split: bool, pixels: int, workgroup: int):

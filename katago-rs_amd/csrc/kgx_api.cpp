@@ -554,6 +554,17 @@ int kg_conv_tile_of(int ks, int ic, int oc, int split, int pixels, int workgroup
   });
 }
 
+int kg_junction_tile_of(int pixels, int workgroup, int* grid, int* tile) {
+  return guarded([&] {
+    if (!grid || !tile) throw std::runtime_error("null output");
+    if (pixels < 1) throw std::runtime_error("bad pixel count");
+    *grid = kgx::junction_grid(pixels);
+    if (workgroup < 0 || workgroup >= *grid) throw std::runtime_error("workgroup out of range");
+    const int t = kgx::junction_tile_of(workgroup);
+    *tile = t * 48 < pixels ? t : -1;
+  });
+}
+
 int kg_conv_weight_load(int ks, int ic, int oc, int split, int q, int wave, int lane, int* src_row, int* src_chunk,
                         int* dst_row, int* dst_chunk) {
   return guarded([&] {

@@ -750,8 +750,7 @@ int conv_igemm_icp(int ks, int ic, int oc, bool split) {
   return round_up(ic, bk);
 }
 
-// The value a float becomes as a compute-type operand (round to nearest even), as a float.
-static float round_operand(float v, int prec) {
+float conv_round_operand(float v, int prec) {
   if (prec == PREC_BF16) {
     uint32_t u;
     std::memcpy(&u, &v, 4);
@@ -781,7 +780,7 @@ void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector
         const float v = w[((size_t)o * ic + i) * taps + t];
         const size_t hi = ((((size_t)(o / bn) * pl) * taps + t) * bn + o % bn) * icp + i;
         out[hi] = v;
-        if (split) out[hi + (size_t)taps * bn * icp] = v - round_operand(v, prec);
+        if (split) out[hi + (size_t)taps * bn * icp] = v - conv_round_operand(v, prec);
       }
 }
 

@@ -1,0 +1,398 @@
+// A nested-bottleneck junction in one launch: block k's exit 1x1 convolution (192 -> 384 channels, added into the
+// trunk) and block k + 1's entry 1x1 convolution (384 -> 192), both on split 16-bit operands (hi*hi + lo*hi +
+// hi*lo per product), over one 48-pixel tile per workgroup (bin2onnx.py:1263-1269: post(bnact(...)) into the trunk,
+// then the next block's pre(bnact(x))).
+//
+// Between the two convolutions the separate kernels pass the trunk's next activation act(bn(x)) through memory as
+// two 16-bit planes (4 bytes per value, written once and read once per junction). Here it stays in LDS: a workgroup
+// computes all 384 trunk channels of its pixels, adds the trunk, stores the trunk once, and multiplies the
+// activation it derives from it by the entry weights in place. Per pixel this moves 192 * 4 (the exit's operand) +
+// 384 * 8 (the trunk read and written) + 192 * 6 (the inner stream and its 16-bit activation) bytes, against
+// 3072 more for the two planes and their read-back. Both products take their weight fragments straight from
+// memory into registers (packed in fragment order, one coalesced 1 KB load per fragment): every workgroup needs all
+// 576 KB of them, which each XCD's L2 holds after the first touch.
+//
+// The arithmetic is that of the two separate implicit-GEMM kernels, in the same order: the exit's accumulator chain
+// runs over its six 32-channel steps in order, each step lo*hi, hi*lo, hi*hi; the entry's twelve steps are summed
+// in two chains, steps {0, 1, 4, 5, 8, 9} and {2, 3, 6, 7, 10, 11} (the separate kernel's two wave groups over its
+// 128-channel stages), then added; the epilogues are the same expressions. So the junction's outputs equal the
+// separate kernels' bit for bit.
+#include "kgx_device.h"
+
+#include <vector>
+
+namespace kgx {
+
+namespace {
+
+constexpr int JCI = kJunctionInner, JCO = kJunctionOuter;
+constexpr int JR = 48;                         // pixels per workgroup (three 16-row MFMA blocks)
+constexpr int JNT = 512;                       // threads: eight waves, two per SIMD
+constexpr int K1 = JCI / 32, K2 = JCO / 32;    // 16x16x32 steps of the exit and the entry product
+constexpr int CB1 = JCO / 16, CB2 = JCI / 16;  // 16-column blocks of the two outputs
+constexpr int FRAG = 64 * 8;                   // elements per packed fragment (64 lanes x 8)
+constexpr int W2OFF = CB1 * K1 * 2 * FRAG;     // the entry's fragments follow the exit's
+constexpr int WELEMS = W2OFF + CB2 * K2 * 2 * FRAG;
+// LDS: the entry's operand (the activation planes, [64-channel slice][plane][pixel][128 bytes], 16-byte chunks
+// swizzled as chunk ^ (pixel / 2 % 8)), then one region that holds in turn the exit's operand (same layout over
+// 192 channels), the exit's float tile [48][384 + 4] and the entry's two float tiles [2][48][192 + 4].
+constexpr int LD1 = JCO + 4, LD2 = JCI + 4;
+constexpr int ACTB = (JCO / 64) * 2 * JR * 128;
+constexpr int A1B = (JCI / 64) * 2 * JR * 128, C1B = JR * LD1 * 4, C2B = 2 * JR * LD2 * 4;
+constexpr int R1B = A1B > C1B ? (A1B > C2B ? A1B : C2B) : (C1B > C2B ? C1B : C2B);
+constexpr int LDSB = ACTB + R1B;
+// Epilogue mappings, the same for every thread (no branch around a memory access, so the compiler's count of the
+// loads in flight stays exact and a later wait for a prefetched weight fragment leaves the trunk's stores in
+// flight): thread t takes channel quads 3 (t % G) + q, q < 3, of pixels t / G + R e, for the exit's G = 32 groups of
+// twelve channels and R = 16 (three pixels each), and the entry's G = 16 and R = 32 (pixels past 48 skipped at the
+// end).
+constexpr int E1 = 3, E2 = 2;
+static_assert(JNT / 64 == 8 && CB1 == 3 * 8 && CB2 == 3 * 4 && K2 == 12, "wave layout assumes 384 and 192 channels");
+
+// The XCD-aware tile order: workgroup g runs on XCD g % 8, and the four 48-pixel tiles of one 192-pixel region go
+// to that region's XCD (region r on XCD r % 8), as every 192-pixel convolution around the junction maps it, so the
+// junction reads its operand from the L2 its producer wrote and its consumer reads the junction's output there.
+__host__ __device__ inline int junction_tile(int g) {
+  const int xcd = g & 7, slot = g >> 3;
+  return 4 * (xcd + 8 * (slot >> 2)) + (slot & 3);
+}
+
+// Waits for this wave's LDS accesses, then for every wave: nothing else. A fence (__syncthreads()) would also wait
+// for the wave's loads and stores in flight (the weight prefetch, the trunk's stores). The compiler moves no memory
+// access across the clobbers, nor the clobbers across the barrier.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0)
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  asm volatile("" ::: "memory");
+}
+
+template <typename T>
+__global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ X, const T* __restrict__ Xlo, int ldx,
+                                                          const T* __restrict__ W, int M, ConvOut eo, ConvOut no) {
+  typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
+  __shared__ __align__(1024) char smem[LDSB];
+  char* const act = smem;
+  char* const r1 = smem + ACTB;
+  const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int r16 = lane & 15, g4 = lane >> 4;
+  const int m0 = junction_tile(blockIdx.x) * JR;
+  if (m0 >= M) return;
+
+  auto mfma = [](const frag_t& a, const frag_t& b, floatx4 c) {
+    if constexpr (std::is_same<T, f16>::value) return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+    else return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  };
+  // Packed weight fragment (column block cb, step ks of K, plane pl): lane l holds w[16 cb + l % 16][32 ks + 8 (l / 16)
+  // .. + 8], the MFMA's B operand.
+  auto wfrag = [&](int base, int cb, int K, int ks, int pl) {
+    return *(const frag_t*)(W + base + ((cb * K + ks) * 2 + pl) * FRAG + lane * 8);
+  };
+  // A operand of 16-pixel block i at step ks, plane pl, from an LDS operand: lane l holds pixel 16 i + l % 16,
+  // channels 32 ks + 8 (l / 16) .. + 8 (the block's pixels share one swizzle, that of l % 16).
+  auto afrag = [&](const char* base, int i, int ks, int pl) {
+    const int chunk = ((ks & 1) * 4 + g4) ^ ((r16 >> 1) & 7);
+    return *(const frag_t*)(base + (((ks >> 1) * 2 + pl) * JR + 16 * i + r16) * 128 + chunk * 16);
+  };
+
+  // Exit product, wave wv: output columns 48 wv .. + 48 (blocks 3 wv + j), all 48 pixels.
+  frag_t b1[2][3][2];
+  auto load_b1 = [&](int slot, int ks) {
+#pragma unroll
+    for (int j = 0; j < 3; j++)
+#pragma unroll
+      for (int pl = 0; pl < 2; pl++) b1[slot][j][pl] = wfrag(0, 3 * wv + j, K1, ks, pl);
+  };
+  load_b1(0, 0);
+  // The exit's operand straight into LDS: 36 loads of 8 pixel rows x 128 bytes (64-channel slice kp, plane pl,
+  // rows 8 grp ..), lane i filling row 8 grp + i / 8 at stored chunk i % 8 from source chunk (i % 8) ^ swizzle.
+  // Rows past M lie beyond the buffer range and read as zero.
+  {
+    const int rb = ldx * (int)sizeof(T), nbytes = min(JR, M - m0) * rb;
+    const T* xb = X + (size_t)m0 * ldx;
+    const T* xlb = Xlo + (size_t)m0 * ldx;
+#pragma unroll
+    for (int u = 0; u < 5; u++) {
+      const int q = u * 8 + wv;
+      if (q < 36) {
+        const int kp = q / 12, pl = (q / 6) & 1, grp = q % 6;
+        const int row = grp * 8 + (lane >> 3), sc = (lane & 7) ^ ((row >> 1) & 7);
+        lds_load16(pl ? xlb : xb, nbytes, r1 + ((kp * 2 + pl) * JR + grp * 8) * 128, row * rb + kp * 128 + sc * 16);
+      }
+    }
+  }
+  // The direct loads are not counted by the compiler: wait for all of this wave's loads, then for every wave.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  load_b1(1, 1);
+
+  // The exit epilogue's inputs: the trunk values it adds to, the emission's scale, bias and board mask (channels
+  // 12 c1 + 4 q of pixels p1 + 16 e; rows past M read row M - 1, never stored). They are issued after the product's
+  // last weight loads (a wait covers every load issued before the one it waits for), in flight during its last
+  // steps.
+  const int c1 = 12 * (tid & 31), p1 = tid >> 5;
+  floatx4 yres[E1][3], es1[3], eb1[3];
+  float mk1[E1];
+  auto load_epi1 = [&]() {
+#pragma unroll
+    for (int e = 0; e < E1; e++) {
+      const int m = min(m0 + p1 + 16 * e, M - 1);
+#pragma unroll
+      for (int q = 0; q < 3; q++) yres[e][q] = *(const floatx4*)(eo.y + (size_t)m * eo.ldy + c1 + 4 * q);
+      mk1[e] = eo.emit.mask[m];
+    }
+#pragma unroll
+    for (int q = 0; q < 3; q++) {
+      es1[q] = *(const floatx4*)(eo.emit.scale + c1 + 4 * q);
+      eb1[q] = *(const floatx4*)(eo.emit.bias + c1 + 4 * q);
+    }
+  };
+
+  floatx4 acc[3][3];
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int j = 0; j < 3; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  {
+    frag_t ah[2][3], al[2][3];
+    auto load_a1 = [&](int set, int ks) {
+#pragma unroll
+      for (int i = 0; i < 3; i++) {
+        ah[set][i] = afrag(r1, i, ks, 0);
+        al[set][i] = afrag(r1, i, ks, 1);
+      }
+    };
+    load_a1(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < K1; ks++) {
+      const int s = ks & 1;
+      if (ks + 1 < K1) load_a1(s ^ 1, ks + 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 3; i++)
+#pragma unroll
+        for (int j = 0; j < 3; j++) acc[i][j] = mfma(al[s][i], b1[s][j][0], acc[i][j]);
+#pragma unroll
+      for (int i = 0; i < 3; i++)
+#pragma unroll
+        for (int j = 0; j < 3; j++) acc[i][j] = mfma(ah[s][i], b1[s][j][1], acc[i][j]);
+#pragma unroll
+      for (int i = 0; i < 3; i++)
+#pragma unroll
+        for (int j = 0; j < 3; j++) acc[i][j] = mfma(ah[s][i], b1[s][j][0], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (ks + 2 < K1) load_b1(s, ks + 2);
+      if (ks + 3 == K1) load_epi1();
+    }
+  }
+
+  // Entry product, wave wv: step chain kg = wv / 4 (steps 2 kg + 4 (p / 2) + p % 2), output columns 48 cg .. + 48
+  // (blocks 3 cg + j, cg = wv % 4), all 48 pixels. Its first two steps' weights load now, ahead of the trunk's
+  // stores (the wait for a load also waits for the stores issued before it).
+  const int kg = wv >> 2, cg = wv & 3;
+  auto kstep = [&](int p) { return 2 * kg + 4 * (p >> 1) + (p & 1); };
+  frag_t b2[2][3][2];
+  auto load_b2 = [&](int slot, int p) {
+#pragma unroll
+    for (int j = 0; j < 3; j++)
+#pragma unroll
+      for (int pl = 0; pl < 2; pl++) b2[slot][j][pl] = wfrag(W2OFF, 3 * cg + j, K2, kstep(p), pl);
+  };
+  load_b2(0, 0);
+  load_b2(1, 1);
+  // And the entry epilogue's per-channel inputs (channels 12 c2 + 4 q of pixels p2 + 32 e).
+  const int c2 = 12 * (tid & 15), p2 = tid >> 4;
+  const int fl2 = store_flags(no);
+  floatx4 es2[3], eb2[3];
+  float mk2[E2];
+  const float* const es2p = no.emit.scale ? no.emit.scale : eo.emit.scale;  // (any readable floats when unused)
+  const float* const eb2p = no.emit.scale ? no.emit.bias : eo.emit.bias;
+  const float* const mk2p = no.emit.scale ? no.emit.mask : eo.emit.mask;
+#pragma unroll
+  for (int q = 0; q < 3; q++) {
+    es2[q] = *(const floatx4*)(es2p + c2 + 4 * q);
+    eb2[q] = *(const floatx4*)(eb2p + c2 + 4 * q);
+  }
+#pragma unroll
+  for (int e = 0; e < E2; e++) mk2[e] = mk2p[min(m0 + p2 + 32 * e, M - 1)];
+
+  // The exit's float tile over its operand's LDS (every wave is done reading the operand first).
+  lds_barrier();
+  float* const C1 = (float*)r1;
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int j = 0; j < 3; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++) C1[(16 * i + 4 * g4 + r) * LD1 + 48 * wv + 16 * j + r16] = acc[i][j][r];
+  lds_barrier();
+
+  // Exit epilogue: the trunk plus the product, stored; the activation act(x * scale + bias) * mask in its two
+  // 16-bit planes (the high part, and the rounding of what it leaves) into the entry's LDS operand. The trunk goes
+  // out through a buffer whose range ends at row M, so rows past it are dropped without a branch.
+  const auto ybuf = __builtin_amdgcn_make_buffer_rsrc(eo.y + (size_t)m0 * eo.ldy, 0,
+                                                      min(JR, M - m0) * eo.ldy * (int)sizeof(float), 0x00020000);
+  auto epi1 = [&](auto act_c) {
+    constexpr int A = decltype(act_c)::value;
+#pragma unroll
+    for (int e = 0; e < E1; e++) {
+      const int p = p1 + 16 * e;
+#pragma unroll
+      for (int q = 0; q < 3; q++) {
+        const int n = c1 + 4 * q;
+        floatx4 v = *(const floatx4*)(C1 + p * LD1 + n);
+        v += yres[e][q];
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ybuf, (p * eo.ldy + n) * 4, 0, 2);
+        float t[4], l[4];
+#pragma unroll
+        for (int k = 0; k < 4; k++) {
+          const float a = v[k] * es1[q][k] + eb1[q][k];
+          t[k] = act_f<A>(a) * mk1[e];
+          l[k] = t[k] - (float)to_t<T>(t[k]);
+        }
+        T hi[4] = {to_t<T>(t[0]), to_t<T>(t[1]), to_t<T>(t[2]), to_t<T>(t[3])};
+        T lo[4] = {to_t<T>(l[0]), to_t<T>(l[1]), to_t<T>(l[2]), to_t<T>(l[3])};
+        const int kp = n >> 6, chunk = ((n & 63) >> 3) ^ ((p >> 1) & 7);
+        char* d = act + ((kp * 2) * JR + p) * 128 + chunk * 16 + (n & 7) * (int)sizeof(T);
+        *(uint2*)d = *(const uint2*)hi;
+        *(uint2*)(d + JR * 128) = *(const uint2*)lo;
+      }
+    }
+  };
+  switch (eo.emit.act) {
+    case ACT_MISH: epi1(std::integral_constant<int, ACT_MISH>{}); break;
+    case ACT_RELU: epi1(std::integral_constant<int, ACT_RELU>{}); break;
+    case ACT_SILU: epi1(std::integral_constant<int, ACT_SILU>{}); break;
+    default: epi1(std::integral_constant<int, ACT_ID>{}); break;
+  }
+  lds_barrier();
+
+  floatx4 acc2[3][3];
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int j = 0; j < 3; j++) acc2[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  {
+    frag_t ah[2][3], al[2][3];
+    auto load_a2 = [&](int set, int p) {
+#pragma unroll
+      for (int i = 0; i < 3; i++) {
+        ah[set][i] = afrag(act, i, kstep(p), 0);
+        al[set][i] = afrag(act, i, kstep(p), 1);
+      }
+    };
+    load_a2(0, 0);
+#pragma unroll
+    for (int p = 0; p < K2 / 2; p++) {
+      const int s = p & 1;
+      if (p + 1 < K2 / 2) load_a2(s ^ 1, p + 1);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 3; i++)
+#pragma unroll
+        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(al[s][i], b2[s][j][0], acc2[i][j]);
+#pragma unroll
+      for (int i = 0; i < 3; i++)
+#pragma unroll
+        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[s][j][1], acc2[i][j]);
+#pragma unroll
+      for (int i = 0; i < 3; i++)
+#pragma unroll
+        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[s][j][0], acc2[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (p + 2 < K2 / 2) load_b2(s, p + 2);
+    }
+  }
+
+  // The two chains' float tiles over the exit's (whose last reads preceded the barrier above).
+  float* const C2 = (float*)r1;
+#pragma unroll
+  for (int i = 0; i < 3; i++)
+#pragma unroll
+    for (int j = 0; j < 3; j++)
+#pragma unroll
+      for (int r = 0; r < 4; r++)
+        C2[(kg * JR + 16 * i + 4 * g4 + r) * LD2 + 48 * cg + 16 * j + r16] = acc2[i][j][r];
+  lds_barrier();
+
+  // Entry epilogue: chain 0 plus chain 1, then the convolution's outputs (the inner stream and its consumer's
+  // activation) as the separate kernel stores them. At the end of the kernel, so these stores may branch.
+  const bool fast = fl2 == (SF_Y | SF_EMIT) && no.emit.act == ACT_MISH;
+#pragma unroll
+  for (int e = 0; e < E2; e++) {
+    const int p = p2 + 32 * e, m = m0 + p;
+    if (p < JR && m < M) {
+#pragma unroll
+      for (int q = 0; q < 3; q++) {
+        const int n = c2 + 4 * q;
+        floatx4 sum = *(const floatx4*)(C2 + p * LD2 + n);
+        sum += *(const floatx4*)(C2 + (JR + p) * LD2 + n);
+        if (fast) {
+          conv_store4<T, ACT_MISH, SF_Y | SF_EMIT>(no, m, n, sum, floatx4{0.f, 0.f, 0.f, 0.f}, 1.f, es2[q], eb2[q],
+                                                   mk2[e]);
+        } else {
+          const floatx4 yacc = (fl2 & SF_ACC) ? *(const floatx4*)(no.y + (size_t)m * no.ldy + n)
+                                              : floatx4{0.f, 0.f, 0.f, 0.f};
+          conv_store4<T>(no, m, n, sum, yacc, (fl2 & SF_ROWMASK) ? no.rowmask[m] : 1.f, es2[q], eb2[q], mk2[e]);
+        }
+      }
+    }
+  }
+}
+
+}  // namespace
+
+int junction_tile_of(int g) { return junction_tile(g); }
+
+int junction_grid(int M) {
+  const int regions = (M + 4 * JR - 1) / (4 * JR);
+  return 32 * ((regions + 7) / 8);
+}
+
+void junction_pack_weights(const float* w_exit, const float* w_entry, int prec, std::vector<float>& out) {
+  out.assign(WELEMS, 0.f);
+  // Fragment (cb, ks, plane) of a K-step weight matrix w [cols][32 K]: lane l, element e holds column
+  // 16 cb + l % 16, channel 32 ks + 8 (l / 16) + e; the low plane holds w - round(w).
+  auto pack = [&](const float* w, int cbs, int K, int base) {
+    for (int cb = 0; cb < cbs; cb++)
+      for (int ks = 0; ks < K; ks++)
+        for (int l = 0; l < 64; l++)
+          for (int e = 0; e < 8; e++) {
+            const float v = w[(size_t)(16 * cb + l % 16) * (32 * K) + 32 * ks + 8 * (l / 16) + e];
+            const size_t at = (size_t)base + (size_t)((cb * K + ks) * 2) * FRAG + l * 8 + e;
+            out[at] = v;
+            out[at + FRAG] = v - conv_round_operand(v, prec);
+          }
+  };
+  pack(w_exit, CB1, K1, 0);
+  pack(w_entry, CB2, K2, W2OFF);
+}
+
+void launch_junction(int prec, const void* x, const void* x_lo, int ldx, const void* w, const ConvOut& eo,
+                     const ConvOut& no, int B, hipStream_t s) {
+  if (prec != PREC_F16 && prec != PREC_BF16) throw std::runtime_error("junction: 16-bit operands only");
+  if (B <= 0) return;
+  if (!x || !x_lo || !w || ldx < JCI || ldx % 8 || ((uintptr_t)x | (uintptr_t)x_lo | (uintptr_t)w) % 16)
+    throw std::runtime_error("junction: operands must be 16-byte aligned rows of at least 192 channels");
+  // The exit's output is the trunk's residual add and the emission of the entry's activation, nothing else.
+  if (!eo.y || !eo.accumulate || eo.y_dead || eo.ldy % 4 || eo.yt || eo.rowmask || eo.colbias || !eo.emit.scale ||
+      !eo.emit.bias || !eo.emit.mask || eo.pool.psum || ((uintptr_t)eo.y | (uintptr_t)eo.emit.scale |
+                                                         (uintptr_t)eo.emit.bias) % 16)
+    throw std::runtime_error("junction: the exit must add into the trunk and emit the entry's activation");
+  if (no.pool.psum || (no.y && (no.ldy % 4 || (uintptr_t)no.y % 16)) || (no.yt && no.ldyt % 4) ||
+      (no.colbias && no.ld_colbias % 4) || (no.emit.scale && (no.emit.ld % 4 || (uintptr_t)no.emit.scale % 16 ||
+                                                              (uintptr_t)no.emit.bias % 16)))
+    throw std::runtime_error("junction: unsupported entry outputs");
+  const int M = B * HW;
+  if (prec == PREC_F16)
+    launch_k(junction_kernel<f16>, junction_grid(M), JNT, 0, s, (const f16*)x, (const f16*)x_lo, ldx, (const f16*)w,
+             M, eo, no);
+  else
+    launch_k(junction_kernel<bf16>, junction_grid(M), JNT, 0, s, (const bf16*)x, (const bf16*)x_lo, ldx,
+             (const bf16*)w, M, eo, no);
+  KGX_CHECK_LAUNCH();
+}
+
+}  // namespace kgx

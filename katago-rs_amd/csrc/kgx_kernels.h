@@ -169,6 +169,22 @@ void conv_igemm_pack_weights(int ks, const float* w, int oc, int ic, std::vector
                              int prec = PREC_F16);
 void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const void* w, int icp, int OC,
                        const ConvOut& o, int B, hipStream_t s, const void* x_lo = nullptr);
+// The value a float becomes as a compute-type operand (round to nearest even), as a float.
+float conv_round_operand(float v, int prec);
+
+// A nested-bottleneck junction in one launch (16-bit handles, split operands): block k's exit 1x1 convolution
+// (kJunctionInner -> kJunctionOuter channels) into `exit_o` (the trunk's residual add, emitting the next block's
+// activation), whose activation feeds block k + 1's entry 1x1 convolution (kJunctionOuter -> kJunctionInner) into
+// `entry_o` without passing through memory (exit_o.emit.out / out_lo are not written). x / x_lo: the exit's split
+// operand (rows of ldx); w: the compute-type conversion of junction_pack_weights' layout of both filters (each
+// [oc][ic]). The results equal the two separate split 1x1 convolutions' bit for bit.
+constexpr int kJunctionInner = 192, kJunctionOuter = 384;
+void junction_pack_weights(const float* w_exit, const float* w_entry, int prec, std::vector<float>& out);
+void launch_junction(int prec, const void* x, const void* x_lo, int ldx, const void* w, const ConvOut& exit_o,
+                     const ConvOut& entry_o, int B, hipStream_t s);
+// The launch's grid over M pixels, and the 48-pixel tile workgroup g computes (tiles past M exit at once).
+int junction_grid(int M);
+int junction_tile_of(int g);
 
 // Network input planes, float NCHW [B][nin][361], to compute-type NHWC rows of ldo channels (zero beyond nin,
 // ldo % 8 == 0), together with the board statistics of launch_mask_prep; with `gl.W` set, the same launch also

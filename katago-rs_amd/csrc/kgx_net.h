@@ -120,6 +120,18 @@ class Net {
   // implicit-GEMM 1x1 does, so that only 3x3 convolutions round their operands to 16 bits.
   bool split_1x1(const ConvDesc& c, int ldx, const ConvOut& o) const;
   void emit_stack(const std::vector<BlockDesc>& blocks, int depth);
+  // A nested block's exit convolution held back while the next block's entry is planned: both then run as one
+  // junction launch (launch_junction), which keeps the activation between them in LDS.
+  struct PendingExit {
+    const ConvDesc* conv = nullptr;
+    const void* x = nullptr;
+    const void* x_lo = nullptr;
+    int ldx = 0;
+    std::shared_ptr<ConvOut> out;
+  };
+  // Whether block b's exit and block `next`'s entry (over a trunk of c channels) run as a junction.
+  bool junction_fits(const BlockDesc& b, const BlockDesc& next, int c) const;
+  std::shared_ptr<ConvOut> emit_junction(const PendingExit& p, const ConvDesc& entry, const ConvOut& entry_o);
   void emit_attention(const BlockDesc& b, int depth);
   void emit_ffn(const BlockDesc& b, int depth);
   std::shared_ptr<ConvOut> emit_token_gemm(const void* A, int lda, const void* Bt, int N, int K, const ConvOut& o,
@@ -146,6 +158,8 @@ class Net {
   size_t ws_cap_ = 0, ws_used_ = 0;
   std::vector<std::pair<void*, size_t>> zero_;           // workspace regions cleared before every eager forward
   ConvMode conv_mode_ = CONV_WINO4;
+  bool junctions_ = true;  // nested-bottleneck junctions in one launch (KGX_JUNCTION=0: two launches)
+  std::unique_ptr<PendingExit> pend_;
   int wino_tm_ = 4;
   int nin_ = 0, nglob_ = 0, nmeta_ = 0, row_len_ = 0;
   std::vector<std::unique_ptr<DeviceBuffer>> mem_;

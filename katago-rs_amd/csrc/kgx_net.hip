@@ -49,6 +49,8 @@ Net::Net(const ModelDesc& m, int device, int max_batch, int prec) : device_(devi
     else if (v == "igemm" && prec != PREC_F32) conv_mode_ = CONV_IGEMM;
   }
   wino_tm_ = conv_mode_ == CONV_WINO4 ? 4 : 2;
+  // Nested-bottleneck junctions in one launch; KGX_JUNCTION=0 plans the two convolutions separately.
+  if (const char* e = std::getenv("KGX_JUNCTION")) junctions_ = std::string(e) != "0";
   build(m);
 }
 
@@ -58,6 +60,7 @@ Net::Net(const ModelDesc& m, const Net& primary, int max_batch, char* ws_base, s
   if (max_batch < 1 || max_batch > primary.max_batch_) throw std::runtime_error("internal: workspace plan batch");
   conv_mode_ = primary.conv_mode_;
   wino_tm_ = primary.wino_tm_;
+  junctions_ = primary.junctions_;
   build(m);
   if (upload_next_ != primary.uploads_.size()) throw std::runtime_error("internal: workspace plan weights differ");
 }
@@ -168,6 +171,37 @@ void* Net::consume(int depth, const BNDesc& bn, int act, const void** lo) {
   st.flip ^= 1;
   st.producer.reset();
   return buf;
+}
+
+bool Net::junction_fits(const BlockDesc& b, const BlockDesc& next, int c) const {
+  auto is1x1 = [](const ConvDesc& d) { return d.ky == 1 && d.kx == 1 && d.dy == 1 && d.dx == 1; };
+  const ConvDesc &ex = b.final_conv, &en = next.regular;
+  return junctions_ && prec_ != PREC_F32 && conv_mode_ == CONV_IGEMM && next.kind == BLOCK_NBT && is1x1(ex) &&
+         is1x1(en) && c == kJunctionOuter && ex.ic == kJunctionInner && ex.oc == kJunctionOuter &&
+         en.ic == kJunctionOuter && en.oc == kJunctionInner && b.regular.oc == kJunctionInner &&
+         ex.w.size() == (size_t)kJunctionInner * kJunctionOuter && en.w.size() == ex.w.size();
+}
+
+std::shared_ptr<ConvOut> Net::emit_junction(const PendingExit& p, const ConvDesc& entry, const ConvOut& entry_o) {
+  std::vector<float> w;
+  junction_pack_weights(p.conv->w.data(), entry.w.data(), prec_, w);
+  const void* dW = upload_t(w);
+  const std::shared_ptr<ConvOut> eo = p.out, no = std::make_shared<ConvOut>(entry_o);
+  const int prec = prec_, ldx = p.ldx;
+  const void *x = p.x, *x_lo = p.x_lo;
+  const double ts = (double)tsize();
+  Op op;
+  op.launch = [=](hipStream_t s, int B) { launch_junction(prec, x, x_lo, ldx, dW, *eo, *no, B, s); };
+  op.cls = "conv1x1_junction";
+  op.flops_row = 2.0 * HW * 2 * kJunctionInner * kJunctionOuter;
+  // The exit's split operand, the trunk read and written, the inner stream written (its emission is counted
+  // through `out`).
+  op.bytes_row = (double)HW * (2.0 * kJunctionInner * ts + 8.0 * kJunctionOuter + 4.0 * kJunctionInner);
+  op.bytes_fixed = 2.0 * 2 * kJunctionInner * kJunctionOuter * ts;
+  op.out = no;
+  op.out_c = kJunctionInner;
+  ops_.push_back(op);
+  return no;
 }
 
 bool Net::split_1x1(const ConvDesc& c, int ldx, const ConvOut& o) const {
@@ -551,7 +585,8 @@ void Net::emit_ffn(const BlockDesc& b, int depth) {
 
 void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
   const int prec = prec_;
-  for (const BlockDesc& b : blocks) {
+  for (size_t bi = 0; bi < blocks.size(); bi++) {
+    const BlockDesc& b = blocks[bi];
     float* x = ss_[depth].x;
     const int c = ss_[depth].c;
     ConvOut res;  // the block's residual add into its stream
@@ -698,7 +733,15 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
         const void* a = consume(depth, b.pre_bn, b.pre_act, split_1x1(b.regular, c, o1) ? &a_lo : nullptr);
         in.c = ci;
         in.producer.reset();
-        in.producer = emit_conv(b.regular, a, c, false, o1, a_lo);
+        if (pend_) {
+          // The previous block's exit convolution was held back for this entry: one junction launch for both.
+          if (pend_->out->emit.out != a || pend_->out->emit.out_lo != a_lo || !a_lo)
+            throw std::runtime_error("internal: junction entry does not consume the held exit");
+          in.producer = emit_junction(*pend_, b.regular, o1);
+          pend_.reset();
+        } else {
+          in.producer = emit_conv(b.regular, a, c, false, o1, a_lo);
+        }
         emit_stack(b.inner, depth + 1);
         // The inner stream ends with this activation: its last producer computes the stream's final value only
         // for the emission, so that sum is not stored.
@@ -706,7 +749,14 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
         const void* a2_lo = nullptr;
         const void* a2 = consume(depth + 1, b.mid_bn, b.mid_act, split_1x1(b.final_conv, ci, res) ? &a2_lo : nullptr);
         if (last) last->y_dead = true;
-        ss_[depth].producer = emit_conv(b.final_conv, a2, ci, false, res, a2_lo);
+        if (a2_lo && bi + 1 < blocks.size() && junction_fits(b, blocks[bi + 1], c)) {
+          // Held back: the next block's entry convolution joins it (its consume attaches this emission).
+          if (pend_) throw std::runtime_error("internal: two exits held back");
+          pend_.reset(new PendingExit{&b.final_conv, a2, a2_lo, ci, std::make_shared<ConvOut>(res)});
+          ss_[depth].producer = pend_->out;
+        } else {
+          ss_[depth].producer = emit_conv(b.final_conv, a2, ci, false, res, a2_lo);
+        }
         break;
       }
       case BLOCK_ATTN:
@@ -819,6 +869,7 @@ void Net::build(const ModelDesc& m) {
 
   // --- Blocks. ---
   emit_stack(m.blocks, 0);
+  if (pend_) throw std::runtime_error("internal: an exit convolution was held back for no entry");
 
   // --- Trunk tip and heads (bin2onnx.py:1489-1531). ---
   for (const ConvDesc* hc : {&m.p1, &m.g1, &m.v1, &m.p2, &m.own})

@@ -81,3 +81,30 @@ def test_geometry_rejects_bad_shapes(kgx):
         kgx.conv_tile_of(3, 192, 192, False, 361, g["grid"])
     with pytest.raises(kgx.KgError, match="through registers"):
         kgx.conv_weight_load(1, 384, 192, True, 0, 0, 0)
+
+
+def test_junction_tiles_cover_every_pixel_once_on_the_convolutions_xcds(kgx):
+    """The junction launch (a nested block's exit 1x1 and the next block's entry 1x1 in one kernel) over batches 1
+    to 64: every 48-pixel tile exactly once, and each on the XCD (workgroup id mod 8) that the 192-pixel
+    convolutions before and after it give its 192-pixel region."""
+    for b in BATCHES:
+        pixels = b * 361
+        grid, _ = kgx.junction_tile_of(pixels, 0)
+        seen = collections.Counter()
+        for wg in range(grid):
+            g, t = kgx.junction_tile_of(pixels, wg)
+            assert g == grid
+            if t < 0:
+                continue
+            assert 0 <= t * 48 < pixels, (b, wg, t)
+            seen[t] += 1
+            assert wg % 8 == (t * 48 // 192) % 8, (b, wg, t)
+        assert set(seen) == set(range(-(-pixels // 48))) and all(v == 1 for v in seen.values()), b
+        # the convolutions' 192-pixel tile of the same pixels runs on the same XCD
+        g3 = kgx.conv_geometry(3, 192, 192, False, pixels)
+        for wg in range(g3["grid"]):
+            mt, _ = kgx.conv_tile_of(3, 192, 192, False, pixels, wg)
+            if mt >= 0:
+                assert wg % 8 == mt % 8
+    with pytest.raises(kgx.KgError, match="workgroup out of range"):
+        kgx.junction_tile_of(361, 10 ** 6)

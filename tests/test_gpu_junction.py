@@ -1,0 +1,66 @@
+"""The nested-bottleneck junction (one block's exit 1x1 convolution, 192 -> 384 into the trunk, and the next block's
+entry 1x1, 384 -> 192, in one launch: launch_junction, kgx_junction.hip) through the C ABI:
+- bit for bit equal to the two separate split-operand launches it replaces (KGX_JUNCTION=0 plans those), on f16 and
+  bf16 handles, at a ragged batch (tiles past the last pixel) and at batch 32, with gpool inner blocks between;
+- the junction net against the float64 oracle and the 16-bit network (the bounds of test_gpu_parity.py);
+- the planning: a net of n nested blocks over 384 / 192 channels runs n - 1 junctions and no separate entry or exit
+  1x1 between them."""
+
+import numpy as np
+import pytest
+
+from test_gpu_parity import check, emulated
+
+pytestmark = pytest.mark.gpu
+
+
+def junction_arch(synth, n=3):
+    inner = [[("res", 192)], [("gpool", 192, 64), ("res", 192)], [("res", 192), ("res", 192)]]
+    return synth.Arch("t-junction", 14, 384, [("nbt", 192, inner[k % 3]) for k in range(n)], mid_c=192, gpool_c=64)
+
+
+def run(kgx, mb, batch, prec, sp, gl, monkeypatch, junction):
+    if junction:
+        monkeypatch.delenv("KGX_JUNCTION", raising=False)
+    else:
+        monkeypatch.setenv("KGX_JUNCTION", "0")
+    net = kgx.Net(mb)
+    h = kgx.Handle(net, batch, prec)
+    h.profile(True)
+    h.profile_reset()
+    out = h.forward(sp, gl)
+    prof = h.profile_read()
+    h.profile(False)
+    again = h.forward(sp, gl)  # graph replay
+    h.close()
+    assert np.array_equal(out, again)
+    return out, prof, net
+
+
+@pytest.mark.parametrize("prec", ["f16", "bf16"])
+@pytest.mark.parametrize("batch", [5, 32])
+def test_junction_equals_the_two_separate_launches(kgx, synth, monkeypatch, prec, batch):
+    print(f"junction vs separate launches: {prec}, batch {batch}", flush=True)
+    mb = synth.write_model(junction_arch(synth, 4), 7)
+    sp, gl, _ = synth.make_inputs(batch, 11, board_sizes=[19, 19, 13, 9, 19, 7])
+    fused, pf, _ = run(kgx, mb, batch, prec, sp, gl, monkeypatch, True)
+    sep, ps, _ = run(kgx, mb, batch, prec, sp, gl, monkeypatch, False)
+    assert pf["conv1x1_junction"]["launches"] == 3 and "conv1x1_junction" not in ps
+    # the separate plan's 1x1s: four entries and four exits; the junction plan keeps the first entry and the last exit
+    sep_1x1 = sum(v["launches"] for k, v in ps.items() if k.startswith("conv1x1_split"))
+    fused_1x1 = sum(v["launches"] for k, v in pf.items() if k.startswith("conv1x1_split"))
+    assert sep_1x1 == 8 and fused_1x1 == 2, (ps.keys(), pf.keys())
+    assert np.all(np.isfinite(fused))
+    assert np.array_equal(fused, sep), f"{prec} batch {batch}: max diff {np.abs(fused - sep).max():.3e}"
+
+
+@pytest.mark.parametrize("prec", ["f16", "bf16"])
+def test_junction_net_matches_oracle(kgx, synth, oracle, monkeypatch, prec):
+    print(f"junction net vs oracle: {prec}", flush=True)
+    mb = synth.write_model(junction_arch(synth, 3), 9)
+    rows = [0, 1, 2, 3]
+    sp, gl, _ = synth.make_inputs(6, 13, board_sizes=[19, 13, 9, 19, 19, 5])
+    out, prof, net = run(kgx, mb, 6, prec, sp, gl, monkeypatch, True)
+    assert prof["conv1x1_junction"]["launches"] == 2
+    ref = oracle.Model(mb).forward(sp[rows], gl[rows])
+    check(out[rows], ref, net.P, net.S, prec, f"junction net", emulated(oracle, mb, prec, sp[rows], gl[rows]))
