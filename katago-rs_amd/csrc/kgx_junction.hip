@@ -43,10 +43,11 @@ constexpr int R1B = A1B > C1B ? (A1B > C2B ? A1B : C2B) : (C1B > C2B ? C1B : C2B
 constexpr int LDSB = ACTB + R1B;
 // Epilogue mappings, the same for every thread (no branch around a memory access, so the compiler's count of the
 // loads in flight stays exact and a later wait for a prefetched weight fragment leaves the trunk's stores in
-// flight): thread t takes channel quads 3 (t % G) + q, q < 3, of pixels t / G + R e, for the exit's G = 32 groups of
-// twelve channels and R = 16 (three pixels each), and the entry's G = 16 and R = 32 (pixels past 48 skipped at the
-// end).
+// flight): thread t takes channel quads t % G + G q, q < 3, of pixels t / G + R e, for the exit's G = 32 and R = 16
+// (three pixels each) and the entry's G = 16 and R = 32 (pixels past 48 skipped at the end). Consecutive lanes
+// take consecutive quads, so each access of a wave covers whole cache lines.
 constexpr int E1 = 3, E2 = 2;
+constexpr int NS = 2;  // weight steps in flight per product (of six per wave)
 static_assert(JNT / 64 == 8 && CB1 == 3 * 8 && CB2 == 3 * 4 && K2 == 12, "wave layout assumes 384 and 192 channels");
 
 // The XCD-aware tile order: workgroup g runs on XCD g % 8, and the four 48-pixel tiles of one 192-pixel region go
@@ -97,15 +98,18 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
     return *(const frag_t*)(base + (((ks >> 1) * 2 + pl) * JR + 16 * i + r16) * 128 + chunk * 16);
   };
 
-  // Exit product, wave wv: output columns 48 wv .. + 48 (blocks 3 wv + j), all 48 pixels.
-  frag_t b1[2][3][2];
+  // Exit product, wave wv: output columns 48 wv .. + 48 (blocks 3 wv + j), all 48 pixels. Its weight fragments go
+  // through a ring of NS steps, the first NS loaded while the operand's direct loads are in flight (the wait for
+  // those covers them too), so that the weights stream from L2 in the time that would otherwise only wait.
+  frag_t b1[NS][3][2];
   auto load_b1 = [&](int slot, int ks) {
 #pragma unroll
     for (int j = 0; j < 3; j++)
 #pragma unroll
       for (int pl = 0; pl < 2; pl++) b1[slot][j][pl] = wfrag(0, 3 * wv + j, K1, ks, pl);
   };
-  load_b1(0, 0);
+#pragma unroll
+  for (int k = 0; k < NS; k++) load_b1(k, k);
   // The exit's operand straight into LDS: 36 loads of 8 pixel rows x 128 bytes (64-channel slice kp, plane pl,
   // rows 8 grp ..), lane i filling row 8 grp + i / 8 at stored chunk i % 8 from source chunk (i % 8) ^ swizzle.
   // Rows past M lie beyond the buffer range and read as zero.
@@ -126,13 +130,12 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
   // The direct loads are not counted by the compiler: wait for all of this wave's loads, then for every wave.
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
-  load_b1(1, 1);
 
   // The exit epilogue's inputs: the trunk values it adds to, the emission's scale, bias and board mask (channels
-  // 12 c1 + 4 q of pixels p1 + 16 e; rows past M read row M - 1, never stored). They are issued after the product's
-  // last weight loads (a wait covers every load issued before the one it waits for), in flight during its last
-  // steps.
-  const int c1 = 12 * (tid & 31), p1 = tid >> 5;
+  // c1 + 128 q .. + 3 of pixels p1 + 16 e; rows past M read row M - 1, never stored). They are issued after the
+  // product's last weight loads (a wait covers every load issued before the one it waits for), in flight during
+  // its last steps.
+  const int c1 = 4 * (tid & 31), p1 = tid >> 5;
   floatx4 yres[E1][3], es1[3], eb1[3];
   float mk1[E1];
   auto load_epi1 = [&]() {
@@ -140,13 +143,13 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
     for (int e = 0; e < E1; e++) {
       const int m = min(m0 + p1 + 16 * e, M - 1);
 #pragma unroll
-      for (int q = 0; q < 3; q++) yres[e][q] = *(const floatx4*)(eo.y + (size_t)m * eo.ldy + c1 + 4 * q);
+      for (int q = 0; q < 3; q++) yres[e][q] = *(const floatx4*)(eo.y + (size_t)m * eo.ldy + c1 + 128 * q);
       mk1[e] = eo.emit.mask[m];
     }
 #pragma unroll
     for (int q = 0; q < 3; q++) {
-      es1[q] = *(const floatx4*)(eo.emit.scale + c1 + 4 * q);
-      eb1[q] = *(const floatx4*)(eo.emit.bias + c1 + 4 * q);
+      es1[q] = *(const floatx4*)(eo.emit.scale + c1 + 128 * q);
+      eb1[q] = *(const floatx4*)(eo.emit.bias + c1 + 128 * q);
     }
   };
 
@@ -173,51 +176,34 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
 #pragma unroll
       for (int i = 0; i < 3; i++)
 #pragma unroll
-        for (int j = 0; j < 3; j++) acc[i][j] = mfma(al[s][i], b1[s][j][0], acc[i][j]);
+        for (int j = 0; j < 3; j++) acc[i][j] = mfma(al[s][i], b1[ks % NS][j][0], acc[i][j]);
 #pragma unroll
       for (int i = 0; i < 3; i++)
 #pragma unroll
-        for (int j = 0; j < 3; j++) acc[i][j] = mfma(ah[s][i], b1[s][j][1], acc[i][j]);
+        for (int j = 0; j < 3; j++) acc[i][j] = mfma(ah[s][i], b1[ks % NS][j][1], acc[i][j]);
 #pragma unroll
       for (int i = 0; i < 3; i++)
 #pragma unroll
-        for (int j = 0; j < 3; j++) acc[i][j] = mfma(ah[s][i], b1[s][j][0], acc[i][j]);
+        for (int j = 0; j < 3; j++) acc[i][j] = mfma(ah[s][i], b1[ks % NS][j][0], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
-      if (ks + 2 < K1) load_b1(s, ks + 2);
-      if (ks + 3 == K1) load_epi1();
+      if (ks + NS < K1) load_b1(ks % NS, ks + NS);
+      if (ks + NS + 1 == K1) load_epi1();
     }
   }
 
   // Entry product, wave wv: step chain kg = wv / 4 (steps 2 kg + 4 (p / 2) + p % 2), output columns 48 cg .. + 48
-  // (blocks 3 cg + j, cg = wv % 4), all 48 pixels. Its first two steps' weights load now, ahead of the trunk's
-  // stores (the wait for a load also waits for the stores issued before it).
+  // (blocks 3 cg + j, cg = wv % 4), all 48 pixels. Its first NS steps' weights load after the exit's float tile is
+  // in LDS and ahead of the trunk's stores (the wait for a load also waits for the stores issued before it), in
+  // flight during the exit epilogue.
   const int kg = wv >> 2, cg = wv & 3;
   auto kstep = [&](int p) { return 2 * kg + 4 * (p >> 1) + (p & 1); };
-  frag_t b2[2][3][2];
+  frag_t b2[NS][3][2];
   auto load_b2 = [&](int slot, int p) {
 #pragma unroll
     for (int j = 0; j < 3; j++)
 #pragma unroll
       for (int pl = 0; pl < 2; pl++) b2[slot][j][pl] = wfrag(W2OFF, 3 * cg + j, K2, kstep(p), pl);
   };
-  load_b2(0, 0);
-  load_b2(1, 1);
-  // And the entry epilogue's per-channel inputs (channels 12 c2 + 4 q of pixels p2 + 32 e).
-  const int c2 = 12 * (tid & 15), p2 = tid >> 4;
-  const int fl2 = store_flags(no);
-  floatx4 es2[3], eb2[3];
-  float mk2[E2];
-  const float* const es2p = no.emit.scale ? no.emit.scale : eo.emit.scale;  // (any readable floats when unused)
-  const float* const eb2p = no.emit.scale ? no.emit.bias : eo.emit.bias;
-  const float* const mk2p = no.emit.scale ? no.emit.mask : eo.emit.mask;
-#pragma unroll
-  for (int q = 0; q < 3; q++) {
-    es2[q] = *(const floatx4*)(es2p + c2 + 4 * q);
-    eb2[q] = *(const floatx4*)(eb2p + c2 + 4 * q);
-  }
-#pragma unroll
-  for (int e = 0; e < E2; e++) mk2[e] = mk2p[min(m0 + p2 + 32 * e, M - 1)];
-
   // The exit's float tile over its operand's LDS (every wave is done reading the operand first).
   lds_barrier();
   float* const C1 = (float*)r1;
@@ -227,6 +213,24 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
     for (int j = 0; j < 3; j++)
 #pragma unroll
       for (int r = 0; r < 4; r++) C1[(16 * i + 4 * g4 + r) * LD1 + 48 * wv + 16 * j + r16] = acc[i][j][r];
+#pragma unroll
+  for (int k = 0; k < NS; k++) load_b2(k, k);
+  // And the entry epilogue's per-channel inputs (channels c2 + 64 q .. + 3 of pixels p2 + 32 e).
+  const int c2 = 4 * (tid & 15), p2 = tid >> 4;
+  const int fl2 = store_flags(no);
+  floatx4 es2[3], eb2[3];
+  float mk2[E2];
+  const float* const es2p = no.emit.scale ? no.emit.scale : eo.emit.scale;  // (any readable floats when unused)
+  const float* const eb2p = no.emit.scale ? no.emit.bias : eo.emit.bias;
+  const float* const mk2p = no.emit.scale ? no.emit.mask : eo.emit.mask;
+#pragma unroll
+  for (int q = 0; q < 3; q++) {
+    es2[q] = *(const floatx4*)(es2p + c2 + 64 * q);
+    eb2[q] = *(const floatx4*)(eb2p + c2 + 64 * q);
+  }
+#pragma unroll
+  for (int e = 0; e < E2; e++) mk2[e] = mk2p[min(m0 + p2 + 32 * e, M - 1)];
+
   lds_barrier();
 
   // Exit epilogue: the trunk plus the product, stored; the activation act(x * scale + bias) * mask in its two
@@ -241,7 +245,7 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
       const int p = p1 + 16 * e;
 #pragma unroll
       for (int q = 0; q < 3; q++) {
-        const int n = c1 + 4 * q;
+        const int n = c1 + 128 * q;
         floatx4 v = *(const floatx4*)(C1 + p * LD1 + n);
         v += yres[e][q];
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ybuf, (p * eo.ldy + n) * 4, 0, 2);
@@ -292,17 +296,17 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
 #pragma unroll
       for (int i = 0; i < 3; i++)
 #pragma unroll
-        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(al[s][i], b2[s][j][0], acc2[i][j]);
+        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(al[s][i], b2[p % NS][j][0], acc2[i][j]);
 #pragma unroll
       for (int i = 0; i < 3; i++)
 #pragma unroll
-        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[s][j][1], acc2[i][j]);
+        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[p % NS][j][1], acc2[i][j]);
 #pragma unroll
       for (int i = 0; i < 3; i++)
 #pragma unroll
-        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[s][j][0], acc2[i][j]);
+        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[p % NS][j][0], acc2[i][j]);
       __builtin_amdgcn_sched_barrier(0);
-      if (p + 2 < K2 / 2) load_b2(s, p + 2);
+      if (p + NS < K2 / 2) load_b2(p % NS, p + NS);
     }
   }
 
@@ -326,7 +330,7 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
     if (p < JR && m < M) {
 #pragma unroll
       for (int q = 0; q < 3; q++) {
-        const int n = c2 + 4 * q;
+        const int n = c2 + 64 * q;
         floatx4 sum = *(const floatx4*)(C2 + p * LD2 + n);
         sum += *(const floatx4*)(C2 + (JR + p) * LD2 + n);
         if (fast) {
