@@ -62,6 +62,17 @@ __host__ inline int gemm_grid(int M, int N, int BM, int BN) {
   return 8 * (((M + BM - 1) / BM + 7) / 8) * ((N + BN - 1) / BN);
 }
 
+// The rotation of x with its partner y (the other half of the head): x cos - y sin for the first half, y sin + x cos
+// for the second, each with one explicit fused multiply-add, so that every tile configuration rounds it alike (a
+// contracted expression may fuse either product, and a row must not depend on the tile it falls in).
+__device__ __forceinline__ floatx4 rope4(floatx4 x, floatx4 y, floatx4 cs, floatx4 sn, bool lo) {
+  floatx4 r;
+#pragma unroll
+  for (int k = 0; k < 4; k++)
+    r[k] = lo ? __builtin_fmaf(x[k], cs[k], -(y[k] * sn[k])) : __builtin_fmaf(y[k], sn[k], x[k] * cs[k]);
+  return r;
+}
+
 template <typename T, typename C, bool AF, bool PRO, int ACT, int EPI>
 // The operands' pointers, strides and sizes lead the arguments (copies of g's fields) so that they are preloaded
 // into SGPRs at wave launch; by-value structs are not, and the first stage's loads would wait for them.
@@ -410,9 +421,47 @@ __global__ __launch_bounds__(C::WM * C::WN * 64, C::MINW) void gemm_kernel(const
                     act_f<ACT_SILU>(a[2]) * b[2], act_f<ACT_SILU>(a[3]) * b[3]);
         }
       }
-    } else if constexpr (EPI == EPI_QKV) {
+    } else if constexpr (EPI == EPI_QKV && NT % CV == 0) {
       // q|k|v projection: each head lies inside the tile, so the rotation partner of column n (n +- dq/2) is
-      // in LDS too.
+      // in LDS too. A thread keeps one column quad for every row it takes (NT is a multiple of CV), so the head,
+      // rotation and table indices are computed once, and the rotation tables are read for all its rows before
+      // the first store (a load after a store that may alias it waits for the store).
+      constexpr int RS = NT / CV;
+      const QkvEpi& q = g.qkv;
+      const int half = q.dq / 2;
+      const int c = (tid % CV) * 4, n = n0 + c, r0 = tid / CV;
+      const bool qk = n < q.nq + q.nk, isq = n < q.nq;
+      const int nn = n - (isq ? 0 : q.nq), hh = nn / q.dq, rr = nn - hh * q.dq;
+      const bool lo = rr < half;
+      const int pp = lo ? rr : rr - half, tab = q.tables == 1 ? 0 : (isq ? hh / (q.H / q.KV) : hh);
+      const bool rot = qk && q.cos;
+      floatx4 cs[EV], sn[EV];
+      if (rot) {
+#pragma unroll
+        for (int v = 0; v < EV; v++) {
+          const int m = min(mp + r0 + RS * v, M - 1);
+          const size_t ti = ((size_t)tab * HW + m % HW) * half + pp;
+          cs[v] = *(const floatx4*)(q.cos + ti);
+          sn[v] = *(const floatx4*)(q.sin + ti);
+        }
+      }
+#pragma unroll
+      for (int v = 0; v < EV; v++) {
+        const int r = r0 + RS * v, m = mp + r;
+        if (m < M && n < N) {
+          floatx4 x = *(const floatx4*)(Et + r * ELD + c);
+          if (qk) {
+            if (rot) {
+              const floatx4 y = *(const floatx4*)(Et + r * ELD + c + (lo ? half : -half));
+              x = rope4(x, y, cs[v], sn[v], lo);
+            }
+            if (isq) x *= q.qscale;
+          }
+          store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, x[0], x[1], x[2], x[3]);
+        }
+      }
+    } else if constexpr (EPI == EPI_QKV) {
+      // (The same on tiles whose thread count is not a multiple of their column quads.)
       const QkvEpi& q = g.qkv;
       const int half = q.dq / 2;
 #pragma unroll
@@ -429,7 +478,7 @@ __global__ __launch_bounds__(C::WM * C::WN * 64, C::MINW) void gemm_kernel(const
               const floatx4 y = *(const floatx4*)(Et + r * ELD + c + (lo ? half : -half));
               const size_t ti = ((size_t)tab * HW + m % HW) * half + pp;
               const floatx4 cs = *(const floatx4*)(q.cos + ti), sn = *(const floatx4*)(q.sin + ti);
-              x = lo ? x * cs - y * sn : y * sn + x * cs;
+              x = rope4(x, y, cs, sn, lo);
             }
             if (isq) x *= q.qscale;
           }
