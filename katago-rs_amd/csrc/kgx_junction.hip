@@ -70,7 +70,8 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-template <typename T>
+// ACT1: the exit's emission activation (ACT_MISH), or -1: the one eo names, chosen per value at run time.
+template <typename T, int ACT1>
 __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ X, const T* __restrict__ Xlo, int ldx,
                                                           const T* __restrict__ W, int M, ConvOut eo, ConvOut no) {
   typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
@@ -215,7 +216,8 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
       for (int r = 0; r < 4; r++) C1[(16 * i + 4 * g4 + r) * LD1 + 48 * wv + 16 * j + r16] = acc[i][j][r];
 #pragma unroll
   for (int k = 0; k < NS; k++) load_b2(k, k);
-  // And the entry epilogue's per-channel inputs (channels c2 + 64 q .. + 3 of pixels p2 + 32 e).
+  // The entry epilogue's per-channel inputs (channels c2 + 64 q .. + 3 of pixels p2 + 32 e), loaded during the
+  // entry product's last block.
   const int c2 = 4 * (tid & 15), p2 = tid >> 4;
   const int fl2 = store_flags(no);
   floatx4 es2[3], eb2[3];
@@ -223,92 +225,103 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
   const float* const es2p = no.emit.scale ? no.emit.scale : eo.emit.scale;  // (any readable floats when unused)
   const float* const eb2p = no.emit.scale ? no.emit.bias : eo.emit.bias;
   const float* const mk2p = no.emit.scale ? no.emit.mask : eo.emit.mask;
+  auto load_epi2 = [&]() {
 #pragma unroll
-  for (int q = 0; q < 3; q++) {
-    es2[q] = *(const floatx4*)(es2p + c2 + 64 * q);
-    eb2[q] = *(const floatx4*)(eb2p + c2 + 64 * q);
-  }
+    for (int q = 0; q < 3; q++) {
+      es2[q] = *(const floatx4*)(es2p + c2 + 64 * q);
+      eb2[q] = *(const floatx4*)(eb2p + c2 + 64 * q);
+    }
 #pragma unroll
-  for (int e = 0; e < E2; e++) mk2[e] = mk2p[min(m0 + p2 + 32 * e, M - 1)];
+    for (int e = 0; e < E2; e++) mk2[e] = mk2p[min(m0 + p2 + 32 * e, M - 1)];
+  };
 
   lds_barrier();
 
   // Exit epilogue: the trunk plus the product, stored; the activation act(x * scale + bias) * mask in its two
   // 16-bit planes (the high part, and the rounding of what it leaves) into the entry's LDS operand. The trunk goes
-  // out through a buffer whose range ends at row M, so rows past it are dropped without a branch.
+  // out through a buffer whose range ends at row M, so rows past it are dropped without a branch. It runs in three
+  // channel groups q (channels c1 + 128 q: the operand's 64-channel slices 2 q and 2 q + 1), and the entry product
+  // in three blocks of two steps, block b reading slices 2 b (chain 0) and 2 b + 1 (chain 1): group q + 1's VALU
+  // work follows block q's MFMAs in each wave's instruction stream, so that it issues while they run, and a
+  // barrier separates the groups. The accumulation order stays that of the separate kernel.
   const auto ybuf = __builtin_amdgcn_make_buffer_rsrc(eo.y + (size_t)m0 * eo.ldy, 0,
                                                       min(JR, M - m0) * eo.ldy * (int)sizeof(float), 0x00020000);
-  auto epi1 = [&](auto act_c) {
+  // Pixel row e of group q; A >= 0 the emission's activation known here, -1 chosen at run time.
+  auto epi1 = [&](auto act_c, int q, int e) {
     constexpr int A = decltype(act_c)::value;
+    const int p = p1 + 16 * e, n = c1 + 128 * q;
+    floatx4 v = *(const floatx4*)(C1 + p * LD1 + n);
+    v += yres[e][q];
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ybuf, (p * eo.ldy + n) * 4, 0, 2);
+    float t[4], l[4];
 #pragma unroll
-    for (int e = 0; e < E1; e++) {
-      const int p = p1 + 16 * e;
-#pragma unroll
-      for (int q = 0; q < 3; q++) {
-        const int n = c1 + 128 * q;
-        floatx4 v = *(const floatx4*)(C1 + p * LD1 + n);
-        v += yres[e][q];
-        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), ybuf, (p * eo.ldy + n) * 4, 0, 2);
-        float t[4], l[4];
-#pragma unroll
-        for (int k = 0; k < 4; k++) {
-          const float a = v[k] * es1[q][k] + eb1[q][k];
-          t[k] = act_f<A>(a) * mk1[e];
-          l[k] = t[k] - (float)to_t<T>(t[k]);
-        }
-        T hi[4] = {to_t<T>(t[0]), to_t<T>(t[1]), to_t<T>(t[2]), to_t<T>(t[3])};
-        T lo[4] = {to_t<T>(l[0]), to_t<T>(l[1]), to_t<T>(l[2]), to_t<T>(l[3])};
-        const int kp = n >> 6, chunk = ((n & 63) >> 3) ^ ((p >> 1) & 7);
-        char* d = act + ((kp * 2) * JR + p) * 128 + chunk * 16 + (n & 7) * (int)sizeof(T);
-        *(uint2*)d = *(const uint2*)hi;
-        *(uint2*)(d + JR * 128) = *(const uint2*)lo;
-      }
+    for (int k = 0; k < 4; k++) {
+      const float a = v[k] * es1[q][k] + eb1[q][k];
+      if constexpr (A >= 0) t[k] = act_f<A>(a) * mk1[e];
+      else t[k] = act_rt(a, eo.emit.act) * mk1[e];
+      l[k] = t[k] - (float)to_t<T>(t[k]);
     }
+    T hi[4] = {to_t<T>(t[0]), to_t<T>(t[1]), to_t<T>(t[2]), to_t<T>(t[3])};
+    T lo[4] = {to_t<T>(l[0]), to_t<T>(l[1]), to_t<T>(l[2]), to_t<T>(l[3])};
+    const int kp = n >> 6, chunk = ((n & 63) >> 3) ^ ((p >> 1) & 7);
+    char* d = act + ((kp * 2) * JR + p) * 128 + chunk * 16 + (n & 7) * (int)sizeof(T);
+    *(uint2*)d = *(const uint2*)hi;
+    *(uint2*)(d + JR * 128) = *(const uint2*)lo;
   };
-  switch (eo.emit.act) {
-    case ACT_MISH: epi1(std::integral_constant<int, ACT_MISH>{}); break;
-    case ACT_RELU: epi1(std::integral_constant<int, ACT_RELU>{}); break;
-    case ACT_SILU: epi1(std::integral_constant<int, ACT_SILU>{}); break;
-    default: epi1(std::integral_constant<int, ACT_ID>{}); break;
-  }
-  lds_barrier();
 
   floatx4 acc2[3][3];
 #pragma unroll
   for (int i = 0; i < 3; i++)
 #pragma unroll
     for (int j = 0; j < 3; j++) acc2[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  {
-    frag_t ah[2][3], al[2][3];
-    auto load_a2 = [&](int set, int p) {
+  frag_t ah[2][3], al[2][3];
+  auto load_a2 = [&](int set, int p) {
 #pragma unroll
-      for (int i = 0; i < 3; i++) {
-        ah[set][i] = afrag(act, i, kstep(p), 0);
-        al[set][i] = afrag(act, i, kstep(p), 1);
-      }
-    };
-    load_a2(0, 0);
-#pragma unroll
-    for (int p = 0; p < K2 / 2; p++) {
-      const int s = p & 1;
-      if (p + 1 < K2 / 2) load_a2(s ^ 1, p + 1);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = 0; i < 3; i++)
-#pragma unroll
-        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(al[s][i], b2[p % NS][j][0], acc2[i][j]);
-#pragma unroll
-      for (int i = 0; i < 3; i++)
-#pragma unroll
-        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[p % NS][j][1], acc2[i][j]);
-#pragma unroll
-      for (int i = 0; i < 3; i++)
-#pragma unroll
-        for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[p % NS][j][0], acc2[i][j]);
-      __builtin_amdgcn_sched_barrier(0);
-      if (p + NS < K2 / 2) load_b2(p % NS, p + NS);
+    for (int i = 0; i < 3; i++) {
+      ah[set][i] = afrag(act, i, kstep(p), 0);
+      al[set][i] = afrag(act, i, kstep(p), 1);
     }
-  }
+  };
+  auto mma2 = [&](int p) {
+    const int s = p & 1;
+#pragma unroll
+    for (int i = 0; i < 3; i++)
+#pragma unroll
+      for (int j = 0; j < 3; j++) acc2[i][j] = mfma(al[s][i], b2[p % NS][j][0], acc2[i][j]);
+#pragma unroll
+    for (int i = 0; i < 3; i++)
+#pragma unroll
+      for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[p % NS][j][1], acc2[i][j]);
+#pragma unroll
+    for (int i = 0; i < 3; i++)
+#pragma unroll
+      for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[p % NS][j][0], acc2[i][j]);
+  };
+  auto run = [&](auto act_c) {
+#pragma unroll
+    for (int e = 0; e < E1; e++) epi1(act_c, 0, e);
+    lds_barrier();
+#pragma unroll
+    for (int b = 0; b < 3; b++) {
+      if (b == 2) load_epi2();
+      load_a2(0, 2 * b);
+      __builtin_amdgcn_sched_barrier(0);
+      mma2(2 * b);
+      load_a2(1, 2 * b + 1);
+      if (b < 2) {
+        epi1(act_c, b + 1, 0);
+        epi1(act_c, b + 1, 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      if (2 * b + NS < K2 / 2) load_b2(0, 2 * b + NS);
+      mma2(2 * b + 1);
+      if (b < 2) epi1(act_c, b + 1, 2);
+      __builtin_amdgcn_sched_barrier(0);
+      if (2 * b + 1 + NS < K2 / 2) load_b2(1, 2 * b + 1 + NS);
+      if (b < 2) lds_barrier();
+    }
+  };
+  run(std::integral_constant<int, ACT1>{});
 
   // The two chains' float tiles over the exit's (whose last reads preceded the barrier above).
   float* const C2 = (float*)r1;
@@ -390,12 +403,13 @@ void launch_junction(int prec, const void* x, const void* x_lo, int ldx, const v
                                                               (uintptr_t)no.emit.bias % 16)))
     throw std::runtime_error("junction: unsupported entry outputs");
   const int M = B * HW;
+  const bool mish = eo.emit.act == ACT_MISH;
   if (prec == PREC_F16)
-    launch_k(junction_kernel<f16>, junction_grid(M), JNT, 0, s, (const f16*)x, (const f16*)x_lo, ldx, (const f16*)w,
-             M, eo, no);
+    launch_k(mish ? junction_kernel<f16, ACT_MISH> : junction_kernel<f16, -1>, junction_grid(M), JNT, 0, s,
+             (const f16*)x, (const f16*)x_lo, ldx, (const f16*)w, M, eo, no);
   else
-    launch_k(junction_kernel<bf16>, junction_grid(M), JNT, 0, s, (const bf16*)x, (const bf16*)x_lo, ldx,
-             (const bf16*)w, M, eo, no);
+    launch_k(mish ? junction_kernel<bf16, ACT_MISH> : junction_kernel<bf16, -1>, junction_grid(M), JNT, 0, s,
+             (const bf16*)x, (const bf16*)x_lo, ldx, (const bf16*)w, M, eo, no);
   KGX_CHECK_LAUNCH();
 }
 

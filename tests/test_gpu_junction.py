@@ -1,7 +1,8 @@
 """The nested-bottleneck junction (one block's exit 1x1 convolution, 192 -> 384 into the trunk, and the next block's
 entry 1x1, 384 -> 192, in one launch: launch_junction, kgx_junction.hip) through the C ABI:
 - bit for bit equal to the two separate split-operand launches it replaces (KGX_JUNCTION=0 plans those), on f16 and
-  bf16 handles, at a ragged batch (tiles past the last pixel) and at batch 32, with gpool inner blocks between;
+  bf16 handles, at a ragged batch (tiles past the last pixel) and at batch 32, with gpool inner blocks between, for
+  mish nets and (the run-time activation kernel) ReLU nets;
 - the junction net against the float64 oracle and the 16-bit network (the bounds of test_gpu_parity.py);
 - the planning: a net of n nested blocks over 384 / 192 channels runs n - 1 junctions and no separate entry or exit
   1x1 between them."""
@@ -14,9 +15,10 @@ from test_gpu_parity import check, emulated
 pytestmark = pytest.mark.gpu
 
 
-def junction_arch(synth, n=3):
+def junction_arch(synth, n=3, act="ACTIVATION_MISH"):
     inner = [[("res", 192)], [("gpool", 192, 64), ("res", 192)], [("res", 192), ("res", 192)]]
-    return synth.Arch("t-junction", 14, 384, [("nbt", 192, inner[k % 3]) for k in range(n)], mid_c=192, gpool_c=64)
+    return synth.Arch("t-junction", 14, 384, [("nbt", 192, inner[k % 3]) for k in range(n)], mid_c=192, gpool_c=64,
+                      act=act)
 
 
 def run(kgx, mb, batch, prec, sp, gl, monkeypatch, junction):
@@ -37,11 +39,13 @@ def run(kgx, mb, batch, prec, sp, gl, monkeypatch, junction):
     return out, prof, net
 
 
-@pytest.mark.parametrize("prec", ["f16", "bf16"])
-@pytest.mark.parametrize("batch", [5, 32])
-def test_junction_equals_the_two_separate_launches(kgx, synth, monkeypatch, prec, batch):
-    print(f"junction vs separate launches: {prec}, batch {batch}", flush=True)
-    mb = synth.write_model(junction_arch(synth, 4), 7)
+@pytest.mark.parametrize("prec,batch,act", [("f16", 5, "ACTIVATION_MISH"), ("bf16", 5, "ACTIVATION_MISH"),
+                                            ("f16", 32, "ACTIVATION_MISH"), ("bf16", 32, "ACTIVATION_MISH"),
+                                            ("f16", 7, "ACTIVATION_RELU")])
+def test_junction_equals_the_two_separate_launches(kgx, synth, monkeypatch, prec, batch, act):
+    """(ReLU nets run the junction's kernel that takes the emission's activation at run time.)"""
+    print(f"junction vs separate launches: {prec}, batch {batch}, {act}", flush=True)
+    mb = synth.write_model(junction_arch(synth, 4, act), 7)
     sp, gl, _ = synth.make_inputs(batch, 11, board_sizes=[19, 19, 13, 9, 19, 7])
     fused, pf, _ = run(kgx, mb, batch, prec, sp, gl, monkeypatch, True)
     sep, ps, _ = run(kgx, mb, batch, prec, sp, gl, monkeypatch, False)
