@@ -29,26 +29,29 @@ constexpr int JCI = kJunctionInner, JCO = kJunctionOuter;
 constexpr int JR = 48;                         // pixels per workgroup (three 16-row MFMA blocks)
 constexpr int JNT = 512;                       // threads: eight waves, two per SIMD
 constexpr int K1 = JCI / 32, K2 = JCO / 32;    // 16x16x32 steps of the exit and the entry product
-constexpr int CB1 = JCO / 16, CB2 = JCI / 16;  // 16-column blocks of the two outputs
+constexpr int CB1 = JCO / 16;                  // 16-column blocks of the exit's output
 constexpr int FRAG = 64 * 8;                   // elements per packed fragment (64 lanes x 8)
 constexpr int W2OFF = CB1 * K1 * 2 * FRAG;     // the entry's fragments follow the exit's
-constexpr int WELEMS = W2OFF + CB2 * K2 * 2 * FRAG;
+// The entry's outputs NO: a nested block's 192 (kJunctionInner), or the heads' p1 | g1 | v1 convolution's 96
+// (kJunctionHead) after the trunk's last exit.
+__host__ __device__ constexpr int junction_welems(int no) { return W2OFF + (no / 16) * K2 * 2 * FRAG; }
 // LDS: the entry's operand (the activation planes, [64-channel slice][plane][pixel][128 bytes], 16-byte chunks
 // swizzled as chunk ^ (pixel / 2 % 8)), then one region that holds in turn the exit's operand (same layout over
-// 192 channels), the exit's float tile [48][384 + 4] and the entry's two float tiles [2][48][192 + 4].
-constexpr int LD1 = JCO + 4, LD2 = JCI + 4;
+// 192 channels), the exit's float tile [48][384 + 4] and the entry's two float tiles [2][48][NO + 4] (at most
+// the exit's).
+constexpr int LD1 = JCO + 4;
 constexpr int ACTB = (JCO / 64) * 2 * JR * 128;
-constexpr int A1B = (JCI / 64) * 2 * JR * 128, C1B = JR * LD1 * 4, C2B = 2 * JR * LD2 * 4;
+constexpr int A1B = (JCI / 64) * 2 * JR * 128, C1B = JR * LD1 * 4, C2B = 2 * JR * (JCI + 4) * 4;
 constexpr int R1B = A1B > C1B ? (A1B > C2B ? A1B : C2B) : (C1B > C2B ? C1B : C2B);
 constexpr int LDSB = ACTB + R1B;
 // Epilogue mappings, the same for every thread (no branch around a memory access, so the compiler's count of the
 // loads in flight stays exact and a later wait for a prefetched weight fragment leaves the trunk's stores in
 // flight): thread t takes channel quads t % G + G q, q < 3, of pixels t / G + R e, for the exit's G = 32 and R = 16
-// (three pixels each) and the entry's G = 16 and R = 32 (pixels past 48 skipped at the end). Consecutive lanes
-// take consecutive quads, so each access of a wave covers whole cache lines.
-constexpr int E1 = 3, E2 = 2;
+// (three pixels each) and the entry's G = NO / 12 and R = 512 / G (pixels past 48 skipped at the end). Consecutive
+// lanes take consecutive quads, so each access of a wave covers whole cache lines.
+constexpr int E1 = 3;
 constexpr int NS = 2;  // weight steps in flight per product (of six per wave)
-static_assert(JNT / 64 == 8 && CB1 == 3 * 8 && CB2 == 3 * 4 && K2 == 12, "wave layout assumes 384 and 192 channels");
+static_assert(JNT / 64 == 8 && CB1 == 3 * 8 && K2 == 12, "wave layout assumes 384 and 192 channels");
 
 // The XCD-aware tile order: workgroup g runs on XCD g % 8, and the four 48-pixel tiles of one 192-pixel region go
 // to that region's XCD (region r on XCD r % 8), as every 192-pixel convolution around the junction maps it, so the
@@ -70,11 +73,15 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// ACT1: the exit's emission activation (ACT_MISH), or -1: the one eo names, chosen per value at run time.
-template <typename T, int ACT1>
+// ACT1: the exit's emission activation (ACT_MISH), or -1: the one eo names, chosen per value at run time. NO: the
+// entry's outputs (192 or 96). A trunk that ends here (eo.y_dead) is read and not stored.
+template <typename T, int ACT1, int NO>
 __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ X, const T* __restrict__ Xlo, int ldx,
                                                           const T* __restrict__ W, int M, ConvOut eo, ConvOut no) {
   typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
+  static_assert(NO == 192 || NO == 96, "entry outputs");
+  constexpr int CB2 = NO / 16, LD2 = NO + 4;
+  constexpr int G2 = NO / 12, R2 = JNT / G2, E2 = (JR + R2 - 1) / R2;  // the entry epilogue's mapping
   __shared__ __align__(1024) char smem[LDSB];
   char* const act = smem;
   char* const r1 = smem + ACTB;
@@ -196,7 +203,10 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
   // (blocks 3 cg + j, cg = wv % 4), all 48 pixels. Its first NS steps' weights load after the exit's float tile is
   // in LDS and ahead of the trunk's stores (the wait for a load also waits for the stores issued before it), in
   // flight during the exit epilogue.
-  const int kg = wv >> 2, cg = wv & 3;
+  // (With 96 outputs, waves with cg >= 2 repeat the columns of cg - 2 and do not write them: every wave then issues
+  // the same instructions.)
+  const int kg = wv >> 2, cg = (wv & 3) % (CB2 / 3);
+  const bool c2own = (wv & 3) < CB2 / 3;
   auto kstep = [&](int p) { return 2 * kg + 4 * (p >> 1) + (p & 1); };
   frag_t b2[NS][3][2];
   auto load_b2 = [&](int slot, int p) {
@@ -216,9 +226,9 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
       for (int r = 0; r < 4; r++) C1[(16 * i + 4 * g4 + r) * LD1 + 48 * wv + 16 * j + r16] = acc[i][j][r];
 #pragma unroll
   for (int k = 0; k < NS; k++) load_b2(k, k);
-  // The entry epilogue's per-channel inputs (channels c2 + 64 q .. + 3 of pixels p2 + 32 e), loaded during the
+  // The entry epilogue's per-channel inputs (channels c2 + 4 G2 q .. + 3 of pixels p2 + R2 e), loaded during the
   // entry product's last block.
-  const int c2 = 4 * (tid & 15), p2 = tid >> 4;
+  const int c2 = 4 * (tid % G2), p2 = tid / G2;
   const int fl2 = store_flags(no);
   floatx4 es2[3], eb2[3];
   float mk2[E2];
@@ -228,11 +238,11 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
   auto load_epi2 = [&]() {
 #pragma unroll
     for (int q = 0; q < 3; q++) {
-      es2[q] = *(const floatx4*)(es2p + c2 + 64 * q);
-      eb2[q] = *(const floatx4*)(eb2p + c2 + 64 * q);
+      es2[q] = *(const floatx4*)(es2p + c2 + 4 * G2 * q);
+      eb2[q] = *(const floatx4*)(eb2p + c2 + 4 * G2 * q);
     }
 #pragma unroll
-    for (int e = 0; e < E2; e++) mk2[e] = mk2p[min(m0 + p2 + 32 * e, M - 1)];
+    for (int e = 0; e < E2; e++) mk2[e] = mk2p[min(m0 + p2 + R2 * e, M - 1)];
   };
 
   lds_barrier();
@@ -244,8 +254,9 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
   // in three blocks of two steps, block b reading slices 2 b (chain 0) and 2 b + 1 (chain 1): group q + 1's VALU
   // work follows block q's MFMAs in each wave's instruction stream, so that it issues while they run, and a
   // barrier separates the groups. The accumulation order stays that of the separate kernel.
-  const auto ybuf = __builtin_amdgcn_make_buffer_rsrc(eo.y + (size_t)m0 * eo.ldy, 0,
-                                                      min(JR, M - m0) * eo.ldy * (int)sizeof(float), 0x00020000);
+  // (A trunk that ends here gets an empty range: its stores are all dropped.)
+  const auto ybuf = __builtin_amdgcn_make_buffer_rsrc(
+      eo.y + (size_t)m0 * eo.ldy, 0, eo.y_dead ? 0 : min(JR, M - m0) * eo.ldy * (int)sizeof(float), 0x00020000);
   // Pixel row e of group q; A >= 0 the emission's activation known here, -1 chosen at run time.
   auto epi1 = [&](auto act_c, int q, int e) {
     constexpr int A = decltype(act_c)::value;
@@ -325,13 +336,15 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
 
   // The two chains' float tiles over the exit's (whose last reads preceded the barrier above).
   float* const C2 = (float*)r1;
+  if (c2own) {
 #pragma unroll
-  for (int i = 0; i < 3; i++)
+    for (int i = 0; i < 3; i++)
 #pragma unroll
-    for (int j = 0; j < 3; j++)
+      for (int j = 0; j < 3; j++)
 #pragma unroll
-      for (int r = 0; r < 4; r++)
-        C2[(kg * JR + 16 * i + 4 * g4 + r) * LD2 + 48 * cg + 16 * j + r16] = acc2[i][j][r];
+        for (int r = 0; r < 4; r++)
+          C2[(kg * JR + 16 * i + 4 * g4 + r) * LD2 + 48 * cg + 16 * j + r16] = acc2[i][j][r];
+  }
   lds_barrier();
 
   // Entry epilogue: chain 0 plus chain 1, then the convolution's outputs (the inner stream and its consumer's
@@ -339,11 +352,11 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
   const bool fast = fl2 == (SF_Y | SF_EMIT) && no.emit.act == ACT_MISH;
 #pragma unroll
   for (int e = 0; e < E2; e++) {
-    const int p = p2 + 32 * e, m = m0 + p;
+    const int p = p2 + R2 * e, m = m0 + p;
     if (p < JR && m < M) {
 #pragma unroll
       for (int q = 0; q < 3; q++) {
-        const int n = c2 + 64 * q;
+        const int n = c2 + 4 * G2 * q;
         floatx4 sum = *(const floatx4*)(C2 + p * LD2 + n);
         sum += *(const floatx4*)(C2 + (JR + p) * LD2 + n);
         if (fast) {
@@ -368,8 +381,9 @@ int junction_grid(int M) {
   return 32 * ((regions + 7) / 8);
 }
 
-void junction_pack_weights(const float* w_exit, const float* w_entry, int prec, std::vector<float>& out) {
-  out.assign(WELEMS, 0.f);
+void junction_pack_weights(const float* w_exit, const float* w_entry, int entry_oc, int prec, std::vector<float>& out) {
+  if (entry_oc != kJunctionInner && entry_oc != kJunctionHead) throw std::runtime_error("junction: entry outputs");
+  out.assign(junction_welems(entry_oc), 0.f);
   // Fragment (cb, ks, plane) of a K-step weight matrix w [cols][32 K]: lane l, element e holds column
   // 16 cb + l % 16, channel 32 ks + 8 (l / 16) + e; the low plane holds w - round(w).
   auto pack = [&](const float* w, int cbs, int K, int base) {
@@ -384,17 +398,19 @@ void junction_pack_weights(const float* w_exit, const float* w_entry, int prec, 
           }
   };
   pack(w_exit, CB1, K1, 0);
-  pack(w_entry, CB2, K2, W2OFF);
+  pack(w_entry, entry_oc / 16, K2, W2OFF);
 }
 
 void launch_junction(int prec, const void* x, const void* x_lo, int ldx, const void* w, const ConvOut& eo,
-                     const ConvOut& no, int B, hipStream_t s) {
+                     const ConvOut& no, int entry_oc, int B, hipStream_t s) {
   if (prec != PREC_F16 && prec != PREC_BF16) throw std::runtime_error("junction: 16-bit operands only");
+  if (entry_oc != kJunctionInner && entry_oc != kJunctionHead) throw std::runtime_error("junction: entry outputs");
   if (B <= 0) return;
   if (!x || !x_lo || !w || ldx < JCI || ldx % 8 || ((uintptr_t)x | (uintptr_t)x_lo | (uintptr_t)w) % 16)
     throw std::runtime_error("junction: operands must be 16-byte aligned rows of at least 192 channels");
-  // The exit's output is the trunk's residual add and the emission of the entry's activation, nothing else.
-  if (!eo.y || !eo.accumulate || eo.y_dead || eo.ldy % 4 || eo.yt || eo.rowmask || eo.colbias || !eo.emit.scale ||
+  // The exit's output is the trunk's residual add (stored, or read only where the trunk ends) and the emission of
+  // the entry's activation, nothing else.
+  if (!eo.y || !eo.accumulate || eo.ldy % 4 || eo.yt || eo.rowmask || eo.colbias || !eo.emit.scale ||
       !eo.emit.bias || !eo.emit.mask || eo.pool.psum || ((uintptr_t)eo.y | (uintptr_t)eo.emit.scale |
                                                          (uintptr_t)eo.emit.bias) % 16)
     throw std::runtime_error("junction: the exit must add into the trunk and emit the entry's activation");
@@ -404,12 +420,21 @@ void launch_junction(int prec, const void* x, const void* x_lo, int ldx, const v
     throw std::runtime_error("junction: unsupported entry outputs");
   const int M = B * HW;
   const bool mish = eo.emit.act == ACT_MISH;
-  if (prec == PREC_F16)
-    launch_k(mish ? junction_kernel<f16, ACT_MISH> : junction_kernel<f16, -1>, junction_grid(M), JNT, 0, s,
-             (const f16*)x, (const f16*)x_lo, ldx, (const f16*)w, M, eo, no);
-  else
-    launch_k(mish ? junction_kernel<bf16, ACT_MISH> : junction_kernel<bf16, -1>, junction_grid(M), JNT, 0, s,
-             (const bf16*)x, (const bf16*)x_lo, ldx, (const bf16*)w, M, eo, no);
+  auto go = [&](auto tc, auto noc) {
+    typedef decltype(tc) TT;
+    constexpr int N = decltype(noc)::value;
+    launch_k(mish ? junction_kernel<TT, ACT_MISH, N> : junction_kernel<TT, -1, N>, junction_grid(M), JNT, 0, s,
+             (const TT*)x, (const TT*)x_lo, ldx, (const TT*)w, M, eo, no);
+  };
+  typedef std::integral_constant<int, kJunctionInner> Inner;
+  typedef std::integral_constant<int, kJunctionHead> Head;
+  if (prec == PREC_F16) {
+    if (entry_oc == kJunctionInner) go(f16(), Inner());
+    else go(f16(), Head());
+  } else {
+    if (entry_oc == kJunctionInner) go(bf16(), Inner());
+    else go(bf16(), Head());
+  }
   KGX_CHECK_LAUNCH();
 }
 

@@ -174,14 +174,16 @@ float conv_round_operand(float v, int prec);
 
 // A nested-bottleneck junction in one launch (16-bit handles, split operands): block k's exit 1x1 convolution
 // (kJunctionInner -> kJunctionOuter channels) into `exit_o` (the trunk's residual add, emitting the next block's
-// activation), whose activation feeds block k + 1's entry 1x1 convolution (kJunctionOuter -> kJunctionInner) into
-// `entry_o` without passing through memory (exit_o.emit.out / out_lo are not written). x / x_lo: the exit's split
-// operand (rows of ldx); w: the compute-type conversion of junction_pack_weights' layout of both filters (each
-// [oc][ic]). The results equal the two separate split 1x1 convolutions' bit for bit.
-constexpr int kJunctionInner = 192, kJunctionOuter = 384;
-void junction_pack_weights(const float* w_exit, const float* w_entry, int prec, std::vector<float>& out);
+// activation), whose activation feeds block k + 1's entry 1x1 convolution (kJunctionOuter -> entry_oc, entry_oc
+// kJunctionInner) into `entry_o` without passing through memory (exit_o.emit.out / out_lo are not written); or,
+// after the trunk's last block, the heads' p1 | g1 | v1 convolution (entry_oc kJunctionHead, exit_o.y_dead: the
+// trunk is read, not stored). x / x_lo: the exit's split operand (rows of ldx); w: the compute-type conversion of
+// junction_pack_weights' layout of both filters (each [oc][ic]). The results equal the two separate split 1x1
+// convolutions' bit for bit.
+constexpr int kJunctionInner = 192, kJunctionOuter = 384, kJunctionHead = 96;
+void junction_pack_weights(const float* w_exit, const float* w_entry, int entry_oc, int prec, std::vector<float>& out);
 void launch_junction(int prec, const void* x, const void* x_lo, int ldx, const void* w, const ConvOut& exit_o,
-                     const ConvOut& entry_o, int B, hipStream_t s);
+                     const ConvOut& entry_o, int entry_oc, int B, hipStream_t s);
 // The launch's grid over M pixels, and the 48-pixel tile workgroup g computes (tiles past M exit at once).
 int junction_grid(int M);
 int junction_tile_of(int g);

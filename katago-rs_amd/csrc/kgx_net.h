@@ -129,7 +129,9 @@ class Net {
     int ldx = 0;
     std::shared_ptr<ConvOut> out;
   };
-  // Whether block b's exit and block `next`'s entry (over a trunk of c channels) run as a junction.
+  // Whether block b's exit (over a trunk of c channels) can start a junction, and whether it and block `next`'s entry
+  // run as one.
+  bool exit_fits(const BlockDesc& b, int c) const;
   bool junction_fits(const BlockDesc& b, const BlockDesc& next, int c) const;
   std::shared_ptr<ConvOut> emit_junction(const PendingExit& p, const ConvDesc& entry, const ConvOut& entry_o);
   void emit_attention(const BlockDesc& b, int depth);
@@ -159,6 +161,7 @@ class Net {
   std::vector<std::pair<void*, size_t>> zero_;           // workspace regions cleared before every eager forward
   ConvMode conv_mode_ = CONV_WINO4;
   bool junctions_ = true;  // nested-bottleneck junctions in one launch (KGX_JUNCTION=0: two launches)
+  bool head_junction_ = false;  // the trunk's last exit may join the heads' first convolution
   std::unique_ptr<PendingExit> pend_;
   int wino_tm_ = 4;
   int nin_ = 0, nglob_ = 0, nmeta_ = 0, row_len_ = 0;

@@ -173,33 +173,41 @@ void* Net::consume(int depth, const BNDesc& bn, int act, const void** lo) {
   return buf;
 }
 
+static bool is_1x1(const ConvDesc& d) { return d.ky == 1 && d.kx == 1 && d.dy == 1 && d.dx == 1; }
+
+bool Net::exit_fits(const BlockDesc& b, int c) const {
+  const ConvDesc& ex = b.final_conv;
+  return junctions_ && prec_ != PREC_F32 && conv_mode_ == CONV_IGEMM && is_1x1(ex) && c == kJunctionOuter &&
+         ex.ic == kJunctionInner && ex.oc == kJunctionOuter && b.regular.oc == kJunctionInner &&
+         ex.w.size() == (size_t)kJunctionInner * kJunctionOuter;
+}
+
 bool Net::junction_fits(const BlockDesc& b, const BlockDesc& next, int c) const {
-  auto is1x1 = [](const ConvDesc& d) { return d.ky == 1 && d.kx == 1 && d.dy == 1 && d.dx == 1; };
-  const ConvDesc &ex = b.final_conv, &en = next.regular;
-  return junctions_ && prec_ != PREC_F32 && conv_mode_ == CONV_IGEMM && next.kind == BLOCK_NBT && is1x1(ex) &&
-         is1x1(en) && c == kJunctionOuter && ex.ic == kJunctionInner && ex.oc == kJunctionOuter &&
-         en.ic == kJunctionOuter && en.oc == kJunctionInner && b.regular.oc == kJunctionInner &&
-         ex.w.size() == (size_t)kJunctionInner * kJunctionOuter && en.w.size() == ex.w.size();
+  const ConvDesc& en = next.regular;
+  return exit_fits(b, c) && next.kind == BLOCK_NBT && is_1x1(en) && en.ic == kJunctionOuter &&
+         en.oc == kJunctionInner && en.w.size() == (size_t)kJunctionInner * kJunctionOuter;
 }
 
 std::shared_ptr<ConvOut> Net::emit_junction(const PendingExit& p, const ConvDesc& entry, const ConvOut& entry_o) {
   std::vector<float> w;
-  junction_pack_weights(p.conv->w.data(), entry.w.data(), prec_, w);
+  const int eoc = entry.oc;
+  junction_pack_weights(p.conv->w.data(), entry.w.data(), eoc, prec_, w);
   const void* dW = upload_t(w);
   const std::shared_ptr<ConvOut> eo = p.out, no = std::make_shared<ConvOut>(entry_o);
   const int prec = prec_, ldx = p.ldx;
   const void *x = p.x, *x_lo = p.x_lo;
   const double ts = (double)tsize();
   Op op;
-  op.launch = [=](hipStream_t s, int B) { launch_junction(prec, x, x_lo, ldx, dW, *eo, *no, B, s); };
-  op.cls = "conv1x1_junction";
-  op.flops_row = 2.0 * HW * 2 * kJunctionInner * kJunctionOuter;
-  // The exit's split operand, the trunk read and written, the inner stream written (its emission is counted
-  // through `out`).
-  op.bytes_row = (double)HW * (2.0 * kJunctionInner * ts + 8.0 * kJunctionOuter + 4.0 * kJunctionInner);
-  op.bytes_fixed = 2.0 * 2 * kJunctionInner * kJunctionOuter * ts;
+  op.launch = [=](hipStream_t s, int B) { launch_junction(prec, x, x_lo, ldx, dW, *eo, *no, eoc, B, s); };
+  const bool head = eoc == kJunctionHead;
+  op.cls = head ? "head_junction" : "conv1x1_junction";
+  op.flops_row = 2.0 * HW * (kJunctionInner + eoc) * kJunctionOuter;
+  // The exit's split operand, the trunk read and (but where it ends, before the heads) written, the entry's float
+  // output written (its emission is counted through `out`).
+  op.bytes_row = (double)HW * (2.0 * kJunctionInner * ts + (head ? 4.0 : 8.0) * kJunctionOuter + 4.0 * eoc);
+  op.bytes_fixed = 2.0 * (kJunctionInner + eoc) * kJunctionOuter * ts;
   op.out = no;
-  op.out_c = kJunctionInner;
+  op.out_c = eoc;
   ops_.push_back(op);
   return no;
 }
@@ -749,7 +757,8 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
         const void* a2_lo = nullptr;
         const void* a2 = consume(depth + 1, b.mid_bn, b.mid_act, split_1x1(b.final_conv, ci, res) ? &a2_lo : nullptr);
         if (last) last->y_dead = true;
-        if (a2_lo && bi + 1 < blocks.size() && junction_fits(b, blocks[bi + 1], c)) {
+        const bool to_heads = depth == 0 && bi + 1 == blocks.size() && head_junction_ && exit_fits(b, c);
+        if (a2_lo && ((bi + 1 < blocks.size() && junction_fits(b, blocks[bi + 1], c)) || to_heads)) {
           // Held back: the next block's entry convolution joins it (its consume attaches this emission).
           if (pend_) throw std::runtime_error("internal: two exits held back");
           pend_.reset(new PendingExit{&b.final_conv, a2, a2_lo, ci, std::make_shared<ConvOut>(res)});
@@ -868,8 +877,11 @@ void Net::build(const ModelDesc& m) {
   ss_[0].producer = emit_conv(m.stem, d_bin_, 0, true, stem_out);
 
   // --- Blocks. ---
+  // The trunk's last exit may join the heads' p1 | g1 | v1 convolution in one junction launch (16-bit handles, a
+  // batch-norm tip, 96 head channels).
+  head_junction_ = m.trunk_norm_kind == 0 && m.p1.oc + m.g1.oc + m.v1.oc == kJunctionHead && is_1x1(m.p1) &&
+                   is_1x1(m.g1) && is_1x1(m.v1) && m.p1.ic == C && m.g1.ic == C && m.v1.ic == C;
   emit_stack(m.blocks, 0);
-  if (pend_) throw std::runtime_error("internal: an exit convolution was held back for no entry");
 
   // --- Trunk tip and heads (bin2onnx.py:1489-1531). ---
   for (const ConvDesc* hc : {&m.p1, &m.g1, &m.v1, &m.p2, &m.own})
@@ -900,8 +912,16 @@ void Net::build(const ModelDesc& m) {
     const void* tip_lo = nullptr;
     const void* tip = consume(0, m.tip_bn, m.tip_act, &tip_lo);
     last->y_dead = true;
-    emit_conv(hconv, tip, C, false, hout, tip_lo);
-    ops_.back().cls = "head_1x1";
+    if (pend_) {
+      // The trunk's last exit was held back for this convolution: one junction launch for both.
+      if (pend_->out != last || !tip_lo || hconv.oc != kJunctionHead)
+        throw std::runtime_error("internal: head junction does not consume the held exit");
+      emit_junction(*pend_, hconv, hout);
+      pend_.reset();
+    } else {
+      emit_conv(hconv, tip, C, false, hout, tip_lo);
+      ops_.back().cls = "head_1x1";
+    }
   } else if (m.trunk_norm_kind == 0) {
     tip_pro = bn_pro(m.tip_bn, m.tip_act);
   } else {
@@ -919,6 +939,7 @@ void Net::build(const ModelDesc& m) {
     ops_.push_back(op);
     head_in = tip;
   }
+  if (pend_) throw std::runtime_error("internal: an exit convolution was held back for no entry");
   if (!(m.trunk_norm_kind == 0 && split_1x1(hconv, C, hout))) {
     // Float operands: float handles, and the trunk-tip RMSNorm's output.
     const float* dWh = upload_f(hconv.w);

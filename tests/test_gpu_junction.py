@@ -1,11 +1,12 @@
 """The nested-bottleneck junction (one block's exit 1x1 convolution, 192 -> 384 into the trunk, and the next block's
-entry 1x1, 384 -> 192, in one launch: launch_junction, kgx_junction.hip) through the C ABI:
+entry 1x1, 384 -> 192, in one launch: launch_junction, kgx_junction.hip), and the head junction (the last block's
+exit and the heads' p1 | g1 | v1 1x1, 384 -> 96, where the trunk ends and is not written), through the C ABI:
 - bit for bit equal to the two separate split-operand launches it replaces (KGX_JUNCTION=0 plans those), on f16 and
   bf16 handles, at a ragged batch (tiles past the last pixel) and at batch 32, with gpool inner blocks between, for
   mish nets and (the run-time activation kernel) ReLU nets;
 - the junction net against the float64 oracle and the 16-bit network (the bounds of test_gpu_parity.py);
-- the planning: a net of n nested blocks over 384 / 192 channels runs n - 1 junctions and no separate entry or exit
-  1x1 between them."""
+- the planning: a net of n nested blocks over 384 / 192 channels runs n - 1 junctions, one head junction and no
+  separate 1x1 but the first block's entry."""
 
 import numpy as np
 import pytest
@@ -50,10 +51,12 @@ def test_junction_equals_the_two_separate_launches(kgx, synth, monkeypatch, prec
     fused, pf, _ = run(kgx, mb, batch, prec, sp, gl, monkeypatch, True)
     sep, ps, _ = run(kgx, mb, batch, prec, sp, gl, monkeypatch, False)
     assert pf["conv1x1_junction"]["launches"] == 3 and "conv1x1_junction" not in ps
-    # the separate plan's 1x1s: four entries and four exits; the junction plan keeps the first entry and the last exit
+    assert pf["head_junction"]["launches"] == 1 and "head_1x1" not in pf
+    assert ps["head_1x1"]["launches"] == 1 and "head_junction" not in ps
+    # the separate plan's 1x1s: four entries and four exits; the junction plan keeps only the first entry
     sep_1x1 = sum(v["launches"] for k, v in ps.items() if k.startswith("conv1x1_split"))
     fused_1x1 = sum(v["launches"] for k, v in pf.items() if k.startswith("conv1x1_split"))
-    assert sep_1x1 == 8 and fused_1x1 == 2, (ps.keys(), pf.keys())
+    assert sep_1x1 == 8 and fused_1x1 == 1, (ps.keys(), pf.keys())
     assert np.all(np.isfinite(fused))
     assert np.array_equal(fused, sep), f"{prec} batch {batch}: max diff {np.abs(fused - sep).max():.3e}"
 
@@ -65,6 +68,21 @@ def test_junction_net_matches_oracle(kgx, synth, oracle, monkeypatch, prec):
     rows = [0, 1, 2, 3]
     sp, gl, _ = synth.make_inputs(6, 13, board_sizes=[19, 13, 9, 19, 19, 5])
     out, prof, net = run(kgx, mb, 6, prec, sp, gl, monkeypatch, True)
-    assert prof["conv1x1_junction"]["launches"] == 2
+    assert prof["conv1x1_junction"]["launches"] == 2 and prof["head_junction"]["launches"] == 1
     ref = oracle.Model(mb).forward(sp[rows], gl[rows])
     check(out[rows], ref, net.P, net.S, prec, f"junction net", emulated(oracle, mb, prec, sp[rows], gl[rows]))
+
+
+def test_head_junction_only_for_96_head_channels(kgx, synth, monkeypatch):
+    """Heads of 64 + 32 + 32 channels keep their own 1x1 launch after the last exit, with the same bits as the
+    separate plan."""
+    print("junction net with 128 head channels", flush=True)
+    arch = junction_arch(synth, 2)
+    arch.p1_c = 64
+    mb = synth.write_model(arch, 5)
+    sp, gl, _ = synth.make_inputs(5, 3, board_sizes=[19, 13, 19, 9, 19])
+    fused, pf, _ = run(kgx, mb, 5, "f16", sp, gl, monkeypatch, True)
+    sep, _, _ = run(kgx, mb, 5, "f16", sp, gl, monkeypatch, False)
+    assert pf["conv1x1_junction"]["launches"] == 1 and "head_junction" not in pf and pf["head_1x1"]["launches"] == 1
+    assert sum(v["launches"] for k, v in pf.items() if k.startswith("conv1x1_split")) == 2
+    assert np.array_equal(fused, sep)
