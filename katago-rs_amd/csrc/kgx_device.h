@@ -181,6 +181,21 @@ __device__ __forceinline__ void lds_load16(const void* base, int nbytes, void* l
                                            (lds_ptr_t)lds, 16, off, 0, 0, 0);
 }
 
+// Touches this workgroup's share of the 128-byte lines of [p, p + nbytes), so that they are in its XCD's L2 when the
+// next launch reads them: workgroup g runs on XCD g mod 8, and the n workgroups of that XCD take lines s + n t (s =
+// g / 8) for thread t, one 4-byte buffer load each (so a launch covers up to n x threads lines per XCD; offsets past
+// the range read as zero without a memory access, so a null range touches nothing). The kernel keeps the returned
+// value live up to its end (l2_touch_keep), which it reaches on every path: the load is not dropped, and no wait
+// for it comes before that point.
+__device__ __forceinline__ int l2_touch(const char* p, int nbytes, int tid) {
+  const int g = blockIdx.x, n = ((int)gridDim.x - (g & 7) + 7) >> 3;
+  const int v = __builtin_amdgcn_raw_buffer_load_b32(__builtin_amdgcn_make_buffer_rsrc((void*)p, 0, nbytes, 0x00020000),
+                                                     ((g >> 3) + n * tid) * 128, 0, 0);
+  asm volatile("" ::: "memory");  // issued here, not next to its use
+  return v;
+}
+__device__ __forceinline__ void l2_touch_keep(int v) { asm volatile("" ::"v"(v)); }
+
 // Winograd F(TM x TM, 3x3) geometry on the 19x19 board.
 template <int TM>
 struct Wino {

@@ -115,7 +115,10 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   const int wm = wl / WN, wn = wl % WN;
   int mt, nt;
   igemm_tile_of(blockIdx.x, (OC + BN - 1) / BN, C::PAIRS, mt, nt);
-  if (mt * BM >= M) return;
+  if (mt * BM >= M) {  // an idle workgroup still touches its share of the next launch's weights
+    l2_touch_keep(l2_touch(o.pf, o.pf_bytes, threadIdx.x));
+    return;
+  }
   const int n0 = nt * BN, m0 = mt * BM;
   const int r16 = lane & 15, g4 = lane >> 4;
 
@@ -459,7 +462,18 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
   // (Not for the 64-column 3x3 without partials: at 256 registers with its early residual loads, it spills.)
   constexpr bool SPEC = !(C::KS == 3 && C::BN == 64 && !POOL);
   const int sfl = store_flags(o);
-  switch (!SPEC ? -1 : !(sfl & SF_EMIT) ? sfl : o.emit.act == ACT_MISH ? sfl : -1) {
+  const int scase = !SPEC ? -1 : !(sfl & SF_EMIT) ? sfl : o.emit.act == ACT_MISH ? sfl : -1;
+  // The next launch's weights into this XCD's L2 while the epilogue runs. Issued after every load that the stores
+  // wait for, and only where the stores load nothing more (the specialized cases other than the column bias's),
+  // since a wait for a later load would include it.
+  bool quiet = false;
+  switch (scase) {
+    case SF_Y: case SF_EMIT: case SF_Y | SF_EMIT: case SF_Y | SF_ACC | SF_EMIT: case SF_Y | SF_ACC | SF_YDEAD | SF_EMIT:
+    case SF_Y | SF_ACC | SF_EMIT | SF_LO: case SF_Y | SF_ACC | SF_YDEAD | SF_EMIT | SF_LO: quiet = true; break;
+    default: break;
+  }
+  const int pfv = l2_touch(o.pf, quiet ? o.pf_bytes : 0, tid);
+  switch (scase) {
     // a global-pooling block's first conv (pooling partials); a block's first conv; a nested block's entry 1x1;
     // a block's last conv, its stream's last, into a split 1x1
     case SF_Y: store_rows(std::integral_constant<int, ACT_ID>{}, std::integral_constant<int, SF_Y>{}); break;
@@ -582,6 +596,7 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
       }
     }
   }
+  l2_touch_keep(pfv);
 }
 
 // Configurations (measured at batch 32, 192 channels): 3x3 with 192 pixels x 48 channels per workgroup (a

@@ -88,7 +88,10 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
   const int tid = threadIdx.x, lane = tid & 63, wv = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int r16 = lane & 15, g4 = lane >> 4;
   const int m0 = junction_tile(blockIdx.x) * JR;
-  if (m0 >= M) return;
+  if (m0 >= M) {  // an idle workgroup still touches its share of the next launch's weights
+    l2_touch_keep(l2_touch(no.pf, no.pf_bytes, tid));
+    return;
+  }
 
   auto mfma = [](const frag_t& a, const frag_t& b, floatx4 c) {
     if constexpr (std::is_same<T, f16>::value) return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -308,13 +311,20 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
 #pragma unroll
       for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[p % NS][j][0], acc2[i][j]);
   };
+  int pfv;
+  const bool fast = fl2 == (SF_Y | SF_EMIT) && no.emit.act == ACT_MISH;  // the entry epilogue's path
   auto run = [&](auto act_c) {
 #pragma unroll
     for (int e = 0; e < E1; e++) epi1(act_c, 0, e);
     lds_barrier();
 #pragma unroll
     for (int b = 0; b < 3; b++) {
-      if (b == 2) load_epi2();
+      if (b == 2) {
+        load_epi2();
+        // The next launch's weights into this XCD's L2 during the last steps (after every load this kernel waits
+        // for, so that no wait includes it; the general epilogue path loads more, and a wait for those would).
+        pfv = l2_touch(no.pf, fast ? no.pf_bytes : 0, tid);
+      }
       load_a2(0, 2 * b);
       __builtin_amdgcn_sched_barrier(0);
       mma2(2 * b);
@@ -349,7 +359,6 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
 
   // Entry epilogue: chain 0 plus chain 1, then the convolution's outputs (the inner stream and its consumer's
   // activation) as the separate kernel stores them. At the end of the kernel, so these stores may branch.
-  const bool fast = fl2 == (SF_Y | SF_EMIT) && no.emit.act == ACT_MISH;
 #pragma unroll
   for (int e = 0; e < E2; e++) {
     const int p = p2 + R2 * e, m = m0 + p;
@@ -370,6 +379,7 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
       }
     }
   }
+  l2_touch_keep(pfv);
 }
 
 }  // namespace

@@ -75,6 +75,10 @@ struct ConvOut {
   void* yt = nullptr; int ldyt = 0;
   Emit emit;
   PoolPart pool;  // implicit-GEMM convolutions only
+  // The weights of the launch that follows (pf_bytes bytes; null: none), which the implicit-GEMM and junction
+  // kernels touch into their XCDs' L2 during their epilogue, one 4-byte load per 128-byte line, so that the next
+  // launch reads them from L2 instead of MALL.
+  const char* pf = nullptr; int pf_bytes = 0;
 };
 
 // Winograd F(tm x tm, 3x3), tm = 4 (36 tile points, 25 tiles per board) or 2 (16 points, 100 tiles).

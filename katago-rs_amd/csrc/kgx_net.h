@@ -40,6 +40,10 @@ struct Op {
   // activation of `out_c` channels per point is counted when present.
   std::shared_ptr<ConvOut> out;
   int out_c = 0;
+  // Weights that every XCD reads (an implicit-GEMM convolution's or a junction's), and the output descriptor through
+  // which the op's kernel touches the next such op's weights into L2 (ConvOut::pf).
+  const void* w = nullptr; size_t w_bytes = 0;
+  std::shared_ptr<ConvOut> pf_sink;
 };
 
 // Planning state of one residual stream (the trunk, or the inner stream of a nested bottleneck block): its float
@@ -162,6 +166,7 @@ class Net {
   ConvMode conv_mode_ = CONV_WINO4;
   bool junctions_ = true;  // nested-bottleneck junctions in one launch (KGX_JUNCTION=0: two launches)
   bool head_junction_ = false;  // the trunk's last exit may join the heads' first convolution
+  bool l2_prefetch_ = true;  // kernels touch the next op's weights into L2 (KGX_L2_PREFETCH=0: off)
   std::unique_ptr<PendingExit> pend_;
   int wino_tm_ = 4;
   int nin_ = 0, nglob_ = 0, nmeta_ = 0, row_len_ = 0;

@@ -51,6 +51,8 @@ Net::Net(const ModelDesc& m, int device, int max_batch, int prec) : device_(devi
   wino_tm_ = conv_mode_ == CONV_WINO4 ? 4 : 2;
   // Nested-bottleneck junctions in one launch; KGX_JUNCTION=0 plans the two convolutions separately.
   if (const char* e = std::getenv("KGX_JUNCTION")) junctions_ = std::string(e) != "0";
+  // Each convolution touches the next one's weights into L2 during its epilogue; KGX_L2_PREFETCH=0 turns it off.
+  if (const char* e = std::getenv("KGX_L2_PREFETCH")) l2_prefetch_ = std::string(e) != "0";
   build(m);
 }
 
@@ -61,6 +63,7 @@ Net::Net(const ModelDesc& m, const Net& primary, int max_batch, char* ws_base, s
   conv_mode_ = primary.conv_mode_;
   wino_tm_ = primary.wino_tm_;
   junctions_ = primary.junctions_;
+  l2_prefetch_ = primary.l2_prefetch_;
   build(m);
   if (upload_next_ != primary.uploads_.size()) throw std::runtime_error("internal: workspace plan weights differ");
 }
@@ -208,6 +211,9 @@ std::shared_ptr<ConvOut> Net::emit_junction(const PendingExit& p, const ConvDesc
   op.bytes_fixed = 2.0 * (kJunctionInner + eoc) * kJunctionOuter * ts;
   op.out = no;
   op.out_c = eoc;
+  op.w = dW;
+  op.w_bytes = w.size() * tsize();
+  op.pf_sink = no;
   ops_.push_back(op);
   return no;
 }
@@ -312,6 +318,9 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
     op.bytes_fixed = (double)taps * ic * oc * ts * (split ? 2 : 1);
     op.out = out;
     op.out_c = oc;
+    op.w = dW;
+    op.w_bytes = w.size() * tsize();
+    op.pf_sink = out;
     ops_.push_back(op);
     return out;
   }
@@ -1064,6 +1073,18 @@ void Net::build(const ModelDesc& m) {
     wino_m_ = alloc_f(wino_m_elems_);
     if (primary_) zero_.emplace_back(wino_m_, wino_m_elems_ * 4);
     else KGX_HIP(hipMemset(wino_m_, 0, wino_m_elems_ * 4));
+  }
+  // Each kernel that can touches the weights of the next op that has weights (at most two ops ahead) into L2.
+  if (l2_prefetch_) {
+    for (size_t i = 0; i < ops_.size(); i++) {
+      if (!ops_[i].pf_sink) continue;
+      for (size_t j = i + 1; j < ops_.size() && j <= i + 1; j++) {
+        if (!ops_[j].w || ops_[j].w_bytes > (size_t)INT32_MAX) continue;
+        ops_[i].pf_sink->pf = (const char*)ops_[j].w;
+        ops_[i].pf_sink->pf_bytes = (int)ops_[j].w_bytes;
+        break;
+      }
+    }
   }
   if (!primary_) KGX_HIP(hipDeviceSynchronize());
 }

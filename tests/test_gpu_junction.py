@@ -86,3 +86,15 @@ def test_head_junction_only_for_96_head_channels(kgx, synth, monkeypatch):
     assert pf["conv1x1_junction"]["launches"] == 1 and "head_junction" not in pf and pf["head_1x1"]["launches"] == 1
     assert sum(v["launches"] for k, v in pf.items() if k.startswith("conv1x1_split")) == 2
     assert np.array_equal(fused, sep)
+
+
+def test_l2_weight_touch_changes_no_bits(kgx, synth, monkeypatch):
+    """Kernels touch the next convolution's weights into L2 during their epilogue (ConvOut::pf); with the touch
+    off (KGX_L2_PREFETCH=0) the outputs are the same bits."""
+    print("junction net with and without the L2 weight touch", flush=True)
+    mb = synth.write_model(junction_arch(synth, 3), 6)
+    sp, gl, _ = synth.make_inputs(9, 4, board_sizes=[19, 13, 19, 9, 19])
+    on, _, _ = run(kgx, mb, 9, "f16", sp, gl, monkeypatch, True)
+    monkeypatch.setenv("KGX_L2_PREFETCH", "0")
+    off, _, _ = run(kgx, mb, 9, "f16", sp, gl, monkeypatch, True)
+    assert np.array_equal(on, off)
