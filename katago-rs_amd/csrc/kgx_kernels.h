@@ -282,6 +282,28 @@ struct RowProgs {
 };
 void launch_row_prog(const RowProg& p, int B, hipStream_t s);
 void launch_row_progs(const RowProgs& ps, int B, hipStream_t s);
+// A global-pooling block's mid activation per 192-pixel tile, with 16-bit compute types: workgroup (tile t, share
+// s) runs on XCD t mod 8 (the XCD of the convolutions' tile t), and for each batch row b that the tile touches (at
+// most two) combines the gpool branch's pooled features from the producer's partials (PoolPart, 192-pixel tiles:
+// mean, mean * s1[b], max), multiplies them by W [3 cg][cr] for its `share` output channels (the row's per-channel
+// bias), and emits out[m][c] = T(act((x[m][c] + bias_row[c]) * scale[c] + bias[c]) * mask[m]) for the tile's pixels
+// and its channels. The matmul sums the same 16 K slices in the same order as the row program (run_row_prog with
+// output splits), so both give the same bits. Then it touches the next op's weights into L2 (pf).
+struct GpoolTile {
+  const long long* psum = nullptr; const float* pmax = nullptr; int cg = 0;
+  const float* area = nullptr; const float* s1 = nullptr;
+  const float* W = nullptr; int cr = 0; int share = 0;
+  const float* x = nullptr; int ldx = 0;
+  const float* scale = nullptr; const float* bias = nullptr; int act = ACT_ID;
+  const float* mask = nullptr;
+  void* out = nullptr; int ldo = 0; int prec = PREC_F16;
+  const char* pf = nullptr; int pf_bytes = 0;
+};
+// The output share gpool_tile_launch uses for cr channels (0: none fits: 64 <= 3 cg <= 384 and cr / 8 a multiple
+// of 8 up to 40 are needed).
+int gpool_tile_share(int cg, int cr);
+void launch_gpool_tile(const GpoolTile& a, int B, hipStream_t s);
+
 // Gives each matmul of `p` whose weights fit a staged copy in LDS (after the program's features), as long as the
 // program's LDS stays within `max_bytes`.
 void row_prog_stage_weights(RowProg& p, size_t max_bytes);

@@ -582,6 +582,162 @@ void launch_row_prog(const RowProg& p, int B, hipStream_t s) {
 }
 
 // ---------------------------------------------------------------------------------------------------------
+// Global-pooling block's mid activation per 192-pixel tile (GpoolTile)
+// ---------------------------------------------------------------------------------------------------------
+constexpr int GT_NT = 256, GT_BM = 192, GT_KS = 16, GT_RV = 4, GT_RW = 12;
+
+int gpool_tile_share(int cg, int cr) {
+  const int share = cr / 8;
+  return cr % 64 == 0 && share <= 40 && 3 * cg >= 64 && 3 * cg <= 384 && 3 * cg * share <= 4 * GT_RW * GT_NT ? share
+                                                                                                        : 0;
+}
+
+template <typename T, int ACT>
+__global__ __launch_bounds__(GT_NT) void gpool_tile_kernel(GpoolTile a, int M) {
+  extern __shared__ float lds[];
+  const int tid = threadIdx.x, g = blockIdx.x, SH = a.share, S = a.cr / SH, IC = 3 * a.cg, cg = a.cg;
+  const int j = g >> 3, t = (g & 7) + 8 * (j / S), c0 = (j % S) * SH;
+  const int m0 = t * GT_BM;
+  if (m0 >= M) {
+    l2_touch_keep(l2_touch(a.pf, a.pf_bytes, tid));
+    return;
+  }
+  const int b0 = m0 / HW, nrow = (min(m0 + GT_BM, M) - 1) / HW - b0 + 1;  // batch rows touched: 1 or 2
+  // LDS: W share [IC][SH], features [2][IC], matmul slices [2][GT_KS][SH], row biases [2][SH], scale and bias
+  // [2][SH], mask [GT_BM].
+  float* const wl = lds;
+  float* const feat = wl + IC * SH;
+  float* const part = feat + 2 * IC;
+  float* const rb = part + 2 * GT_KS * SH;
+  float* const esb = rb + 2 * SH;
+  float* const mk = esb + 2 * SH;
+  // Every load first: this thread's x vectors (8 channels each), the pooled partials of (row, channel), the mask,
+  // the weight share and the batch-norm share.
+  const int n8 = SH / 8, nv = GT_BM * n8;
+  floatx4 ex[GT_RV][2];
+#pragma unroll
+  for (int k = 0; k < GT_RV; k++) {
+    const int v = tid + k * GT_NT, p = v / n8, m = min(m0 + p, M - 1);
+    if (v < nv) {
+      const float* xp = a.x + (size_t)m * a.ldx + c0 + (v - p * n8) * 8;
+      ex[k][0] = *(const floatx4*)xp;
+      ex[k][1] = *(const floatx4*)(xp + 4);
+    }
+  }
+  const int pr = tid / cg, pc = tid - pr * cg;
+  long long pps[3] = {0, 0, 0};
+  float ppm[3] = {-FLT_MAX, -FLT_MAX, -FLT_MAX}, area = 1.f, s1 = 0.f;
+  if (pr < nrow) {
+    const int b = b0 + pr, t0 = b * HW / GT_BM, t1 = (b * HW + HW - 1) / GT_BM;
+#pragma unroll
+    for (int q = 0; q < 3; q++) {
+      const int tq = t0 + q;
+      if (tq <= t1) {
+        const size_t at = (size_t)(tq * 2 + (tq * GT_BM / HW == b ? 0 : 1)) * cg + pc;
+        pps[q] = a.psum[at];
+        ppm[q] = a.pmax[at];
+      }
+    }
+    area = a.area[b];
+    s1 = a.s1[b];
+  }
+  const float mkv = tid < GT_BM && m0 + tid < M ? a.mask[m0 + tid] : 0.f;
+  const int w4 = IC * SH / 4, q4 = SH / 4;
+  floatx4 wr[GT_RW];
+#pragma unroll
+  for (int k = 0; k < GT_RW; k++) {
+    const int v = tid + k * GT_NT;
+    if (v < w4) {
+      const int i = v / q4;
+      wr[k] = *(const floatx4*)(a.W + (size_t)i * a.cr + c0 + (v - i * q4) * 4);
+    }
+  }
+  const float esv = tid < 2 * SH ? (tid < SH ? a.scale[c0 + tid] : a.bias[c0 + tid - SH]) : 0.f;
+#pragma unroll
+  for (int k = 0; k < GT_RW; k++) {
+    const int v = tid + k * GT_NT;
+    if (v < w4) *(floatx4*)(wl + 4 * v) = wr[k];
+  }
+  if (tid < GT_BM) mk[tid] = mkv;
+  if (tid < 2 * SH) esb[tid] = esv;
+  // The row's pooled features (as the row program forms them from partials).
+  if (pr < nrow) {
+    const float sum = (float)((double)(pps[0] + pps[1] + pps[2]) / (double)kPoolFix);
+    const float mx = fmaxf(fmaxf(ppm[0], ppm[1]), ppm[2]);
+    const float mean = sum / area;
+    feat[pr * IC + pc] = mean;
+    feat[pr * IC + cg + pc] = mean * s1;
+    feat[pr * IC + 2 * cg + pc] = mx;
+  }
+  __syncthreads();
+  // The matmul: slice ks of output o of row r sums inputs ks, ks + 16, ... in order; the row bias then sums the
+  // slices in order (row_mm's order with one 64-output chunk over 16 waves).
+  for (int task = tid; task < nrow * SH * GT_KS; task += GT_NT) {
+    const int r = task / (SH * GT_KS), rem = task - r * SH * GT_KS, ks = rem / SH, o = rem - ks * SH;
+    const float* fr = feat + r * IC;
+    float acc = 0.f;
+    for (int i = ks; i < IC; i += GT_KS) acc += fr[i] * wl[i * SH + o];
+    part[(r * GT_KS + ks) * SH + o] = acc;
+  }
+  __syncthreads();
+  if (tid < nrow * SH) {
+    const int r = tid / SH, o = tid - r * SH;
+    float v = 0.f;
+    for (int k = 0; k < GT_KS; k++) v += part[(r * GT_KS + k) * SH + o];
+    rb[r * SH + o] = act_rt(v + 0.f, ACT_ID);
+  }
+  __syncthreads();
+  const int pfv = l2_touch(a.pf, a.pf_bytes, tid);
+#pragma unroll
+  for (int k = 0; k < GT_RV; k++) {
+    const int v = tid + k * GT_NT, p = v / n8, m = m0 + p;
+    if (v < nv && m < M) {
+      const int cl = (v - p * n8) * 8, r = m / HW - b0;
+      const float mm = mk[p];
+      float tv[8];
+#pragma unroll
+      for (int e = 0; e < 8; e++) tv[e] = (ex[k][e >> 2][e & 3] + rb[r * SH + cl + e]) * esb[cl + e] + esb[SH + cl + e];
+#pragma unroll
+      for (int e = 0; e < 8; e++) tv[e] = ACT == ACT_ID ? tv[e] * mm : act_f<ACT>(tv[e]) * mm;
+      u32x4 w;
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const T l = to_t<T>(tv[2 * e]), h = to_t<T>(tv[2 * e + 1]);
+        w[e] = __builtin_bit_cast(unsigned short, l) | ((unsigned)__builtin_bit_cast(unsigned short, h) << 16);
+      }
+      *(u32x4*)((unsigned short*)a.out + (size_t)m * a.ldo + c0 + cl) = w;
+    }
+  }
+  l2_touch_keep(pfv);
+}
+
+void launch_gpool_tile(const GpoolTile& a, int B, hipStream_t s) {
+  const int M = B * HW;
+  if (M <= 0) return;
+  if (a.share != gpool_tile_share(a.cg, a.cr) || !a.share || !a.psum || !a.pmax || !a.area || !a.s1 || !a.W ||
+      !a.x || !a.scale || !a.bias || !a.mask || !a.out || a.ldx % 4 || a.ldo % 8 || a.x == nullptr ||
+      ((uintptr_t)a.x | (uintptr_t)a.out | (uintptr_t)a.W) % 16 || (a.prec != PREC_F16 && a.prec != PREC_BF16))
+    throw std::runtime_error("gpool tile: unsupported layout");
+  const int T = (M + GT_BM - 1) / GT_BM, S = a.cr / a.share, IC = 3 * a.cg;
+  const size_t lds = ((size_t)IC * a.share + 2 * IC + 2 * GT_KS * a.share + 4 * a.share + GT_BM) * sizeof(float);
+  const dim3 grid(8 * ((T + 7) / 8) * S);
+  auto go = [&](auto t, auto act) {
+    launch_k(gpool_tile_kernel<decltype(t), decltype(act)::value>, grid, GT_NT, lds, s, a, M);
+  };
+  auto by_act = [&](auto t) {
+    switch (a.act) {
+      case ACT_RELU: go(t, std::integral_constant<int, ACT_RELU>{}); break;
+      case ACT_MISH: go(t, std::integral_constant<int, ACT_MISH>{}); break;
+      case ACT_SILU: go(t, std::integral_constant<int, ACT_SILU>{}); break;
+      default: go(t, std::integral_constant<int, ACT_ID>{}); break;
+    }
+  };
+  if (a.prec == PREC_F16) by_act(f16());
+  else by_act(bf16());
+  KGX_CHECK_LAUNCH();
+}
+
+// ---------------------------------------------------------------------------------------------------------
 // Head: policy p2 conv and ownership conv per board point, written into the readback rows
 // ---------------------------------------------------------------------------------------------------------
 // Sixteen lanes per board point: lane l of a point takes channels l, l + 16, ... of p1 and of v1 (at most 16 HK of

@@ -167,6 +167,7 @@ class Net {
   bool junctions_ = true;  // nested-bottleneck junctions in one launch (KGX_JUNCTION=0: two launches)
   bool head_junction_ = false;  // the trunk's last exit may join the heads' first convolution
   bool l2_prefetch_ = true;  // kernels touch the next op's weights into L2 (KGX_L2_PREFETCH=0: off)
+  bool gpool_tile_ = true;   // gpool blocks' mid activation per pixel tile (KGX_GPOOL_TILE=0: per row)
   std::unique_ptr<PendingExit> pend_;
   int wino_tm_ = 4;
   int nin_ = 0, nglob_ = 0, nmeta_ = 0, row_len_ = 0;

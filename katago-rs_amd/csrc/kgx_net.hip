@@ -53,6 +53,8 @@ Net::Net(const ModelDesc& m, int device, int max_batch, int prec) : device_(devi
   if (const char* e = std::getenv("KGX_JUNCTION")) junctions_ = std::string(e) != "0";
   // Each convolution touches the next one's weights into L2 during its epilogue; KGX_L2_PREFETCH=0 turns it off.
   if (const char* e = std::getenv("KGX_L2_PREFETCH")) l2_prefetch_ = std::string(e) != "0";
+  // A global-pooling block's mid activation per pixel tile; KGX_GPOOL_TILE=0 plans the per-row program instead.
+  if (const char* e = std::getenv("KGX_GPOOL_TILE")) gpool_tile_ = std::string(e) != "0";
   build(m);
 }
 
@@ -64,6 +66,7 @@ Net::Net(const ModelDesc& m, const Net& primary, int max_batch, char* ws_base, s
   wino_tm_ = primary.wino_tm_;
   junctions_ = primary.junctions_;
   l2_prefetch_ = primary.l2_prefetch_;
+  gpool_tile_ = primary.gpool_tile_;
   build(m);
   if (upload_next_ != primary.uploads_.size()) throw std::runtime_error("internal: workspace plan weights differ");
 }
@@ -718,6 +721,33 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
             rp.mm[0].w4 = 3 * cg * share / 4;
             rp.lds_floats = woff + 3 * cg * share;
           }
+        }
+        const int gts = gpool_tile_share(cg, cr);
+        if (fuse && psum && gts > 0 && gpool_tile_) {
+          // The same arithmetic per 192-pixel tile on the convolutions' XCDs (GpoolTile): a workgroup reads the
+          // x rows and writes the emission where the convolutions before and after it write and read them.
+          GpoolTile gt;
+          gt.psum = psum; gt.pmax = pmax; gt.cg = cg; gt.area = area_; gt.s1 = s1_;
+          gt.W = rp.mm[0].W; gt.cr = cr; gt.share = gts;
+          gt.x = tmp; gt.ldx = ct; gt.scale = me.scale; gt.bias = me.bias; gt.act = me.act; gt.mask = mask_;
+          gt.out = me.out; gt.ldo = me.ld; gt.prec = prec;
+          const std::shared_ptr<ConvOut> sink = std::make_shared<ConvOut>();  // the next op's weights (pf)
+          Op op;
+          op.launch = [=](hipStream_t s, int B) {
+            GpoolTile g = gt;
+            g.pf = sink->pf;
+            g.pf_bytes = sink->pf_bytes;
+            launch_gpool_tile(g, B, s);
+          };
+          op.cls = "gpool_tile";
+          op.bytes_row = (double)HW * cr * (4 + tsize());
+          op.flops_row = 2.0 * 3 * cg * cr;
+          op.w = gt.W;
+          op.w_bytes = (size_t)3 * cg * cr * sizeof(float);
+          op.pf_sink = sink;
+          ops_.push_back(op);
+          ss_[depth].producer = emit_conv(b.final_conv, mid_, cr, false, res);
+          break;
         }
         Op pool;
         pool.launch = [=](hipStream_t s, int B) { launch_row_prog(rp, B, s); };
