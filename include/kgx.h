@@ -303,6 +303,17 @@ int kg_conv_weight_chunk(int row, int chunk);
  * `workgroup` computes (-1 when it exits at once). No counterpart in the reference: the index map its kernel uses,
  * for host-side checks. */
 int kg_junction_tile_of(int pixels, int workgroup, int* grid, int* tile);
+/* The gpool blocks' tile launch (a global-pooling block's mid activation per 192-pixel tile: pooled features,
+ * row-bias matmul, emission) over `pixels` pixels for a block of gpool_channels pooled and regular_channels
+ * regular channels: its workgroup count, the 192-pixel tile of workgroup `workgroup` (-1 when it exits at once) and
+ * the regular channels it emits [first_channel, first_channel + channels). No counterpart in the reference: the
+ * index map its kernel uses, for host-side checks. */
+int kg_gpool_tile_of(int pixels, int gpool_channels, int regular_channels, int workgroup, int* grid, int* tile,
+                     int* first_channel, int* channels);
+/* The 128-byte line (of the next op's weights) that thread `thread` of workgroup `workgroup` of a `grid`-workgroup
+ * launch touches into its XCD's L2 (workgroup g runs on XCD g mod 8; lines past the weights are not read). No
+ * counterpart in the reference: the index map the kernels use, for host-side checks. */
+int kg_l2_touch_line(int grid, int workgroup, int thread, int* line);
 
 #ifdef __cplusplus
 }

@@ -37,7 +37,7 @@ EXPORTS = [
     "kg_get_output", "kg_profile_enable", "kg_profile_reset", "kg_profile_read",
     "kg_model_version_features", "kg_meta_encoder_channels", "kg_copy_outputs", "kg_run_static",
     "kg_get_output_async", "kg_wait", "kg_get_output_eval", "kg_post_outputs",
-    "kg_conv_geometry", "kg_conv_tile_of", "kg_conv_weight_load", "kg_conv_weight_chunk", "kg_junction_tile_of",
+    "kg_conv_geometry", "kg_conv_tile_of", "kg_conv_weight_load", "kg_conv_weight_chunk", "kg_junction_tile_of", "kg_gpool_tile_of", "kg_l2_touch_line",
     "kg_featurize", "kg_featurize_rows", "kg_evaluate_positions",
 ]
 # Completion callback of kg_get_output_async: (user, status).
@@ -215,6 +215,8 @@ def lib():
         L.kg_conv_weight_load.argtypes = [ci, ci, ci, ci, ci, ci, ci] + [ctypes.POINTER(ci)] * 4
         L.kg_conv_weight_chunk.argtypes = [ci, ci]
         L.kg_junction_tile_of.argtypes = [ci, ci, ctypes.POINTER(ci), ctypes.POINTER(ci)]
+        L.kg_gpool_tile_of.argtypes = [ci, ci, ci, ci] + [ctypes.POINTER(ci)] * 4
+        L.kg_l2_touch_line.argtypes = [ci, ci, ci, ctypes.POINTER(ci)]
         _ = cf
         _lib = L
     return _lib
@@ -268,6 +270,21 @@ def junction_tile_of(pixels: int, workgroup: int):
     grid, tile = ctypes.c_int(), ctypes.c_int()
     _check(lib().kg_junction_tile_of(pixels, workgroup, ctypes.byref(grid), ctypes.byref(tile)))
     return grid.value, tile.value
+
+
+def gpool_tile_of(pixels: int, gpool_channels: int, regular_channels: int, workgroup: int):
+    """(workgroups of the gpool tile launch, the 192-pixel tile of `workgroup` or -1, its first regular channel,
+    its channel count)."""
+    out = [ctypes.c_int() for _ in range(4)]
+    _check(lib().kg_gpool_tile_of(pixels, gpool_channels, regular_channels, workgroup, *[ctypes.byref(o) for o in out]))
+    return tuple(o.value for o in out)
+
+
+def l2_touch_line(grid: int, workgroup: int, thread: int) -> int:
+    """The 128-byte line of the next op's weights that a thread of a `grid`-workgroup launch touches into L2."""
+    line = ctypes.c_int()
+    _check(lib().kg_l2_touch_line(grid, workgroup, thread, ctypes.byref(line)))
+    return line.value
 
 
 def conv_tile_of(ks: int, ic: int, oc: int, split: bool, pixels: int, workgroup: int):

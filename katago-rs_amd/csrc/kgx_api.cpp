@@ -565,6 +565,32 @@ int kg_junction_tile_of(int pixels, int workgroup, int* grid, int* tile) {
   });
 }
 
+int kg_gpool_tile_of(int pixels, int gpool_channels, int regular_channels, int workgroup, int* grid, int* tile,
+                     int* first_channel, int* channels) {
+  return guarded([&] {
+    if (!grid || !tile || !first_channel || !channels) throw std::runtime_error("null output");
+    if (pixels < 1) throw std::runtime_error("bad pixel count");
+    const int share = kgx::gpool_tile_share(gpool_channels, regular_channels);
+    if (!share) throw std::runtime_error("no tile share fits these channel counts");
+    const int shares = regular_channels / share;
+    *grid = kgx::gpool_tile_grid(pixels, shares);
+    if (workgroup < 0 || workgroup >= *grid) throw std::runtime_error("workgroup out of range");
+    int t, s;
+    kgx::gpool_tile_of(workgroup, shares, t, s);
+    *tile = t * kgx::kGpoolTileRows < pixels ? t : -1;
+    *first_channel = s * share;
+    *channels = share;
+  });
+}
+
+int kg_l2_touch_line(int grid, int workgroup, int thread, int* line) {
+  return guarded([&] {
+    if (!line) throw std::runtime_error("null output");
+    if (grid < 1 || workgroup < 0 || workgroup >= grid || thread < 0) throw std::runtime_error("bad launch index");
+    *line = kgx::l2_touch_line(workgroup, grid, thread);
+  });
+}
+
 int kg_conv_weight_load(int ks, int ic, int oc, int split, int q, int wave, int lane, int* src_row, int* src_chunk,
                         int* dst_row, int* dst_chunk) {
   return guarded([&] {

@@ -188,9 +188,8 @@ __device__ __forceinline__ void lds_load16(const void* base, int nbytes, void* l
 // value live up to its end (l2_touch_keep), which it reaches on every path: the load is not dropped, and no wait
 // for it comes before that point.
 __device__ __forceinline__ int l2_touch(const char* p, int nbytes, int tid) {
-  const int g = blockIdx.x, n = ((int)gridDim.x - (g & 7) + 7) >> 3;
   const int v = __builtin_amdgcn_raw_buffer_load_b32(__builtin_amdgcn_make_buffer_rsrc((void*)p, 0, nbytes, 0x00020000),
-                                                     ((g >> 3) + n * tid) * 128, 0, 0);
+                                                     l2_touch_line(blockIdx.x, gridDim.x, tid) * 128, 0, 0);
   asm volatile("" ::: "memory");  // issued here, not next to its use
   return v;
 }

@@ -63,6 +63,13 @@ struct PoolPart {
   int rpt = 0, C = 0;
 };
 
+// The 128-byte line of the next op's weights (ConvOut::pf) that thread tid of workgroup g of a grid-workgroup launch
+// touches (l2_touch): workgroup g runs on XCD g mod 8, and the n workgroups of that XCD take lines s + n tid, s =
+// g / 8, so the XCD touches each of its first n x threads lines once.
+__host__ __device__ inline int l2_touch_line(int g, int grid, int tid) {
+  return (g >> 3) + ((grid - (g & 7) + 7) >> 3) * tid;
+}
+
 // Output of a convolution or GEMM, element (m, n) with accumulated value v:
 // v += colbias[m / HW][n]; v *= rowmask[m]; yt = T(v); y = (accumulate ? y : 0) + v; then the emission from y.
 struct ConvOut {
@@ -299,9 +306,19 @@ struct GpoolTile {
   void* out = nullptr; int ldo = 0; int prec = PREC_F16;
   const char* pf = nullptr; int pf_bytes = 0;
 };
-// The output share gpool_tile_launch uses for cr channels (0: none fits: 64 <= 3 cg <= 384 and cr / 8 a multiple
+// The output share launch_gpool_tile uses for cr channels (0: none fits: 64 <= 3 cg <= 384 and cr / 8 a multiple
 // of 8 up to 40 are needed).
 int gpool_tile_share(int cg, int cr);
+// Its launch over M pixels with `shares` channel shares: 8 ceil(tiles / 8) shares workgroups; workgroup g takes
+// tile (g mod 8) + 8 ((g / 8) / shares) (on XCD g mod 8, the convolutions' XCD of that tile) and share
+// (g / 8) mod shares; tiles past the last pixel exit at once.
+constexpr int kGpoolTileRows = 192;
+inline int gpool_tile_grid(int M, int shares) { return 8 * ((M + kGpoolTileRows * 8 - 1) / (kGpoolTileRows * 8)) * shares; }
+__host__ __device__ inline void gpool_tile_of(int g, int shares, int& tile, int& share) {
+  const int j = g >> 3;
+  tile = (g & 7) + 8 * (j / shares);
+  share = j % shares;
+}
 void launch_gpool_tile(const GpoolTile& a, int B, hipStream_t s);
 
 // Gives each matmul of `p` whose weights fit a staged copy in LDS (after the program's features), as long as the

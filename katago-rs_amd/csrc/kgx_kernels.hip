@@ -584,7 +584,7 @@ void launch_row_prog(const RowProg& p, int B, hipStream_t s) {
 // ---------------------------------------------------------------------------------------------------------
 // Global-pooling block's mid activation per 192-pixel tile (GpoolTile)
 // ---------------------------------------------------------------------------------------------------------
-constexpr int GT_NT = 256, GT_BM = 192, GT_KS = 16, GT_RV = 4, GT_RW = 12;
+constexpr int GT_NT = 256, GT_BM = kGpoolTileRows, GT_KS = 16, GT_RV = 4, GT_RW = 12;
 
 int gpool_tile_share(int cg, int cr) {
   const int share = cr / 8;
@@ -595,8 +595,10 @@ int gpool_tile_share(int cg, int cr) {
 template <typename T, int ACT>
 __global__ __launch_bounds__(GT_NT) void gpool_tile_kernel(GpoolTile a, int M) {
   extern __shared__ float lds[];
-  const int tid = threadIdx.x, g = blockIdx.x, SH = a.share, S = a.cr / SH, IC = 3 * a.cg, cg = a.cg;
-  const int j = g >> 3, t = (g & 7) + 8 * (j / S), c0 = (j % S) * SH;
+  const int tid = threadIdx.x, SH = a.share, IC = 3 * a.cg, cg = a.cg;
+  int t, sh;
+  gpool_tile_of(blockIdx.x, a.cr / SH, t, sh);
+  const int c0 = sh * SH;
   const int m0 = t * GT_BM;
   if (m0 >= M) {
     l2_touch_keep(l2_touch(a.pf, a.pf_bytes, tid));
@@ -718,9 +720,9 @@ void launch_gpool_tile(const GpoolTile& a, int B, hipStream_t s) {
       !a.x || !a.scale || !a.bias || !a.mask || !a.out || a.ldx % 4 || a.ldo % 8 || a.x == nullptr ||
       ((uintptr_t)a.x | (uintptr_t)a.out | (uintptr_t)a.W) % 16 || (a.prec != PREC_F16 && a.prec != PREC_BF16))
     throw std::runtime_error("gpool tile: unsupported layout");
-  const int T = (M + GT_BM - 1) / GT_BM, S = a.cr / a.share, IC = 3 * a.cg;
+  const int IC = 3 * a.cg;
   const size_t lds = ((size_t)IC * a.share + 2 * IC + 2 * GT_KS * a.share + 4 * a.share + GT_BM) * sizeof(float);
-  const dim3 grid(8 * ((T + 7) / 8) * S);
+  const dim3 grid(gpool_tile_grid(M, a.cr / a.share));
   auto go = [&](auto t, auto act) {
     launch_k(gpool_tile_kernel<decltype(t), decltype(act)::value>, grid, GT_NT, lds, s, a, M);
   };

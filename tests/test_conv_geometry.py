@@ -108,3 +108,36 @@ def test_junction_tiles_cover_every_pixel_once_on_the_convolutions_xcds(kgx):
                 assert wg % 8 == mt % 8
     with pytest.raises(kgx.KgError, match="workgroup out of range"):
         kgx.junction_tile_of(361, 10 ** 6)
+
+
+@pytest.mark.parametrize("cg,cr", [(64, 192), (128, 128)])
+def test_gpool_tiles_cover_every_tile_and_channel_once_on_the_convolutions_xcds(kgx, cg, cr):
+    """The gpool blocks' tile launch over batches 1 to 64: every (192-pixel tile, channel share) pair exactly once,
+    the shares partition the regular channels, and tile t runs on XCD t mod 8, where the convolutions before and
+    after it (192-pixel tiles) run it."""
+    for b in BATCHES:
+        pixels = b * 361
+        grid, _, _, share = kgx.gpool_tile_of(pixels, cg, cr, 0)
+        assert cr % share == 0 and share % 8 == 0
+        seen = collections.Counter()
+        for wg in range(grid):
+            g, t, c0, n = kgx.gpool_tile_of(pixels, cg, cr, wg)
+            assert g == grid and n == share
+            if t < 0:
+                continue
+            assert 0 <= t * 192 < pixels and 0 <= c0 < cr and c0 % share == 0, (b, wg, t, c0)
+            assert wg % 8 == t % 8, (b, wg, t)
+            seen[(t, c0)] += 1
+        want = {(t, c) for t in range(-(-pixels // 192)) for c in range(0, cr, share)}
+        assert set(seen) == want and all(v == 1 for v in seen.values()), b
+    with pytest.raises(kgx.KgError, match="no tile share"):
+        kgx.gpool_tile_of(361, 32, 96, 0)
+
+
+@pytest.mark.parametrize("grid,threads", [(256, 512), (512, 256), (61 * 4, 512), (8 * 8 * 8, 256), (13, 64)])
+def test_l2_touch_covers_each_line_once_per_xcd(kgx, grid, threads):
+    """Each XCD's workgroups (g mod 8) touch lines 0 .. n x threads - 1 of the next op's weights once each."""
+    for x in range(8):
+        wgs = [g for g in range(x, grid, 8)]
+        lines = collections.Counter(kgx.l2_touch_line(grid, g, t) for g in wgs for t in range(threads))
+        assert set(lines) == set(range(len(wgs) * threads)) and all(v == 1 for v in lines.values()), (grid, x)
