@@ -17,6 +17,11 @@
 // in two chains, steps {0, 1, 4, 5, 8, 9} and {2, 3, 6, 7, 10, 11} (the separate kernel's two wave groups over its
 // 128-channel stages), then added; the epilogues are the same expressions. So the junction's outputs equal the
 // separate kernels' bit for bit.
+//
+// The stem junction (STEM) is the same launch with the network's stem in place of the exit: a 3x3 convolution of
+// the packed input planes (at most 32 channels, 16-bit operands, one plane) into the trunk, with the row's global
+// bias added (bin2onnx.py:1466-1492), then the first nested block's entry 1x1. Its nine taps are nine steps in tap
+// order over the 48-pixel tile's rows and their 20-row halo, staged in LDS, as the separate kernel sums them.
 #include "kgx_device.h"
 
 #include <vector>
@@ -73,13 +78,21 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("" ::: "memory");
 }
 
+// The stem's packed fragments: [column block][tap] single-plane fragments, then the entry's.
+constexpr int KS3 = 9;                       // the stem's steps: one per tap, 32 channels each
+constexpr int W2STEM = CB1 * KS3 * FRAG;
+constexpr int SR = JR + 40, SRB = 80;        // the stem's staged pixel rows (tile and halos), bytes per LDS row
+
 // ACT1: the exit's emission activation (ACT_MISH), or -1: the one eo names, chosen per value at run time. NO: the
-// entry's outputs (192 or 96). A trunk that ends here (eo.y_dead) is read and not stored.
-template <typename T, int ACT1, int NO>
+// entry's outputs (192 or 96). A trunk that ends here (eo.y_dead) is read and not stored. STEM: the exit is the
+// network's stem (X: packed input rows of ldx <= 32 channels; eo adds the row's global bias, eo.colbias, instead of
+// a residual).
+template <typename T, int ACT1, int NO, bool STEM>
 __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ X, const T* __restrict__ Xlo, int ldx,
                                                           const T* __restrict__ W, int M, ConvOut eo, ConvOut no) {
   typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
   static_assert(NO == 192 || NO == 96, "entry outputs");
+  constexpr int W2 = STEM ? W2STEM : W2OFF;  // the entry's fragments
   constexpr int CB2 = NO / 16, LD2 = NO + 4;
   constexpr int G2 = NO / 12, R2 = JNT / G2, E2 = (JR + R2 - 1) / R2;  // the entry epilogue's mapping
   __shared__ __align__(1024) char smem[LDSB];
@@ -109,43 +122,10 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
     return *(const frag_t*)(base + (((ks >> 1) * 2 + pl) * JR + 16 * i + r16) * 128 + chunk * 16);
   };
 
-  // Exit product, wave wv: output columns 48 wv .. + 48 (blocks 3 wv + j), all 48 pixels. Its weight fragments go
-  // through a ring of NS steps, the first NS loaded while the operand's direct loads are in flight (the wait for
-  // those covers them too), so that the weights stream from L2 in the time that would otherwise only wait.
-  frag_t b1[NS][3][2];
-  auto load_b1 = [&](int slot, int ks) {
-#pragma unroll
-    for (int j = 0; j < 3; j++)
-#pragma unroll
-      for (int pl = 0; pl < 2; pl++) b1[slot][j][pl] = wfrag(0, 3 * wv + j, K1, ks, pl);
-  };
-#pragma unroll
-  for (int k = 0; k < NS; k++) load_b1(k, k);
-  // The exit's operand straight into LDS: 36 loads of 8 pixel rows x 128 bytes (64-channel slice kp, plane pl,
-  // rows 8 grp ..), lane i filling row 8 grp + i / 8 at stored chunk i % 8 from source chunk (i % 8) ^ swizzle.
-  // Rows past M lie beyond the buffer range and read as zero.
-  {
-    const int rb = ldx * (int)sizeof(T), nbytes = min(JR, M - m0) * rb;
-    const T* xb = X + (size_t)m0 * ldx;
-    const T* xlb = Xlo + (size_t)m0 * ldx;
-#pragma unroll
-    for (int u = 0; u < 5; u++) {
-      const int q = u * 8 + wv;
-      if (q < 36) {
-        const int kp = q / 12, pl = (q / 6) & 1, grp = q % 6;
-        const int row = grp * 8 + (lane >> 3), sc = (lane & 7) ^ ((row >> 1) & 7);
-        lds_load16(pl ? xlb : xb, nbytes, r1 + ((kp * 2 + pl) * JR + grp * 8) * 128, row * rb + kp * 128 + sc * 16);
-      }
-    }
-  }
-  // The direct loads are not counted by the compiler: wait for all of this wave's loads, then for every wave.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-
-  // The exit epilogue's inputs: the trunk values it adds to, the emission's scale, bias and board mask (channels
-  // c1 + 128 q .. + 3 of pixels p1 + 16 e; rows past M read row M - 1, never stored). They are issued after the
-  // product's last weight loads (a wait covers every load issued before the one it waits for), in flight during
-  // its last steps.
+  // The exit epilogue's inputs: the trunk values it adds to (the stem: the row's global bias), the emission's scale,
+  // bias and board mask (channels c1 + 128 q .. + 3 of pixels p1 + 16 e; rows past M read row M - 1, never
+  // stored). They are issued after the product's last weight loads (a wait covers every load issued before the one
+  // it waits for), in flight during its last steps.
   const int c1 = 4 * (tid & 31), p1 = tid >> 5;
   floatx4 yres[E1][3], es1[3], eb1[3];
   float mk1[E1];
@@ -154,7 +134,9 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
     for (int e = 0; e < E1; e++) {
       const int m = min(m0 + p1 + 16 * e, M - 1);
 #pragma unroll
-      for (int q = 0; q < 3; q++) yres[e][q] = *(const floatx4*)(eo.y + (size_t)m * eo.ldy + c1 + 128 * q);
+      for (int q = 0; q < 3; q++)
+        yres[e][q] = STEM ? *(const floatx4*)(eo.colbias + (size_t)(m / HW) * eo.ld_colbias + c1 + 128 * q)
+                          : *(const floatx4*)(eo.y + (size_t)m * eo.ldy + c1 + 128 * q);
       mk1[e] = eo.emit.mask[m];
     }
 #pragma unroll
@@ -169,36 +151,126 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
   for (int i = 0; i < 3; i++)
 #pragma unroll
     for (int j = 0; j < 3; j++) acc[i][j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  {
-    frag_t ah[2][3], al[2][3];
-    auto load_a1 = [&](int set, int ks) {
+  if constexpr (STEM) {
+    // The stem, wave wv: output columns 48 wv .. + 48 (blocks 3 wv + j), all 48 pixels, over the nine taps in order
+    // (one 16x16x32 step each: 32 channels, those past ldx zero). The pixel rows [m0 - 20, m0 + 68) go into LDS
+    // (rows off the batch and channels past ldx as zeros, from loads of clamped rows) while the ring's first
+    // weights are in flight.
+    const int sr = tid >> 2, sc = tid & 3, sg = m0 - 20 + sr;
+    const u32x4 rv = *(const u32x4*)(X + (size_t)min(max(sg, 0), M - 1) * ldx + (8 * sc < ldx ? 8 * sc : 0));
+    frag_t b1[NS][3];
+    auto load_b1 = [&](int slot, int t) {
+#pragma unroll
+      for (int j = 0; j < 3; j++) b1[slot][j] = *(const frag_t*)(W + ((3 * wv + j) * KS3 + t) * FRAG + lane * 8);
+    };
+#pragma unroll
+    for (int k = 0; k < NS; k++) load_b1(k, k);
+    const bool sok = sg >= 0 && sg < M && 8 * sc < ldx;
+    if (tid < SR * 4) *(u32x4*)(r1 + sr * SRB + sc * 16) = sok ? rv : u32x4{0, 0, 0, 0};
+    else if (tid < SR * 4 + SRB / 16) *(u32x4*)(r1 + SR * SRB + (tid - SR * 4) * 16) = u32x4{0, 0, 0, 0};  // zero row
+    // Tap validity of this lane's pixels (bit t: the neighbour at tap t is on the board); off-board neighbours,
+    // and pixels past M, read the zero row.
+    unsigned vmask[3];
+#pragma unroll
+    for (int i = 0; i < 3; i++) {
+      const int m = m0 + 16 * i + r16;
+      unsigned bits = 0;
+      if (m < M) {
+        const int pt = m % HW, y = pt / POS, x = pt - y * POS;
+#pragma unroll
+        for (int t = 0; t < KS3; t++)
+          if ((unsigned)(y + t / 3 - 1) < (unsigned)POS && (unsigned)(x + t % 3 - 1) < (unsigned)POS) bits |= 1u << t;
+      }
+      vmask[i] = bits;
+    }
+    lds_barrier();
+    frag_t a[2][3];
+    auto load_a = [&](int set, int t) {
+      const int shift = (t / 3 - 1) * POS + (t % 3 - 1);
 #pragma unroll
       for (int i = 0; i < 3; i++) {
-        ah[set][i] = afrag(r1, i, ks, 0);
-        al[set][i] = afrag(r1, i, ks, 1);
+        const int row = (vmask[i] >> t) & 1 ? 16 * i + r16 + 20 + shift : SR;
+        a[set][i] = *(const frag_t*)(r1 + row * SRB + g4 * 16);
       }
     };
-    load_a1(0, 0);
+    load_a(0, 0);
 #pragma unroll
-    for (int ks = 0; ks < K1; ks++) {
-      const int s = ks & 1;
-      if (ks + 1 < K1) load_a1(s ^ 1, ks + 1);
+    for (int t = 0; t < KS3; t++) {
+      if (t + 1 < KS3) load_a((t + 1) & 1, t + 1);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < 3; i++)
 #pragma unroll
-        for (int j = 0; j < 3; j++) acc[i][j] = mfma(al[s][i], b1[ks % NS][j][0], acc[i][j]);
-#pragma unroll
-      for (int i = 0; i < 3; i++)
-#pragma unroll
-        for (int j = 0; j < 3; j++) acc[i][j] = mfma(ah[s][i], b1[ks % NS][j][1], acc[i][j]);
-#pragma unroll
-      for (int i = 0; i < 3; i++)
-#pragma unroll
-        for (int j = 0; j < 3; j++) acc[i][j] = mfma(ah[s][i], b1[ks % NS][j][0], acc[i][j]);
+        for (int j = 0; j < 3; j++) acc[i][j] = mfma(a[t & 1][i], b1[t % NS][j], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
-      if (ks + NS < K1) load_b1(ks % NS, ks + NS);
-      if (ks + NS + 1 == K1) load_epi1();
+      if (t + NS < KS3) load_b1(t % NS, t + NS);
+      if (t + NS + 1 == KS3) load_epi1();
+    }
+  } else {
+    // Exit product, wave wv: output columns 48 wv .. + 48 (blocks 3 wv + j), all 48 pixels. Its weight fragments go
+    // through a ring of NS steps, the first NS loaded while the operand's direct loads are in flight (the wait for
+    // those covers them too), so that the weights stream from L2 in the time that would otherwise only wait.
+    frag_t b1[NS][3][2];
+    auto load_b1 = [&](int slot, int ks) {
+#pragma unroll
+      for (int j = 0; j < 3; j++)
+#pragma unroll
+        for (int pl = 0; pl < 2; pl++) b1[slot][j][pl] = wfrag(0, 3 * wv + j, K1, ks, pl);
+    };
+#pragma unroll
+    for (int k = 0; k < NS; k++) load_b1(k, k);
+    // The exit's operand straight into LDS: 36 loads of 8 pixel rows x 128 bytes (64-channel slice kp, plane pl,
+    // rows 8 grp ..), lane i filling row 8 grp + i / 8 at stored chunk i % 8 from source chunk (i % 8) ^ swizzle.
+    // Rows past M lie beyond the buffer range and read as zero.
+    {
+      const int rb = ldx * (int)sizeof(T), nbytes = min(JR, M - m0) * rb;
+      const T* xb = X + (size_t)m0 * ldx;
+      const T* xlb = Xlo + (size_t)m0 * ldx;
+#pragma unroll
+      for (int u = 0; u < 5; u++) {
+        const int q = u * 8 + wv;
+        if (q < 36) {
+          const int kp = q / 12, pl = (q / 6) & 1, grp = q % 6;
+          const int row = grp * 8 + (lane >> 3), sc = (lane & 7) ^ ((row >> 1) & 7);
+          lds_load16(pl ? xlb : xb, nbytes, r1 + ((kp * 2 + pl) * JR + grp * 8) * 128, row * rb + kp * 128 + sc * 16);
+        }
+      }
+    }
+    // The direct loads are not counted by the compiler: wait for all of this wave's loads, then for every wave.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+
+    {
+      frag_t ah[2][3], al[2][3];
+      auto load_a1 = [&](int set, int ks) {
+#pragma unroll
+        for (int i = 0; i < 3; i++) {
+          ah[set][i] = afrag(r1, i, ks, 0);
+          al[set][i] = afrag(r1, i, ks, 1);
+        }
+      };
+      load_a1(0, 0);
+#pragma unroll
+      for (int ks = 0; ks < K1; ks++) {
+        const int s = ks & 1;
+        if (ks + 1 < K1) load_a1(s ^ 1, ks + 1);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+#pragma unroll
+          for (int j = 0; j < 3; j++) acc[i][j] = mfma(al[s][i], b1[ks % NS][j][0], acc[i][j]);
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+#pragma unroll
+          for (int j = 0; j < 3; j++) acc[i][j] = mfma(ah[s][i], b1[ks % NS][j][1], acc[i][j]);
+#pragma unroll
+        for (int i = 0; i < 3; i++)
+#pragma unroll
+          for (int j = 0; j < 3; j++) acc[i][j] = mfma(ah[s][i], b1[ks % NS][j][0], acc[i][j]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks + NS < K1) load_b1(ks % NS, ks + NS);
+        if (ks + NS + 1 == K1) load_epi1();
+      }
     }
   }
 
@@ -216,7 +288,7 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
 #pragma unroll
     for (int j = 0; j < 3; j++)
 #pragma unroll
-      for (int pl = 0; pl < 2; pl++) b2[slot][j][pl] = wfrag(W2OFF, 3 * cg + j, K2, kstep(p), pl);
+      for (int pl = 0; pl < 2; pl++) b2[slot][j][pl] = wfrag(W2, 3 * cg + j, K2, kstep(p), pl);
   };
   // The exit's float tile over its operand's LDS (every wave is done reading the operand first).
   lds_barrier();
@@ -391,24 +463,44 @@ int junction_grid(int M) {
   return 32 * ((regions + 7) / 8);
 }
 
+// Fragment (cb, ks, plane) of a K-step weight matrix w [cols][32 K] at `base`: lane l, element e holds column
+// 16 cb + l % 16, channel 32 ks + 8 (l / 16) + e; the low plane holds w - round(w).
+static void pack_split(const float* w, int cbs, int K, size_t base, int prec, std::vector<float>& out) {
+  for (int cb = 0; cb < cbs; cb++)
+    for (int ks = 0; ks < K; ks++)
+      for (int l = 0; l < 64; l++)
+        for (int e = 0; e < 8; e++) {
+          const float v = w[(size_t)(16 * cb + l % 16) * (32 * K) + 32 * ks + 8 * (l / 16) + e];
+          const size_t at = base + (size_t)((cb * K + ks) * 2) * FRAG + l * 8 + e;
+          out[at] = v;
+          out[at + FRAG] = v - conv_round_operand(v, prec);
+        }
+}
+
 void junction_pack_weights(const float* w_exit, const float* w_entry, int entry_oc, int prec, std::vector<float>& out) {
   if (entry_oc != kJunctionInner && entry_oc != kJunctionHead) throw std::runtime_error("junction: entry outputs");
   out.assign(junction_welems(entry_oc), 0.f);
-  // Fragment (cb, ks, plane) of a K-step weight matrix w [cols][32 K]: lane l, element e holds column
-  // 16 cb + l % 16, channel 32 ks + 8 (l / 16) + e; the low plane holds w - round(w).
-  auto pack = [&](const float* w, int cbs, int K, int base) {
-    for (int cb = 0; cb < cbs; cb++)
-      for (int ks = 0; ks < K; ks++)
-        for (int l = 0; l < 64; l++)
-          for (int e = 0; e < 8; e++) {
-            const float v = w[(size_t)(16 * cb + l % 16) * (32 * K) + 32 * ks + 8 * (l / 16) + e];
-            const size_t at = (size_t)base + (size_t)((cb * K + ks) * 2) * FRAG + l * 8 + e;
-            out[at] = v;
-            out[at + FRAG] = v - conv_round_operand(v, prec);
-          }
-  };
-  pack(w_exit, CB1, K1, 0);
-  pack(w_entry, entry_oc / 16, K2, W2OFF);
+  pack_split(w_exit, CB1, K1, 0, prec, out);
+  pack_split(w_entry, entry_oc / 16, K2, W2OFF, prec, out);
+}
+
+int stem_junction_welems(int no) { return W2STEM + (no / 16) * K2 * 2 * FRAG; }
+
+void stem_junction_pack_weights(const float* w_stem, int ic, const float* w_entry, int entry_oc, int prec,
+                                std::vector<float>& out) {
+  if (entry_oc != kJunctionInner) throw std::runtime_error("stem junction: entry outputs");
+  if (ic < 1 || ic > 32) throw std::runtime_error("stem junction: at most 32 input channels");
+  out.assign(stem_junction_welems(entry_oc), 0.f);
+  // Stem fragment (cb, t), one plane: lane l, element e holds w[16 cb + l % 16][8 (l / 16) + e][t] (zero past ic).
+  for (int cb = 0; cb < CB1; cb++)
+    for (int t = 0; t < KS3; t++)
+      for (int l = 0; l < 64; l++)
+        for (int e = 0; e < 8; e++) {
+          const int ch = 8 * (l / 16) + e;
+          out[(size_t)(cb * KS3 + t) * FRAG + l * 8 + e] =
+              ch < ic ? w_stem[((size_t)(16 * cb + l % 16) * ic + ch) * KS3 + t] : 0.f;
+        }
+  pack_split(w_entry, entry_oc / 16, K2, W2STEM, prec, out);
 }
 
 void launch_junction(int prec, const void* x, const void* x_lo, int ldx, const void* w, const ConvOut& eo,
@@ -433,8 +525,8 @@ void launch_junction(int prec, const void* x, const void* x_lo, int ldx, const v
   auto go = [&](auto tc, auto noc) {
     typedef decltype(tc) TT;
     constexpr int N = decltype(noc)::value;
-    launch_k(mish ? junction_kernel<TT, ACT_MISH, N> : junction_kernel<TT, -1, N>, junction_grid(M), JNT, 0, s,
-             (const TT*)x, (const TT*)x_lo, ldx, (const TT*)w, M, eo, no);
+    launch_k(mish ? junction_kernel<TT, ACT_MISH, N, false> : junction_kernel<TT, -1, N, false>, junction_grid(M),
+             JNT, 0, s, (const TT*)x, (const TT*)x_lo, ldx, (const TT*)w, M, eo, no);
   };
   typedef std::integral_constant<int, kJunctionInner> Inner;
   typedef std::integral_constant<int, kJunctionHead> Head;
@@ -445,6 +537,34 @@ void launch_junction(int prec, const void* x, const void* x_lo, int ldx, const v
     if (entry_oc == kJunctionInner) go(bf16(), Inner());
     else go(bf16(), Head());
   }
+  KGX_CHECK_LAUNCH();
+}
+
+void launch_stem_junction(int prec, const void* x, int ldx, const void* w, const ConvOut& eo, const ConvOut& no,
+                          int B, hipStream_t s) {
+  if (prec != PREC_F16 && prec != PREC_BF16) throw std::runtime_error("stem junction: 16-bit operands only");
+  if (B <= 0) return;
+  if (!x || !w || ldx < 8 || ldx > 32 || ldx % 8 || ((uintptr_t)x | (uintptr_t)w) % 16)
+    throw std::runtime_error("stem junction: packed input rows of 8 to 32 channels, 16-byte aligned");
+  // The stem's output is the trunk (stored), its row bias and the emission of the entry's activation, nothing else.
+  if (!eo.y || eo.accumulate || eo.y_dead || eo.ldy % 4 || eo.yt || eo.rowmask || !eo.colbias || eo.ld_colbias % 4 ||
+      !eo.emit.scale || !eo.emit.bias || !eo.emit.mask || eo.pool.psum ||
+      ((uintptr_t)eo.y | (uintptr_t)eo.colbias | (uintptr_t)eo.emit.scale | (uintptr_t)eo.emit.bias) % 16)
+    throw std::runtime_error("stem junction: the stem must store the trunk with its row bias and emit the entry's "
+                             "activation");
+  if (no.pool.psum || (no.y && (no.ldy % 4 || (uintptr_t)no.y % 16)) || (no.yt && no.ldyt % 4) ||
+      (no.colbias && no.ld_colbias % 4) || (no.emit.scale && (no.emit.ld % 4 || (uintptr_t)no.emit.scale % 16 ||
+                                                              (uintptr_t)no.emit.bias % 16)))
+    throw std::runtime_error("stem junction: unsupported entry outputs");
+  const int M = B * HW;
+  const bool mish = eo.emit.act == ACT_MISH;
+  auto go = [&](auto tc) {
+    typedef decltype(tc) TT;
+    launch_k(mish ? junction_kernel<TT, ACT_MISH, kJunctionInner, true> : junction_kernel<TT, -1, kJunctionInner, true>,
+             junction_grid(M), JNT, 0, s, (const TT*)x, (const TT*)x, ldx, (const TT*)w, M, eo, no);
+  };
+  if (prec == PREC_F16) go(f16());
+  else go(bf16());
   KGX_CHECK_LAUNCH();
 }
 

@@ -197,6 +197,14 @@ void launch_junction(int prec, const void* x, const void* x_lo, int ldx, const v
                      const ConvOut& entry_o, int entry_oc, int B, hipStream_t s);
 // The launch's grid over M pixels, and the 48-pixel tile workgroup g computes (tiles past M exit at once).
 int junction_grid(int M);
+// The stem junction: the network's stem, a 3x3 convolution of the packed input rows (ldx <= 32 channels, one 16-bit
+// plane) into the trunk with its row bias (eo: y stored, colbias, the emission of the entry's activation), and the
+// first nested block's entry 1x1 (384 -> 192, split operands), in one launch over junction_grid(M) workgroups.
+// Weights: stem_junction_pack_weights of the stem's filters [384][ic][3][3] and the entry's [192][384].
+void stem_junction_pack_weights(const float* w_stem, int ic, const float* w_entry, int entry_oc, int prec,
+                                std::vector<float>& out);
+void launch_stem_junction(int prec, const void* x, int ldx, const void* w, const ConvOut& eo, const ConvOut& no,
+                          int B, hipStream_t s);
 int junction_tile_of(int g);
 
 // Network input planes, float NCHW [B][nin][361], to compute-type NHWC rows of ldo channels (zero beyond nin,

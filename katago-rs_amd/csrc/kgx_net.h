@@ -132,11 +132,16 @@ class Net {
     const void* x_lo = nullptr;
     int ldx = 0;
     std::shared_ptr<ConvOut> out;
+    bool stem = false;  // the network's stem (x: the packed input rows), joined with the first block's entry
   };
   // Whether block b's exit (over a trunk of c channels) can start a junction, and whether it and block `next`'s entry
   // run as one.
   bool exit_fits(const BlockDesc& b, int c) const;
   bool junction_fits(const BlockDesc& b, const BlockDesc& next, int c) const;
+  // Whether the stem (into stem_out) and the first block's entry run as one stem junction.
+  bool stem_junction_fits(const ModelDesc& m, const ConvOut& stem_out) const;
+  // The input packing launch of a stem convolution c over the float NCHW input x; icin: the packed channels.
+  const void* emit_input_pack(const ConvDesc& c, const void* x, int& icin);
   std::shared_ptr<ConvOut> emit_junction(const PendingExit& p, const ConvDesc& entry, const ConvOut& entry_o);
   void emit_attention(const BlockDesc& b, int depth);
   void emit_ffn(const BlockDesc& b, int depth);

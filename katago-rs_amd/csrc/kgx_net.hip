@@ -188,6 +188,17 @@ bool Net::exit_fits(const BlockDesc& b, int c) const {
          ex.w.size() == (size_t)kJunctionInner * kJunctionOuter;
 }
 
+bool Net::stem_junction_fits(const ModelDesc& m, const ConvOut& stem_out) const {
+  const ConvDesc& st = m.stem;
+  if (!junctions_ || prec_ == PREC_F32 || conv_mode_ != CONV_IGEMM || m.blocks.empty()) return false;
+  const BlockDesc& b = m.blocks[0];
+  const ConvDesc& en = b.regular;
+  return st.ky == 3 && st.kx == 3 && st.dy == 1 && st.dx == 1 && st.oc == kJunctionOuter && st.ic >= 1 &&
+         st.ic <= 32 && st.w.size() == (size_t)kJunctionOuter * st.ic * 9 && igemm_eligible(st, true, 0, stem_out) &&
+         stem_out.colbias && b.kind == BLOCK_NBT && is_1x1(en) && en.ic == kJunctionOuter &&
+         en.oc == kJunctionInner && en.w.size() == (size_t)kJunctionInner * kJunctionOuter;
+}
+
 bool Net::junction_fits(const BlockDesc& b, const BlockDesc& next, int c) const {
   const ConvDesc& en = next.regular;
   return exit_fits(b, c) && next.kind == BLOCK_NBT && is_1x1(en) && en.ic == kJunctionOuter &&
@@ -197,21 +208,31 @@ bool Net::junction_fits(const BlockDesc& b, const BlockDesc& next, int c) const 
 std::shared_ptr<ConvOut> Net::emit_junction(const PendingExit& p, const ConvDesc& entry, const ConvOut& entry_o) {
   std::vector<float> w;
   const int eoc = entry.oc;
-  junction_pack_weights(p.conv->w.data(), entry.w.data(), eoc, prec_, w);
+  if (p.stem) stem_junction_pack_weights(p.conv->w.data(), p.conv->ic, entry.w.data(), eoc, prec_, w);
+  else junction_pack_weights(p.conv->w.data(), entry.w.data(), eoc, prec_, w);
   const void* dW = upload_t(w);
   const std::shared_ptr<ConvOut> eo = p.out, no = std::make_shared<ConvOut>(entry_o);
   const int prec = prec_, ldx = p.ldx;
   const void *x = p.x, *x_lo = p.x_lo;
   const double ts = (double)tsize();
   Op op;
-  op.launch = [=](hipStream_t s, int B) { launch_junction(prec, x, x_lo, ldx, dW, *eo, *no, eoc, B, s); };
-  const bool head = eoc == kJunctionHead;
-  op.cls = head ? "head_junction" : "conv1x1_junction";
-  op.flops_row = 2.0 * HW * (kJunctionInner + eoc) * kJunctionOuter;
-  // The exit's split operand, the trunk read and (but where it ends, before the heads) written, the entry's float
-  // output written (its emission is counted through `out`).
-  op.bytes_row = (double)HW * (2.0 * kJunctionInner * ts + (head ? 4.0 : 8.0) * kJunctionOuter + 4.0 * eoc);
-  op.bytes_fixed = 2.0 * (kJunctionInner + eoc) * kJunctionOuter * ts;
+  if (p.stem) {
+    op.launch = [=](hipStream_t s, int B) { launch_stem_junction(prec, x, ldx, dW, *eo, *no, B, s); };
+    op.cls = "stem_junction";
+    op.flops_row = 2.0 * HW * (9.0 * p.conv->ic * kJunctionOuter + (double)kJunctionOuter * eoc);
+    // The packed input planes, the trunk written, the entry's float output written.
+    op.bytes_row = (double)HW * (ldx * ts + 4.0 * kJunctionOuter + 4.0 * eoc);
+    op.bytes_fixed = (9.0 * p.conv->ic + 2.0 * eoc) * kJunctionOuter * ts;
+  } else {
+    op.launch = [=](hipStream_t s, int B) { launch_junction(prec, x, x_lo, ldx, dW, *eo, *no, eoc, B, s); };
+    const bool head = eoc == kJunctionHead;
+    op.cls = head ? "head_junction" : "conv1x1_junction";
+    op.flops_row = 2.0 * HW * (kJunctionInner + eoc) * kJunctionOuter;
+    // The exit's split operand, the trunk read and (but where it ends, before the heads) written, the entry's float
+    // output written (its emission is counted through `out`).
+    op.bytes_row = (double)HW * (2.0 * kJunctionInner * ts + (head ? 4.0 : 8.0) * kJunctionOuter + 4.0 * eoc);
+    op.bytes_fixed = 2.0 * (kJunctionInner + eoc) * kJunctionOuter * ts;
+  }
   op.out = no;
   op.out_c = eoc;
   op.w = dW;
@@ -268,6 +289,23 @@ bool Net::igemm_eligible(const ConvDesc& c, bool nchw, int ldx, const ConvOut& o
          (nchw || (c.ic % 8 == 0 && ldx % 8 == 0));
 }
 
+// The network input planes packed once into compute-type NHWC rows of icin = round_up(ic, 8) channels (0/1 planes
+// are exact in 16 bits), with the board statistics and the stem's global bias in the same launch.
+const void* Net::emit_input_pack(const ConvDesc& c, const void* x, int& icin) {
+  const int prec = prec_, ic = c.ic, ld = round_up(ic, 8);
+  icin = ld;
+  void* packed = alloc_bytes((size_t)max_batch_ * HW * ld * tsize());
+  const float* bin = (const float*)x;
+  float *mask = mask_, *area = area_, *s1 = s1_, *s2 = s2_;
+  Op pk;
+  const InputGlobal gl = stem_glob_;
+  pk.launch = [=](hipStream_t s, int B) { launch_input_prep(prec, bin, ic, packed, ld, mask, area, s1, s2, B, s, gl); };
+  pk.cls = "input_prep";
+  pk.bytes_row = (double)HW * ic * 4 + (double)HW * ld * tsize() + HW * 4.0;
+  ops_.push_back(pk);
+  return packed;
+}
+
 std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ldx, bool nchw, const ConvOut& o,
                                         const void* x_lo) {
   const int prec = prec_;
@@ -287,21 +325,8 @@ std::shared_ptr<ConvOut> Net::emit_conv(const ConvDesc& c, const void* x, int ld
     const void* xin = x;
     int ldin = ldx, icin = ic;
     if (nchw) {
-      // The network input planes are packed once into compute-type NHWC rows (0/1 planes are exact in 16 bits),
-      // with the board statistics in the same launch.
-      icin = ldin = round_up(ic, 8);
-      void* packed = alloc_bytes((size_t)max_batch_ * HW * icin * tsize());
-      const float* bin = (const float*)x;
-      float *mask = mask_, *area = area_, *s1 = s1_, *s2 = s2_;
-      Op pk;
-      const InputGlobal gl = stem_glob_;
-      pk.launch = [=](hipStream_t s, int B) {
-        launch_input_prep(prec, bin, ic, packed, icin, mask, area, s1, s2, B, s, gl);
-      };
-      pk.cls = "input_prep";
-      pk.bytes_row = (double)HW * ic * 4 + (double)HW * icin * ts + HW * 4.0;
-      ops_.push_back(pk);
-      xin = packed;
+      xin = emit_input_pack(c, x, icin);
+      ldin = icin;
     }
     const int icp = conv_igemm_icp(ks, icin, oc, split), taps = ks * ks;
     // Filters over the (zero-padded) input channels icin, then packed per output tile (split: high and low planes).
@@ -913,7 +938,15 @@ void Net::build(const ModelDesc& m) {
     ops_.push_back(op);
   }
   stem_out.colbias = gbias;
-  ss_[0].producer = emit_conv(m.stem, d_bin_, 0, true, stem_out);
+  if (stem_junction_fits(m, stem_out)) {
+    // Held back: the first block's entry convolution joins the stem (its consume attaches the stem's emission).
+    int icin = 0;
+    const void* packed = emit_input_pack(m.stem, d_bin_, icin);
+    pend_.reset(new PendingExit{&m.stem, packed, nullptr, icin, std::make_shared<ConvOut>(stem_out), true});
+    ss_[0].producer = pend_->out;
+  } else {
+    ss_[0].producer = emit_conv(m.stem, d_bin_, 0, true, stem_out);
+  }
 
   // --- Blocks. ---
   // The trunk's last exit may join the heads' p1 | g1 | v1 convolution in one junction launch (16-bit handles, a

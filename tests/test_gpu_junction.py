@@ -1,12 +1,14 @@
 """The nested-bottleneck junction (one block's exit 1x1 convolution, 192 -> 384 into the trunk, and the next block's
 entry 1x1, 384 -> 192, in one launch: launch_junction, kgx_junction.hip), and the head junction (the last block's
-exit and the heads' p1 | g1 | v1 1x1, 384 -> 96, where the trunk ends and is not written), through the C ABI:
+exit and the heads' p1 | g1 | v1 1x1, 384 -> 96, where the trunk ends and is not written), and the stem junction
+(the network's stem, a 3x3 convolution of the packed input into the trunk, and the first block's entry 1x1), through
+the C ABI:
 - bit for bit equal to the two separate split-operand launches it replaces (KGX_JUNCTION=0 plans those), on f16 and
   bf16 handles, at a ragged batch (tiles past the last pixel) and at batch 32, with gpool inner blocks between, for
   mish nets and (the run-time activation kernel) ReLU nets;
 - the junction net against the float64 oracle and the 16-bit network (the bounds of test_gpu_parity.py);
-- the planning: a net of n nested blocks over 384 / 192 channels runs n - 1 junctions, one head junction and no
-  separate 1x1 but the first block's entry."""
+- the planning: a net of n nested blocks over 384 / 192 channels runs a stem junction, n - 1 junctions, one head
+  junction and no separate 1x1 or stem convolution."""
 
 import numpy as np
 import pytest
@@ -53,10 +55,12 @@ def test_junction_equals_the_two_separate_launches(kgx, synth, monkeypatch, prec
     assert pf["conv1x1_junction"]["launches"] == 3 and "conv1x1_junction" not in ps
     assert pf["head_junction"]["launches"] == 1 and "head_1x1" not in pf
     assert ps["head_1x1"]["launches"] == 1 and "head_junction" not in ps
-    # the separate plan's 1x1s: four entries and four exits; the junction plan keeps only the first entry
+    assert pf["stem_junction"]["launches"] == 1 and "conv3x3_n96" not in pf
+    assert ps["conv3x3_n96"]["launches"] == 1 and "stem_junction" not in ps
+    # the separate plan's 1x1s: four entries and four exits; the junction plan keeps none
     sep_1x1 = sum(v["launches"] for k, v in ps.items() if k.startswith("conv1x1_split"))
     fused_1x1 = sum(v["launches"] for k, v in pf.items() if k.startswith("conv1x1_split"))
-    assert sep_1x1 == 8 and fused_1x1 == 1, (ps.keys(), pf.keys())
+    assert sep_1x1 == 8 and fused_1x1 == 0, (ps.keys(), pf.keys())
     assert np.all(np.isfinite(fused))
     assert np.array_equal(fused, sep), f"{prec} batch {batch}: max diff {np.abs(fused - sep).max():.3e}"
 
@@ -69,6 +73,7 @@ def test_junction_net_matches_oracle(kgx, synth, oracle, monkeypatch, prec):
     sp, gl, _ = synth.make_inputs(6, 13, board_sizes=[19, 13, 9, 19, 19, 5])
     out, prof, net = run(kgx, mb, 6, prec, sp, gl, monkeypatch, True)
     assert prof["conv1x1_junction"]["launches"] == 2 and prof["head_junction"]["launches"] == 1
+    assert prof["stem_junction"]["launches"] == 1
     ref = oracle.Model(mb).forward(sp[rows], gl[rows])
     check(out[rows], ref, net.P, net.S, prec, f"junction net", emulated(oracle, mb, prec, sp[rows], gl[rows]))
 
@@ -84,7 +89,8 @@ def test_head_junction_only_for_96_head_channels(kgx, synth, monkeypatch):
     fused, pf, _ = run(kgx, mb, 5, "f16", sp, gl, monkeypatch, True)
     sep, _, _ = run(kgx, mb, 5, "f16", sp, gl, monkeypatch, False)
     assert pf["conv1x1_junction"]["launches"] == 1 and "head_junction" not in pf and pf["head_1x1"]["launches"] == 1
-    assert sum(v["launches"] for k, v in pf.items() if k.startswith("conv1x1_split")) == 2
+    assert pf["stem_junction"]["launches"] == 1
+    assert sum(v["launches"] for k, v in pf.items() if k.startswith("conv1x1_split")) == 1
     assert np.array_equal(fused, sep)
 
 
