@@ -35,7 +35,8 @@ def run(kgx, mb, batch, prec, sp, gl, monkeypatch, tile):
 
 
 @pytest.mark.parametrize("prec,batch,act", [("f16", 5, "ACTIVATION_MISH"), ("bf16", 7, "ACTIVATION_MISH"),
-                                            ("f16", 32, "ACTIVATION_MISH"), ("f16", 3, "ACTIVATION_RELU")])
+                                            ("f16", 32, "ACTIVATION_MISH"), ("f16", 3, "ACTIVATION_RELU"),
+                                            ("f16", 1, "ACTIVATION_MISH")])
 def test_gpool_tile_equals_the_row_program(kgx, synth, monkeypatch, prec, batch, act):
     print(f"gpool tile vs row program: {prec}, batch {batch}, {act}", flush=True)
     mb = synth.write_model(gpool_arch(synth, act), 12)

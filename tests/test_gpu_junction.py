@@ -44,7 +44,7 @@ def run(kgx, mb, batch, prec, sp, gl, monkeypatch, junction):
 
 @pytest.mark.parametrize("prec,batch,act", [("f16", 5, "ACTIVATION_MISH"), ("bf16", 5, "ACTIVATION_MISH"),
                                             ("f16", 32, "ACTIVATION_MISH"), ("bf16", 32, "ACTIVATION_MISH"),
-                                            ("f16", 7, "ACTIVATION_RELU")])
+                                            ("f16", 7, "ACTIVATION_RELU"), ("f16", 1, "ACTIVATION_MISH")])
 def test_junction_equals_the_two_separate_launches(kgx, synth, monkeypatch, prec, batch, act):
     """(ReLU nets run the junction's kernel that takes the emission's activation at run time.)"""
     print(f"junction vs separate launches: {prec}, batch {batch}, {act}", flush=True)
