@@ -828,35 +828,55 @@ void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const v
 // compute-type NHWC rows of ldo channels (zero beyond nin, 16-byte stores), and the board statistics of
 // launch_mask_prep: mask = plane 0, area = its sum, s1 = (sqrt(area) - 14) 0.1, s2 = (sqrt(area) - 14)^2 0.01 - 0.1.
 // Workgroups (b, 1) compute the row's global-input bias of the stem instead (when `gl.W` is set).
+constexpr int IP_C = 32, IP_G = 32;  // the input packing's most planes (packed channels) and globals
+
 template <typename T>
 __global__ __launch_bounds__(384) void input_prep_kernel(const float* __restrict__ bin, int nin, T* __restrict__ out,
                                                          int ldo, float* __restrict__ mask, float* __restrict__ area,
                                                          float* __restrict__ s1, float* __restrict__ s2,
                                                          InputGlobal gl) {
   const int b = blockIdx.x, p = threadIdx.x;
+  // Every load is issued before any is used, from clamped (in-range) indices with no branch around it, so that a
+  // thread waits for one round trip instead of one per load; the values past the real ones are then replaced.
   if (blockIdx.y == 1) {
+    // Up to IP_G globals in flight per output; the sum runs over i < nglob in order, as one multiply-add each.
     for (int o = p; o < gl.C; o += 384) {
+      float g[IP_G], w[IP_G];
+#pragma unroll
+      for (int i = 0; i < IP_G; i++) {
+        const int ic = min(i, gl.nglob - 1);
+        g[i] = gl.glob[(size_t)b * gl.nglob + ic];
+        w[i] = gl.W[(size_t)ic * gl.C + o];
+      }
       float acc = 0.f;
-      for (int i = 0; i < gl.nglob; i++) acc += gl.glob[(size_t)b * gl.nglob + i] * gl.W[(size_t)i * gl.C + o];
+#pragma unroll
+      for (int i = 0; i < IP_G; i++)
+        if (i < gl.nglob) acc += g[i] * w[i];
       gl.out[(size_t)b * gl.C + o] = acc;
     }
     return;
   }
   __shared__ float red[6];
-  const float* src = bin + (size_t)b * nin * HW + p;
+  const float* src = bin + (size_t)b * nin * HW + min(p, HW - 1);
   float mk = 0.f;
+  float v[IP_C];
+#pragma unroll
+  for (int c = 0; c < IP_C; c++) v[c] = src[(size_t)min(c, nin - 1) * HW];
+#pragma unroll
+  for (int c = 0; c < IP_C; c++)
+    if (c >= nin) v[c] = 0.f;
   if (p < HW) {
     T* o = out + ((size_t)b * HW + p) * ldo;
-    for (int c0 = 0; c0 < ldo; c0 += 8) {
-      float v[8];
 #pragma unroll
-      for (int k = 0; k < 8; k++) v[k] = c0 + k < nin ? src[(size_t)(c0 + k) * HW] : 0.f;
-      T t[8];
+    for (int c0 = 0; c0 < IP_C; c0 += 8) {
+      if (c0 < ldo) {
+        T t[8];
 #pragma unroll
-      for (int k = 0; k < 8; k++) t[k] = to_t<T>(v[k]);
-      *(u32x4*)(o + c0) = *(const u32x4*)t;
-      if (c0 == 0) mk = v[0];
+        for (int k = 0; k < 8; k++) t[k] = to_t<T>(v[c0 + k]);
+        *(u32x4*)(o + c0) = *(const u32x4*)t;
+      }
     }
+    mk = v[0];
     mask[(size_t)b * HW + p] = mk;
   }
   float sum = mk;
@@ -875,8 +895,9 @@ __global__ __launch_bounds__(384) void input_prep_kernel(const float* __restrict
 
 void launch_input_prep(int prec, const float* bin, int nin, void* out, int ldo, float* mask, float* area, float* s1,
                        float* s2, int B, hipStream_t s, const InputGlobal& gl) {
-  if (ldo % 8 != 0 || ldo < nin) throw std::runtime_error("input_prep: bad packed channel count");
-  if (gl.W && (!gl.glob || !gl.out || gl.C < 1 || gl.nglob < 0))
+  if (ldo % 8 != 0 || ldo < nin || ldo > IP_C || nin < 1)
+    throw std::runtime_error("input_prep: bad packed channel count");
+  if (gl.W && (!gl.glob || !gl.out || gl.C < 1 || gl.nglob < 1 || gl.nglob > IP_G))
     throw std::runtime_error("input_prep: bad global-input bias arguments");
   const dim3 grid(B, gl.W ? 2 : 1);
   if (prec == PREC_F16)

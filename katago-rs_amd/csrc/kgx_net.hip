@@ -285,8 +285,9 @@ bool Net::igemm_eligible(const ConvDesc& c, bool nchw, int ldx, const ConvOut& o
   const bool k3 = c.ky == 3 && c.kx == 3 && c.dy == 1 && c.dx == 1, k1 = c.ky == 1 && c.kx == 1;
   const bool strides4 = (!o.y || o.ldy % 4 == 0) && (!o.yt || o.ldyt % 4 == 0) &&
                         (!o.colbias || o.ld_colbias % 4 == 0) && (!o.emit.scale || o.emit.ld % 4 == 0);
+  // (The network input is packed by input_prep_kernel, up to 32 planes.)
   return conv_mode_ == CONV_IGEMM && (k3 || k1) && c.oc % 4 == 0 && strides4 &&
-         (nchw || (c.ic % 8 == 0 && ldx % 8 == 0));
+         (nchw ? c.ic <= 32 : c.ic % 8 == 0 && ldx % 8 == 0);
 }
 
 // The network input planes packed once into compute-type NHWC rows of icin = round_up(ic, 8) channels (0/1 planes
@@ -906,7 +907,7 @@ void Net::build(const ModelDesc& m) {
   // (bin2onnx.py:1477-1488), one workgroup per row. Without a metadata encoder, and when the stem packs its
   // input planes (implicit GEMM), the input packing launch computes it (one launch less).
   float* gbias = alloc_f((size_t)max_batch_ * C);
-  if (m.meta_version == 0 && nglob_ > 0 && igemm_eligible(m.stem, true, 0, stem_out)) {
+  if (m.meta_version == 0 && nglob_ > 0 && nglob_ <= 32 && igemm_eligible(m.stem, true, 0, stem_out)) {
     stem_glob_.glob = d_glob_; stem_glob_.nglob = nglob_;
     stem_glob_.W = upload_f(m.stem_mm.w); stem_glob_.C = C;
     stem_glob_.out = gbias;
