@@ -465,7 +465,8 @@ __global__ __launch_bounds__(256) void bias_act_kernel(const float* __restrict__
   if (c >= C || m >= rows) return;
   float a = x[(size_t)m * ldx + c];
   if (prebias) a += prebias[(size_t)(m / HW) * ldpb + c];
-  out[(size_t)m * ldo + c] = to_t<T>(act_rt(a * scale[c] + bias[c], act) * mask[m]);
+  const float z = a * scale[c] + bias[c];
+  out[(size_t)m * ldo + c] = to_t<T>(sizeof(T) == 2 ? act16_rt(z, act, mask[m]) : act_rt(z, act) * mask[m]);
 }
 
 // Eight channels per thread: two 16-byte loads of x (and of the per-row bias), one 16-byte store of the result.
@@ -493,8 +494,9 @@ __global__ __launch_bounds__(256) void bias_act8_kernel(const float* __restrict_
   T t[8];
 #pragma unroll
   for (int e = 0; e < 4; e++) {
-    t[e] = to_t<T>(act_f<ACT>(a0[e] * s0[e] + b0[e]) * mk);
-    t[4 + e] = to_t<T>(act_f<ACT>(a1[e] * s1[e] + b1[e]) * mk);
+    const float x0 = a0[e] * s0[e] + b0[e], x1 = a1[e] * s1[e] + b1[e];
+    t[e] = to_t<T>(sizeof(T) == 2 ? act16<ACT>(x0, mk) : act_f<ACT>(x0) * mk);
+    t[4 + e] = to_t<T>(sizeof(T) == 2 ? act16<ACT>(x1, mk) : act_f<ACT>(x1) * mk);
   }
   *(u32x4*)(out + (size_t)m * ldo + c) = *(const u32x4*)t;
 }

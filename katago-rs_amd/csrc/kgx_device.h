@@ -70,6 +70,35 @@ __device__ __forceinline__ float act_rt(float a, int kind) {
   }
 }
 
+// act(a) * mk for a value stored as a 16-bit operand with no low plane. Mish is the same function as act_f's,
+// written as b - 2 b q with b = a * mk, q = 1 / (e (e + 2) + 2), e = exp(a): eight instructions where act_f's form
+// and the mask take thirteen. It needs no clamp or select: a large a gives e = inf, q = 0 and the result b. For
+// negative a the difference cancels, an absolute error of a few float ulps of a, far below the 16-bit rounding that
+// follows. The result is pinned as a float (an empty asm), so that no kernel fuses the last multiply-add into the
+// conversion to 16 bits: one rounding there instead of two would make kernels that emit the same activation differ
+// in the last bit.
+template <int ACT>
+__device__ __forceinline__ float act16(float a, float mk) {
+  if constexpr (ACT == ACT_MISH) {
+    const float e = __expf(a);
+    const float q = __builtin_amdgcn_rcpf(__builtin_fmaf(e, e + 2.f, 2.f));
+    const float b = a * mk;
+    float r = __builtin_fmaf(-2.f * b, q, b);
+    asm("" : "+v"(r));
+    return r;
+  } else {
+    return act_f<ACT>(a) * mk;
+  }
+}
+__device__ __forceinline__ float act16_rt(float a, int kind, float mk) {
+  switch (kind) {
+    case ACT_RELU: return act16<ACT_RELU>(a, mk);
+    case ACT_MISH: return act16<ACT_MISH>(a, mk);
+    case ACT_SILU: return act16<ACT_SILU>(a, mk);
+    default: return a * mk;
+  }
+}
+
 template <typename T>
 __device__ __forceinline__ T to_t(float v) { return (T)v; }
 
@@ -104,7 +133,9 @@ __device__ __forceinline__ void conv_store(const ConvOut& o, int m, int n, float
     if (!o.y_dead) *p = v;
   }
   if (o.emit.scale) {
-    const float a = act_rt(v * o.emit.scale[n] + o.emit.bias[n], o.emit.act) * o.emit.mask[m];
+    const float x = v * o.emit.scale[n] + o.emit.bias[n];
+    const float a = sizeof(T) == 2 && !o.emit.out_lo ? act16_rt(x, o.emit.act, o.emit.mask[m])
+                                                     : act_rt(x, o.emit.act) * o.emit.mask[m];
     const T hi = to_t<T>(a);
     ((T*)o.emit.out)[(size_t)m * o.emit.ld + n] = hi;
     if (o.emit.out_lo) ((T*)o.emit.out_lo)[(size_t)m * o.emit.ld + n] = to_t<T>(a - (float)hi);
@@ -155,11 +186,13 @@ __device__ __forceinline__ void conv_store4(const ConvOut& o, int m, int n, floa
   }
   if (fl & SF_EMIT) {
     float t[4];
+    // (16-bit operands without a low plane take act16's form.)
+    const bool h16 = sizeof(T) == 2 && !(fl & SF_LO);
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       const float a = v[e] * es[e] + eb[e];
-      if constexpr (ACT >= 0) t[e] = act_f<ACT>(a) * mk;
-      else t[e] = act_rt(a, o.emit.act) * mk;
+      if constexpr (ACT >= 0) t[e] = h16 ? act16<ACT>(a, mk) : act_f<ACT>(a) * mk;
+      else t[e] = h16 ? act16_rt(a, o.emit.act, mk) : act_rt(a, o.emit.act) * mk;
     }
     store4<T>((T*)o.emit.out + (size_t)m * o.emit.ld + n, t[0], t[1], t[2], t[3]);
     if (fl & SF_LO) {

@@ -493,7 +493,7 @@ __global__ __launch_bounds__(C::WM * C::WN * 64, C::MINW) void gemm_kernel(const
           floatx4 x = *(const floatx4*)(Et + r * ELD + c);
           if constexpr (EPI == EPI_YTMISH) {
 #pragma unroll
-            for (int q = 0; q < 4; q++) x[q] = act_f<ACT_MISH>(x[q]);
+            for (int q = 0; q < 4; q++) x[q] = sizeof(T) == 2 ? act16<ACT_MISH>(x[q], 1.f) : act_f<ACT_MISH>(x[q]);
           }
           store4<T>((T*)o.yt + (size_t)m * o.ldyt + n, x[0], x[1], x[2], x[3]);
         }

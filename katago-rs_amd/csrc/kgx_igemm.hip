@@ -473,7 +473,11 @@ __global__ __launch_bounds__(C::NT, C::MINW) void igemm_kernel(const T* __restri
     default: break;
   }
   const int pfv = l2_touch(o.pf, quiet ? o.pf_bytes : 0, tid);
-  switch (scase) {
+  // With pooling partials the regular columns are a plain float output (the host admits no other), or nothing when
+  // the stream is dead: only that path is built, which keeps the kernel's code to what it runs.
+  if constexpr (POOL) {
+    if (scase == SF_Y) store_rows(std::integral_constant<int, ACT_ID>{}, std::integral_constant<int, SF_Y>{});
+  } else switch (scase) {
     // a global-pooling block's first conv (pooling partials); a block's first conv; a nested block's entry 1x1;
     // a block's last conv, its stream's last, into a split 1x1
     case SF_Y: store_rows(std::integral_constant<int, ACT_ID>{}, std::integral_constant<int, SF_Y>{}); break;

@@ -458,9 +458,14 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
 #pragma unroll
             for (int e = 0; e < 8; e++) t[e] = act_f<ACT_RELU>(t[e]) * m;
             break;
-          case ACT_MISH:
+          case ACT_MISH:  // (16-bit outputs in act16's form)
+            if (E.prec != PREC_F32) {
 #pragma unroll
-            for (int e = 0; e < 8; e++) t[e] = act_f<ACT_MISH>(t[e]) * m;
+              for (int e = 0; e < 8; e++) t[e] = act16<ACT_MISH>(t[e], m);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; e++) t[e] = act_f<ACT_MISH>(t[e]) * m;
+            }
             break;
           case ACT_SILU:
 #pragma unroll
@@ -700,7 +705,7 @@ __global__ __launch_bounds__(GT_NT) void gpool_tile_kernel(GpoolTile a, int M) {
 #pragma unroll
       for (int e = 0; e < 8; e++) tv[e] = (ex[k][e >> 2][e & 3] + rb[r * SH + cl + e]) * esb[cl + e] + esb[SH + cl + e];
 #pragma unroll
-      for (int e = 0; e < 8; e++) tv[e] = ACT == ACT_ID ? tv[e] * mm : act_f<ACT>(tv[e]) * mm;
+      for (int e = 0; e < 8; e++) tv[e] = ACT == ACT_ID ? tv[e] * mm : act16<ACT>(tv[e], mm);
       u32x4 w;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
@@ -1458,7 +1463,7 @@ __global__ __launch_bounds__(256) void ffn_act_kernel(const float* __restrict__ 
   const float a = u[r * ldu + f];
   float v;
   if constexpr (GATED) v = act_f<ACT_SILU>(a) * u[r * ldu + F + f];
-  else v = act_f<ACT_MISH>(a);
+  else v = sizeof(T) == 2 ? act16<ACT_MISH>(a, 1.f) : act_f<ACT_MISH>(a);  // as the fused FFN epilogue
   h[r * ldh + f] = to_t<T>(v);
 }
 
