@@ -163,7 +163,7 @@ __device__ __forceinline__ void store4(T* p, float a, float b, float c, float d)
 enum StoreFlags {
   SF_COLBIAS = 1, SF_ROWMASK = 2, SF_YT = 4, SF_Y = 8, SF_ACC = 16, SF_YDEAD = 32, SF_EMIT = 64, SF_LO = 128
 };
-__device__ __forceinline__ int store_flags(const ConvOut& o) {
+__host__ __device__ inline int store_flags(const ConvOut& o) {
   return (o.colbias ? SF_COLBIAS : 0) | (o.rowmask ? SF_ROWMASK : 0) | (o.yt ? SF_YT : 0) | (o.y ? SF_Y : 0) |
          (o.y && o.accumulate ? SF_ACC : 0) | (o.y && o.y_dead ? SF_YDEAD : 0) | (o.emit.scale ? SF_EMIT : 0) |
          (o.emit.scale && o.emit.out_lo ? SF_LO : 0);
