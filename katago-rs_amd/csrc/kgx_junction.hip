@@ -86,8 +86,9 @@ constexpr int SR = JR + 40, SRB = 80;        // the stem's staged pixel rows (ti
 // ACT1: the exit's emission activation (ACT_MISH), or -1: the one eo names, chosen per value at run time. NO: the
 // entry's outputs (192 or 96). A trunk that ends here (eo.y_dead) is read and not stored. STEM: the exit is the
 // network's stem (X: packed input rows of ldx <= 32 channels; eo adds the row's global bias, eo.colbias, instead of
-// a residual).
-template <typename T, int ACT1, int NO, bool STEM>
+// a residual). SC2 >= 0: the entry's store case (store_flags of no: SF_Y | SF_EMIT emitting mish, or SF_Y), fixed by
+// the launch so that the kernel holds only that store path; -1: chosen from the arguments.
+template <typename T, int ACT1, int NO, bool STEM, int SC2 = -1>
 __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ X, const T* __restrict__ Xlo, int ldx,
                                                           const T* __restrict__ W, int M, ConvOut eo, ConvOut no) {
   typedef typename std::conditional<std::is_same<T, f16>::value, half8, bf16x8>::type frag_t;
@@ -384,7 +385,8 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
       for (int j = 0; j < 3; j++) acc2[i][j] = mfma(ah[s][i], b2[p % NS][j][0], acc2[i][j]);
   };
   int pfv;
-  const bool fast = fl2 == (SF_Y | SF_EMIT) && no.emit.act == ACT_MISH;  // the entry epilogue's path
+  // The entry epilogue's path: a specialized store (which loads nothing more), or the general one.
+  const bool fast = SC2 >= 0 || (fl2 == (SF_Y | SF_EMIT) && no.emit.act == ACT_MISH);
   auto run = [&](auto act_c) {
 #pragma unroll
     for (int e = 0; e < E1; e++) epi1(act_c, 0, e);
@@ -440,10 +442,12 @@ __global__ __launch_bounds__(JNT, 1) void junction_kernel(const T* __restrict__ 
         const int n = c2 + 4 * G2 * q;
         floatx4 sum = *(const floatx4*)(C2 + p * LD2 + n);
         sum += *(const floatx4*)(C2 + (JR + p) * LD2 + n);
-        if (fast) {
+        if constexpr (SC2 == SF_Y) {
+          conv_store4<T, ACT_ID, SF_Y>(no, m, n, sum, floatx4{0.f, 0.f, 0.f, 0.f}, 1.f, es2[q], eb2[q], mk2[e]);
+        } else if (SC2 == (SF_Y | SF_EMIT) || fast) {
           conv_store4<T, ACT_MISH, SF_Y | SF_EMIT>(no, m, n, sum, floatx4{0.f, 0.f, 0.f, 0.f}, 1.f, es2[q], eb2[q],
                                                    mk2[e]);
-        } else {
+        } else if constexpr (SC2 < 0) {
           const floatx4 yacc = (fl2 & SF_ACC) ? *(const floatx4*)(no.y + (size_t)m * no.ldy + n)
                                               : floatx4{0.f, 0.f, 0.f, 0.f};
           conv_store4<T>(no, m, n, sum, yacc, (fl2 & SF_ROWMASK) ? no.rowmask[m] : 1.f, es2[q], eb2[q], mk2[e]);
@@ -522,11 +526,18 @@ void launch_junction(int prec, const void* x, const void* x_lo, int ldx, const v
     throw std::runtime_error("junction: unsupported entry outputs");
   const int M = B * HW;
   const bool mish = eo.emit.act == ACT_MISH;
+  // The entry's store case for a kernel that holds only that store path (the networks' two), else -1.
+  const int fl2 = store_flags(no);
+  const int sc2 = !mish ? -1
+                  : entry_oc == kJunctionInner && fl2 == (SF_Y | SF_EMIT) && no.emit.act == ACT_MISH ? SF_Y | SF_EMIT
+                  : entry_oc == kJunctionHead && fl2 == SF_Y ? SF_Y : -1;
   auto go = [&](auto tc, auto noc) {
     typedef decltype(tc) TT;
     constexpr int N = decltype(noc)::value;
-    launch_k(mish ? junction_kernel<TT, ACT_MISH, N, false> : junction_kernel<TT, -1, N, false>, junction_grid(M),
-             JNT, 0, s, (const TT*)x, (const TT*)x_lo, ldx, (const TT*)w, M, eo, no);
+    constexpr int SPEC2 = N == kJunctionInner ? SF_Y | SF_EMIT : SF_Y;
+    launch_k(!mish ? junction_kernel<TT, -1, N, false>
+                   : sc2 >= 0 ? junction_kernel<TT, ACT_MISH, N, false, SPEC2> : junction_kernel<TT, ACT_MISH, N, false>,
+             junction_grid(M), JNT, 0, s, (const TT*)x, (const TT*)x_lo, ldx, (const TT*)w, M, eo, no);
   };
   typedef std::integral_constant<int, kJunctionInner> Inner;
   typedef std::integral_constant<int, kJunctionHead> Head;
@@ -558,9 +569,12 @@ void launch_stem_junction(int prec, const void* x, int ldx, const void* w, const
     throw std::runtime_error("stem junction: unsupported entry outputs");
   const int M = B * HW;
   const bool mish = eo.emit.act == ACT_MISH;
+  const bool spec2 = mish && store_flags(no) == (SF_Y | SF_EMIT) && no.emit.act == ACT_MISH;
   auto go = [&](auto tc) {
     typedef decltype(tc) TT;
-    launch_k(mish ? junction_kernel<TT, ACT_MISH, kJunctionInner, true> : junction_kernel<TT, -1, kJunctionInner, true>,
+    launch_k(!mish ? junction_kernel<TT, -1, kJunctionInner, true>
+                   : spec2 ? junction_kernel<TT, ACT_MISH, kJunctionInner, true, SF_Y | SF_EMIT>
+                           : junction_kernel<TT, ACT_MISH, kJunctionInner, true>,
              junction_grid(M), JNT, 0, s, (const TT*)x, (const TT*)x, ldx, (const TT*)w, M, eo, no);
   };
   if (prec == PREC_F16) go(f16());
