@@ -682,8 +682,22 @@ __global__ __launch_bounds__(GT_NT) void gpool_tile_kernel(GpoolTile a, int M) {
   for (int task = tid; task < nrow * SH * GT_KS; task += GT_NT) {
     const int r = task / (SH * GT_KS), rem = task - r * SH * GT_KS, ks = rem / SH, o = rem - ks * SH;
     const float* fr = feat + r * IC;
+    const float* wo = wl + o;
     float acc = 0.f;
-    for (int i = ks; i < IC; i += GT_KS) acc += fr[i] * wl[i * SH + o];
+    // Four inputs' LDS reads issued before their four multiply-adds (in input order), so that a thread waits for
+    // LDS once per four inputs instead of once per input.
+    int i = ks;
+    for (; i + 3 * GT_KS < IC; i += 4 * GT_KS) {
+      float f[4], w[4];
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        f[j] = fr[i + j * GT_KS];
+        w[j] = wo[(i + j * GT_KS) * SH];
+      }
+#pragma unroll
+      for (int j = 0; j < 4; j++) acc += f[j] * w[j];
+    }
+    for (; i < IC; i += GT_KS) acc += fr[i] * wo[i * SH];
     part[(r * GT_KS + ks) * SH + o] = acc;
   }
   __syncthreads();
