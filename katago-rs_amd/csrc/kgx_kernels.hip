@@ -499,8 +499,9 @@ __device__ void run_row_prog(const RowProg& P, int b, int split, int nsplit, flo
 // single program's last matmul.
 __global__ __launch_bounds__(RP_NT) void row_prog_kernel(RowProgs PS) {
   extern __shared__ float lds[];
-  if (PS.n > 1) run_row_prog(PS.p[blockIdx.y], blockIdx.x, 0, 1, lds);
-  else run_row_prog(PS.p[0], blockIdx.x, blockIdx.y, gridDim.y, lds);
+  // One call site, so that the program's code is in the kernel once.
+  const bool several = PS.n > 1;
+  run_row_prog(PS.p[several ? blockIdx.y : 0], blockIdx.x, several ? 0 : blockIdx.y, several ? 1 : gridDim.y, lds);
 }
 
 bool row_emit_fits(int OC, int splits) {
