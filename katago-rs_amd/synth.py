@@ -59,6 +59,7 @@ class Arch:
     policy_channels: int = 0           # v17 only (2 or 4); derived otherwise
     rope_theta: float = 100.0
     qk_gain: float = 1.0               # scale of the attention q and k projections (scores scale by its square)
+    mid_bn_gain: float = 1.0           # scale of ordinary residual blocks' mid batch-norm gamma and beta
 
 
 # Block specs:
@@ -222,12 +223,12 @@ class _Writer:
         self.floats(w.transpose(2, 3, 1, 0))
         return w
 
-    def bn(self, base, c):
+    def bn(self, base, c, gain=1.0):
         self.tok(self.name(base), c, 1e-5, 1, 1)
         mean = self.rng.normal(0.0, 0.1, c)
         var = self.rng.uniform(0.5, 1.5, c)
-        gamma = self.rng.uniform(0.8, 1.2, c)
-        beta = self.rng.normal(0.0, 0.1, c)
+        gamma = self.rng.uniform(0.8, 1.2, c) * gain
+        beta = self.rng.normal(0.0, 0.1, c) * gain
         self.floats(mean)
         self.floats(var)
         self.floats(gamma)
@@ -275,7 +276,7 @@ def _write_block(w: _Writer, arch: Arch, spec, c: int, gain: float) -> dict:
         w.tok("ordinary_block", w.name("res"))
         t["pre_bn"] = w.bn("bn", c); t["pre_act"] = w.act("act", a)
         t["regular"] = w.conv("conv", 3, c, cm)
-        t["mid_bn"] = w.bn("bn", cm); t["mid_act"] = w.act("act", a)
+        t["mid_bn"] = w.bn("bn", cm, gain=arch.mid_bn_gain); t["mid_act"] = w.act("act", a)
         t["final"] = w.conv("conv", 3, cm, c, gain=gain)
     elif kind == "gpool":
         cr, cg = spec[1], spec[2]

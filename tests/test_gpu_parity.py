@@ -198,6 +198,32 @@ def test_sharp_attention_matches_the_16bit_network(kgx, synth, oracle, prec, qk_
 
 
 @pytest.mark.parametrize("prec", ["f16", "bf16"])
+def test_mish_at_extreme_inputs_matches_the_16bit_network(kgx, synth, oracle, prec):
+    """16-bit emissions compute mish as b - 2 b q with b = a * mask, q = 1 / (e (e + 2) + 2), e = exp(a), with no
+    clamp or select: for a above 88.7, e overflows to infinity and q to 0, leaving b; for large negative a the two
+    terms cancel. The residual blocks' mid batch norm scaled 50x drives the second convolution's input activation
+    to |a| of about a hundred, so both regions occur on every board. Held to the 16-bit network (the oracle with
+    the same operand rounding) with the emulation bound, outputs finite; the absolute f16 bound does not apply to a
+    network this far from unit scale."""
+    import dataclasses
+    arch = dataclasses.replace(synth.tiny_nets()["t_res"], mid_bn_gain=50.0)
+    mb = synth.write_model(arch, 9)
+    sp, gl, _ = synth.make_inputs(5, 21, board_sizes=[19, 13, 9, 19, 7])
+    net = kgx.Net(mb)
+    h = kgx.Handle(net, 5, prec)
+    out = h.forward(sp, gl)
+    h.close()
+    ref = oracle.Model(mb).forward(sp, gl)
+    ref_q = emulated(oracle, mb, prec, sp, gl)
+    assert np.all(np.isfinite(out))
+    fmt = errors(ref_q, ref, net.P, net.S)
+    for k, (e, s) in errors(out, ref_q, net.P, net.S).items():
+        bound = 2.0 * fmt[k][0] + 1e-4 * max(1.0, s)
+        print(f"mid bn x50 [{prec}] {k}: |gpu - {prec} network| {e:.2e}, format {fmt[k][0]:.2e}, |ref| {s:.2e}")
+        assert e <= bound, f"mid bn x50 [{prec}] {k}: {e:.3e} > {bound:.3e}"
+
+
+@pytest.mark.parametrize("prec", ["f16", "bf16"])
 def test_gpool_widths_the_row_emission_does_not_fit(kgx, synth, oracle, prec):
     """A global-pooling block whose regular width has no share of a multiple of 8 channels (20): 16-bit handles
     then emit the biased mid activation with a separate bias_act launch instead of in the row program."""
