@@ -5,9 +5,11 @@
 // and tanh ownership from white's perspective). The legality of each move (history.is_legal plus any dagger ban)
 // is an input: it needs the rules engine, which stays with the caller.
 //
-// One workgroup of 384 threads per row: a thread per policy position (362) and per ownership point (361), block
-// reductions for the softmax's maximum and sum, and thread 0 for the scalar value and score fields, in double
-// as the reference computes them.
+// One workgroup of 384 threads per row: a thread per policy position (362) and per ownership point (361), a block
+// reduction for the softmax's maximum, thread 0 for its sum (in position order) and for the scalar value and score
+// fields, in double as the reference computes them. The arithmetic is the reference's operation by operation (this
+// file is compiled without contraction into fused multiply-adds, as Rust does not contract), with glibc's expf and a
+// correctly rounded tanhf, so that the results equal the reference's bit for bit.
 #include "kgx_device.h"
 
 #include <cmath>
@@ -31,6 +33,61 @@ __device__ __forceinline__ int sym_dst(int h, int w, int sym) {
 }
 
 __device__ __forceinline__ double soft_plus(double x) { return x > 40.0 ? x : log(1.0 + exp(x)); }
+
+// expf as glibc computes it (the reference calls its port of glibc's, crates/katago-core/src/port/math.rs:634-680,
+// so the policy probabilities match bit for bit): exp(x) = 2^(k/32) 2^(r/32) with x 32/ln 2 = k + r, r in [-1/2, 1/2]
+// (found with fused multiply-adds in double), 2^(k/32) from a table of the doubles nearest 2^(i/32) (the entry minus
+// i 2^47, so that adding k 2^47 puts k / 32 into the exponent) and 2^(r/32) from a cubic in r with the minimax
+// coefficients of ARM's optimized-routines expf; then one rounding to float. Over every float in [-110, 90] it
+// gives the host glibc's expf bit for bit. Below log(2^-150) the result is 0, up to log(2^-149) the least subnormal,
+// as glibc's underflow paths return.
+__device__ const unsigned long long kExp2fTab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
+};
+__device__ float expf_glibc(float x) {
+  const unsigned u = __float_as_uint(x), abstop = (u >> 20) & 0x7ff;
+  if (abstop >= (0x42b00000u >> 20)) {  // |x| >= 88, or x is not finite
+    if (u == 0xff800000u) return 0.f;
+    if (abstop >= (0x7f800000u >> 20)) return x + x;
+    if (x > __uint_as_float(0x42b17217u)) return __uint_as_float(0x7f800000u);
+    if (x < __uint_as_float(0xc2cff1b4u)) return 0.f;
+    if (x < __uint_as_float(0xc2ce8ecfu)) return __uint_as_float(1u);
+  }
+  const double inv_ln2_n = 0x1.71547652b82fep+5, shift = 0x1.8p+52;
+  const double xd = (double)x;
+  double kd = __builtin_fma(inv_ln2_n, xd, shift);
+  const unsigned long long ki = (unsigned long long)__double_as_longlong(kd);
+  kd -= shift;
+  const double r = __builtin_fma(inv_ln2_n, xd, -kd);
+  const double sc = __longlong_as_double((long long)(kExp2fTab[ki % 32] + (ki << 47)));
+  const double z = __builtin_fma(0x1.c6af84b912394p-5 / 32768.0, r, 0x1.ebfce50fac4f3p-3 / 1024.0);
+  const double r2 = r * r;
+  double y = __builtin_fma(0x1.62e42ff0c52d6p-1 / 32.0, r, 1.0);
+  y = __builtin_fma(z, r2, y);
+  y *= sc;
+  return (float)y;
+}
+
+// tanhf correctly rounded, as the reference's (port/math.rs:804-853, glibc 2.44's): the double tanh rounded to
+// float. It differs from the correct rounding only where the double's own error (an ulp or two of a double) straddles
+// a float rounding boundary, about one value in 2^27.
+__device__ float tanhf_cr(float x) {
+  const float ax = fabsf(x);
+  if (!(ax >= 0x1p-13f && ax < 10.0f)) {
+    if (x != x) return x + x;
+    if (ax < 0x1p-13f) return x;  // tanh(x) = x - x^3/3 + ... rounds to x
+    return x > 0.f ? 1.f : -1.f;   // 1 - tanh(x) < 2^-27: rounds to 1
+  }
+  const float t = (float)tanh((double)ax);
+  return x > 0.f ? t : -t;
+}
 
 // Block reductions over the 6 waves.
 __device__ float block_max(float v, float* red) {
@@ -64,7 +121,7 @@ __global__ __launch_bounds__(PNT) void post_kernel(const float* __restrict__ raw
   const PostRow pr = rows[r];
   const float* row = raw + (size_t)r * row_len;
   const float* own_raw = row + m.P * NPOL + 3 + m.S;
-  __shared__ float pol[NPOL], own[HW], red[PNT / 64];
+  __shared__ float pol[NPOL], own[HW], red[PNT / 64 + NPOL + 2];  // (red: the block reductions, then the numerators)
 
   // copy_outputs: the optimism mix of the first two policy channels (P = 2, or P = 4 from version 16) and the
   // inverse symmetry of the policy's board part and of the ownership.
@@ -88,22 +145,27 @@ __global__ __launch_bounds__(PNT) void post_kernel(const float* __restrict__ raw
   // NNEvaluator's policy: illegal moves at -1e30, the others scaled by outputScaleMultiplier / temperature; the
   // softmax over all positions; optionally the pass prior capped at 19x the other moves' sum (floored at 1e-20);
   // legal moves get p / sum (or 1 / #legal when everything rounded to 0), the others -1.
+  // The maximum starts at -1e25 and the sum is taken in position order by one thread, as the reference's loops
+  // (nneval.rs:1235-1262), so that every probability is the reference's to the bit.
   const bool lg = t < NPOL && legal[(size_t)r * NPOL + t] != 0;
   const float v = t < NPOL ? (lg ? pol[t] * pr.policy_scale : -1e30f) : -INFINITY;
-  const float mx = block_max(v, red);
+  const float mx = fmaxf(-1e25f, block_max(v, red));
   const float nlegal = block_sum(lg ? 1.f : 0.f, red);
-  float e = t < NPOL ? expf(v - mx) : 0.f;
-  float sum;
-  if (pr.passing_hacks) {
-    sum = block_sum(t < HW ? e : 0.f, red);
-    if (t == HW) e = fmaxf(1e-20f, fminf(e, sum * 19.f));
-    __syncthreads();
-    if (t == HW) red[0] = e;
-    __syncthreads();
-    sum += red[0];
-  } else {
-    sum = block_sum(e, red);
+  float e = t < NPOL ? expf_glibc(v - mx) : 0.f;
+  float* const es = red + PNT / 64;  // [NPOL] the numerators, then [1] the sum
+  if (t < NPOL) es[t] = e;
+  __syncthreads();
+  if (t == 0) {
+    float s = 0.f;
+    for (int i = 0; i < HW; i++) s += es[i];
+    float ep = es[HW];
+    if (pr.passing_hacks) ep = fmaxf(1e-20f, fminf(ep, s * 19.f));
+    es[NPOL] = ep;
+    es[NPOL + 1] = s + ep;
   }
+  __syncthreads();
+  if (t == HW) e = es[NPOL];
+  const float sum = es[NPOL + 1];
   float* o = out + (size_t)r * POST_LEN;
   if (t < NPOL) {
     float p;
@@ -119,7 +181,7 @@ __global__ __launch_bounds__(PNT) void post_kernel(const float* __restrict__ raw
     const int y = t / POS, x = t % POS;
     float w = 0.f;
     if (y < pr.board_y && x < pr.board_x) {
-      const float th = tanhf(own[t]);
+      const float th = tanhf_cr(own[t]);
       w = pr.white_to_move ? th : -th;
     }
     o[NPOL + 9 + t] = w;
