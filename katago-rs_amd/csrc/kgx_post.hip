@@ -11,6 +11,7 @@
 // file is compiled without contraction into fused multiply-adds, as Rust does not contract), with glibc's expf and a
 // correctly rounded tanhf, so that the results equal the reference's bit for bit.
 #include "kgx_device.h"
+#include "kgx_expf.h"
 
 #include <cmath>
 
@@ -36,21 +37,9 @@ __device__ __forceinline__ double soft_plus(double x) { return x > 40.0 ? x : lo
 
 // expf as glibc computes it (the reference calls its port of glibc's, crates/katago-core/src/port/math.rs:634-680,
 // so the policy probabilities match bit for bit): exp(x) = 2^(k/32) 2^(r/32) with x 32/ln 2 = k + r, r in [-1/2, 1/2]
-// (found with fused multiply-adds in double), 2^(k/32) from a table of the doubles nearest 2^(i/32) (the entry minus
-// i 2^47, so that adding k 2^47 puts k / 32 into the exponent) and 2^(r/32) from a cubic in r with the minimax
-// coefficients of ARM's optimized-routines expf; then one rounding to float. Over every float in [-110, 90] it
-// gives the host glibc's expf bit for bit. Below log(2^-150) the result is 0, up to log(2^-149) the least subnormal,
-// as glibc's underflow paths return.
-__device__ const unsigned long long kExp2fTab[32] = {
-    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
-    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
-    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
-    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
-    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
-    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
-    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
-    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL,
-};
+// (found with fused multiply-adds in double), 2^(k/32) from a table and 2^(r/32) from a cubic (kgx_expf.h), then one
+// rounding to float. Below log(2^-150) the result is 0, up to log(2^-149) the least subnormal, as glibc's underflow
+// paths return. tests/expf_check.cpp checks the same steps and constants against the host's glibc expf.
 __device__ float expf_glibc(float x) {
   const unsigned u = __float_as_uint(x), abstop = (u >> 20) & 0x7ff;
   if (abstop >= (0x42b00000u >> 20)) {  // |x| >= 88, or x is not finite
@@ -60,16 +49,15 @@ __device__ float expf_glibc(float x) {
     if (x < __uint_as_float(0xc2cff1b4u)) return 0.f;
     if (x < __uint_as_float(0xc2ce8ecfu)) return __uint_as_float(1u);
   }
-  const double inv_ln2_n = 0x1.71547652b82fep+5, shift = 0x1.8p+52;
   const double xd = (double)x;
-  double kd = __builtin_fma(inv_ln2_n, xd, shift);
+  double kd = __builtin_fma(kgx_exp2f_invln2n, xd, kgx_exp2f_shift);
   const unsigned long long ki = (unsigned long long)__double_as_longlong(kd);
-  kd -= shift;
-  const double r = __builtin_fma(inv_ln2_n, xd, -kd);
-  const double sc = __longlong_as_double((long long)(kExp2fTab[ki % 32] + (ki << 47)));
-  const double z = __builtin_fma(0x1.c6af84b912394p-5 / 32768.0, r, 0x1.ebfce50fac4f3p-3 / 1024.0);
+  kd -= kgx_exp2f_shift;
+  const double r = __builtin_fma(kgx_exp2f_invln2n, xd, -kd);
+  const double sc = __longlong_as_double((long long)(kgx_exp2f_tab[ki % 32] + (ki << 47)));
+  const double z = __builtin_fma(kgx_exp2f_c0, r, kgx_exp2f_c1);
   const double r2 = r * r;
-  double y = __builtin_fma(0x1.62e42ff0c52d6p-1 / 32.0, r, 1.0);
+  double y = __builtin_fma(kgx_exp2f_c2, r, 1.0);
   y = __builtin_fma(z, r2, y);
   y *= sc;
   return (float)y;
