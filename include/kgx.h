@@ -314,6 +314,11 @@ int kg_gpool_tile_of(int pixels, int gpool_channels, int regular_channels, int w
  * launch touches into its XCD's L2 (workgroup g runs on XCD g mod 8; lines past the weights are not read). No
  * counterpart in the reference: the index map the kernels use, for host-side checks. */
 int kg_l2_touch_line(int grid, int workgroup, int thread, int* line);
+/* The transformer RMSNorm launch over `rows` token rows of `channels` channels, when the rows were written in row
+ * tiles of `region` rows (tile r on XCD r mod 8; 0: no such tiles): its workgroup count, and the rows
+ * [first_row, first_row + count) of workgroup `workgroup` (count 0 when it exits at once). No counterpart in the
+ * reference: the index map its kernel uses, for host-side checks. */
+int kg_rmsnorm_rows_of(int rows, int channels, int region, int workgroup, int* grid, int* first_row, int* count);
 
 #ifdef __cplusplus
 }

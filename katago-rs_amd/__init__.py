@@ -37,7 +37,7 @@ EXPORTS = [
     "kg_get_output", "kg_profile_enable", "kg_profile_reset", "kg_profile_read",
     "kg_model_version_features", "kg_meta_encoder_channels", "kg_copy_outputs", "kg_run_static",
     "kg_get_output_async", "kg_wait", "kg_get_output_eval", "kg_post_outputs",
-    "kg_conv_geometry", "kg_conv_tile_of", "kg_conv_weight_load", "kg_conv_weight_chunk", "kg_junction_tile_of", "kg_gpool_tile_of", "kg_l2_touch_line",
+    "kg_conv_geometry", "kg_conv_tile_of", "kg_conv_weight_load", "kg_conv_weight_chunk", "kg_junction_tile_of", "kg_gpool_tile_of", "kg_l2_touch_line", "kg_rmsnorm_rows_of",
     "kg_featurize", "kg_featurize_rows", "kg_evaluate_positions",
 ]
 # Completion callback of kg_get_output_async: (user, status).
@@ -217,6 +217,7 @@ def lib():
         L.kg_junction_tile_of.argtypes = [ci, ci, ctypes.POINTER(ci), ctypes.POINTER(ci)]
         L.kg_gpool_tile_of.argtypes = [ci, ci, ci, ci] + [ctypes.POINTER(ci)] * 4
         L.kg_l2_touch_line.argtypes = [ci, ci, ci, ctypes.POINTER(ci)]
+        L.kg_rmsnorm_rows_of.argtypes = [ci, ci, ci, ci] + [ctypes.POINTER(ci)] * 3
         _ = cf
         _lib = L
     return _lib
@@ -285,6 +286,14 @@ def l2_touch_line(grid: int, workgroup: int, thread: int) -> int:
     line = ctypes.c_int()
     _check(lib().kg_l2_touch_line(grid, workgroup, thread, ctypes.byref(line)))
     return line.value
+
+
+def rmsnorm_rows_of(rows: int, channels: int, region: int, workgroup: int):
+    """(workgroups of the RMSNorm launch, the first row of `workgroup`, its row count) when the rows were written in
+    row tiles of `region` rows on XCD (tile mod 8)."""
+    out = [ctypes.c_int() for _ in range(3)]
+    _check(lib().kg_rmsnorm_rows_of(rows, channels, region, workgroup, *[ctypes.byref(o) for o in out]))
+    return tuple(o.value for o in out)
 
 
 def conv_tile_of(ks: int, ic: int, oc: int, split: bool, pixels: int, workgroup: int):

@@ -591,6 +591,21 @@ int kg_l2_touch_line(int grid, int workgroup, int thread, int* line) {
   });
 }
 
+int kg_rmsnorm_rows_of(int rows, int channels, int region, int workgroup, int* grid, int* first_row, int* count) {
+  return guarded([&] {
+    if (!grid || !first_row || !count) throw std::runtime_error("null output");
+    if (rows < 1 || region < 0) throw std::runtime_error("bad row count or tile");
+    const int per_wg = kgx::rmsnorm_rows_per_workgroup(channels);
+    if (!per_wg) throw std::runtime_error("this channel count takes the scalar RMSNorm kernel");
+    if (region % per_wg) region = 0;
+    *grid = kgx::rmsnorm_grid(rows, region, per_wg);
+    if (workgroup < 0 || workgroup >= *grid) throw std::runtime_error("workgroup out of range");
+    const int f = kgx::rmsnorm_first_row(workgroup, region, per_wg);
+    *first_row = f;
+    *count = f < rows ? std::min(per_wg, rows - f) : 0;
+  });
+}
+
 int kg_conv_weight_load(int ks, int ic, int oc, int split, int q, int wave, int lane, int* src_row, int* src_chunk,
                         int* dst_row, int* dst_chunk) {
   return guarded([&] {

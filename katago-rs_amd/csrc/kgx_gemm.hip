@@ -595,41 +595,65 @@ static void gemm_launch(const GemmArgs& g, hipStream_t s) {
   }
 }
 
+// The tile a GEMM runs on (gemm_cfg launches it; gemm_row_tile reports its rows).
+enum GemmTile { GT_HEADF, GT_HEAD, GT_NARROW, GT_MID, GT_QKV, GT_WIDE, GT_SMALL };
+static GemmTile gemm_tile_choice(const GemmArgs& g, int tsize, bool af) {
+  const int bkh = 64, bk = tsize == 2 ? bkh : bkh / 2;
+  if (g.N > 64 && g.N <= 96 && g.K % 64 == 0 && tsize == 4) return GT_HEADF;
+  if (g.N > 64 && g.N <= 96 && g.K % bk == 0) return GT_HEAD;
+  if (g.N > 128 && g.N <= 192 && g.K % bk == 0) return GT_NARROW;
+  if (g.N > 192 && g.N <= 384 && g.K % bk == 0 && af) return GT_NARROW;
+  if (af) return GT_SMALL;  // (float-A prologue kernels are not built on the wide tile: their staging registers spill there)
+  if (tsize == 2) {
+    // Also when a short-K GEMM's last round of 128x128 tiles would be under a quarter full.
+    const long wide_tiles = (long)((g.M + 127) / 128) * ((g.N + 127) / 128);
+    const bool tail = (wide_tiles % 512) * 4 < 512 && g.K <= 512;
+    if (g.N > 128 && g.K % bk == 0 && !g.qkv.dq && g.Z == 1 && (wide_tiles < 512 || tail)) return GT_MID;
+    if (g.qkv.dq && g.N > 128 && g.K % bk == 0 && g.Z == 1 && wide_tiles < 1024) return GT_QKV;
+    // Also for a GEMM whose 128x128 grid is under three rounds with its last round under half full (the batch-64
+    // nets' N = 512 and 768 out projections and FFN2: b10c512h8 out 35.2 -> 31.5 us, +0.9 % end to end; tf3-b11c768
+    // FFN2 173.6 -> 167.3 us, out 65.9 -> 60.5, +0.5 %).
+    const long last = wide_tiles % 512;
+    if (!g.qkv.dq && g.N > 128 && g.K % bk == 0 && g.Z == 1 && wide_tiles < 3 * 512 && last > 0 && 2 * last < 512)
+      return GT_QKV;
+  }
+  if (g.N > 128 && g.K % bk == 0 && (long)((g.M + 127) / 128) * ((g.N + 127) / 128) * g.Z >= 256) return GT_WIDE;
+  return GT_SMALL;
+}
+
+int gemm_row_tile(int prec, int M, int N, int K) {
+  GemmArgs g;
+  g.M = M; g.N = N; g.K = K;
+  switch (gemm_tile_choice(g, prec == PREC_F32 ? 4 : 2, false)) {
+    case GT_HEADF: return CfgHeadF::BM;
+    case GT_HEAD: return CfgHead::BM;
+    case GT_NARROW: return CfgNarrow::BM;
+    case GT_MID: return CfgMid::BM;
+    case GT_QKV: return CfgQkv::BM;
+    case GT_WIDE: return CfgWide::BM;
+    default: return CfgSmall::BM;
+  }
+}
+
 template <typename T, bool AF, bool PRO, int ACT>
 static void gemm_cfg(const GemmArgs& g, hipStream_t s) {
-  const int bkh = 64, bk = sizeof(T) == 2 ? bkh : bkh / 2;
-  if (g.N > 64 && g.N <= 96 && g.K % 64 == 0 && sizeof(T) == 4) {
-    if constexpr (sizeof(T) == 4) gemm_launch<T, CfgHeadF, AF, PRO, ACT>(g, s);  // (built for float only)
-  } else if (g.N > 64 && g.N <= 96 && g.K % bk == 0) gemm_launch<T, CfgHead, AF, PRO, ACT>(g, s);
-  else if (g.N > 128 && g.N <= 192 && g.K % bk == 0) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
-  else if (g.N > 192 && g.N <= 384 && g.K % bk == 0 && AF) gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s);
-  else if constexpr (!AF) {
-    // (Float-A prologue kernels are not built on the wide tile: their staging registers spill there.)
-    if constexpr (sizeof(T) == 2) {
-      // Also when a short-K GEMM's last round of 128x128 tiles would be under a quarter full.
-      const long wide_tiles = (long)((g.M + 127) / 128) * ((g.N + 127) / 128);
-      const bool tail = (wide_tiles % 512) * 4 < 512 && g.K <= 512;
-      if (g.N > 128 && g.K % bk == 0 && !g.qkv.dq && g.Z == 1 && (wide_tiles < 512 || tail)) {
-        gemm_launch<T, CfgMid, AF, PRO, ACT>(g, s);
-        return;
-      }
-      if (g.qkv.dq && g.N > 128 && g.K % bk == 0 && g.Z == 1 && wide_tiles < 1024) {
-        gemm_launch<T, CfgQkv, AF, PRO, ACT>(g, s);
-        return;
-      }
-      // Also for a GEMM whose 128x128 grid is under three rounds with its last round under half full (the batch-64
-      // nets' N = 512 and 768 out projections and FFN2: b10c512h8 out 35.2 -> 31.5 us, +0.9 % end to end; tf3-b11c768
-      // FFN2 173.6 -> 167.3 us, out 65.9 -> 60.5, +0.5 %).
-      const long last = wide_tiles % 512;
-      if (!g.qkv.dq && g.N > 128 && g.K % bk == 0 && g.Z == 1 && wide_tiles < 3 * 512 && last > 0 && 2 * last < 512) {
-        gemm_launch<T, CfgQkv, AF, PRO, ACT>(g, s);
-        return;
-      }
-    }
-    if (g.N > 128 && g.K % bk == 0 && (long)((g.M + 127) / 128) * ((g.N + 127) / 128) * g.Z >= 256)
-      gemm_launch<T, CfgWide, AF, PRO, ACT>(g, s);
-    else gemm_launch<T, CfgSmall, AF, PRO, ACT>(g, s);
-  } else gemm_launch<T, CfgSmall, AF, PRO, ACT>(g, s);
+  switch (gemm_tile_choice(g, (int)sizeof(T), AF)) {
+    case GT_HEADF:
+      if constexpr (sizeof(T) == 4) gemm_launch<T, CfgHeadF, AF, PRO, ACT>(g, s);  // (built for float only)
+      break;
+    case GT_HEAD: gemm_launch<T, CfgHead, AF, PRO, ACT>(g, s); break;
+    case GT_NARROW: gemm_launch<T, CfgNarrow, AF, PRO, ACT>(g, s); break;
+    case GT_MID:
+      if constexpr (sizeof(T) == 2 && !AF) gemm_launch<T, CfgMid, AF, PRO, ACT>(g, s);
+      break;
+    case GT_QKV:
+      if constexpr (sizeof(T) == 2 && !AF) gemm_launch<T, CfgQkv, AF, PRO, ACT>(g, s);
+      break;
+    case GT_WIDE:
+      if constexpr (!AF) gemm_launch<T, CfgWide, AF, PRO, ACT>(g, s);
+      break;
+    default: gemm_launch<T, CfgSmall, AF, PRO, ACT>(g, s); break;
+  }
 }
 
 template <typename T>

@@ -138,6 +138,8 @@ struct GemmArgs {
   bool vec_epi = false;  // set by launch_gemm: the four-column vector epilogue applies
 };
 void launch_gemm(int prec, const GemmArgs& g, hipStream_t s);
+// The rows of the row tile that launch_gemm runs a plain GEMM of these sizes on (row tile r on XCD r mod 8).
+int gemm_row_tile(int prec, int M, int N, int K);
 
 // Implicit-GEMM 1x1 / 3x3 "same" convolution on 16-bit operands: x compute-type NHWC rows of ldx (IC channels,
 // IC % 8 == 0), w the compute-type conversion of conv_igemm_pack_weights' layout (icp = conv_igemm_icp(ks, IC)),
@@ -353,9 +355,25 @@ void launch_head_spatial(const HeadSpatialArgs& a, int B, hipStream_t s);
 // stream, without a DMA engine's start-up. Both pointers 16-byte aligned.
 void launch_readback(const float* src, float* host_dst, size_t n, hipStream_t s);
 
+// The first row of RMSNorm workgroup g when each takes per_wg consecutive rows: g per_wg, or (region > 0: the rows
+// written in row tiles of `region` rows, tile r on XCD r mod 8, and region a multiple of per_wg) share `sub` of tile
+// x + 8 k, x = g mod 8 being the workgroup's XCD.
+__host__ __device__ inline int rmsnorm_first_row(int g, int region, int per_wg) {
+  if (region <= 0) return g * per_wg;
+  const int wpr = region / per_wg, slot = g >> 3, k = slot / wpr, sub = slot - k * wpr;
+  return ((g & 7) + 8 * k) * region + sub * per_wg;
+}
+__host__ __device__ inline int rmsnorm_grid(int rows, int region, int per_wg) {
+  return region > 0 ? 8 * ((rows + 8 * region - 1) / (8 * region)) * (region / per_wg) : (rows + per_wg - 1) / per_wg;
+}
+// Rows per workgroup of the vector RMSNorm kernel for rows of C channels (0: C takes the scalar kernel).
+int rmsnorm_rows_per_workgroup(int C);
+
 // Per-token RMSNorm of transformer blocks: out = x * (1/sqrt(sum(x^2)/C + eps)) * w * mask[row] (compute type).
+// region > 0: x was written in row tiles of `region` rows, tile r on XCD r mod 8, and each workgroup takes its rows
+// from a tile of its own XCD, so that they come from the L2 that holds them.
 void launch_rmsnorm_tok(int prec, const float* x, int ldx, int C, const float* w, float eps, const float* mask,
-                        void* out, int ldo, int rows, hipStream_t s);
+                        void* out, int ldo, int rows, hipStream_t s, int region = 0);
 
 // Trunk-tip RMSNorm: act(x * rms * gamma + beta) * mask, rms per point or over the board (spatial).
 void launch_tip_rms(const float* x, int C, const float* gamma, const float* beta, float eps, bool spatial, int act,

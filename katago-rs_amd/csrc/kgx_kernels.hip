@@ -890,12 +890,12 @@ template <typename T, int NV, int LPR>
 __global__ __launch_bounds__(256) void rmsnorm_lanes_kernel(const float* __restrict__ x, int ldx, int C,
                                                             const float* __restrict__ w, float eps,
                                                             const float* __restrict__ mask, T* __restrict__ out,
-                                                            int ldo, int rows) {
+                                                            int ldo, int rows, int region) {
   // Two passes (row groups per lane group) when a pass covers at most two rows of a wave, else one: two to four rows
   // per wave (C = 512 at 64 lanes per row is slower at four rows per wave than at two).
-  constexpr int lpr = LPR, rg = 64 / LPR, PASSES = rg <= 2 ? 2 : 1;
+  constexpr int lpr = LPR, rg = 64 / LPR, PASSES = rg <= 2 ? 2 : 1, PER_WG = 4 * rg * PASSES;
   const int lane = threadIdx.x & 63, g = lane / lpr, l = lane - g * lpr;
-  const int row0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * rg * PASSES + g;
+  const int row0 = rmsnorm_first_row(blockIdx.x, region, PER_WG) + (threadIdx.x >> 6) * rg * PASSES + g;
   floatx4 v[PASSES][NV][2], wv[NV][2];
 #pragma unroll
   for (int p = 0; p < PASSES; p++) {
@@ -940,51 +940,63 @@ __global__ __launch_bounds__(256) void rmsnorm_lanes_kernel(const float* __restr
 
 template <typename T, int NV, int LPR>
 static void rmsnorm_lanes(const float* x, int ldx, int C, const float* w, float eps, const float* mask, T* out, int ldo,
-                          int rows, hipStream_t s) {
+                          int rows, hipStream_t s, int region) {
   constexpr int rg = 64 / LPR, per_wg = 4 * rg * (rg <= 2 ? 2 : 1);
-  launch_k(rmsnorm_lanes_kernel<T, NV, LPR>, (rows + per_wg - 1) / per_wg, 256, 0, s, x, ldx, C, w, eps, mask, out, ldo, rows);
+  if (region % per_wg) region = 0;  // (a tile that is not whole workgroups: consecutive rows)
+  launch_k(rmsnorm_lanes_kernel<T, NV, LPR>, rmsnorm_grid(rows, region, per_wg), 256, 0, s, x, ldx, C, w, eps, mask, out,
+           ldo, rows, region);
 }
 
 template <typename T, int LPR>
 static bool rmsnorm_nv(int nv, const float* x, int ldx, int C, const float* w, float eps, const float* mask, T* out,
-                       int ldo, int rows, hipStream_t s) {
+                       int ldo, int rows, hipStream_t s, int region) {
   switch (nv) {
-    case 1: rmsnorm_lanes<T, 1, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s); return true;
-    case 2: rmsnorm_lanes<T, 2, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s); return true;
-    case 3: rmsnorm_lanes<T, 3, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s); return true;
-    case 4: rmsnorm_lanes<T, 4, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s); return true;
+    case 1: rmsnorm_lanes<T, 1, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s, region); return true;
+    case 2: rmsnorm_lanes<T, 2, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s, region); return true;
+    case 3: rmsnorm_lanes<T, 3, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s, region); return true;
+    case 4: rmsnorm_lanes<T, 4, LPR>(x, ldx, C, w, eps, mask, out, ldo, rows, s, region); return true;
     default: return false;
   }
+}
+
+int rmsnorm_rows_per_workgroup(int C) {
+  const int v8 = C / 8;
+  if (C % 8 || v8 < 1) return 0;
+  int lpr = 64;
+  while (lpr > 4 && v8 % lpr) lpr >>= 1;
+  if (v8 % lpr || v8 / lpr > 4) return 0;
+  const int rg = 64 / lpr;
+  return 4 * rg * (rg <= 2 ? 2 : 1);
 }
 
 // The lane layout of a row of C channels: LPR = the largest power of two up to 64 dividing C / 8, NV = C / (8 LPR);
 // layouts with more than four vectors per lane take the scalar kernel.
 template <typename T>
 static bool rmsnorm_vec(const float* x, int ldx, int C, const float* w, float eps, const float* mask, T* out, int ldo,
-                        int rows, hipStream_t s) {
+                        int rows, hipStream_t s, int region) {
   const int v8 = C / 8;
   int lpr = 64;
   while (lpr > 4 && v8 % lpr) lpr >>= 1;
   if (v8 % lpr) return false;
   const int nv = v8 / lpr;
   switch (lpr) {
-    case 64: return rmsnorm_nv<T, 64>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s);
-    case 32: return rmsnorm_nv<T, 32>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s);
-    case 16: return rmsnorm_nv<T, 16>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s);
-    case 8: return rmsnorm_nv<T, 8>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s);
-    default: return rmsnorm_nv<T, 4>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s);
+    case 64: return rmsnorm_nv<T, 64>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s, region);
+    case 32: return rmsnorm_nv<T, 32>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s, region);
+    case 16: return rmsnorm_nv<T, 16>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s, region);
+    case 8: return rmsnorm_nv<T, 8>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s, region);
+    default: return rmsnorm_nv<T, 4>(nv, x, ldx, C, w, eps, mask, out, ldo, rows, s, region);
   }
 }
 
 void launch_rmsnorm_tok(int prec, const float* x, int ldx, int C, const float* w, float eps, const float* mask,
-                        void* out, int ldo, int rows, hipStream_t s) {
+                        void* out, int ldo, int rows, hipStream_t s, int region) {
   const int tsz = prec == PREC_F32 ? 4 : 2;
   if (rows > 0 && C % 8 == 0 && ldx % 4 == 0 && ldo % (16 / tsz) == 0 &&
       ((uintptr_t)x | (uintptr_t)w) % 16 == 0 && (uintptr_t)out % 16 == 0) {
     bool done;
-    if (prec == PREC_F16) done = rmsnorm_vec<f16>(x, ldx, C, w, eps, mask, (f16*)out, ldo, rows, s);
-    else if (prec == PREC_BF16) done = rmsnorm_vec<bf16>(x, ldx, C, w, eps, mask, (bf16*)out, ldo, rows, s);
-    else done = rmsnorm_vec<float>(x, ldx, C, w, eps, mask, (float*)out, ldo, rows, s);
+    if (prec == PREC_F16) done = rmsnorm_vec<f16>(x, ldx, C, w, eps, mask, (f16*)out, ldo, rows, s, region);
+    else if (prec == PREC_BF16) done = rmsnorm_vec<bf16>(x, ldx, C, w, eps, mask, (bf16*)out, ldo, rows, s, region);
+    else done = rmsnorm_vec<float>(x, ldx, C, w, eps, mask, (float*)out, ldo, rows, s, region);
     if (done) {
       KGX_CHECK_LAUNCH();
       return;

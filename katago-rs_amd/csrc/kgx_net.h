@@ -174,6 +174,9 @@ class Net {
   bool l2_prefetch_ = true;  // kernels touch the next op's weights into L2 (KGX_L2_PREFETCH=0: off)
   bool gpool_tile_ = true;   // gpool blocks' mid activation per pixel tile (KGX_GPOOL_TILE=0: per row)
   std::unique_ptr<PendingExit> pend_;
+  // The token GEMM that last added into a residual stream (its N and K; 0 when another op wrote the stream last): the
+  // RMSNorm that reads the stream next takes its rows in that GEMM's row tiles, on the XCDs that wrote them.
+  int res_n_ = 0, res_k_ = 0;
   int wino_tm_ = 4;
   int nin_ = 0, nglob_ = 0, nmeta_ = 0, row_len_ = 0;
   std::vector<std::unique_ptr<DeviceBuffer>> mem_;

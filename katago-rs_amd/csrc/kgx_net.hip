@@ -534,7 +534,11 @@ void Net::emit_attention(const BlockDesc& b, int depth) {
   void* nrm = nrm_;
   const float* mask = mask_;
   Op rn;
-  rn.launch = [=](hipStream_t s, int B) { launch_rmsnorm_tok(prec, x, c, c, lnw, eps, mask, nrm, c, B * HW, s); };
+  const int rn_n = res_n_, rn_k = res_k_;
+  rn.launch = [=](hipStream_t s, int B) {
+    const int region = rn_n ? gemm_row_tile(prec, B * HW, rn_n, rn_k) : 0;
+    launch_rmsnorm_tok(prec, x, c, c, lnw, eps, mask, nrm, c, B * HW, s, region);
+  };
   rn.cls = "rmsnorm";
   rn.bytes_row = (double)HW * c * (4 + tsize());
   ops_.push_back(rn);
@@ -564,6 +568,8 @@ void Net::emit_attention(const BlockDesc& b, int depth) {
   ConvOut oo;
   oo.y = x; oo.ldy = c; oo.accumulate = true; oo.rowmask = mask;
   ss_[depth].producer = emit_token_gemm(ao_, H * dv, dWo, c, H * dv, oo, "token_gemm_out");
+  res_n_ = c;
+  res_k_ = H * dv;
 }
 
 // TransformerFFNBlock (bin2onnx.py:1423-1438): RMSNorm, linear1 (| gate), SiLU(l1) * gate (the plain FFN, which
@@ -598,7 +604,11 @@ void Net::emit_ffn(const BlockDesc& b, int depth) {
   void* nrm = nrm_;
   const float* mask = mask_;
   Op rn;
-  rn.launch = [=](hipStream_t s, int B) { launch_rmsnorm_tok(prec, x, c, c, lnw, eps, mask, nrm, c, B * HW, s); };
+  const int rn_n = res_n_, rn_k = res_k_;
+  rn.launch = [=](hipStream_t s, int B) {
+    const int region = rn_n ? gemm_row_tile(prec, B * HW, rn_n, rn_k) : 0;
+    launch_rmsnorm_tok(prec, x, c, c, lnw, eps, mask, nrm, c, B * HW, s, region);
+  };
   rn.cls = "rmsnorm";
   rn.bytes_row = (double)HW * c * (4 + tsize());
   ops_.push_back(rn);
@@ -627,6 +637,8 @@ void Net::emit_ffn(const BlockDesc& b, int depth) {
   ConvOut o2;
   o2.y = x; o2.ldy = c; o2.accumulate = true; o2.rowmask = mask;
   ss_[depth].producer = emit_token_gemm(h_, F, dW2, c, F, o2, "token_gemm_ffn2");
+  res_n_ = c;
+  res_k_ = F;
 }
 
 void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
@@ -639,6 +651,7 @@ void Net::emit_stack(const std::vector<BlockDesc>& blocks, int depth) {
     res.y = x;
     res.ldy = c;
     res.accumulate = true;
+    if (b.kind != BLOCK_ATTN && b.kind != BLOCK_FFN) res_n_ = res_k_ = 0;
     switch (b.kind) {
       case BLOCK_RES: {
         // x += conv2(bnact(conv1(bnact(x)))) (bin2onnx.py:1243-1249); conv1 writes only conv2's activation.

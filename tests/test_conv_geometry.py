@@ -141,3 +141,23 @@ def test_l2_touch_covers_each_line_once_per_xcd(kgx, grid, threads):
         wgs = [g for g in range(x, grid, 8)]
         lines = collections.Counter(kgx.l2_touch_line(grid, g, t) for g in wgs for t in range(threads))
         assert set(lines) == set(range(len(wgs) * threads)) and all(v == 1 for v in lines.values()), (grid, x)
+
+
+@pytest.mark.parametrize("channels", [384, 512, 768])
+@pytest.mark.parametrize("region", [0, 64, 96, 128, 192, 40])
+def test_rmsnorm_rows_cover_each_row_once_from_its_tile_xcd(kgx, channels, region):
+    """The RMSNorm launch after a residual token GEMM: every token row is taken once, and (region > 0, a multiple
+    of the rows per workgroup) a workgroup's rows lie in one row tile of `region` rows that was written on its own
+    XCD (tile r on XCD r mod 8; workgroup g runs on XCD g mod 8). A region that is not whole workgroups (40) falls
+    back to consecutive rows."""
+    for batch in (1, 5, 32, 64):
+        rows = batch * 361
+        grid, _, _ = kgx.rmsnorm_rows_of(rows, channels, region, 0)
+        seen = collections.Counter()
+        for g in range(grid):
+            _, first, count = kgx.rmsnorm_rows_of(rows, channels, region, g)
+            for r in range(first, first + count):
+                seen[r] += 1
+            if count and region in (64, 96, 128, 192):
+                assert (first // region) % 8 == g % 8 and (first + count - 1) // region == first // region, (g, first)
+        assert set(seen) == set(range(rows)) and all(v == 1 for v in seen.values()), (channels, region, batch)
