@@ -785,29 +785,46 @@ __global__ __launch_bounds__(256) void head_spatial_kernel(HeadSpatialArgs a) {
     vt[k] = okv ? a.v1_shift[c] : 0.f;
     wo[k] = okv ? a.w_own[c] : 0.f;
   }
+  // The slot's HS_PTS / 16 points: every load of all of them first (clamped points, no branch around a load), so that
+  // the thread waits for memory once, then the sums; points past the row compute on the clamped copy and store nothing.
+  constexpr int NP = HS_PTS / 16;
   const int p_end = min(HW, ((int)blockIdx.x + 1) * HS_PTS);
-  for (int pos = blockIdx.x * HS_PTS + slot; pos < p_end; pos += 16) {
+  float hp[NP][HK], hv[NP][HK], mkp[NP];
+#pragma unroll
+  for (int i = 0; i < NP; i++) {
+    const int pos = min(blockIdx.x * HS_PTS + slot + 16 * i, p_end - 1);
     const float* h = a.H + ((size_t)b * HW + pos) * a.ldh;
-    const float mk = a.mask[(size_t)b * HW + pos];
+    mkp[i] = a.mask[(size_t)b * HW + pos];
+#pragma unroll
+    for (int k = 0; k < HK; k++) {
+      const int c = l16 + 16 * k;
+      hp[i][k] = h[a.p1_off + min(c, a.c_p1 - 1)];
+      hv[i][k] = h[a.v1_off + min(c, a.c_v1 - 1)];
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < NP; i++) {
+    const int pos = blockIdx.x * HS_PTS + slot + 16 * i;
+    const float mk = mkp[i];
     float pol[4] = {0.f, 0.f, 0.f, 0.f}, own = 0.f;
 #pragma unroll
     for (int k = 0; k < HK; k++) {
       const int c = l16 + 16 * k;
       if (c < a.c_p1) {
-        const float v = act_f<ACT>((h[a.p1_off + c] + pb[k]) * ps[k] + pt[k]) * mk;
+        const float v = act_f<ACT>((hp[i][k] + pb[k]) * ps[k] + pt[k]) * mk;
 #pragma unroll
         for (int p = 0; p < 4; p++) pol[p] += v * w2[k][p];
       }
-      if (c < a.c_v1) own += act_f<ACT>(h[a.v1_off + c] * vs[k] + vt[k]) * mk * wo[k];
+      if (c < a.c_v1) own += act_f<ACT>(hv[i][k] * vs[k] + vt[k]) * mk * wo[k];
     }
-    // The 16 lanes of a point share its trip count, so the exchanges stay within active lanes.
+    // The 16 lanes of a point run every step alike, so the exchanges stay within active lanes.
 #pragma unroll
     for (int off = 8; off > 0; off >>= 1) {
 #pragma unroll
       for (int p = 0; p < 4; p++) pol[p] += __shfl_xor(pol[p], off);
       own += __shfl_xor(own, off);
     }
-    if (l16 == 0) {
+    if (l16 == 0 && pos < p_end) {
       float* row = a.out + (size_t)b * a.row_len;
 #pragma unroll
       for (int p = 0; p < 4; p++)
@@ -831,6 +848,7 @@ static void head_spatial_launch(const HeadSpatialArgs& a, int B, hipStream_t s) 
 void launch_head_spatial(const HeadSpatialArgs& a, int B, hipStream_t s) {
   if (a.P > 4) throw std::runtime_error("head: more than 4 policy channels");
   if (a.p1_act != a.v1_act) throw std::runtime_error("head: p1 and v1 activations differ");
+  if (a.c_p1 < 1 || a.c_v1 < 1) throw std::runtime_error("head: no p1 or v1 channels");  // (the loads clamp to them)
   const int c = std::max(a.c_p1, a.c_v1);
   if (c <= 32) head_spatial_launch<2>(a, B, s);
   else if (c <= 64) head_spatial_launch<4>(a, B, s);
