@@ -314,8 +314,10 @@ __device__ void row_mm(const RowMM& m, int b, float* lds, float* red, int o_begi
           wv[j] = i < m.IC ? wcol[(size_t)i * wst] : 0.f;
           xv[j] = i < m.IC ? (gin ? gin[i] : lin[i]) : 0.f;
         }
+        // Explicit fused multiply-adds, as in the gpool tile kernel's matmul, which gives the same bits: the
+        // compiler's contraction of a multiply and an add may differ between the two loops.
 #pragma unroll
-        for (int j = 0; j < KB; j++) acc += xv[j] * wv[j];
+        for (int j = 0; j < KB; j++) acc = __builtin_fmaf(xv[j], wv[j], acc);
       }
     }
     red[w * 64 + lane] = acc;
@@ -696,9 +698,9 @@ __global__ __launch_bounds__(GT_NT) void gpool_tile_kernel(GpoolTile a, int M) {
         w[j] = wo[(i + j * GT_KS) * SH];
       }
 #pragma unroll
-      for (int j = 0; j < 4; j++) acc += f[j] * w[j];
+      for (int j = 0; j < 4; j++) acc = __builtin_fmaf(f[j], w[j], acc);  // (fused, as in row_mm)
     }
-    for (; i < IC; i += GT_KS) acc += fr[i] * wo[i * SH];
+    for (; i < IC; i += GT_KS) acc = __builtin_fmaf(fr[i], wo[i * SH], acc);
     part[(r * GT_KS + ks) * SH + o] = acc;
   }
   __syncthreads();

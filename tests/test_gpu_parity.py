@@ -197,6 +197,30 @@ def test_sharp_attention_matches_the_16bit_network(kgx, synth, oracle, prec, qk_
         assert e <= bound, f"qk_gain {qk_gain} [{prec}] {k}: {e:.3e} > {bound:.3e}"
 
 
+@pytest.mark.parametrize("prec", ["f32", "f16"])
+@pytest.mark.parametrize("p1,v1", [(48, 64), (96, 80)])
+def test_head_widths_match_oracle(kgx, synth, oracle, p1, v1, prec):
+    """Policy and value heads wider than the configs' 32 channels: the spatial heads' lanes then hold 4 and 8
+    channels each (head_spatial_kernel's HK), and the row programs pool 48 to 96 channels in one or two chunks;
+    against the oracle."""
+    import dataclasses
+    print(f"heads p1 {p1} v1 {v1} [{prec}]", flush=True)
+    arch = dataclasses.replace(synth.tiny_nets()["t_res"], p1_c=p1, v1_c=v1)
+    mb = synth.write_model(arch, 4)
+    sp, gl, _ = synth.make_inputs(6, 8, board_sizes=[19, 13, 9, 19, 7, 19])
+    net = kgx.Net(mb)
+    h = kgx.Handle(net, 6, prec)
+    h.profile(True)
+    h.profile_reset()
+    out = h.forward(sp, gl)
+    prof = h.profile_read()
+    h.profile(False)
+    h.close()
+    assert prof["row_prog_heads"]["launches"] == 1 and prof["head"]["launches"] == 1, prof.keys()
+    check(out, oracle.Model(mb).forward(sp, gl), net.P, net.S, prec, f"heads {p1}/{v1}",
+          emulated(oracle, mb, prec, sp, gl))
+
+
 @pytest.mark.parametrize("prec", ["f16", "bf16"])
 def test_mish_at_extreme_inputs_matches_the_16bit_network(kgx, synth, oracle, prec):
     """16-bit emissions compute mish as b - 2 b q with b = a * mask, q = 1 / (e (e + 2) + 2), e = exp(a), with no
