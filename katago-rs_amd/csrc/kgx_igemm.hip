@@ -852,10 +852,12 @@ void launch_conv_igemm(int prec, int ks, const void* x, int ldx, int IC, const v
   KGX_CHECK_LAUNCH();
 }
 
-// Network input of one batch row per workgroup (one thread per board point): the planes, float NCHW [nin][361], to
-// compute-type NHWC rows of ldo channels (zero beyond nin, 16-byte stores), and the board statistics of
-// launch_mask_prep: mask = plane 0, area = its sum, s1 = (sqrt(area) - 14) 0.1, s2 = (sqrt(area) - 14)^2 0.01 - 0.1.
-// Workgroups (b, 1) compute the row's global-input bias of the stem instead (when `gl.W` is set).
+// Network input of one batch row and one group of 8 packed channels per workgroup (one thread per board point):
+// the planes, float NCHW [nin][361], to compute-type NHWC rows of ldo channels (zero beyond nin, one 16-byte store
+// per point), and, in the row's first group, the board statistics of launch_mask_prep: mask = plane 0, area = its
+// sum, s1 = (sqrt(area) - 14) 0.1, s2 = (sqrt(area) - 14)^2 0.01 - 0.1. Workgroups (b, ldo / 8) compute the row's
+// global-input bias of the stem instead (when `gl.W` is set). Groups of 8 channels spread the input's first touch
+// over four times as many CUs as whole rows did (each CU's share of cache lines in flight is what its time waits on).
 constexpr int IP_C = 32, IP_G = 32;  // the input packing's most planes (packed channels) and globals
 
 template <typename T>
@@ -863,10 +865,10 @@ __global__ __launch_bounds__(384) void input_prep_kernel(const float* __restrict
                                                          int ldo, float* __restrict__ mask, float* __restrict__ area,
                                                          float* __restrict__ s1, float* __restrict__ s2,
                                                          InputGlobal gl) {
-  const int b = blockIdx.x, p = threadIdx.x;
+  const int b = blockIdx.x, p = threadIdx.x, grp = blockIdx.y;
   // Every load is issued before any is used, from clamped (in-range) indices with no branch around it, so that a
   // thread waits for one round trip instead of one per load; the values past the real ones are then replaced.
-  if (blockIdx.y == 1) {
+  if (grp == ldo / 8) {
     // Up to IP_G globals in flight per output; the sum runs over i < nglob in order, as one multiply-add each.
     for (int o = p; o < gl.C; o += 384) {
       float g[IP_G], w[IP_G];
@@ -885,25 +887,23 @@ __global__ __launch_bounds__(384) void input_prep_kernel(const float* __restrict
     return;
   }
   __shared__ float red[6];
+  const int c0 = grp * 8;
   const float* src = bin + (size_t)b * nin * HW + min(p, HW - 1);
-  float mk = 0.f;
-  float v[IP_C];
+  float v[8];
 #pragma unroll
-  for (int c = 0; c < IP_C; c++) v[c] = src[(size_t)min(c, nin - 1) * HW];
+  for (int c = 0; c < 8; c++) v[c] = src[(size_t)min(c0 + c, nin - 1) * HW];
 #pragma unroll
-  for (int c = 0; c < IP_C; c++)
-    if (c >= nin) v[c] = 0.f;
+  for (int c = 0; c < 8; c++)
+    if (c0 + c >= nin) v[c] = 0.f;
   if (p < HW) {
-    T* o = out + ((size_t)b * HW + p) * ldo;
+    T t[8];
 #pragma unroll
-    for (int c0 = 0; c0 < IP_C; c0 += 8) {
-      if (c0 < ldo) {
-        T t[8];
-#pragma unroll
-        for (int k = 0; k < 8; k++) t[k] = to_t<T>(v[c0 + k]);
-        *(u32x4*)(o + c0) = *(const u32x4*)t;
-      }
-    }
+    for (int k = 0; k < 8; k++) t[k] = to_t<T>(v[k]);
+    *(u32x4*)(out + ((size_t)b * HW + p) * ldo + c0) = *(const u32x4*)t;
+  }
+  if (grp != 0) return;
+  float mk = 0.f;
+  if (p < HW) {
     mk = v[0];
     mask[(size_t)b * HW + p] = mk;
   }
@@ -927,7 +927,7 @@ void launch_input_prep(int prec, const float* bin, int nin, void* out, int ldo, 
     throw std::runtime_error("input_prep: bad packed channel count");
   if (gl.W && (!gl.glob || !gl.out || gl.C < 1 || gl.nglob < 1 || gl.nglob > IP_G))
     throw std::runtime_error("input_prep: bad global-input bias arguments");
-  const dim3 grid(B, gl.W ? 2 : 1);
+  const dim3 grid(B, ldo / 8 + (gl.W ? 1 : 0));
   if (prec == PREC_F16)
     launch_k(input_prep_kernel<f16>, grid, 384, 0, s, bin, nin, (f16*)out, ldo, mask, area, s1, s2, gl);
   else if (prec == PREC_BF16)
